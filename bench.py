@@ -1,0 +1,218 @@
+"""Benchmark of the MI355X sparse projection-and-pool layer (one JSON line on stdout).
+
+Workload (BASELINE.json metric "train-step ms & G edge-MAC/s at 100M neurons fan-in 8, B=256"):
+one training step of the C2-shaped layer -- N = 100,663,296 neurons, fan-in 8, D = 4096 inputs,
+B = 256 tokens, pools of 1024 (G = 98,304), ReLU + sum pooling, fp32 X / W / moments -- made of
+the fused forward, the recompute backward (dX, dW and db into fp32 main_grad) and the fused
+AdamW step (lr 1e-3, betas 0.9/0.999, eps 1e-8, wd 0).  Synthetic seeded data: indices uniform
+and distinct per neuron, W ~ N(0, 1/8), bias 0, X and dY ~ N(0, 1).  The forward-only time of the
+same layer (the headline forward) is reported beside it.
+
+value = useful edge-MACs per second of the whole step (B * N * 8 / step time, one pass, as the
+reference's useful_tflops(passes=1), sparse_pooling/benchmarks/common.py:80-82).
+
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+# MI355X published peaks
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+
+CFG = dict(N=100_663_296, K=8, D=4096, B=256, pool=1024)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def algorithmic(kernel: str, B: int, N: int, K: int, D: int, G: int, x_bytes: int = 4):
+    """(bytes, flops) per launch of a kernel: each input read once, each output written once."""
+    E = N * K
+    if kernel == "fwd_kernel":
+        return 4 * E + 4 * E + 4 * N + B * D * x_bytes + 4 * B * G, 2 * B * E
+    if kernel == "bwd_w_kernel":
+        # params + X once, dW/db read-modify-write, per-neuron {w, mask} record written
+        return 4 * E + 4 * E + 4 * N + B * D * x_bytes + 8 * E + 8 * N + 4 * E + N * B // 8, 4 * B * E
+    if kernel == "dx_kernel":
+        # edge records, each neuron's {w, mask} record once per edge, dX partials
+        return 4 * E + E * (4 + B // 8) + 4 * B * D, 2 * B * E
+    if kernel == "adam_kernel":
+        return 32 * (E + N), 12 * (E + N)
+    return None, None
+
+
+def cpu_baseline(groups: int, steps: int):
+    import torch
+
+    from granulelayer_amd.synthetic import make_problem
+    from oracle.reference_port import PortStep
+
+    pr = make_problem("C2", device="cpu", seed=0, groups=groups)
+    st = PortStep(pr.idx, pr.w, pr.b, pr.layout.counts_tensor("cpu"), pr.layout.slots_per_group, pool="sum")
+    x = pr.x.float()
+    st.step(x, pr.dy)  # warm-up
+    times = [st.step(x, pr.dy)["step"] for _ in range(steps)]
+    t = sorted(times)[len(times) // 2]
+    macs = pr.B * pr.edges
+    return {"value": round(macs / t / 1e9, 4), "unit": "G edge-MAC/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"C2 train step (fwd+bwd+torch.optim.Adam) on {groups} of 98,304 pools "
+                       f"({groups * 1024:,} neurons, B=256, D=4096), materialising torch restatement of "
+                       f"sparse_pooling/reference on the host; median of {steps} steps = {t * 1e3:.1f} ms; "
+                       f"cpu: {cpu_model()}, os.cpu_count()={os.cpu_count()}")}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-groups", type=int, default=192, help="pools in the CPU baseline's sample")
+    ap.add_argument("--cpu-steps", type=int, default=5)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: this build measures one MI355X (--gpus {args.gpus} requested); "
+              "multi-GPU sharding is described in DESIGN.md but not implemented", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    from granulelayer_amd import FusedAdamW, SparsePoolingLayer
+    from granulelayer_amd._native import KernelTrace
+
+    N, K, D, B, pool = CFG["N"], CFG["K"], CFG["D"], CFG["B"], CFG["pool"]
+    G = N // pool
+    dev = torch.device("cuda", 0)
+    t0 = time.time()
+    log(f"building layer N={N:,} K={K} D={D} G={G:,} on {torch.cuda.get_device_name(0)}")
+    lay = SparsePoolingLayer(D, N, G, fan_in=K, shared_neurons=None, pooling="sum", dtype=torch.float32,
+                             device=dev, seed=0)
+    lay.enable_main_grad()
+    opt = FusedAdamW(lay.parameters(), lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, moments="fp32")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    x = torch.randn(B, D, generator=gen, device=dev)
+    dy = torch.randn(B, G, generator=gen, device=dev)
+    torch.cuda.synchronize()
+    log(f"layer ready in {time.time() - t0:.1f} s")
+
+    def step():
+        y = lay(x)
+        y.backward(dy)
+        opt.step()
+
+    for i in range(args.warmup):
+        step()
+        torch.cuda.synchronize()
+        log(f"warmup step {i + 1}/{args.warmup} done")
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with KernelTrace(max_launches=32 * args.steps) as tr:
+        ev0.record()
+        w0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        ev1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - w0
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    ktimes = tr.times_ms()
+    log(f"timed {args.steps} steps: {ms_step:.3f} ms/step (wall {wall / args.steps * 1e3:.3f} ms)")
+
+    # forward only (BASELINE C2 headline), same layer
+    with torch.no_grad():
+        for _ in range(2):
+            lay(x)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            lay(x)
+        e1.record()
+        torch.cuda.synchronize()
+    fwd_ms = e0.elapsed_time(e1) / args.steps
+    log(f"forward only: {fwd_ms:.3f} ms")
+
+    E = N * K
+    kernels = {}
+    for name, ts in ktimes.items():
+        avg = sum(ts) / len(ts)
+        by, fl = algorithmic(name, B, N, K, D, G)
+        rec = {"ms": round(avg, 4), "launches": len(ts)}
+        if by is not None:
+            rec["hbm_frac"] = round(by / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+            rec["valu_frac"] = round(fl / (avg * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4)
+        kernels[name] = rec
+    dom = max(ktimes, key=lambda n: sum(ktimes[n]) / args.steps)
+    dom_ms = sum(ktimes[dom]) / len(ktimes[dom])
+    by, fl = algorithmic(dom, B, N, K, D, G)
+    if dom == "adam_kernel":
+        roof = {"bound": "hbm", "achieved": round(by / (dom_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s"}
+    else:
+        roof = {"bound": "valu", "achieved": round(fl / (dom_ms * 1e-3) / 1e12, 2), "peak": FP32_PEAK_TFLOPS,
+                "unit": "TFLOP/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["kernel"] = dom
+    roof["ms"] = round(dom_ms, 4)
+    roof["traffic"] = None
+    roof["hbm_frac_algorithmic"] = round(by / (dom_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+
+    value = B * E / (ms_step * 1e-3) / 1e9
+    out = {
+        "metric": "train-step ms & G edge-MAC/s at 100M neurons fan-in 8, B=256; % of HBM peak",
+        "value": round(value, 2),
+        "unit": "G edge-MAC/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded: uniform distinct indices, W~N(0,1/8), bias 0, X and dY ~N(0,1))",
+        "config": {"workload": "C2-shaped train step: fwd + recompute bwd (dX, dW, db) + fused AdamW",
+                   "neurons": N, "fan_in": K, "d_in": D, "batch": B, "pool": pool, "groups": G,
+                   "pooling": "sum(relu)", "x_dtype": "f32", "moments": "f32", "parallelism": "single GPU"},
+        "fwd_ms": round(fwd_ms, 3),
+        "fwd_G_edge_macs_per_s": round(B * E / (fwd_ms * 1e-3) / 1e9, 2),
+        "kernels": kernels,
+        "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline: {args.cpu_groups} pools x {args.cpu_steps} steps")
+        out["cpu_baseline"] = cpu_baseline(args.cpu_groups, args.cpu_steps)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

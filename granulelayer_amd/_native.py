@@ -1,0 +1,177 @@
+"""ctypes binding of the HIP library (include/granulelayer_amd.h).
+
+The library is loaded from ``granulelayer_amd/lib/libgranulelayer_amd.so`` (built in-tree by
+``granulelayer_amd.build``).  At load the binding refuses a library whose ABI version or struct
+layouts differ from the structures below, like the reference's native bridge
+(sparse_pooling/backends/cuda/runtime.py:103-120, check_abi).  There is no fallback: every
+entry point of the product path raises if the library is missing or refuses a call.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgranulelayer_amd.so"
+ABI_VERSION = 1
+
+GL_ACT = {"identity": 0, "relu": 1}
+GL_POOL = {"mean": 0, "sum": 1}
+GL_DTYPE_F32, GL_DTYPE_BF16 = 0, 1
+
+_P, _I32, _I64, _SZ, _F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
+
+
+class GlFwdArgs(ctypes.Structure):
+    _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
+                ("K", _I32), ("act", _I32), ("pool", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
+                ("pre", _P), ("ws", _P), ("ws_bytes", _SZ)]
+
+
+class GlBwdArgs(ctypes.Structure):
+    _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
+                ("K", _I32), ("act", _I32), ("pool", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
+                ("g_pre", _P), ("dW", _P), ("db", _P), ("dX", _P), ("edges", _P), ("edges_bytes", _SZ),
+                ("ws", _P), ("ws_bytes", _SZ)]
+
+
+class GlEdgeArgs(ctypes.Structure):
+    _fields_ = [("idx", _P), ("counts", _P), ("D", _I32), ("G", _I32), ("S", _I32), ("K", _I32), ("edges", _P),
+                ("edges_bytes", _SZ), ("ws", _P), ("ws_bytes", _SZ)]
+
+
+class GlAdamArgs(ctypes.Structure):
+    _fields_ = [("p", _P), ("g", _P), ("m", _P), ("v", _P), ("n", _I64), ("moments_dtype", _I32), ("lr", _F),
+                ("beta1", _F), ("beta2", _F), ("eps", _F), ("weight_decay", _F), ("bc1", _F), ("bc2", _F)]
+
+
+STRUCTS = (GlFwdArgs, GlBwdArgs, GlEdgeArgs, GlAdamArgs)  # gl_struct_layout ids 0..3
+# every symbol include/granulelayer_amd.h declares
+EXPORTS = ("gl_abi_version", "gl_struct_layout", "gl_error_string", "gl_fwd_workspace", "gl_fwd", "gl_edges_size",
+           "gl_edges_build", "gl_bwd_workspace", "gl_bwd", "gl_adam", "gl_trace_begin", "gl_trace_end")
+KERNEL_NAMES = {1: "tile_x_kernel", 2: "fwd_kernel", 3: "fwd_finalize_kernel", 4: "c1t_kernel", 5: "bwd_w_kernel",
+                6: "dx_kernel", 7: "dx_reduce_kernel", 8: "adam_kernel", 9: "edges_build"}
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+def struct_layout(st) -> list:
+    return [ctypes.sizeof(st)] + [getattr(st, name).offset for name, _ in st._fields_]
+
+
+class Library:
+    """One loaded copy of the HIP library with typed entry points."""
+
+    def __init__(self, path: Path = LIB_PATH):
+        if not Path(path).exists():
+            raise NativeError(f"HIP library not found at {path}; build it with `python -m granulelayer_amd.build` "
+                              "(the MI355X path has no CPU or PyTorch fallback)")
+        self.path = Path(path)
+        self.lib = ctypes.CDLL(str(path))
+        L = self.lib
+        L.gl_abi_version.restype = ctypes.c_int
+        L.gl_struct_layout.restype = ctypes.c_int
+        L.gl_struct_layout.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_longlong), ctypes.c_int]
+        L.gl_error_string.restype = ctypes.c_char_p
+        L.gl_error_string.argtypes = [ctypes.c_int]
+        for name, st in (("gl_fwd", GlFwdArgs), ("gl_bwd", GlBwdArgs), ("gl_edges_build", GlEdgeArgs),
+                         ("gl_adam", GlAdamArgs)):
+            f = getattr(L, name)
+            f.restype, f.argtypes = ctypes.c_int, [ctypes.POINTER(st), _P]
+        for name, st in (("gl_fwd_workspace", GlFwdArgs), ("gl_bwd_workspace", GlBwdArgs)):
+            f = getattr(L, name)
+            f.restype, f.argtypes = ctypes.c_int, [ctypes.POINTER(st), ctypes.POINTER(_SZ)]
+        L.gl_trace_begin.restype = ctypes.c_int
+        L.gl_trace_begin.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(_I32), ctypes.c_int]
+        L.gl_trace_end.restype = ctypes.c_int
+        L.gl_trace_end.argtypes = []
+        L.gl_edges_size.restype = ctypes.c_int
+        L.gl_edges_size.argtypes = [ctypes.POINTER(GlEdgeArgs), ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]
+        self.check_abi()
+
+    def check_abi(self):
+        v = self.lib.gl_abi_version()
+        if v != ABI_VERSION:
+            raise NativeError(f"{self.path}: ABI version {v} != {ABI_VERSION} (stale library; rebuild)")
+        for which, st in enumerate(STRUCTS):
+            buf = (ctypes.c_longlong * 64)()
+            n = self.lib.gl_struct_layout(which, buf, 64)
+            want = struct_layout(st)
+            if n != len(want) or list(buf[:n]) != want:
+                raise NativeError(f"{self.path}: {st.__name__} layout mismatch (native {list(buf[:max(n, 0)])}, "
+                                  f"binding {want})")
+
+    def error(self, code: int) -> str:
+        return self.lib.gl_error_string(code).decode()
+
+    def call(self, name: str, *args):
+        r = getattr(self.lib, name)(*args)
+        if r != 0:
+            raise NativeError(f"{name} failed (code {r}: {self.error(r)})")
+        return r
+
+    def size_query(self, name: str, args) -> int:
+        out = _SZ(0)
+        self.call(name, ctypes.byref(args), ctypes.byref(out))
+        return int(out.value)
+
+    def edges_size(self, args: GlEdgeArgs):
+        e, w = _SZ(0), _SZ(0)
+        self.call("gl_edges_size", ctypes.byref(args), ctypes.byref(e), ctypes.byref(w))
+        return int(e.value), int(w.value)
+
+
+class KernelTrace:
+    """Per-kernel GPU time of the library's launches inside a ``with`` block, from HIP events
+    recorded around every launch on its own stream (gl_trace_begin / gl_trace_end).
+
+        with KernelTrace(max_launches=64) as tr:
+            ...                                # library calls
+        tr.times_ms()  -> {"fwd_kernel": [ms, ...], ...}
+    """
+
+    def __init__(self, max_launches: int = 256, lib: "Library" = None):
+        import torch
+
+        self.lib = lib or library()
+        self.events = [torch.cuda.Event(enable_timing=True) for _ in range(2 * max_launches)]
+        self._handles = (ctypes.c_void_p * (2 * max_launches))(*[e.cuda_event for e in self.events])
+        self._ids = (_I32 * max_launches)()
+        self.n = 0
+        self.max = max_launches
+
+    def __enter__(self):
+        for e in self.events:  # materialise the HIP events
+            if e.cuda_event == 0:
+                raise NativeError("torch event not created")
+        self.lib.call("gl_trace_begin", self._handles, self._ids, self.max)
+        return self
+
+    def __exit__(self, *exc):
+        self.n = self.lib.lib.gl_trace_end()
+        return False
+
+    def times_ms(self) -> dict:
+        import torch
+
+        torch.cuda.synchronize()
+        out = {}
+        for i in range(self.n):
+            name = KERNEL_NAMES.get(int(self._ids[i]), str(int(self._ids[i])))
+            out.setdefault(name, []).append(self.events[2 * i].elapsed_time(self.events[2 * i + 1]))
+        return out
+
+
+_lock = threading.Lock()
+_library = None
+
+
+def library() -> Library:
+    """The process-wide library (loaded on first use)."""
+    global _library
+    with _lock:
+        if _library is None:
+            _library = Library()
+        return _library

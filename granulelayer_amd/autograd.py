@@ -1,0 +1,215 @@
+"""Custom autograd: forward saves no hidden activations; backward recomputes them.
+
+Mirrors sparse_pooling/autograd.py for the single-level Mean / Sum path:
+
+* ``Level1Runtime`` (autograd.py:68-300): executes the fused kernels of one layer, holds no
+  tensor of size [B, H], records ``last_info``;
+* ``SparsePoolFunction`` (autograd.py:380-414): saves (x, W, b, pre), recomputes in backward,
+  routes dW/db into fp32 ``main_grad`` buffers when present (autograd.py:357-363);
+* ``fit_policy`` / ``resolve_policy`` / ``AUTO_POLICY`` (autograd.py:30-65).
+
+The only executor is the HIP backend (granulelayer_amd.backend); there is no Triton or PyTorch
+fallback, so a runtime on a CPU device refuses to run.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, Optional
+
+import torch
+
+from .config import DEFAULT_WORKSPACE_BUDGET, LevelSpec, PhysicalPlan, resolve_reduction
+from .layout import SparseLayout
+
+AUTO_POLICY = {"max": "save_winners", "topk_mean": "save_winners", "mean": "minimal_stats",
+               "logmeanexp": "minimal_stats", "power_mean": "minimal_stats", "softmax_weighted": "minimal_stats",
+               "sum": "minimal_stats"}
+
+
+def resolve_policy(level: LevelSpec, requested: str) -> str:
+    if requested == "auto":
+        return AUTO_POLICY[level.type]
+    if requested == "save_winners" and level.type not in ("max", "topk_mean"):
+        return "minimal_stats"  # no winners to save; the reference's documented fallback
+    return requested
+
+
+def fit_policy(rt: "Level1Runtime", policy: str, batch: int) -> str:
+    rt.last_info.pop("policy_fallback", None)
+    return policy
+
+
+def act_torch(x: torch.Tensor, name: str) -> torch.Tensor:
+    if name == "identity":
+        return x
+    if name == "relu":
+        return torch.relu(x)
+    raise NotImplementedError(f"out-activation {name!r}")
+
+
+def dact_torch(x: torch.Tensor, name: str) -> torch.Tensor:
+    if name == "identity":
+        return torch.ones_like(x)
+    if name == "relu":
+        return (x > 0).to(x.dtype)
+    raise NotImplementedError(f"out-activation {name!r}")
+
+
+@dataclass
+class Units:
+    """Level-1 pooling units (kernels/ops.py:30-56): one unit per group for a single level."""
+
+    S: int
+    BPS: int
+    nps: Optional[int]
+    counts: torch.Tensor
+
+    @property
+    def U(self) -> int:
+        return self.counts.numel()
+
+
+class Level1Runtime:
+    """Executes the fused level-1 kernels for one layer (sparse_pooling/autograd.py:68-300)."""
+
+    def __init__(self, layout: SparseLayout, idx: torch.Tensor, level: LevelSpec, plan: PhysicalPlan,
+                 nps: Optional[int] = None, workspace_budget: int = DEFAULT_WORKSPACE_BUDGET,
+                 backend: Optional[object] = None):
+        reason = level.hip_reason()
+        if reason:
+            raise NotImplementedError(reason)
+        if layout.shared_indices:
+            raise NotImplementedError("Mode B (block-shared indices) is not on the MI355X path")
+        if nps is not None:
+            raise NotImplementedError("semantic two-level pooling is not on the MI355X path")
+        if plan.backend == "triton":
+            raise NotImplementedError("backend='triton': the MI355X build has no Triton path (use 'hip')")
+        self.layout = layout
+        self.idx = idx
+        self.level = level
+        self.plan = plan
+        self.counts_i32 = layout.counts_tensor(idx.device).contiguous()
+        self.units = Units(1, layout.blocks_per_group, None, self.counts_i32.to(torch.float32))
+        self.workspace_budget = workspace_budget
+        if backend is None and idx.is_cuda:
+            from .backend import backend_for
+
+            backend = backend_for(idx.device)
+        self.backend = backend
+        self.last_info: Dict = {}
+        self.det = False
+
+    def check_devices(self, *tensors):
+        dev = self.idx.device
+        for t in tensors:
+            if t is not None and t.device != dev:
+                raise ValueError(f"tensor on {t.device} but the layer's parameters are on {dev} "
+                                 "(move the input or the layer)")
+
+    def _require_backend(self):
+        if self.backend is None:
+            raise RuntimeError(f"parameters on {self.idx.device}: the MI355X path runs on a ROCm GPU only "
+                               "(no CPU / PyTorch fallback)")
+
+    def resolve_reduction(self, B: int) -> bool:
+        mode, why, _ = resolve_reduction(self.plan)
+        self.det = mode == "deterministic"
+        self.last_info["reduction"] = {"mode": mode, "reason": why}
+        return self.det
+
+    def describe_execution(self) -> Dict:
+        out = {"backend": "hip"}
+        if self.backend is not None:
+            out["build"] = self.backend.build_info()
+        return out
+
+    # ---------------------------------------------------------------- forward
+    def forward(self, x: torch.Tensor, w, b, track_ids: bool = False) -> Dict[str, torch.Tensor]:
+        """Merged statistics: {'pre': [B, U]} (the pooled value before the out-activation)."""
+        self.check_devices(x, w, b)
+        self._require_backend()
+        self.resolve_reduction(x.shape[0])
+        out = self.backend.forward(self, x, w, b, False)
+        self.last_info["forward_backend"] = "hip"
+        return out
+
+    # --------------------------------------------------------------- backward
+    def backward(self, x, w, b, g_pre: torch.Tensor, saved: Dict[str, torch.Tensor], policy: str,
+                 dw_buf: torch.Tensor, db_buf: torch.Tensor, recomputed: bool = False) -> torch.Tensor:
+        """Accumulate dW/db into the fp32 buffers, return dX (fp32, [B, D])."""
+        self.last_info["policy"] = policy
+        self.check_devices(x, w, b, g_pre, dw_buf, db_buf)
+        self._require_backend()
+        self.resolve_reduction(x.shape[0])
+        self.last_info["recomputed_stats"] = recomputed
+        self.last_info["backward_backend"] = "hip"
+        return self.backend.backward(self, x, w, b, g_pre, saved, dw_buf, db_buf)
+
+
+def _compute_operands(x, w, b, compute_dtype):
+    """Operands of the kernels (autograd.py:349-354).  The HIP kernels compute in fp32 with fp32
+    weights and accept fp32 or bf16 inputs; a bf16 compute dtype rounds x, W and b to bf16 first,
+    as the reference's cast does, then runs the same fp32 arithmetic."""
+    if compute_dtype == torch.bfloat16:
+        xc = x.to(torch.bfloat16).contiguous()
+        wc = w.to(torch.bfloat16).to(torch.float32)
+        bc = b.to(torch.bfloat16).to(torch.float32)
+    elif compute_dtype == torch.float32:
+        xc = x if x.dtype in (torch.float32, torch.bfloat16) else x.to(torch.float32)
+        xc = xc.contiguous()
+        wc = w if w.dtype == torch.float32 else w.to(torch.float32)
+        bc = b if b.dtype == torch.float32 else b.to(torch.float32)
+    else:
+        raise NotImplementedError(f"compute dtype {compute_dtype} (the MI355X path computes fp32 or bf16 operands)")
+    return xc, wc.contiguous(), bc.contiguous()
+
+
+def _grad_buffers(w, b):
+    mg_w = getattr(w, "main_grad", None)
+    mg_b = getattr(b, "main_grad", None)
+    if mg_w is not None and mg_b is not None:
+        return mg_w, mg_b, True
+    return (torch.zeros(w.shape, device=w.device, dtype=torch.float32),
+            torch.zeros(b.shape, device=b.device, dtype=torch.float32), False)
+
+
+def _saved_stats(level: LevelSpec, out: Dict[str, torch.Tensor], policy: str) -> Dict[str, torch.Tensor]:
+    if policy == "recompute_stats":
+        return {}
+    return {"pre": out["pre"]}
+
+
+class SparsePoolFunction(torch.autograd.Function):
+    """Single level: y [B, G] = out_act(pool(sparse_projection(x)))."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, rt: Level1Runtime, policy: str, compute_dtype):
+        policy = fit_policy(rt, policy, x.shape[0])
+        xc, wc, bc = _compute_operands(x, w, b, compute_dtype)
+        lv = rt.level
+        out = rt.forward(xc, wc, bc, track_ids=False)
+        pre = out["pre"]
+        y = act_torch(pre, lv.out_activation)
+        saved = _saved_stats(lv, out, policy)
+        ctx.rt, ctx.policy, ctx.compute_dtype = rt, policy, compute_dtype
+        ctx.saved_keys = list(saved.keys())
+        ctx.save_for_backward(x, w, b, *saved.values())
+        rt.last_info["checkpoint_bytes"] = sum(t.numel() * t.element_size() for t in saved.values())
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w, b, *svals = ctx.saved_tensors
+        saved = dict(zip(ctx.saved_keys, svals))
+        rt: Level1Runtime = ctx.rt
+        lv = rt.level
+        xc, wc, bc = _compute_operands(x, w, b, ctx.compute_dtype)
+        recomputed = "pre" not in saved
+        if recomputed:
+            saved.update(rt.forward(xc, wc, bc, track_ids=True))
+        g_pre = dy.float() * dact_torch(saved["pre"], lv.out_activation)
+        dw_buf, db_buf, use_main = _grad_buffers(w, b)
+        dx = rt.backward(xc, wc, bc, g_pre.contiguous(), saved, ctx.policy, dw_buf, db_buf, recomputed)
+        gw = None if use_main else dw_buf.to(w.dtype)
+        gb = None if use_main else db_buf.to(b.dtype)
+        return dx.to(x.dtype, memory_format=torch.contiguous_format), gw, gb, None, None, None

@@ -1,0 +1,199 @@
+"""HIP backend object: the drop-in boundary of the reference's native backend.
+
+``HipBackend`` exposes the two methods the reference's ``Level1Runtime`` calls on its native
+backend (sparse_pooling/autograd.py:220-223 and :265-267; implemented for CUDA at
+sparse_pooling/backends/cuda/runtime.py:339-712):
+
+    forward(rt, x, w, b, track_ids)                     -> {"pre": [B, U] fp32}
+    backward(rt, x, w, b, g_pre, stats, dw_buf, db_buf) -> dX [B, D] fp32 (dW/db accumulated)
+
+plus ``adam`` (the FusedAdamW launch, sparse_pooling/optim.py:116-123) and ``edges`` (the
+input-major edge list the deterministic dX kernel consumes, built once per index tensor).
+
+Every launch runs under ``torch.cuda.device(<tensor device>)`` on that device's current stream,
+asynchronously; buffers (outputs and workspace) are allocated by PyTorch and passed as raw
+pointers.  Any refusal of the native library raises ``NativeError``; there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from typing import Dict, Optional
+
+import torch
+
+from . import _native as N
+
+
+def _ptr(t: Optional[torch.Tensor]) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def _stream(dev) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _x_operand(x: torch.Tensor):
+    """(tensor, dtype code, row stride) of the input: fp32 or bf16, unit feature stride."""
+    if x.dim() != 2:
+        raise ValueError(f"x must be [B, D] (got {tuple(x.shape)})")
+    if x.dtype == torch.float32:
+        code = N.GL_DTYPE_F32
+    elif x.dtype == torch.bfloat16:
+        code = N.GL_DTYPE_BF16
+    else:
+        raise TypeError(f"x must be float32 or bfloat16 (got {x.dtype})")
+    if x.stride(1) != 1 or x.stride(0) < x.shape[1]:
+        x = x.contiguous()
+    return x, code, x.stride(0)
+
+
+def _f32(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32 (got {t.dtype})")
+    return t.contiguous()
+
+
+class HipBackend:
+    """The MI355X HIP backend (one per process; the library is device-independent)."""
+
+    _instance = None
+    _lock = threading.Lock()
+
+    def __init__(self, lib: Optional[N.Library] = None):
+        self.lib = lib or N.library()
+
+    @classmethod
+    def get(cls) -> "HipBackend":
+        with cls._lock:
+            if cls._instance is None:
+                cls._instance = cls()
+            return cls._instance
+
+    def build_info(self) -> Dict:
+        return {"library": str(self.lib.path), "abi_version": N.ABI_VERSION, "arch": "gfx950"}
+
+    # ------------------------------------------------------------------ helpers
+    @staticmethod
+    def _layer(rt):
+        L = rt.layout
+        G, S, K = L.groups, L.slots_per_group, L.fan_in
+        return L, G, S, K
+
+    @staticmethod
+    def _codes(rt):
+        lv = rt.level
+        reason = lv.hip_reason()
+        if reason:
+            raise NotImplementedError(reason)
+        return N.GL_ACT[lv.activation], N.GL_POOL[lv.type]
+
+    @staticmethod
+    def _check(rt, x, w, b):
+        L = rt.layout
+        dev = rt.idx.device
+        for name, t in (("x", x), ("weight", w), ("bias", b)):
+            if t.device != dev:
+                raise ValueError(f"{name} on {t.device} but the layer's parameters are on {dev}")
+        if not dev.type == "cuda":
+            raise RuntimeError("the HIP backend needs the layer on a ROCm GPU (no CPU path)")
+        if x.shape[-1] != L.input_dim:
+            raise ValueError(f"x has {x.shape[-1]} features, layer expects {L.input_dim}")
+        if tuple(w.shape) != tuple(L.weight_shape) or tuple(b.shape) != tuple(L.bias_shape):
+            raise ValueError("weight / bias shapes do not match the layout")
+
+    # ------------------------------------------------------------------ forward
+    def forward(self, rt, x, w, b, track_ids: bool = False) -> Dict[str, torch.Tensor]:
+        self._check(rt, x, w, b)
+        L, G, S, K = self._layer(rt)
+        act, pool = self._codes(rt)
+        x, xcode, sxb = _x_operand(x)
+        w, b = _f32(w, "weight"), _f32(b, "bias")
+        B = x.shape[0]
+        pre = torch.empty((B, G), device=x.device, dtype=torch.float32)
+        if B == 0:
+            return {"pre": pre}
+        a = N.GlFwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=L.input_dim, G=G, S=S, K=K, act=act, pool=pool,
+                        idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32), pre=_ptr(pre))
+        with torch.cuda.device(x.device):
+            need = self.lib.size_query("gl_fwd_workspace", a)
+            ws = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)
+            a.ws, a.ws_bytes = _ptr(ws), need
+            self.lib.call("gl_fwd", ctypes.byref(a), ctypes.c_void_p(_stream(x.device)))
+        rt.last_info["workspace_bytes"] = need
+        return {"pre": pre}
+
+    # ------------------------------------------------------------------ edges
+    def edges(self, rt) -> torch.Tensor:
+        """Input-major edge structure of rt's index tensor (built once, cached on rt)."""
+        key = (rt.idx.data_ptr(), rt.idx._version)
+        cached = getattr(rt, "_hip_edges", None)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        L, G, S, K = self._layer(rt)
+        a = N.GlEdgeArgs(idx=_ptr(rt.idx), counts=_ptr(rt.counts_i32), D=L.input_dim, G=G, S=S, K=K)
+        dev = rt.idx.device
+        with torch.cuda.device(dev):
+            eb, wb = self.lib.edges_size(a)
+            edges = torch.empty(eb, device=dev, dtype=torch.uint8)
+            ws = torch.empty(max(wb, 1), device=dev, dtype=torch.uint8)
+            a.edges, a.edges_bytes, a.ws, a.ws_bytes = _ptr(edges), eb, _ptr(ws), wb
+            self.lib.call("gl_edges_build", ctypes.byref(a), ctypes.c_void_p(_stream(dev)))
+        # the scratch returns to PyTorch's stream-ordered cache: later allocations on this stream
+        # are ordered after the build
+        rt._hip_edges = (key, edges)
+        return edges
+
+    # ------------------------------------------------------------------ backward
+    def backward(self, rt, x, w, b, g_pre, stats, dw_buf, db_buf) -> torch.Tensor:
+        self._check(rt, x, w, b)
+        L, G, S, K = self._layer(rt)
+        act, pool = self._codes(rt)
+        x, xcode, sxb = _x_operand(x)
+        w, b = _f32(w, "weight"), _f32(b, "bias")
+        g_pre = _f32(g_pre, "g_pre")
+        B, D = x.shape
+        if tuple(g_pre.shape) != (B, G):
+            raise ValueError(f"g_pre must be [{B}, {G}] (got {tuple(g_pre.shape)})")
+        for name, t, shape in (("dw_buf", dw_buf, L.weight_shape), ("db_buf", db_buf, L.bias_shape)):
+            if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != tuple(shape):
+                raise ValueError(f"{name} must be a contiguous float32 tensor of shape {tuple(shape)}")
+        dx = torch.empty((B, D), device=x.device, dtype=torch.float32)
+        if B == 0:
+            return dx
+        edges = self.edges(rt)
+        a = N.GlBwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=D, G=G, S=S, K=K, act=act, pool=pool,
+                        idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32), g_pre=_ptr(g_pre),
+                        dW=_ptr(dw_buf), db=_ptr(db_buf), dX=_ptr(dx), edges=_ptr(edges),
+                        edges_bytes=edges.numel())
+        with torch.cuda.device(x.device):
+            need = self.lib.size_query("gl_bwd_workspace", a)
+            ws = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)
+            a.ws, a.ws_bytes = _ptr(ws), need
+            self.lib.call("gl_bwd", ctypes.byref(a), ctypes.c_void_p(_stream(x.device)))
+        rt.last_info["backward_workspace_bytes"] = need
+        return dx
+
+    # ------------------------------------------------------------------ optimizer
+    def adam(self, p, g, m, v, lr, beta1, beta2, eps, weight_decay, bc1, bc2):
+        """In-place fused AdamW over fp32 p (and fp32 g); m/v fp32 or bf16."""
+        for name, t in (("param", p), ("grad", g)):
+            if t.dtype != torch.float32 or not t.is_contiguous():
+                raise TypeError(f"{name} must be a contiguous float32 tensor")
+        if m.dtype != v.dtype or m.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError("moments must both be float32 or bfloat16")
+        if not (p.numel() == g.numel() == m.numel() == v.numel()):
+            raise ValueError("param, grad and moments must have the same number of elements")
+        a = N.GlAdamArgs(p=_ptr(p), g=_ptr(g), m=_ptr(m), v=_ptr(v), n=p.numel(),
+                         moments_dtype=N.GL_DTYPE_F32 if m.dtype == torch.float32 else N.GL_DTYPE_BF16,
+                         lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, bc1=bc1, bc2=bc2)
+        with torch.cuda.device(p.device):
+            self.lib.call("gl_adam", ctypes.byref(a), ctypes.c_void_p(_stream(p.device)))
+
+
+def backend_for(device) -> HipBackend:
+    """Backend of a device (the reference's backends.cuda.runtime.backend_for, runtime.py:188-197)."""
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise RuntimeError(f"no HIP backend for {dev}: the MI355X path needs a ROCm GPU")
+    return HipBackend.get()

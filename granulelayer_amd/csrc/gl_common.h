@@ -1,0 +1,82 @@
+// Shared definitions of the granulelayer_amd HIP library (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+#include "../../include/granulelayer_amd.h"
+
+namespace gl {
+
+// ---- tiling constants ---------------------------------------------------------------------
+// X is staged feature-major in LDS, 4 tokens per 16-byte slot: one ds_read_b128 gathers one
+// input feature for 4 tokens.
+constexpr int BT = 4;
+// dX: features per range (one register accumulator row each) and slots per edge-list unit.
+constexpr int FW = 16;
+constexpr int US = 1024;
+// input-major edge record: n_local (12 bits) | k << 12 (5 bits) | f_local << 17 (5 bits)
+constexpr int REC_N_BITS = 12;
+constexpr int REC_K_BITS = 5;
+// largest token chunk of one backward pass (bounds the per-neuron mask record)
+constexpr int BWD_TOKEN_CHUNK = 1024;
+
+constexpr int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
+constexpr long long round_up(long long a, long long b) { return (a + b - 1) / b * b; }
+
+// Tokens of one dX wave (64 lanes x T slots) for a chunk of B tokens.
+inline int dx_slots(int B) {
+  int t = ceil_div(B, 64);
+  return t < 4 ? (t < 1 ? 1 : t) : 4;
+}
+inline int dx_cap(int B) { return (int)round_up(B, 64 * dx_slots(B)); }
+// per-neuron activation-mask record of the backward: one bit per token of the padded chunk
+// (an even number of 32-bit words: the dX kernel reads 64-bit words)
+inline int mask_stride(int B) { return dx_cap(B) / 32; }
+
+#define GL_CHECK_LAUNCH()                                   \
+  do {                                                      \
+    hipError_t e_ = hipGetLastError();                      \
+    if (e_ != hipSuccess) return (int)e_;                   \
+  } while (0)
+
+#define GL_TRY(x)                                           \
+  do {                                                      \
+    int r_ = (x);                                           \
+    if (r_ != 0) return r_;                                 \
+  } while (0)
+
+__device__ __forceinline__ float load_x(const float* p, long long i) { return p[i]; }
+__device__ __forceinline__ float load_x(const __hip_bfloat16* p, long long i) {
+  // bf16 -> fp32 is exact: the 16 bits become the high half of the fp32 pattern
+  unsigned short u = reinterpret_cast<const unsigned short*>(p)[i];
+  return __uint_as_float((unsigned)u << 16);
+}
+
+// A copy of v the optimiser cannot see through: address arithmetic that depends on it is
+// computed where it is used instead of being hoisted out of the token loop and kept live in
+// registers for the whole kernel.
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// DPP move (row/quad patterns) as a float
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the total.  Fixed reduction tree.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<0xB1>(v);   // quad_perm(1,0,3,2)
+  v += dpp<0x4E>(v);   // quad_perm(2,3,0,1)
+  v += dpp<0x141>(v);  // row_half_mirror
+  v += dpp<0x140>(v);  // row_mirror
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+}  // namespace gl

@@ -1,0 +1,232 @@
+// Forward: fused sparse projection -> activation -> pool (sum / mean), neuron-stationary.
+//
+// Each wave owns a "chunk": up to 64*NPL consecutive slots of one group, NPL neurons per lane
+// (slot s_lo + j*64 + lane).  Index records, weights and bias of the chunk are loaded into VGPRs
+// once; the wave then streams every token tile of X through LDS (4 tokens per 16-byte slot,
+// feature-major), gathers one slot per (neuron, k) with ds_read_b128, accumulates z in fp32,
+// applies the activation and reduces the chunk's per-token sum across the wave.  The hidden
+// tensor [B, H] never exists; only per-(chunk, token) partial sums are written and a finalize
+// kernel merges the chunks of a group in a fixed order (reference: fwd_pool_kernel +
+// merge_finalize, sparse_pooling/kernels/triton_fused.py:289-358, kernels/ops.py:182-199).
+#include "gl_common.h"
+#include "gl_internal.h"
+
+namespace gl {
+
+// X [B, D] (fp32 | bf16, row stride sxb) -> XT [n_tiles][D][BT] fp32; tokens >= B are zero.
+template <typename XT>
+__global__ void __launch_bounds__(256) tile_x_kernel(const XT* __restrict__ X, long long sxb, int B, int D, int b0,
+                                                     int n_tiles, float4* __restrict__ out) {
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  long long total = (long long)n_tiles * D;
+  if (i >= total) return;
+  int t = (int)(i / D), d = (int)(i % D);
+  float v[BT];
+#pragma unroll
+  for (int j = 0; j < BT; ++j) {
+    int b = b0 + t * BT + j;
+    v[j] = b < B ? load_x(X, (long long)b * sxb + d) : 0.f;
+  }
+  out[i] = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+int launch_tile_x(const void* X, long long sxb, int x_dtype, int B, int D, int b0, int n_tiles, float4* xt,
+                  hipStream_t s) {
+  long long total = (long long)n_tiles * D;
+  dim3 grid((unsigned)ceil_div(total, 256));
+  if (x_dtype == GL_DTYPE_F32)
+    GL_LAUNCH(GL_KERNEL_TILE_X, tile_x_kernel<float>, grid, dim3(256), 0, s, (const float*)X, sxb, B, D, b0, n_tiles, xt);
+  else
+    GL_LAUNCH(GL_KERNEL_TILE_X, tile_x_kernel<__hip_bfloat16>, grid, dim3(256), 0, s, (const __hip_bfloat16*)X, sxb, B, D,
+                       b0, n_tiles, xt);
+  GL_CHECK_LAUNCH();
+  return 0;
+}
+
+struct FwdK {
+  const float4* xt;       // [n_tiles][D] float4
+  const int32_t* idx;
+  const float* W;
+  const float* bias;
+  const int32_t* counts;
+  float* part;            // [n_chunks][b_pad]
+  long long n_chunks;
+  int D, S, cpg, n_tiles, b_pad;
+};
+
+template <int K, int NPL, int WAVES, int ACT>
+__global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
+  extern __shared__ float4 xs[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  long long chunk = (long long)blockIdx.x * WAVES + wave;
+  const bool active = chunk < p.n_chunks;
+  if (!active) chunk = p.n_chunks - 1;  // idle waves of the last block recompute a real chunk, store nothing
+  const long long g = chunk / p.cpg;
+  const int s_lo = (int)(chunk % p.cpg) * 64 * NPL;
+  const int n_g = p.counts[g];
+
+  unsigned addr[NPL][K];
+  float w[NPL][K];
+  float bias[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int s = s_lo + j * 64 + lane;
+    const bool valid = s < n_g;
+    const long long n = g * p.S + (s < p.S ? s : p.S - 1);  // in-bounds address; invalid slots masked
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      int d = p.idx[n * K + k];
+      d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
+      addr[j][k] = (unsigned)d * 16u;
+      const float wl = p.W[n * K + k];
+      w[j][k] = valid ? wl : 0.f;
+    }
+    const float bl = p.bias[n];
+    bias[j] = valid ? bl : 0.f;
+  }
+
+  const char* xsb = reinterpret_cast<const char*>(xs);
+  for (int t = 0; t < p.n_tiles; ++t) {
+    __syncthreads();
+    const float4* src = p.xt + (long long)t * p.D;
+    for (int i = threadIdx.x; i < p.D; i += WAVES * 64) xs[i] = src[i];
+    __syncthreads();
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const float4 xv = *reinterpret_cast<const float4*>(xsb + addr[j][k]);
+        z0 = __builtin_fmaf(xv.x, w[j][k], z0);
+        z1 = __builtin_fmaf(xv.y, w[j][k], z1);
+        z2 = __builtin_fmaf(xv.z, w[j][k], z2);
+        z3 = __builtin_fmaf(xv.w, w[j][k], z3);
+      }
+      if (ACT == GL_ACT_RELU) {
+        z0 = __builtin_fmaxf(z0, 0.f);
+        z1 = __builtin_fmaxf(z1, 0.f);
+        z2 = __builtin_fmaxf(z2, 0.f);
+        z3 = __builtin_fmaxf(z3, 0.f);
+      }
+      a0 += z0;
+      a1 += z1;
+      a2 += z2;
+      a3 += z3;
+    }
+    a0 = wave_sum(a0);
+    a1 = wave_sum(a1);
+    a2 = wave_sum(a2);
+    a3 = wave_sum(a3);
+    if (active && lane == 0)
+      *reinterpret_cast<float4*>(p.part + chunk * p.b_pad + (long long)t * BT) = make_float4(a0, a1, a2, a3);
+  }
+}
+
+// pre[b, g] = scale_g * sum_{c < cpg} part[g*cpg + c, b]  (fixed order), tiled transpose.
+__global__ void __launch_bounds__(256) fwd_finalize_kernel(const float* __restrict__ part, const int32_t* __restrict__ counts,
+                                                           float* __restrict__ pre, int B, int G, int cpg, int b_pad,
+                                                           int b0, int pool) {
+  __shared__ float tile[32][33];
+  const int g0 = blockIdx.x * 32, bb0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int r = ty; r < 32; r += 8) {
+    const int g = g0 + r, b = bb0 + tx;
+    float v = 0.f;
+    if (g < G && b < b_pad) {
+      const float* src = part + (long long)g * cpg * b_pad + b;
+      for (int c = 0; c < cpg; ++c) v += src[(long long)c * b_pad];
+      if (pool == GL_POOL_MEAN) v = v / (float)counts[g];
+    }
+    tile[r][tx] = v;
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const int b = bb0 + r, g = g0 + tx;
+    if (g < G && b0 + b < B && b < b_pad) pre[(long long)(b0 + b) * G + g] = tile[tx][r];
+  }
+}
+
+// ---- host side -------------------------------------------------------------------------------
+struct FwdPlan {
+  int npl, waves, cpg, n_tiles, b_pad;
+  long long n_chunks;
+  size_t lds, xt_bytes, part_bytes;
+};
+
+static FwdPlan fwd_plan(const GlFwdArgs* a) {
+  FwdPlan q;
+  q.npl = 64 / a->K;  // 8 neurons per lane at K = 8, 4 at K = 16 (~140 VGPRs of parameters)
+  q.waves = a->D * 16 > 65536 ? 8 : 4;
+  q.cpg = ceil_div(a->S, 64 * q.npl);
+  q.n_chunks = (long long)a->G * q.cpg;
+  q.n_tiles = ceil_div(a->B, BT);
+  q.b_pad = q.n_tiles * BT;
+  q.lds = (size_t)a->D * 16;
+  q.xt_bytes = (size_t)round_up((long long)q.n_tiles * a->D * 16, 256);
+  q.part_bytes = (size_t)round_up((long long)q.n_chunks * q.b_pad * 4, 256);
+  return q;
+}
+
+template <int K, int NPL, int WAVES, int ACT>
+static int launch_fwd(const FwdK& k, hipStream_t s, size_t lds) {
+  auto fn = fwd_kernel<K, NPL, WAVES, ACT>;
+  GL_TRY(set_lds_limit((const void*)fn, lds));
+  dim3 grid((unsigned)ceil_div(k.n_chunks, WAVES));
+  GL_LAUNCH(GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), lds, s, k);
+  GL_CHECK_LAUNCH();
+  return 0;
+}
+
+template <int ACT>
+static int launch_fwd_act(int K, int waves, const FwdK& k, hipStream_t s, size_t lds) {
+  if (K == 8) return waves == 8 ? launch_fwd<8, 8, 8, ACT>(k, s, lds) : launch_fwd<8, 8, 4, ACT>(k, s, lds);
+  return waves == 8 ? launch_fwd<16, 4, 8, ACT>(k, s, lds) : launch_fwd<16, 4, 4, ACT>(k, s, lds);
+}
+
+int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const float* W,
+                const float* bias, const int32_t* counts, int x_dtype) {
+  if (!X || !idx || !W || !bias || !counts) return GL_ERR_ARG;
+  if (B < 1 || D < 1 || G < 1 || S < 1) return GL_ERR_ARG;
+  if (K != 8 && K != 16) return GL_ERR_UNSUPPORTED;
+  if (act != GL_ACT_IDENTITY && act != GL_ACT_RELU) return GL_ERR_UNSUPPORTED;
+  if (pool != GL_POOL_MEAN && pool != GL_POOL_SUM) return GL_ERR_UNSUPPORTED;
+  if (x_dtype != GL_DTYPE_F32 && x_dtype != GL_DTYPE_BF16) return GL_ERR_UNSUPPORTED;
+  if ((long long)G * S > (1LL << 31) / 16) return GL_ERR_UNSUPPORTED;
+  if ((size_t)D * 16 > max_lds_bytes()) return GL_ERR_LDS;
+  return 0;
+}
+
+}  // namespace gl
+
+using namespace gl;
+
+extern "C" int gl_fwd_workspace(const GlFwdArgs* a, size_t* bytes) {
+  if (!a || !bytes) return GL_ERR_ARG;
+  GL_TRY(check_layer(a->B, a->D, a->G, a->S, a->K, a->act, a->pool, a->X, a->idx, a->W, a->bias, a->counts,
+                     a->x_dtype));
+  FwdPlan q = fwd_plan(a);
+  *bytes = q.xt_bytes + q.part_bytes;
+  return 0;
+}
+
+extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
+  if (!a || !a->pre) return GL_ERR_ARG;
+  size_t need = 0;
+  GL_TRY(gl_fwd_workspace(a, &need));
+  if (!a->ws || a->ws_bytes < need) return GL_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  FwdPlan q = fwd_plan(a);
+  float4* xt = (float4*)a->ws;
+  float* part = (float*)((char*)a->ws + q.xt_bytes);
+  GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, 0, q.n_tiles, xt, s));
+  FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles, q.b_pad};
+  GL_TRY(a->act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU>(a->K, q.waves, k, s, q.lds)
+                                : launch_fwd_act<GL_ACT_IDENTITY>(a->K, q.waves, k, s, q.lds));
+  dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(q.b_pad, 32));
+  GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_kernel, grid, dim3(256), 0, s, part, a->counts, a->pre, a->B, a->G, q.cpg, q.b_pad,
+                     0, a->pool);
+  GL_CHECK_LAUNCH();
+  return 0;
+}

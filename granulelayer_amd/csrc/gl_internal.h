@@ -1,0 +1,42 @@
+// Internal declarations shared by the library's translation units.
+#pragma once
+
+#include "gl_common.h"
+
+namespace gl {
+
+// LDS available to one workgroup on the current device (queried once per device).
+size_t max_lds_bytes();
+// Raise a kernel's dynamic-LDS limit when it needs more than the 64 KiB default.
+int set_lds_limit(const void* kernel, size_t bytes);
+
+int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const float* W,
+                const float* bias, const int32_t* counts, int x_dtype);
+
+// X rows [b0, b0 + n_tiles*BT) -> token tiles [n_tiles][D] float4 (zero past B).
+int launch_tile_x(const void* X, long long sxb, int x_dtype, int B, int D, int b0, int n_tiles, float4* xt,
+                  hipStream_t s);
+
+// Launch trace (gl_trace_begin): record an event pair around one kernel launch.
+void trace_before(hipStream_t s, int kernel_id);
+void trace_after(hipStream_t s);
+// hipLaunchKernelGGL wrapped by the launch trace; the stream is the launch's 5th argument
+#define GL_LAUNCH(id, kernel, grid, block, lds, stream, ...)                        \
+  do {                                                                             \
+    ::gl::trace_before((stream), (id));                                            \
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);              \
+    ::gl::trace_after((stream));                                                   \
+  } while (0)
+
+// Edge structure header (device buffer begins with it; arrays follow at the stated offsets).
+struct EdgeHeader {
+  uint32_t magic;        // GL_EDGE_MAGIC
+  int32_t D, G, S, K;
+  int32_t fw, us;        // features per range, slots per unit
+  int32_t FR, P, U;      // feature ranges, pieces per group, units (= G * P)
+  uint32_t nseg, n_edges;
+  uint64_t off_seg_ptr, off_seg_unit, off_seg_begin, off_rec;  // byte offsets from the header
+};
+constexpr uint32_t GL_EDGE_MAGIC = 0x474c4531u;  // "GLE1"
+
+}  // namespace gl

@@ -1,0 +1,160 @@
+/*
+ * granulelayer_amd -- C ABI of the MI355X (gfx950) sparse projection -> activation -> pool path.
+ *
+ * One layer: H neurons in G pools ("groups") of S padded slots; slot s of group g is a valid
+ * neuron iff s < counts[g].  Every neuron owns a fan-in record of K input indices (the
+ * reference's "Mode A", sparse_pooling/layout.py:1-34, SparseLayout(shared_indices=False)):
+ *
+ *   z[b,n]   = sum_k X[b, idx[n,k]] * W[n,k] + bias[n]
+ *   pre[b,g] = scale_g * sum_{s < counts[g]} act(z[b, g*S+s])     scale_g = 1/counts[g] (mean) | 1 (sum)
+ *
+ * Conventions (the same as the reference's native ABI, sparse_pooling/backends/cuda/runtime.py:34-44):
+ *   - every entry point returns 0 on success, a negative GL_ERR_* code when the library refuses
+ *     the arguments, or a positive hipError_t when a launch failed;
+ *   - the caller owns every buffer (inputs, outputs and workspace); the library never allocates
+ *     device memory; sizes of workspaces come from the *_workspace / gl_edges_size queries;
+ *   - work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the default stream) on
+ *     the current HIP device; no host synchronisation happens inside any entry point;
+ *   - all reductions have a fixed owner and order: repeated calls give bitwise-identical results.
+ *     No floating-point atomics are used anywhere.
+ */
+#ifndef GRANULELAYER_AMD_H
+#define GRANULELAYER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GL_ABI_VERSION 1
+
+enum {
+  GL_OK = 0,
+  GL_ERR_ARG = -1,          /* invalid argument, shape or null pointer */
+  GL_ERR_UNSUPPORTED = -2,  /* valid request this build does not implement (e.g. K not in {8,16}) */
+  GL_ERR_WORKSPACE = -3,    /* workspace / output buffer smaller than required */
+  GL_ERR_LDS = -4,          /* the input tile (D features x 4 tokens) exceeds the device's LDS */
+  GL_ERR_EDGES = -5,        /* edge structure built for a different layer shape */
+  GL_ERR_DEVICE = -7        /* no current HIP device or attribute query failed */
+};
+enum { GL_ACT_IDENTITY = 0, GL_ACT_RELU = 1 };
+enum { GL_POOL_MEAN = 0, GL_POOL_SUM = 1 };
+enum { GL_DTYPE_F32 = 0, GL_DTYPE_BF16 = 1 };
+
+/* Forward arguments.  Replaces the reference's FwdArgs + sp_fwd
+ * (sparse_pooling/kernels/cuda/sparse_pool_fwd.cuh:23-38, sparse_pool.cu:12-23, mirrored in
+ * backends/cuda/runtime.py:48-60) for the Mode-A path that the reference runs on Triton
+ * (kernels/ops.py:104-154 fused_forward_states + :182-199 merge_finalize). */
+typedef struct GlFwdArgs {
+  const void* X;          /* [B, D] input, row stride sxb elements, dtype x_dtype */
+  int64_t sxb;
+  int32_t x_dtype;        /* GL_DTYPE_F32 | GL_DTYPE_BF16 */
+  int32_t B, D, G, S, K;  /* tokens, inputs, groups, padded slots per group, fan-in (8 | 16) */
+  int32_t act, pool;      /* GL_ACT_*, GL_POOL_* */
+  const int32_t* idx;     /* [G*S, K] input indices in [0, D) */
+  const float* W;         /* [G*S, K] */
+  const float* bias;      /* [G*S] */
+  const int32_t* counts;  /* [G] valid neurons per group, 1 <= counts[g] <= S */
+  float* pre;             /* out [B, G]: pooled value before the (identity) out-activation */
+  void* ws;               /* workspace of gl_fwd_workspace() bytes */
+  size_t ws_bytes;
+} GlFwdArgs;
+
+/* Backward arguments.  Replaces the reference's BwdArgs + sp_bwd (sparse_pool_bwd.cuh:45-66,
+ * sparse_pool.cu:33-43, runtime.py:70-84) for the Mode-A path the reference runs on Triton
+ * (autograd.py:275-300 _triton_backward, kernels/ops.py:242-278). */
+typedef struct GlBwdArgs {
+  const void* X;
+  int64_t sxb;
+  int32_t x_dtype;
+  int32_t B, D, G, S, K;
+  int32_t act, pool;
+  const int32_t* idx;
+  const float* W;
+  const float* bias;
+  const int32_t* counts;
+  const float* g_pre;     /* [B, G] dL/dpre (fp32) */
+  float* dW;              /* [G*S, K] ACCUMULATED (+=), e.g. W.main_grad; padded slots untouched */
+  float* db;              /* [G*S] ACCUMULATED (+=) */
+  float* dX;              /* out [B, D] fp32, overwritten */
+  const void* edges;      /* input-major edge structure from gl_edges_build() for this idx/counts */
+  size_t edges_bytes;
+  void* ws;               /* workspace of gl_bwd_workspace() bytes */
+  size_t ws_bytes;
+} GlBwdArgs;
+
+/* Input-major (transposed) edge list of a layer, built once per index tensor.  It has no
+ * reference counterpart: the reference's Mode-A dX is an fp32 atomic scatter
+ * (sparse_pooling/kernels/triton_fused.py:442-445); this structure turns it into a
+ * deterministic segmented reduction (the fixed-owner pattern of kernels/cuda/sg_det.cu:1-46). */
+typedef struct GlEdgeArgs {
+  const int32_t* idx;
+  const int32_t* counts;
+  int32_t D, G, S, K;
+  void* edges;            /* out, gl_edges_size() bytes */
+  size_t edges_bytes;
+  void* ws;               /* scratch, gl_edges_size() bytes */
+  size_t ws_bytes;
+} GlEdgeArgs;
+
+/* Fused AdamW step.  Replaces the Triton _adamw_kernel launch of FusedAdamW.step
+ * (sparse_pooling/optim.py:26-64, 116-123) for fp32 parameters (HAS_MASTER = STOCH = False):
+ *   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2;  upd = (m/bc1) / (sqrt(v/bc2) + eps)
+ *   p = p (1 - lr wd) - lr upd;  g = 0 (fused zero_grad) */
+typedef struct GlAdamArgs {
+  float* p;
+  float* g;
+  void* m;                /* fp32 or bf16 (moments_dtype) */
+  void* v;
+  int64_t n;
+  int32_t moments_dtype;  /* GL_DTYPE_F32 | GL_DTYPE_BF16 */
+  float lr, beta1, beta2, eps, weight_decay, bc1, bc2;
+} GlAdamArgs;
+
+/* ABI identity: version and struct layouts (sizeof, then every field offset in declaration
+ * order) so a binding can refuse a mismatched library.  Replaces sp_abi_version /
+ * sp_struct_layout (sparse_pooling/kernels/cuda/abi.cu:17-62, checked in runtime.py:103-120).
+ * which: 0 GlFwdArgs, 1 GlBwdArgs, 2 GlEdgeArgs, 3 GlAdamArgs.  Returns the number of values
+ * written (or needed, when n is too small), negative on an unknown struct. */
+int gl_abi_version(void);
+int gl_struct_layout(int which, long long* out, int n);
+const char* gl_error_string(int code);
+
+/* Forward.  gl_fwd_workspace writes the workspace size for these arguments to *bytes. */
+int gl_fwd_workspace(const GlFwdArgs* a, size_t* bytes);
+int gl_fwd(const GlFwdArgs* a, void* stream);
+
+/* Edge structure: sizes (output and scratch) for a layer shape, then the build. */
+int gl_edges_size(const GlEdgeArgs* a, size_t* edges_bytes, size_t* ws_bytes);
+int gl_edges_build(const GlEdgeArgs* a, void* stream);
+
+/* Backward: dW/db accumulated, dX written.  Recomputes z (nothing of size [B, H] is saved by
+ * the forward).  gl_bwd_workspace writes the workspace size to *bytes. */
+int gl_bwd_workspace(const GlBwdArgs* a, size_t* bytes);
+int gl_bwd(const GlBwdArgs* a, void* stream);
+
+/* Fused AdamW (in place). */
+int gl_adam(const GlAdamArgs* a, void* stream);
+
+/* Kernel ids reported by the trace below. */
+enum {
+  GL_KERNEL_TILE_X = 1, GL_KERNEL_FWD = 2, GL_KERNEL_FWD_FINALIZE = 3, GL_KERNEL_C1T = 4, GL_KERNEL_BWD_W = 5,
+  GL_KERNEL_DX = 6, GL_KERNEL_DX_REDUCE = 7, GL_KERNEL_ADAM = 8, GL_KERNEL_EDGES = 9
+};
+
+/* Launch trace for benchmarks and tests (process-wide, not for concurrent callers): after
+ * gl_trace_begin, the i-th kernel launch of the library records events[2i] before and
+ * events[2i+1] after itself on its stream and stores its GL_KERNEL_* id in kernel_ids[i],
+ * for up to n_pairs launches; gl_trace_end stops recording and returns the number of launches
+ * recorded.  events are hipEvent_t handles owned by the caller.  Replaces the reference's
+ * PHASE_EVENTS hook (sparse_pooling/backends/cuda/runtime.py:131-148). */
+int gl_trace_begin(void** events, int32_t* kernel_ids, int n_pairs);
+int gl_trace_end(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GRANULELAYER_AMD_H */

@@ -1,0 +1,150 @@
+/*
+ * TEST INFRASTRUCTURE ONLY -- the CPU oracle of the sparse projection -> activation -> pool path.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library, and
+ * only as the checker.  The product path (granulelayer_amd) never links or calls it.
+ *
+ * It restates the reference's Mode-A arithmetic (every neuron owns its own fan-in record) in plain
+ * C with float64 accumulation, so fp32 GPU results are compared against a more exact value:
+ *
+ *   z[b,n]  = sum_k x[b, idx[n,k]] * w[n,k] + bias[n]
+ *             sparse_pooling/reference/pytorch_reference.py:29-47 (Mode-A branch :43-46),
+ *             sparse_pooling/kernels/triton_fused.py:253-264 (_tile_z Mode A)
+ *   a       = act(z)                 pytorch_reference.py:19-26 (identity | relu)
+ *   pre[b,g]= scale_g * sum_{s < n_g} a[b, g*S+s]
+ *             mean: scale_g = 1/n_g   pytorch_reference.py:78-79, kernels/ops.py:198-199
+ *             sum : scale_g = 1       (mean * n_g; BASELINE's "sum pooling")
+ *   backward (kernels/ops.py:242-249 dense_coefficients, triton_fused.py:364-374 _dz_from_z,
+ *             triton_fused.py:402-445 _bwd_tile Mode A, autograd.py:399-414):
+ *     c1[b,g] = dy[b,g] * scale_g ;  dz[b,n] = c1 * act'(z)   (relu: z > 0, so 0 at z == 0)
+ *     db[n]  += sum_b dz ;  dW[n,k] += sum_b dz * x[b, idx[n,k]] ;  dX[b, idx[n,k]] += dz * w[n,k]
+ *   padded slots (s >= n_g) are masked out of every sum (triton_fused.py:330-338, 428-431).
+ *
+ *   Adam (sparse_pooling/optim.py:26-64, fp32 parameters: HAS_MASTER=False, STOCH=False):
+ *     m = b1*m + (1-b1)*g ; v = b2*v + (1-b2)*g*g ; upd = (m/bc1) / (sqrt(v/bc2) + eps)
+ *     p = p*(1 - lr*wd) - lr*upd ; g = 0        evaluated in fp32, in this order, unfused.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off), output oracle/_build/libgl_oracle.so.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+static inline double act_f(double z, int act) { return act == 1 ? (z > 0.0 ? z : 0.0) : z; }
+static inline double dact_f(double z, int act) { return act == 1 ? (z > 0.0 ? 1.0 : 0.0) : 1.0; }
+
+/* Pre-activation of neuron n for token row xb (float64 accumulation in k order); *mag receives
+ * sum_k |x w| + |bias|, the scale of the fp32 rounding error of z. */
+static inline double neuron_z(const float* xb, const int32_t* idx, const float* w, const float* bias, long n, int K,
+                              double* mag) {
+  double z = 0.0, m = 0.0;
+  for (int k = 0; k < K; ++k) {
+    double t = (double)xb[idx[n * K + k]] * (double)w[n * K + k];
+    z += t;
+    m += fabs(t);
+  }
+  if (mag) *mag = m + fabs((double)bias[n]);
+  return z + (double)bias[n];
+}
+
+/*
+ * Forward.  x [B, D] fp32 (bf16 inputs are widened exactly by the caller); idx/w [G*S, K];
+ * bias [G*S]; counts [G]; pool 0 = mean, 1 = sum; act 0 = identity, 1 = relu.
+ * pre [B, G] float64.  mag (optional, [B, G]): scale_g * sum_s (sum_k |x w| + |bias|), the
+ * magnitude the rounding error of an fp32 evaluation of pre is proportional to.
+ */
+void glo_forward_f64(int B, int D, int G, int S, int K, const float* x, const int32_t* idx, const float* w,
+                     const float* bias, const int32_t* counts, int act, int pool, double* pre, double* mag) {
+  for (int b = 0; b < B; ++b) {
+    const float* xb = x + (size_t)b * D;
+    for (int g = 0; g < G; ++g) {
+      double s = 0.0, m = 0.0, zm;
+      int n_g = counts[g];
+      for (int sl = 0; sl < n_g; ++sl) {
+        s += act_f(neuron_z(xb, idx, w, bias, (long)g * S + sl, K, &zm), act);
+        m += zm;
+      }
+      pre[(size_t)b * G + g] = pool == 0 ? s / (double)n_g : s;
+      if (mag) mag[(size_t)b * G + g] = pool == 0 ? m / (double)n_g : m;
+    }
+  }
+}
+
+/*
+ * Backward.  dy [B, G] fp32 is dL/dpre (the out-activation of mean/sum is identity).
+ * dW [G*S, K], db [G*S], dX [B, D] are float64 and ACCUMULATED (+=), like main_grad.
+ *
+ * Optional error-scale outputs (same shapes, accumulated; pass NULL to skip):
+ *   mag*  sum of |terms| of every gradient sum (the scale of fp32 summation error);
+ *   unc*  contribution of (token, neuron) pairs whose relu mask an fp32 evaluation of z may
+ *         decide differently: |z| <= amb * (sum_k |x w| + |bias|).  Their terms use the float64
+ *         mask in dW/db/dX and are added as |term| to unc*.
+ */
+void glo_backward_f64(int B, int D, int G, int S, int K, const float* x, const int32_t* idx, const float* w,
+                      const float* bias, const int32_t* counts, int act, int pool, const float* dy, double* dW,
+                      double* db, double* dX, double amb, double* magW, double* magb, double* magX, double* uncW,
+                      double* uncb, double* uncX) {
+  for (int b = 0; b < B; ++b) {
+    const float* xb = x + (size_t)b * D;
+    double* dxb = dX + (size_t)b * D;
+    for (int g = 0; g < G; ++g) {
+      int n_g = counts[g];
+      double c1 = (double)dy[(size_t)b * G + g] * (pool == 0 ? 1.0 / (double)n_g : 1.0);
+      for (int sl = 0; sl < n_g; ++sl) {
+        long n = (long)g * S + sl;
+        double zm;
+        double z = neuron_z(xb, idx, w, bias, n, K, &zm);
+        double dz = c1 * dact_f(z, act);
+        int ambiguous = act == 1 && fabs(z) <= amb * zm;
+        db[n] += dz;
+        if (magb) magb[n] += fabs(dz);
+        if (ambiguous && uncb) uncb[n] += fabs(c1);
+        for (int k = 0; k < K; ++k) {
+          int d = idx[n * K + k];
+          dW[n * K + k] += dz * (double)xb[d];
+          dxb[d] += dz * (double)w[n * K + k];
+          if (magW) magW[n * K + k] += fabs(dz * (double)xb[d]);
+          if (magX) magX[(size_t)b * D + d] += fabs(dz * (double)w[n * K + k]);
+          if (ambiguous && uncW) uncW[n * K + k] += fabs(c1 * (double)xb[d]);
+          if (ambiguous && uncX) uncX[(size_t)b * D + d] += fabs(c1 * (double)w[n * K + k]);
+        }
+      }
+    }
+  }
+}
+
+/* round-to-nearest-even fp32 -> bf16 -> fp32 (torch's .to(torch.bfloat16) for finite values) */
+static inline float bf16_round(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u) { /* inf / nan: keep, quiet nan */
+    if (u & 0x007fffffu) u |= 0x00400000u;
+    u &= 0xffff0000u;
+  } else {
+    uint32_t lsb = (u >> 16) & 1u;
+    u = (u + 0x7fffu + lsb) & 0xffff0000u;
+  }
+  float r;
+  memcpy(&r, &u, 4);
+  return r;
+}
+
+/*
+ * Fused AdamW step over n fp32 parameters, in place; g is zeroed (fused zero_grad).
+ * moments_bf16: m, v are stored rounded to bf16 (values kept in fp32 arrays here).
+ */
+void glo_adam_f32(long n, float* p, float* g, float* m, float* v, float lr, float b1, float b2, float eps, float wd,
+                  float bc1, float bc2, int moments_bf16) {
+  for (long i = 0; i < n; ++i) {
+    float gi = g[i];
+    float mi = b1 * m[i] + (1.0f - b1) * gi;
+    float vi = b2 * v[i] + (1.0f - b2) * gi * gi;
+    float upd = (mi / bc1) / (sqrtf(vi / bc2) + eps);
+    float pi = p[i] * (1.0f - lr * wd) - lr * upd;
+    m[i] = moments_bf16 ? bf16_round(mi) : mi;
+    v[i] = moments_bf16 ? bf16_round(vi) : vi;
+    g[i] = 0.0f;
+    p[i] = pi;
+  }
+}

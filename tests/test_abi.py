@@ -1,0 +1,76 @@
+"""The C-ABI library loads and exports every symbol include/granulelayer_amd.h declares; the
+ctypes structures match the native layouts; argument refusal happens before any device use.
+Runs on the CPU (no compute calls)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from granulelayer_amd import _native as N
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "granulelayer_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(gl_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_binding_exports():
+    assert declared_functions() == sorted(N.EXPORTS)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = N.library()
+    for name in declared_functions():
+        assert hasattr(lib.lib, name), name
+    assert lib.lib.gl_abi_version() == N.ABI_VERSION
+
+
+@pytest.mark.parametrize("which", range(len(N.STRUCTS)))
+def test_struct_layouts_match(which):
+    lib = N.library()
+    buf = (ctypes.c_longlong * 64)()
+    n = lib.lib.gl_struct_layout(which, buf, 64)
+    assert list(buf[:n]) == N.struct_layout(N.STRUCTS[which])
+
+
+def test_abi_check_rejects_a_shifted_struct(monkeypatch):
+    """A binding whose struct differs from the library's must refuse to load (the reference's
+    test_device_runtime.py:136-151 pattern)."""
+
+    class Shifted(ctypes.Structure):
+        _fields_ = [("pad", ctypes.c_int32)] + list(N.GlFwdArgs._fields_)
+
+    monkeypatch.setattr(N, "STRUCTS", (Shifted,) + N.STRUCTS[1:])
+    with pytest.raises(N.NativeError, match="layout mismatch"):
+        N.Library()
+
+
+def test_unknown_struct_and_error_strings():
+    lib = N.library()
+    assert lib.lib.gl_struct_layout(99, None, 0) < 0
+    for code in (0, -1, -2, -3, -4, -5, -7):
+        assert lib.error(code)
+
+
+def test_arguments_are_refused_before_device_use():
+    lib = N.library()
+    a = N.GlFwdArgs(B=4, D=64, G=2, S=32, K=8)  # null pointers
+    out = ctypes.c_size_t()
+    assert lib.lib.gl_fwd_workspace(ctypes.byref(a), ctypes.byref(out)) == -1
+    assert lib.lib.gl_fwd(ctypes.byref(a), None) == -1
+    b = N.GlBwdArgs(B=4, D=64, G=2, S=32, K=8)
+    assert lib.lib.gl_bwd(ctypes.byref(b), None) == -1
+    e = N.GlEdgeArgs(D=64, G=2, S=32, K=12)
+    assert lib.lib.gl_edges_size(ctypes.byref(e), ctypes.byref(out), ctypes.byref(out)) == -2
+    m = N.GlAdamArgs(n=-1)
+    assert lib.lib.gl_adam(ctypes.byref(m), None) == -1
+    m = N.GlAdamArgs(n=0)
+    assert lib.lib.gl_adam(ctypes.byref(m), None) == 0
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(N.NativeError, match="not found"):
+        N.Library(tmp_path / "nope.so")

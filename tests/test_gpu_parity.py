@@ -1,0 +1,253 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle on identical seeded inputs.
+
+fp32 bar (conftest.assert_parity): |got - want| <= 1e-6 + 1e-5 * mag (+ the contribution of relu
+masks an fp32 z may decide either way) elementwise, mag being the oracle's sum of |terms| of that
+output, and a whole-tensor relative error <= 1e-5 (north star: rel 1e-5 / abs 1e-6);
+integer / layout outputs: bit-exact.  The oracle accumulates in float64.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close, assert_parity, gpu_available, rel_err
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a ROCm GPU")]
+
+from granulelayer_amd import LevelSpec, PhysicalPlan, SparseLayout, SparsePoolingLayer, init_parameters  # noqa: E402
+from granulelayer_amd.autograd import Level1Runtime  # noqa: E402
+from granulelayer_amd.backend import HipBackend  # noqa: E402
+from oracle import oracle as O  # noqa: E402
+
+DEV = "cuda"
+
+
+def make_case(D, H, G, K, B, seed=0, x_dtype=torch.float32, bias_std=0.3):
+    L = SparseLayout(D, H, G, K, 8, False)
+    idx, w, b = init_parameters(L, "cpu", torch.float32, seed=seed, bias_std=bias_std)
+    gen = torch.Generator().manual_seed(seed + 1000)
+    x = torch.randn(B, D, generator=gen).to(x_dtype)
+    dy = torch.randn(B, G, generator=gen)
+    return L, idx, w, b, x, dy
+
+
+def flat(L, idx, w, b):
+    K = L.fan_in
+    return idx.reshape(-1, K).numpy(), w.reshape(-1, K).numpy(), b.reshape(-1).numpy()
+
+
+def runtime(L, idx, pool, act):
+    return Level1Runtime(L, idx.to(DEV), LevelSpec(pool, activation=act), PhysicalPlan())
+
+
+FWD_CASES = [
+    # D, H, G, K, B, x dtype
+    (64, 3000, 8, 8, 1, torch.float32),
+    (64, 3000, 8, 8, 37, torch.float32),
+    (128, 4099, 16, 8, 130, torch.float32),
+    (1024, 20011, 16, 8, 64, torch.bfloat16),
+    (1024, 65536, 64, 8, 256, torch.float32),
+    (96, 5000, 7, 16, 33, torch.float32),
+    (4096, 16384, 16, 8, 8, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", FWD_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
+@pytest.mark.parametrize("pool,act", [("mean", "relu"), ("sum", "relu"), ("mean", "identity"), ("sum", "identity")])
+def test_forward_matches_oracle(case, pool, act):
+    D, H, G, K, B, xdt = case
+    L, idx, w, b, x, _ = make_case(D, H, G, K, B, x_dtype=xdt)
+    rt = runtime(L, idx, pool, act)
+    pre = rt.forward(x.to(DEV), w.to(DEV), b.to(DEV))["pre"].cpu().numpy()
+    fi, fw, fb = flat(L, idx, w, b)
+    want, mag = O.forward(x.float().numpy(), fi, fw, fb, L.counts_tensor("cpu").numpy(), L.slots_per_group, act, pool,
+                          with_mag=True)
+    assert_parity(pre, want, mag, what=f"pre {pool}/{act}")
+    assert rt.last_info["forward_backend"] == "hip"
+
+
+BWD_CASES = [
+    (64, 3000, 8, 8, 64, torch.float32),
+    (128, 4099, 16, 8, 37, torch.float32),
+    (1024, 20011, 16, 8, 64, torch.bfloat16),
+    (96, 5000, 7, 16, 33, torch.float32),
+    (1024, 65536, 64, 8, 300, torch.float32),
+    (2048, 40000, 40, 8, 1100, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", BWD_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
+@pytest.mark.parametrize("pool,act", [("mean", "relu"), ("sum", "relu"), ("sum", "identity")])
+def test_backward_matches_oracle(case, pool, act):
+    D, H, G, K, B, xdt = case
+    L, idx, w, b, x, dy = make_case(D, H, G, K, B, x_dtype=xdt)
+    rt = runtime(L, idx, pool, act)
+    dw = torch.zeros(L.weight_shape, device=DEV)
+    db = torch.zeros(L.bias_shape, device=DEV)
+    dx = rt.backward(x.to(DEV), w.to(DEV), b.to(DEV), dy.to(DEV), {}, "minimal_stats", dw, db).cpu().numpy()
+    fi, fw, fb = flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    wdW, wdb, wdX, bnd = O.backward(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, dy.numpy(), act, pool,
+                                    with_bounds=True)
+    (mW, mb, mX), (uW, ub, uX) = bnd["mag"], bnd["unc"]
+    assert_parity(dx, wdX, mX, uX, what="dX")
+    assert_parity(dw.cpu().numpy().reshape(-1, K), wdW, mW, uW, what="dW")
+    assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, ub, what="db")
+    # padded slots receive no gradient
+    valid = L.valid_mask("cpu").reshape(-1).numpy()
+    assert not dw.cpu().numpy().reshape(-1, K)[~valid].any()
+
+
+def _read_edges(edges: torch.Tensor):
+    raw = edges.cpu().numpy()
+    h = np.frombuffer(raw[:48].tobytes(), dtype=np.int32)
+    offs = np.frombuffer(raw[48:80].tobytes(), dtype=np.uint64).astype(np.int64)
+    FR, nseg, ne = int(h[7]), int(np.uint32(h[10])), int(np.uint32(h[11]))
+    u32 = lambda off, n: np.frombuffer(raw[off:off + 4 * n].tobytes(), dtype=np.uint32)  # noqa: E731
+    return dict(magic=int(np.uint32(h[0])), FR=FR, nseg=nseg, n_edges=ne, seg_ptr=u32(offs[0], FR + 1),
+                seg_unit=u32(offs[1], nseg).astype(np.int32), seg_begin=u32(offs[2], nseg + 1), rec=u32(offs[3], ne))
+
+
+@pytest.mark.parametrize("D,H,G,K", [(64, 3000, 8, 8), (1024, 20011, 16, 8), (96, 5000, 7, 16), (300, 9000, 3, 8)])
+def test_edge_list_is_bit_exact(D, H, G, K):
+    L, idx, w, b, x, _ = make_case(D, H, G, K, 1)
+    rt = runtime(L, idx, "mean", "relu")
+    e = _read_edges(HipBackend.get().edges(rt))
+    fi, _, _ = flat(L, idx, w, b)
+    want = O.xedges(fi, L.counts_tensor("cpu").numpy(), L.slots_per_group, D, 16, 1024)
+    assert e["magic"] == 0x474C4531
+    assert e["n_edges"] == len(want["rec"])
+    assert np.array_equal(e["rec"], want["rec"])
+    assert np.array_equal(e["seg_ptr"].astype(np.int64), want["seg_ptr"])
+    assert np.array_equal(e["seg_unit"], want["seg_unit"])
+    assert np.array_equal(e["seg_begin"].astype(np.int64), want["seg_begin"])
+
+
+@pytest.mark.parametrize("moments", ["fp32", "bf16"])
+@pytest.mark.parametrize("n", [10_001, 812_345])
+def test_adam_matches_oracle(moments, n):
+    gen = torch.Generator().manual_seed(3)
+    p = torch.randn(n, generator=gen)
+    m = torch.zeros(n)
+    v = torch.zeros(n)
+    mdt = torch.bfloat16 if moments == "bf16" else torch.float32
+    pd, md, vd = p.to(DEV), m.to(mdt).to(DEV), v.to(mdt).to(DEV)
+    po, mo, vo = p.numpy().copy(), m.numpy().copy(), v.numpy().copy()
+    for t in range(1, 6):
+        g = torch.randn(n, generator=gen)
+        gd = g.to(DEV)
+        HipBackend.get().adam(pd, gd, md, vd, 1e-2, 0.9, 0.999, 1e-8, 0.1, 1 - 0.9 ** t, 1 - 0.999 ** t)
+        O.adam(po, g.numpy().copy(), mo, vo, 1e-2, 0.9, 0.999, 1e-8, 0.1, t, moments_bf16=(moments == "bf16"))
+        assert float(gd.abs().max()) == 0.0, "fused zero_grad"
+    assert_close(pd.cpu().numpy(), po, what="p")
+    assert_close(md.float().cpu().numpy(), mo, what="m")
+    assert_close(vd.float().cpu().numpy(), vo, what="v")
+    exact = float((pd.cpu().numpy() == po).mean())
+    print(f"adam {moments} n={n}: {exact * 100:.3f}% of parameters bitwise equal to the oracle")
+
+
+def test_layer_autograd_and_main_grad():
+    D, H, G, K, B = 256, 12000, 12, 8, 48
+    lay = SparsePoolingLayer(D, H, G, fan_in=K, shared_neurons=None, pooling="mean", dtype=torch.float32,
+                             device=DEV, seed=4, bias_std=0.2)
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(B, D, generator=gen).to(DEV).requires_grad_(True)
+    dy = torch.randn(B, G, generator=gen).to(DEV)
+    y = lay(x)
+    (y * dy).sum().backward()
+    L = lay.layout
+    fi, fw, fb = flat(L, lay.indices.cpu(), lay.weight.detach().cpu(), lay.bias.detach().cpu())
+    counts = L.counts_tensor("cpu").numpy()
+    want_y, mag_y = O.forward(x.detach().cpu().numpy(), fi, fw, fb, counts, L.slots_per_group, "relu", "mean",
+                              with_mag=True)
+    wdW, wdb, wdX, bnd = O.backward(x.detach().cpu().numpy(), fi, fw, fb, counts, L.slots_per_group,
+                                    dy.cpu().numpy(), "relu", "mean", with_bounds=True)
+    (mW, mb, mX), (uW, ub, uX) = bnd["mag"], bnd["unc"]
+    assert_parity(y.detach().cpu().numpy(), want_y, mag_y, what="y")
+    assert_parity(x.grad.cpu().numpy(), wdX, mX, uX, what="dx")
+    assert_parity(lay.weight.grad.cpu().numpy().reshape(-1, K), wdW, mW, uW, what="dW")
+    assert_parity(lay.bias.grad.cpu().numpy().reshape(-1), wdb, mb, ub, what="db")
+    assert lay.last_info["forward_backend"] == "hip" and lay.last_info["backward_backend"] == "hip"
+    # main_grad: routed there, accumulates across two backward calls
+    lay.enable_main_grad()
+    lay.weight.grad = None
+    lay(x.detach()).sum().backward()
+    g1 = lay.weight.main_grad.clone()
+    assert lay.weight.grad is None
+    lay(x.detach()).sum().backward()
+    assert torch.allclose(lay.weight.main_grad, 2 * g1, rtol=1e-6, atol=1e-9)
+    lay.zero_main_grad()
+    assert float(lay.weight.main_grad.abs().max()) == 0.0
+
+
+def test_recompute_is_bitwise_deterministic():
+    D, H, G, K, B = 1024, 40000, 16, 8, 96
+    L, idx, w, b, x, dy = make_case(D, H, G, K, B, seed=5, bias_std=0.1)
+    rt = runtime(L, idx, "mean", "relu")
+    args = (x.to(DEV), w.to(DEV), b.to(DEV))
+    a = rt.forward(*args)["pre"]
+    c = rt.forward(*args)["pre"]
+    assert torch.equal(a, c)
+    outs = []
+    for _ in range(3):
+        dw = torch.zeros(L.weight_shape, device=DEV)
+        db = torch.zeros(L.bias_shape, device=DEV)
+        dx = rt.backward(*args, dy.to(DEV), {}, "minimal_stats", dw, db)
+        outs.append((dx, dw, db))
+    for o in outs[1:]:
+        for p, q in zip(o, outs[0]):
+            assert torch.equal(p, q)
+
+
+def test_inplace_param_update_between_fwd_and_bwd_is_rejected():
+    lay = SparsePoolingLayer(64, 3000, 8, shared_neurons=None, pooling="mean", dtype=torch.float32, device=DEV)
+    x = torch.randn(4, 64, device=DEV)
+    y = lay(x)
+    with torch.no_grad():
+        lay.weight.add_(1.0)
+    with pytest.raises(RuntimeError):
+        y.sum().backward()
+
+
+def test_no_hidden_activation_is_materialized():
+    """[B, H] in fp32 would be 2 GiB; a training step's transient memory must stay below 1/20 of
+    it (the reference's bound, tests/test_recomputation.py:69-86).  The persistent input-major
+    edge list (the size of the indices) is built by a first step, like the layer's runtime."""
+    B, H = 256, 2_000_000
+    lay = SparsePoolingLayer(1024, H, 2048, shared_neurons=None, pooling="mean", dtype=torch.float32, device=DEV)
+    lay.enable_main_grad()
+    x = torch.randn(B, 1024, device=DEV, requires_grad=True)
+    lay(x).square().mean().backward()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    y = lay(x)
+    y.square().mean().backward()
+    torch.cuda.synchronize()
+    extra = torch.cuda.max_memory_allocated() - base
+    assert extra < B * H * 4 / 20, f"peak extra {extra / 2**20:.0f} MiB suggests materialisation"
+
+
+def test_sampled_pools_at_scale():
+    """4M neurons (4096 pools of 1024, D=4096, B=256): the HIP result of 24 randomly chosen pools
+    against the oracle run on just those pools."""
+    from granulelayer_amd.synthetic import make_problem
+
+    pr = make_problem("C2", device="cpu", seed=0, groups=4096)
+    L = pr.layout
+    rt = Level1Runtime(L, pr.idx.to(DEV), LevelSpec("sum"), PhysicalPlan())
+    pre = rt.forward(pr.x.to(DEV), pr.w.to(DEV), pr.b.to(DEV))["pre"].cpu().numpy()
+    dw = torch.zeros(L.weight_shape, device=DEV)
+    db = torch.zeros(L.bias_shape, device=DEV)
+    rt.backward(pr.x.to(DEV), pr.w.to(DEV), pr.b.to(DEV), pr.dy.to(DEV), {}, "minimal_stats", dw, db)
+    pools = np.sort(np.random.default_rng(0).choice(L.groups, 24, replace=False))
+    S, K = L.slots_per_group, L.fan_in
+    sl = np.concatenate([np.arange(g * S, (g + 1) * S) for g in pools])
+    fi, fw, fb = flat(L, pr.idx, pr.w, pr.b)
+    counts = np.full(len(pools), S, np.int32)
+    want, mag = O.forward(pr.x.numpy(), fi[sl], fw[sl], fb[sl], counts, S, "relu", "sum", with_mag=True)
+    assert_parity(pre[:, pools], want, mag, what="pre (sampled pools)")
+    wdW, wdb, _, bnd = O.backward(pr.x.numpy(), fi[sl], fw[sl], fb[sl], counts, S, pr.dy.numpy()[:, pools], "relu",
+                                  "sum", with_bounds=True)
+    (mW, mb, _), (uW, ub, _) = bnd["mag"], bnd["unc"]
+    assert_parity(dw.cpu().numpy().reshape(-1, K)[sl], wdW, mW, uW, what="dW (sampled pools)")
+    assert_parity(db.cpu().numpy().reshape(-1)[sl], wdb, mb, ub, what="db (sampled pools)")

@@ -1,0 +1,255 @@
+"""Pins the CPU oracle (oracle/) before anything is compared against it.
+
+Every oracle function is checked by a route that does not retype its formula:
+  forward   -- a dense-GEMM formulation through torch.matmul (float64), a hand-computed known
+               answer, one-hot inputs (closed form), mean = sum / n_g, masking of padded slots;
+  backward  -- torch autograd of the dense formulation, float64 central differences;
+  adam      -- torch.optim.AdamW / Adam (library) and the step-1 closed form;
+  partition -- the invariants of the reference's test_partition_enumerates_exactly_H;
+  xedges    -- a brute-force per-feature enumeration written with plain Python loops.
+Each check is chosen so that a dropped term, wrong sign, wrong index or transposed operand fails.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close, rel_err
+
+
+def random_problem(rng, B, D, G, S, K, ragged=True, bias_std=0.3):
+    counts = rng.integers(max(1, S // 2), S + 1, size=G).astype(np.int32) if ragged else np.full(G, S, np.int32)
+    idx = np.zeros((G * S, K), np.int32)
+    w = np.zeros((G * S, K), np.float32)
+    b = np.zeros(G * S, np.float32)
+    for g in range(G):
+        for s in range(counts[g]):
+            n = g * S + s
+            idx[n] = np.sort(rng.choice(D, K, replace=False))
+            w[n] = rng.standard_normal(K).astype(np.float32) / np.sqrt(K)
+            b[n] = rng.standard_normal() * bias_std
+    x = rng.standard_normal((B, D)).astype(np.float32)
+    return x, idx, w, b, counts
+
+
+def dense_forward(x, idx, w, b, counts, S, act, pool):
+    """float64 torch formulation through a dense [N, D] weight matrix and torch.matmul."""
+    x = torch.as_tensor(x, dtype=torch.float64)
+    G = len(counts)
+    N, K = idx.shape
+    D = x.shape[1]
+    valid = (torch.arange(S)[None, :] < torch.as_tensor(counts)[:, None]).reshape(-1)
+    Wd = torch.zeros(N, D, dtype=torch.float64)
+    Wd.scatter_(1, torch.as_tensor(idx, dtype=torch.int64), torch.as_tensor(w, dtype=torch.float64))
+    Wd = Wd * valid[:, None]
+    z = torch.matmul(x, Wd.T) + torch.as_tensor(b, dtype=torch.float64) * valid
+    a = torch.relu(z) if act == "relu" else z
+    a = a * valid
+    s = a.reshape(x.shape[0], G, S).sum(-1)
+    return s / torch.as_tensor(counts, dtype=torch.float64) if pool == "mean" else s
+
+
+@pytest.mark.parametrize("act", ["relu", "identity"])
+@pytest.mark.parametrize("pool", ["mean", "sum"])
+@pytest.mark.parametrize("B,D,G,S,K", [(3, 16, 2, 32, 8), (5, 40, 3, 64, 8), (2, 64, 2, 32, 16)])
+def test_forward_matches_dense_gemm(oracle, act, pool, B, D, G, S, K):
+    rng = np.random.default_rng(1)
+    x, idx, w, b, counts = random_problem(rng, B, D, G, S, K)
+    got = oracle.forward(x, idx, w, b, counts, S, act, pool)
+    want = dense_forward(x, idx, w, b, counts, S, act, pool).numpy()
+    assert_close(got, want, rtol=1e-12, atol=1e-12, what="forward")
+
+
+def test_forward_known_answer(oracle):
+    # neuron 0: x0*1 + x2*2 + 0.5 = 7.5 ; neuron 1: -x1 + 0.25*x3 - 0.25 = -1.25
+    x = np.array([[1.0, 2.0, 3.0, 4.0]], np.float32)
+    idx = np.array([[0, 2], [1, 3]], np.int32)
+    w = np.array([[1.0, 2.0], [-1.0, 0.25]], np.float32)
+    b = np.array([0.5, -0.25], np.float32)
+    c2 = np.array([2], np.int32)
+    assert oracle.forward(x, idx, w, b, c2, 2, "relu", "sum")[0, 0] == 7.5
+    assert oracle.forward(x, idx, w, b, c2, 2, "relu", "mean")[0, 0] == 3.75
+    assert oracle.forward(x, idx, w, b, c2, 2, "identity", "sum")[0, 0] == 6.25
+    assert oracle.forward(x, idx, w, b, c2, 2, "identity", "mean")[0, 0] == 3.125
+    # neuron 1 padded away: only neuron 0 counts
+    assert oracle.forward(x, idx, w, b, np.array([1], np.int32), 2, "identity", "mean")[0, 0] == 7.5
+
+
+def test_forward_one_hot_inputs(oracle):
+    rng = np.random.default_rng(2)
+    B, D, G, S, K = 24, 24, 3, 32, 8
+    _, idx, w, b, counts = random_problem(rng, B, D, G, S, K, bias_std=0.0)
+    x = np.eye(D, dtype=np.float32)  # token d is the one-hot vector e_d
+    got = oracle.forward(x, idx, w, b, counts, S, "identity", "sum")
+    want = np.zeros((D, G))
+    for g in range(G):
+        for s in range(counts[g]):
+            n = g * S + s
+            for k in range(K):
+                want[idx[n, k], g] += w[n, k]
+    assert_close(got, want, rtol=1e-12, atol=1e-12, what="one-hot")
+
+
+def test_mean_is_sum_over_count_and_padding_is_masked(oracle):
+    rng = np.random.default_rng(3)
+    B, D, G, S, K = 4, 32, 3, 64, 8
+    x, idx, w, b, counts = random_problem(rng, B, D, G, S, K)
+    s = oracle.forward(x, idx, w, b, counts, S, "relu", "sum")
+    m = oracle.forward(x, idx, w, b, counts, S, "relu", "mean")
+    assert_close(m * counts[None, :], s, rtol=1e-14, atol=0, what="mean*n")
+    # garbage in padded slots must not change anything
+    w2, b2, idx2 = w.copy(), b.copy(), idx.copy()
+    for g in range(G):
+        for sl in range(counts[g], S):
+            n = g * S + sl
+            w2[n] = 100.0
+            b2[n] = 50.0
+            idx2[n] = np.arange(K)
+    assert np.array_equal(oracle.forward(x, idx2, w2, b2, counts, S, "relu", "sum"), s)
+
+
+@pytest.mark.parametrize("act", ["relu", "identity"])
+@pytest.mark.parametrize("pool", ["mean", "sum"])
+def test_backward_matches_autograd(oracle, act, pool):
+    rng = np.random.default_rng(4)
+    B, D, G, S, K = 6, 48, 3, 32, 8
+    x, idx, w, b, counts = random_problem(rng, B, D, G, S, K)
+    dy = rng.standard_normal((B, G)).astype(np.float32)
+    dW, db, dX = oracle.backward(x, idx, w, b, counts, S, dy, act, pool)
+    # autograd through the dense formulation
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    N = G * S
+    valid = (torch.arange(S)[None, :] < torch.as_tensor(counts)[:, None]).reshape(-1)
+    wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
+    bt = torch.tensor(b, dtype=torch.float64, requires_grad=True)
+    Wd = torch.zeros(N, D, dtype=torch.float64).scatter(1, torch.as_tensor(idx, dtype=torch.int64), wt)
+    z = torch.matmul(xt, (Wd * valid[:, None]).T) + bt * valid
+    a = (torch.relu(z) if act == "relu" else z) * valid
+    s = a.reshape(B, G, S).sum(-1)
+    y = s / torch.as_tensor(counts, dtype=torch.float64) if pool == "mean" else s
+    (y * torch.as_tensor(dy, dtype=torch.float64)).sum().backward()
+    assert_close(dX, xt.grad.numpy(), rtol=1e-12, atol=1e-12, what="dX")
+    assert_close(dW, (wt.grad * valid[:, None]).numpy(), rtol=1e-12, atol=1e-12, what="dW")
+    assert_close(db, (bt.grad * valid).numpy(), rtol=1e-12, atol=1e-12, what="db")
+
+
+def test_backward_accumulates_and_finite_differences(oracle):
+    rng = np.random.default_rng(5)
+    B, D, G, S, K = 3, 20, 2, 32, 8
+    x, idx, w, b, counts = random_problem(rng, B, D, G, S, K)
+    dy = rng.standard_normal((B, G)).astype(np.float32)
+    dW, db, dX = oracle.backward(x, idx, w, b, counts, S, dy, "identity", "mean")
+    # directional derivative along a random input direction v (identity activation: exact)
+    v = rng.standard_normal((B, D))
+    h = 1e-3
+
+    def f(xx):
+        return float((oracle.forward(xx.astype(np.float32), idx, w, b, counts, S, "identity", "mean") * dy).sum())
+
+    fd = (f(x + h * v) - f(x - h * v)) / (2 * h)
+    assert abs(fd - float((dX * v).sum())) < 1e-3 * max(1.0, abs(fd))
+    # the bias gradient of a valid neuron is sum_b dy[b, g] / n_g
+    g0 = 1
+    assert abs(db[g0 * S] - dy[:, g0].astype(np.float64).sum() / counts[g0]) < 1e-12
+
+
+def _torch_adamw(p0, grads, lr, b1, b2, eps, wd):
+    q = torch.nn.Parameter(torch.tensor(p0))
+    opt = torch.optim.AdamW([q], lr=lr, betas=(b1, b2), eps=eps, weight_decay=wd)
+    for g in grads:
+        q.grad = torch.tensor(g)
+        opt.step()
+    return q.detach().numpy()
+
+
+@pytest.mark.parametrize("wd", [0.0, 0.1])
+def test_adam_matches_torch_adamw(oracle, wd):
+    rng = np.random.default_rng(6)
+    n = 4099
+    p0 = rng.standard_normal(n).astype(np.float32)
+    grads = [rng.standard_normal(n).astype(np.float32) for _ in range(5)]
+    p, m, v = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    for t, g in enumerate(grads, 1):
+        gg = g.copy()
+        oracle.adam(p, gg, m, v, 1e-2, 0.9, 0.999, 1e-8, wd, t)
+        assert not gg.any(), "fused zero_grad"
+    want = _torch_adamw(p0, grads, 1e-2, 0.9, 0.999, 1e-8, wd)
+    # The reference evaluates (1 - beta) in fp32 (optim.py:44-45: fl(1 - fl(0.999)) is 1.3e-5
+    # off 0.001) while torch uses the double constant, so the two fp32 recurrences drift apart by
+    # ~1e-5 of each update; a dropped term or a wrong bias correction moves p by ~lr per step.
+    assert np.abs(p - want).max() < 1e-4 * 1e-2 * len(grads)
+    assert rel_err(p, want) < 1e-6
+
+
+def test_adam_step1_closed_form(oracle):
+    rng = np.random.default_rng(7)
+    n = 1000
+    p0 = rng.standard_normal(n).astype(np.float32)
+    g = rng.standard_normal(n).astype(np.float32)
+    p, m, v = p0.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    oracle.adam(p, g.copy(), m, v, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1)
+    want = p0.astype(np.float64) - 1e-3 * g / (np.abs(g) + 1e-8)
+    assert_close(p, want, rtol=1e-6, atol=1e-7, what="step 1")
+    assert_close(m, 0.1 * g.astype(np.float64), rtol=1e-6, atol=0, what="m")
+    # (1 - beta2) is formed in fp32 from fl(0.999): 1.3e-5 below 0.001 (see the AdamW test)
+    assert_close(v, 0.001 * g.astype(np.float64) ** 2, rtol=2e-5, atol=0, what="v")
+
+
+def test_adam_bf16_moments_are_rounded_like_torch(oracle):
+    rng = np.random.default_rng(8)
+    n = 2048
+    p = rng.standard_normal(n).astype(np.float32)
+    g = rng.standard_normal(n).astype(np.float32)
+    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    oracle.adam(p, g.copy(), m, v, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, moments_bf16=True)
+    m_fp32 = (np.float32(0.9) * np.float32(0) + np.float32(0.1) * g).astype(np.float32)
+    want = torch.tensor(m_fp32).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(m, want)
+
+
+@pytest.mark.parametrize("H,G", [(100_000_000, 1024), (5000, 16), (1000, 7), (4_194_304, 4096)])
+def test_partition_enumerates_exactly_H(oracle, H, G):
+    counts, offsets, S = oracle.partition(H, G)
+    assert int(counts.sum()) == H
+    assert offsets[0] == 0
+    assert np.array_equal(offsets[1:], offsets[:-1] + counts[:-1])
+    assert int(counts.max() - counts.min()) <= 1
+    assert S >= counts.max() and S % 32 == 0
+
+
+def _xedges_bruteforce(idx, counts, S, D, Fw, US):
+    G = len(counts)
+    P = -(-S // US)
+    K = idx.shape[1]
+    out = []  # (F, u, f_local, eid, n, k)
+    for F in range(-(-D // Fw)):
+        for u in range(G * P):
+            g, piece = divmod(u, P)
+            for f in range(Fw):
+                d = F * Fw + f
+                for s in range(piece * US, min((piece + 1) * US, counts[g])):
+                    n = g * S + s
+                    for k in range(K):
+                        if idx[n, k] == d:
+                            out.append((F, u, f, n * K + k, n, k))
+    return out
+
+
+@pytest.mark.parametrize("D,G,S,K,Fw,US", [(40, 3, 32, 8, 16, 1024), (64, 2, 96, 8, 16, 32), (48, 2, 64, 16, 16, 64)])
+def test_xedges_matches_bruteforce(oracle, D, G, S, K, Fw, US):
+    rng = np.random.default_rng(9)
+    _, idx, _, _, counts = random_problem(rng, 1, D, G, S, K)
+    e = oracle.xedges(idx, counts, S, D, Fw, US)
+    want = _xedges_bruteforce(idx, counts, S, D, Fw, US)
+    assert len(e["rec"]) == len(want) == int(counts.sum()) * K
+    P = -(-S // US)
+    got = []
+    for F in range(e["FR"]):
+        for si in range(e["seg_ptr"][F], e["seg_ptr"][F + 1]):
+            u = int(e["seg_unit"][si])
+            g, piece = divmod(u, P)
+            for j in range(e["seg_begin"][si], e["seg_begin"][si + 1]):
+                r = int(e["rec"][j])
+                nl, k, f = r & 4095, (r >> 12) & 31, (r >> 17) & 31
+                n = g * S + piece * US + nl
+                got.append((F, u, f, n * K + k, n, k))
+    assert got == want
