@@ -137,6 +137,9 @@ class KernelTrace:
 
         self.lib = lib or library()
         self.events = [torch.cuda.Event(enable_timing=True) for _ in range(2 * max_launches)]
+        for e in self.events:  # torch creates the HIP event on its first record
+            e.record()
+        torch.cuda.synchronize()
         self._handles = (ctypes.c_void_p * (2 * max_launches))(*[e.cuda_event for e in self.events])
         self._ids = (_I32 * max_launches)()
         self.n = 0

@@ -54,7 +54,7 @@ struct BwK {
   int D, S, cpg, n_tiles, cap, rs;
 };
 
-template <int K, int NPL, int WAVES, int ACT>
+template <int K, int NPL, int WAVES, int ACT, int PF>
 __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   extern __shared__ float4 xs[];
   const int lane = threadIdx.x & 63;
@@ -91,6 +91,10 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   }
   const float* c1row = p.c1t + g * p.cap;
   const char* xsb = reinterpret_cast<const char*>(xs);
+  // token tiles are staged as in the forward (PF > 0: next tile prefetched into registers)
+  constexpr int NT = WAVES * 64;
+  PrefetchRegs<PF> pf;
+  if constexpr (PF > 0) pf.load(p.xt, NT);
 
   // 8 token tiles (32 tokens) per mask word; the word is stored after the inner loop
   for (int t0 = 0; t0 < p.n_tiles; t0 += 8) {
@@ -100,10 +104,17 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
     const int t1 = t0 + 8 < p.n_tiles ? t0 + 8 : p.n_tiles;
     for (int t = t0; t < t1; ++t) {
       __syncthreads();
-      const float4* src = p.xt + (long long)t * p.D;
-      for (int i = threadIdx.x; i < p.D; i += WAVES * 64) xs[i] = src[i];
+      if constexpr (PF > 0) {
+        pf.store(xs, NT);
+      } else {
+        const float4* src = p.xt + (long long)t * p.D;
+        for (int i = threadIdx.x; i < p.D; i += NT) xs[i] = src[i];
+      }
       __syncthreads();
-      const float4 c1 = *reinterpret_cast<const float4*>(c1row + t * BT);
+      const float4 c1 = *reinterpret_cast<const float4*>(c1row + t * BT);  // issued before the prefetch
+      if constexpr (PF > 0) {
+        if (t + 1 < p.n_tiles) pf.load(p.xt + (long long)(t + 1) * p.D, NT);
+      }
 #pragma unroll
       for (int j = 0; j < NPL; ++j) {
         float4 x[K];
@@ -168,8 +179,80 @@ struct DxK {
   int D, S, K, P, U, Q, UQ, cap, rs, n_tc;
 };
 
+// Edges are consumed in batches of DX_BATCH.  One inline-assembly block requests, with scalar
+// loads, the weight and the T 64-bit mask words of every edge of the batch plus the records of
+// the next batch, then waits once: a wave pays one memory round trip per batch, and the loads,
+// the wait and the destination registers sit in one statement so no compiler-inserted copy can
+// read a register before its load has landed.  The edges of one unit segment come sorted by
+// feature; a register run accumulates consecutive edges of one feature and is added to that
+// feature's accumulator -- a lane-private LDS column, so the feature index may vary at run time --
+// when the feature changes.
+constexpr int DX_BATCH = 4;
+
+template <int T>
+struct MaskWords;
+template <>
+struct MaskWords<1> {
+  typedef unsigned __attribute__((ext_vector_type(2))) v;
+};
+template <>
+struct MaskWords<2> {
+  typedef unsigned __attribute__((ext_vector_type(4))) v;
+};
+template <>
+struct MaskWords<4> {
+  typedef unsigned __attribute__((ext_vector_type(8))) v;
+};
+typedef unsigned __attribute__((ext_vector_type(4))) u32x4;
+
+#define GL_SLOAD_MASK(T) (T == 1 ? "s_load_dwordx2" : (T == 2 ? "s_load_dwordx4" : "s_load_dwordx8"))
+
+template <int T>
+__device__ __forceinline__ void dx_batch_loads(const float* w0, const float* w1, const float* w2, const float* w3,
+                                               const void* m0p, const void* m1p, const void* m2p, const void* m3p,
+                                               const void* recp, float (&w)[DX_BATCH],
+                                               typename MaskWords<T>::v (&m)[DX_BATCH], u32x4& rec) {
+  unsigned wb0, wb1, wb2, wb3;
+  if constexpr (T == 1) {
+    asm volatile(
+        "s_load_dword %0, %9, 0x0\n s_load_dword %1, %10, 0x0\n s_load_dword %2, %11, 0x0\n"
+        "s_load_dword %3, %12, 0x0\n s_load_dwordx2 %4, %13, 0x0\n s_load_dwordx2 %5, %14, 0x0\n"
+        "s_load_dwordx2 %6, %15, 0x0\n s_load_dwordx2 %7, %16, 0x0\n s_load_dwordx4 %8, %17, 0x0\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(wb0), "=&s"(wb1), "=&s"(wb2), "=&s"(wb3), "=&s"(m[0]), "=&s"(m[1]), "=&s"(m[2]), "=&s"(m[3]),
+          "=&s"(rec)
+        : "s"(w0), "s"(w1), "s"(w2), "s"(w3), "s"(m0p), "s"(m1p), "s"(m2p), "s"(m3p), "s"(recp)
+        : "memory");
+  } else if constexpr (T == 2) {
+    asm volatile(
+        "s_load_dword %0, %9, 0x0\n s_load_dword %1, %10, 0x0\n s_load_dword %2, %11, 0x0\n"
+        "s_load_dword %3, %12, 0x0\n s_load_dwordx4 %4, %13, 0x0\n s_load_dwordx4 %5, %14, 0x0\n"
+        "s_load_dwordx4 %6, %15, 0x0\n s_load_dwordx4 %7, %16, 0x0\n s_load_dwordx4 %8, %17, 0x0\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(wb0), "=&s"(wb1), "=&s"(wb2), "=&s"(wb3), "=&s"(m[0]), "=&s"(m[1]), "=&s"(m[2]), "=&s"(m[3]),
+          "=&s"(rec)
+        : "s"(w0), "s"(w1), "s"(w2), "s"(w3), "s"(m0p), "s"(m1p), "s"(m2p), "s"(m3p), "s"(recp)
+        : "memory");
+  } else {
+    asm volatile(
+        "s_load_dword %0, %9, 0x0\n s_load_dword %1, %10, 0x0\n s_load_dword %2, %11, 0x0\n"
+        "s_load_dword %3, %12, 0x0\n s_load_dwordx8 %4, %13, 0x0\n s_load_dwordx8 %5, %14, 0x0\n"
+        "s_load_dwordx8 %6, %15, 0x0\n s_load_dwordx8 %7, %16, 0x0\n s_load_dwordx4 %8, %17, 0x0\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(wb0), "=&s"(wb1), "=&s"(wb2), "=&s"(wb3), "=&s"(m[0]), "=&s"(m[1]), "=&s"(m[2]), "=&s"(m[3]),
+          "=&s"(rec)
+        : "s"(w0), "s"(w1), "s"(w2), "s"(w3), "s"(m0p), "s"(m1p), "s"(m2p), "s"(m3p), "s"(recp)
+        : "memory");
+  }
+  w[0] = __uint_as_float(wb0);
+  w[1] = __uint_as_float(wb1);
+  w[2] = __uint_as_float(wb2);
+  w[3] = __uint_as_float(wb3);
+}
+
 template <int T>
 __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
+  __shared__ float acc[FW][T][64];  // lane-private columns: no barrier needed
   const int lane = threadIdx.x;
   const int bid = blockIdx.x;
   const int tc = bid % p.n_tc;
@@ -193,37 +276,69 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
     }
     hi = a;
   }
-  float acc[FW][T];
 #pragma unroll
   for (int f = 0; f < FW; ++f)
 #pragma unroll
-    for (int j = 0; j < T; ++j) acc[f][j] = 0.f;
+    for (int j = 0; j < T; ++j) acc[f][j][lane] = 0.f;
 
   const int tok0 = tc * 64 * T + lane;
+  const uint32_t* mask_tc = p.mask + (long long)tc * 2 * T;  // this wave's 64-bit words of every record
   for (int si = lo; si < hi; ++si) {
     const int u = p.seg_unit[si];
-    unsigned e = p.seg_begin[si];
+    const unsigned e0 = p.seg_begin[si];
     const unsigned e1 = p.seg_begin[si + 1];
     const long long g = u / p.P;
     const long long nb = g * p.S + (long long)(u % p.P) * US;
     float c1[T];
 #pragma unroll
     for (int j = 0; j < T; ++j) c1[j] = p.c1t[g * p.cap + tok0 + j * 64];
-    unsigned r = p.rec[e];
+    float run[T];
 #pragma unroll
-    for (int f = 0; f < FW; ++f) {
-      while (e < e1 && (int)((r >> (REC_N_BITS + REC_K_BITS)) & 31) == f) {
-        const long long n = nb + (r & ((1u << REC_N_BITS) - 1));
-        const int k = (r >> REC_N_BITS) & ((1 << REC_K_BITS) - 1);
-        const float wv = p.W[n * p.K + k];
-        const uint64_t* mk = reinterpret_cast<const uint64_t*>(p.mask + n * p.rs) + tc * T;
+    for (int j = 0; j < T; ++j) run[j] = 0.f;
+    // records of the first batch (the record array carries DX_BATCH entries of padding)
+    const u32x4 r0 = *reinterpret_cast<const u32x4*>(p.rec + e0);
+    unsigned r[DX_BATCH] = {r0[0], r0[1], r0[2], r0[3]};
+    int fcur = (int)(r[0] >> (REC_N_BITS + REC_K_BITS));
+    for (unsigned e = e0; e < e1; e += DX_BATCH) {
+      const float* wp[DX_BATCH];
+      const void* mp[DX_BATCH];
 #pragma unroll
-        for (int j = 0; j < T; ++j)
-          acc[f][j] = __builtin_fmaf(__builtin_amdgcn_inverse_ballot_w64(mk[j]) ? c1[j] : 0.f, wv, acc[f][j]);
-        ++e;
-        if (e < e1) r = p.rec[e];
+      for (int i = 0; i < DX_BATCH; ++i) {
+        // past the segment end: reuse the first edge (in bounds; its contribution is skipped)
+        const unsigned ri = e + i < e1 ? r[i] : r[0];
+        const long long n = nb + (ri & ((1u << REC_N_BITS) - 1));
+        const int k = (ri >> REC_N_BITS) & ((1 << REC_K_BITS) - 1);
+        wp[i] = p.W + n * p.K + k;
+        mp[i] = mask_tc + n * p.rs;
       }
+      float wv[DX_BATCH];
+      typename MaskWords<T>::v mv[DX_BATCH];
+      u32x4 rn;
+      dx_batch_loads<T>(wp[0], wp[1], wp[2], wp[3], mp[0], mp[1], mp[2], mp[3], p.rec + e + DX_BATCH, wv, mv, rn);
+#pragma unroll
+      for (int i = 0; i < DX_BATCH; ++i) {
+        if (e + i < e1) {
+          const int f = (int)(r[i] >> (REC_N_BITS + REC_K_BITS));
+          if (f != fcur) {
+#pragma unroll
+            for (int j = 0; j < T; ++j) {
+              acc[fcur][j][lane] += run[j];
+              run[j] = 0.f;
+            }
+            fcur = f;
+          }
+#pragma unroll
+          for (int j = 0; j < T; ++j) {
+            const uint64_t mj = (uint64_t)mv[i][2 * j] | ((uint64_t)mv[i][2 * j + 1] << 32);
+            run[j] = __builtin_fmaf(__builtin_amdgcn_inverse_ballot_w64(mj) ? c1[j] : 0.f, wv[i], run[j]);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < DX_BATCH; ++i) r[i] = rn[i];
     }
+#pragma unroll
+    for (int j = 0; j < T; ++j) acc[fcur][j][lane] += run[j];
   }
   float* out = p.part + (long long)q * p.D * p.cap;
 #pragma unroll
@@ -231,7 +346,7 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
     const int d = F * FW + f;
     if (d < p.D) {
 #pragma unroll
-      for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j * 64] = acc[f][j];
+      for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j * 64] = acc[f][j][lane];
     }
   }
 }
@@ -269,7 +384,7 @@ static BwdPlan bwd_plan(int B, int D, int G, int S, int K) {
   BwdPlan q;
   q.bc_max = B < BWD_TOKEN_CHUNK ? B : BWD_TOKEN_CHUNK;
   q.npl = 48 / K;  // 6 neurons per lane at K = 8, 3 at K = 16
-  q.waves = D * 16 > 65536 ? 8 : 4;
+  q.waves = 8;
   q.cpg = ceil_div(S, 64 * q.npl);
   q.n_chunks = (long long)G * q.cpg;
   q.tiles_max = ceil_div(q.bc_max, BT);
@@ -311,28 +426,43 @@ void edge_layout(int D, int G, int S, int K, EdgeHeader* h, size_t* total) {
   h->off_seg_begin = off;
   off += round_up((q.nseg_max + 1) * 4LL, 256);
   h->off_rec = off;
-  off += round_up(q.e_max * 4LL, 256);
+  off += round_up((q.e_max + 8) * 4LL, 256);  // padding: the dX kernel reads records in batches
   *total = off;
 }
 
-template <int K, int NPL, int WAVES, int ACT>
+template <int K, int NPL, int WAVES, int ACT, int PF>
 static int launch_bwd_w(const BwK& k, hipStream_t s, size_t lds) {
-  auto fn = bwd_w_kernel<K, NPL, WAVES, ACT>;
+  auto fn = bwd_w_kernel<K, NPL, WAVES, ACT, PF>;
   GL_TRY(set_lds_limit((const void*)fn, lds));
   GL_LAUNCH(GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)), dim3(WAVES * 64), lds, s, k);
   GL_CHECK_LAUNCH();
   return 0;
 }
 
-template <int ACT>
-static int launch_bwd_w_act(int K, int waves, const BwK& k, hipStream_t s, size_t lds) {
-  if (K == 8) return waves == 8 ? launch_bwd_w<8, 6, 8, ACT>(k, s, lds) : launch_bwd_w<8, 6, 4, ACT>(k, s, lds);
-  return waves == 8 ? launch_bwd_w<16, 3, 8, ACT>(k, s, lds) : launch_bwd_w<16, 3, 4, ACT>(k, s, lds);
+// 8 waves per workgroup; next-tile register prefetch when D is a multiple of 512 and needs at
+// most MAXPF float4 per thread (the dW accumulators leave no room for more)
+template <int ACT, int K, int NPL, int MAXPF>
+static int launch_bwd_w_pf(int D, const BwK& k, hipStream_t s, size_t lds) {
+  int pf = D % 512 == 0 ? D / 512 : 0;
+  if (pf > MAXPF) pf = 0;
+  switch (pf) {
+    case 1: return launch_bwd_w<K, NPL, 8, ACT, 1>(k, s, lds);
+    case 2: return launch_bwd_w<K, NPL, 8, ACT, 2>(k, s, lds);
+    case 4: return launch_bwd_w<K, NPL, 8, ACT, 4>(k, s, lds);
+    case 8: return launch_bwd_w<K, NPL, 8, ACT, 8>(k, s, lds);
+    default: return launch_bwd_w<K, NPL, 8, ACT, 0>(k, s, lds);
+  }
 }
 
-static int launch_bwd_w_any(int K, int waves, int act, const BwK& k, hipStream_t s, size_t lds) {
-  return act == GL_ACT_RELU ? launch_bwd_w_act<GL_ACT_RELU>(K, waves, k, s, lds)
-                            : launch_bwd_w_act<GL_ACT_IDENTITY>(K, waves, k, s, lds);
+template <int ACT>
+static int launch_bwd_w_act(int K, int D, const BwK& k, hipStream_t s, size_t lds) {
+  if (K == 8) return launch_bwd_w_pf<ACT, 8, 6, 8>(D, k, s, lds);
+  return launch_bwd_w_pf<ACT, 16, 3, 4>(D, k, s, lds);
+}
+
+static int launch_bwd_w_any(int K, int D, int act, const BwK& k, hipStream_t s, size_t lds) {
+  return act == GL_ACT_RELU ? launch_bwd_w_act<GL_ACT_RELU>(K, D, k, s, lds)
+                            : launch_bwd_w_act<GL_ACT_IDENTITY>(K, D, k, s, lds);
 }
 
 static int launch_dx(int T, const DxK& k, int FR, hipStream_t s) {
@@ -340,7 +470,6 @@ static int launch_dx(int T, const DxK& k, int FR, hipStream_t s) {
   switch (T) {
     case 1: GL_LAUNCH(GL_KERNEL_DX, dx_kernel<1>, grid, dim3(64), 0, s, k); break;
     case 2: GL_LAUNCH(GL_KERNEL_DX, dx_kernel<2>, grid, dim3(64), 0, s, k); break;
-    case 3: GL_LAUNCH(GL_KERNEL_DX, dx_kernel<3>, grid, dim3(64), 0, s, k); break;
     default: GL_LAUNCH(GL_KERNEL_DX, dx_kernel<4>, grid, dim3(64), 0, s, k); break;
   }
   GL_CHECK_LAUNCH();
@@ -390,7 +519,7 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     GL_CHECK_LAUNCH();
     BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, q.n_chunks,
            a->D, a->S, q.cpg, n_tiles, cap, rs};
-    GL_TRY(launch_bwd_w_any(a->K, q.waves, a->act, bk, s, q.lds));
+    GL_TRY(launch_bwd_w_any(a->K, a->D, a->act, bk, s, q.lds));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
            (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, a->W, part,
            a->D, a->S, a->K, q.P, q.U, q.Q, q.UQ, cap, rs, cap / (64 * T)};

@@ -13,8 +13,8 @@ namespace gl {
 // X is staged feature-major in LDS, 4 tokens per 16-byte slot: one ds_read_b128 gathers one
 // input feature for 4 tokens.
 constexpr int BT = 4;
-// dX: features per range (one register accumulator row each) and slots per edge-list unit.
-constexpr int FW = 16;
+// dX: features per range (one accumulator row each) and slots per edge-list unit.
+constexpr int FW = 8;
 constexpr int US = 1024;
 // input-major edge record: n_local (12 bits) | k << 12 (5 bits) | f_local << 17 (5 bits)
 constexpr int REC_N_BITS = 12;
@@ -25,11 +25,8 @@ constexpr int BWD_TOKEN_CHUNK = 1024;
 constexpr int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
 constexpr long long round_up(long long a, long long b) { return (a + b - 1) / b * b; }
 
-// Tokens of one dX wave (64 lanes x T slots) for a chunk of B tokens.
-inline int dx_slots(int B) {
-  int t = ceil_div(B, 64);
-  return t < 4 ? (t < 1 ? 1 : t) : 4;
-}
+// Tokens of one dX wave: 64 lanes x T slots, T in {1, 2, 4}, for a chunk of B tokens.
+inline int dx_slots(int B) { return B <= 64 ? 1 : (B <= 128 ? 2 : 4); }
 inline int dx_cap(int B) { return (int)round_up(B, 64 * dx_slots(B)); }
 // per-neuron activation-mask record of the backward: one bit per token of the padded chunk
 // (an even number of 32-bit words: the dX kernel reads 64-bit words)
@@ -61,6 +58,28 @@ __device__ __forceinline__ int opaque(int v) {
   asm volatile("" : "+v"(v));
   return v;
 }
+
+// PF float4 slots per thread kept in one register vector (a plain array of float4 is placed in
+// scratch memory by the compiler when PF > 1).
+template <int PF>
+struct PrefetchRegs {
+  typedef float vec __attribute__((ext_vector_type(PF > 0 ? 4 * PF : 4)));
+  vec r;
+  __device__ __forceinline__ void load(const float4* __restrict__ src, int stride) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const float4 v = src[threadIdx.x + i * stride];
+      r[4 * i] = v.x;
+      r[4 * i + 1] = v.y;
+      r[4 * i + 2] = v.z;
+      r[4 * i + 3] = v.w;
+    }
+  }
+  __device__ __forceinline__ void store(float4* dst, int stride) const {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) dst[threadIdx.x + i * stride] = make_float4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
+  }
+};
 
 // DPP move (row/quad patterns) as a float
 template <int CTRL>

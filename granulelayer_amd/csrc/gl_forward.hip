@@ -54,7 +54,7 @@ struct FwdK {
   int D, S, cpg, n_tiles, b_pad;
 };
 
-template <int K, int NPL, int WAVES, int ACT>
+template <int K, int NPL, int WAVES, int ACT, int PF>
 __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   extern __shared__ float4 xs[];
   const int lane = threadIdx.x & 63;
@@ -87,11 +87,27 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   }
 
   const char* xsb = reinterpret_cast<const char*>(xs);
+  // Token tile t (D float4 slots) is staged into LDS.  PF > 0 (D == PF * WAVES * 64): each
+  // thread holds PF slots of the next tile in registers, loaded while the current tile is
+  // computed, so the global-load latency hides behind the gathers; PF == 0: direct copy.
+  constexpr int NT = WAVES * 64;
+  PrefetchRegs<PF> pf;
+  if constexpr (PF > 0) pf.load(p.xt, NT);
   for (int t = 0; t < p.n_tiles; ++t) {
     __syncthreads();
-    const float4* src = p.xt + (long long)t * p.D;
-    for (int i = threadIdx.x; i < p.D; i += WAVES * 64) xs[i] = src[i];
+    if constexpr (PF > 0) {
+      pf.store(xs, NT);
+    } else {
+      const float4* src = p.xt + (long long)t * p.D;
+      for (int e = threadIdx.x; e < p.D; e += NT) xs[e] = src[e];
+    }
     __syncthreads();
+    if constexpr (PF > 0) {
+      if (t + 1 < p.n_tiles) {
+        const float4* src = p.xt + (long long)(t + 1) * p.D;
+        pf.load(src, NT);
+      }
+    }
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
@@ -158,7 +174,7 @@ struct FwdPlan {
 static FwdPlan fwd_plan(const GlFwdArgs* a) {
   FwdPlan q;
   q.npl = 64 / a->K;  // 8 neurons per lane at K = 8, 4 at K = 16 (~140 VGPRs of parameters)
-  q.waves = a->D * 16 > 65536 ? 8 : 4;
+  q.waves = 8;
   q.cpg = ceil_div(a->S, 64 * q.npl);
   q.n_chunks = (long long)a->G * q.cpg;
   q.n_tiles = ceil_div(a->B, BT);
@@ -169,9 +185,9 @@ static FwdPlan fwd_plan(const GlFwdArgs* a) {
   return q;
 }
 
-template <int K, int NPL, int WAVES, int ACT>
+template <int K, int NPL, int WAVES, int ACT, int PF>
 static int launch_fwd(const FwdK& k, hipStream_t s, size_t lds) {
-  auto fn = fwd_kernel<K, NPL, WAVES, ACT>;
+  auto fn = fwd_kernel<K, NPL, WAVES, ACT, PF>;
   GL_TRY(set_lds_limit((const void*)fn, lds));
   dim3 grid((unsigned)ceil_div(k.n_chunks, WAVES));
   GL_LAUNCH(GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), lds, s, k);
@@ -179,10 +195,25 @@ static int launch_fwd(const FwdK& k, hipStream_t s, size_t lds) {
   return 0;
 }
 
+// 8 waves per workgroup (one workgroup per CU at D = 4096); the next tile is prefetched into
+// registers when D is a multiple of the 512 threads and needs at most 16 float4 per thread
+template <int ACT, int K, int NPL>
+static int launch_fwd_pf(int D, const FwdK& k, hipStream_t s, size_t lds) {
+  const int pf = D % 512 == 0 ? D / 512 : 0;
+  switch (pf) {
+    case 1: return launch_fwd<K, NPL, 8, ACT, 1>(k, s, lds);
+    case 2: return launch_fwd<K, NPL, 8, ACT, 2>(k, s, lds);
+    case 4: return launch_fwd<K, NPL, 8, ACT, 4>(k, s, lds);
+    case 8: return launch_fwd<K, NPL, 8, ACT, 8>(k, s, lds);
+    case 16: return launch_fwd<K, NPL, 8, ACT, 16>(k, s, lds);
+    default: return launch_fwd<K, NPL, 8, ACT, 0>(k, s, lds);
+  }
+}
+
 template <int ACT>
-static int launch_fwd_act(int K, int waves, const FwdK& k, hipStream_t s, size_t lds) {
-  if (K == 8) return waves == 8 ? launch_fwd<8, 8, 8, ACT>(k, s, lds) : launch_fwd<8, 8, 4, ACT>(k, s, lds);
-  return waves == 8 ? launch_fwd<16, 4, 8, ACT>(k, s, lds) : launch_fwd<16, 4, 4, ACT>(k, s, lds);
+static int launch_fwd_act(int K, int D, const FwdK& k, hipStream_t s, size_t lds) {
+  if (K == 8) return launch_fwd_pf<ACT, 8, 8>(D, k, s, lds);
+  return launch_fwd_pf<ACT, 16, 4>(D, k, s, lds);
 }
 
 int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const float* W,
@@ -222,8 +253,8 @@ extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
   float* part = (float*)((char*)a->ws + q.xt_bytes);
   GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, 0, q.n_tiles, xt, s));
   FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles, q.b_pad};
-  GL_TRY(a->act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU>(a->K, q.waves, k, s, q.lds)
-                                : launch_fwd_act<GL_ACT_IDENTITY>(a->K, q.waves, k, s, q.lds));
+  GL_TRY(a->act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU>(a->K, a->D, k, s, q.lds)
+                                : launch_fwd_act<GL_ACT_IDENTITY>(a->K, a->D, k, s, q.lds));
   dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(q.b_pad, 32));
   GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_kernel, grid, dim3(256), 0, s, part, a->counts, a->pre, a->B, a->G, q.cpg, q.b_pad,
                      0, a->pool);
