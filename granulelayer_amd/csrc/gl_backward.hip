@@ -49,9 +49,9 @@ struct BwK {
   const float* __restrict__ c1t;
   float* dW;
   float* db;
-  uint32_t* mask;  // [G*S][rs] activation-mask words
-  long long n_chunks;
-  int D, S, cpg, n_tiles, cap, rs;
+  uint32_t* mask;  // [n_tc][G*S][mw2] activation-mask words (one slab per dX token slice)
+  long long n_chunks, NS;
+  int D, S, cpg, n_tiles, cap, mw2;
 };
 
 template <int K, int NPL, int WAVES, int ACT, int PF>
@@ -146,13 +146,14 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
       }
     }
     const int ln = opaque(lane);  // address math kept local (see opaque())
-    uint32_t* mrow = p.mask + (g * p.S + s_lo + ln) * p.rs + (t0 >> 3);
+    const int word = t0 >> 3;
+    uint32_t* mrow = p.mask + ((long long)(word / p.mw2) * p.NS + g * p.S + s_lo + ln) * p.mw2 + word % p.mw2;
 #pragma unroll
     for (int j = 0; j < NPL; ++j)
-      if (active && s_lo + j * 64 + ln < n_g) mrow[(long long)j * 64 * p.rs] = mw[j];
+      if (active && s_lo + j * 64 + ln < n_g) mrow[(long long)j * 64 * p.mw2] = mw[j];
   }
+  // mask words of tokens past the chunk are never written: their c1 is zero, so dX ignores them
   if (!active) return;
-  const int words_written = (p.n_tiles + 7) >> 3;
   const int ln = opaque(lane);
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
@@ -162,8 +163,6 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
 #pragma unroll
     for (int k = 0; k < K; ++k) p.dW[n * K + k] += dw[j][k];
     p.db[n] += dbv[j];
-    uint32_t* r = p.mask + n * p.rs;
-    for (int wi = words_written; wi < p.rs; ++wi) r[wi] = 0u;  // tokens of the padded chunk tail
   }
 }
 
@@ -172,173 +171,198 @@ struct DxK {
   const uint32_t* __restrict__ seg_ptr;
   const int32_t* __restrict__ seg_unit;
   const uint32_t* __restrict__ seg_begin;
-  const float* __restrict__ c1t;
-  const uint32_t* __restrict__ mask;
+  const float* __restrict__ c1t;     // [G][cap]
+  const uint32_t* __restrict__ mask;  // [n_tc][NS][2T]
   const float* __restrict__ W;
   float* part;  // [Q][D][cap]
-  int D, S, K, P, U, Q, UQ, cap, rs, n_tc;
+  long long NS;
+  int D, S, P, U, QL, UQ, FR, cap, n_tc;
 };
 
-// Edges are consumed in batches of DX_BATCH.  One inline-assembly block requests, with scalar
-// loads, the weight and the T 64-bit mask words of every edge of the batch plus the records of
-// the next batch, then waits once: a wave pays one memory round trip per batch, and the loads,
-// the wait and the destination registers sit in one statement so no compiler-inserted copy can
-// read a register before its load has landed.  The edges of one unit segment come sorted by
-// feature; a register run accumulates consecutive edges of one feature and is added to that
-// feature's accumulator -- a lane-private LDS column, so the feature index may vary at run time --
-// when the feature changes.
-constexpr int DX_BATCH = 4;
-
+// ---- dX ----------------------------------------------------------------------------------------
+// One wave owns FW consecutive features, one range of UQ units and 64*T tokens (lane = token,
+// slot j = token + 64 j).  It walks the input-major edges of its features unit by unit, in the
+// stored order, and for every edge (n, k) -> d adds c1[b, g(n)] * [mask[n, b]] * W[n, k] to the
+// register accumulator of d.
+//
+// Edges are taken in chunks of up to 64 (one segment, or a 64-edge piece of a long one).  The
+// lanes first gather, one edge each, the chunk's records, weights and mask words with vector
+// loads (64 independent requests per instruction: random scalar loads would be limited by the
+// scalar cache's miss rate); the gathers of the next chunk are issued before the current chunk is
+// computed.  The compute loop then broadcasts edge i's weight and 64-bit mask words to the token
+// lanes with v_readlane (SGPR operands: the weight feeds the FMA, each mask word is the lane mask
+// of a v_cndmask) and accumulates into acc[f] through a branch tree on the uniform feature f.
 template <int T>
-struct MaskWords;
-template <>
-struct MaskWords<1> {
-  typedef unsigned __attribute__((ext_vector_type(2))) v;
+struct DxGather {
+  unsigned rec;
+  float w;
+  unsigned m[2 * T];
 };
-template <>
-struct MaskWords<2> {
-  typedef unsigned __attribute__((ext_vector_type(4))) v;
-};
-template <>
-struct MaskWords<4> {
-  typedef unsigned __attribute__((ext_vector_type(8))) v;
-};
-typedef unsigned __attribute__((ext_vector_type(4))) u32x4;
 
-#define GL_SLOAD_MASK(T) (T == 1 ? "s_load_dwordx2" : (T == 2 ? "s_load_dwordx4" : "s_load_dwordx8"))
+struct DxChunk {
+  int si;           // segment index
+  unsigned e, end;  // chunk begin, segment end (edge positions)
+  int u;            // unit of the segment
+};
 
-template <int T>
-__device__ __forceinline__ void dx_batch_loads(const float* w0, const float* w1, const float* w2, const float* w3,
-                                               const void* m0p, const void* m1p, const void* m2p, const void* m3p,
-                                               const void* recp, float (&w)[DX_BATCH],
-                                               typename MaskWords<T>::v (&m)[DX_BATCH], u32x4& rec) {
-  unsigned wb0, wb1, wb2, wb3;
-  if constexpr (T == 1) {
-    asm volatile(
-        "s_load_dword %0, %9, 0x0\n s_load_dword %1, %10, 0x0\n s_load_dword %2, %11, 0x0\n"
-        "s_load_dword %3, %12, 0x0\n s_load_dwordx2 %4, %13, 0x0\n s_load_dwordx2 %5, %14, 0x0\n"
-        "s_load_dwordx2 %6, %15, 0x0\n s_load_dwordx2 %7, %16, 0x0\n s_load_dwordx4 %8, %17, 0x0\n"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&s"(wb0), "=&s"(wb1), "=&s"(wb2), "=&s"(wb3), "=&s"(m[0]), "=&s"(m[1]), "=&s"(m[2]), "=&s"(m[3]),
-          "=&s"(rec)
-        : "s"(w0), "s"(w1), "s"(w2), "s"(w3), "s"(m0p), "s"(m1p), "s"(m2p), "s"(m3p), "s"(recp)
-        : "memory");
-  } else if constexpr (T == 2) {
-    asm volatile(
-        "s_load_dword %0, %9, 0x0\n s_load_dword %1, %10, 0x0\n s_load_dword %2, %11, 0x0\n"
-        "s_load_dword %3, %12, 0x0\n s_load_dwordx4 %4, %13, 0x0\n s_load_dwordx4 %5, %14, 0x0\n"
-        "s_load_dwordx4 %6, %15, 0x0\n s_load_dwordx4 %7, %16, 0x0\n s_load_dwordx4 %8, %17, 0x0\n"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&s"(wb0), "=&s"(wb1), "=&s"(wb2), "=&s"(wb3), "=&s"(m[0]), "=&s"(m[1]), "=&s"(m[2]), "=&s"(m[3]),
-          "=&s"(rec)
-        : "s"(w0), "s"(w1), "s"(w2), "s"(w3), "s"(m0p), "s"(m1p), "s"(m2p), "s"(m3p), "s"(recp)
-        : "memory");
+__device__ __forceinline__ void dx_next(const DxK& p, DxChunk& c, int hi) {
+  if (c.e + 64 < c.end) {
+    c.e += 64;
   } else {
-    asm volatile(
-        "s_load_dword %0, %9, 0x0\n s_load_dword %1, %10, 0x0\n s_load_dword %2, %11, 0x0\n"
-        "s_load_dword %3, %12, 0x0\n s_load_dwordx8 %4, %13, 0x0\n s_load_dwordx8 %5, %14, 0x0\n"
-        "s_load_dwordx8 %6, %15, 0x0\n s_load_dwordx8 %7, %16, 0x0\n s_load_dwordx4 %8, %17, 0x0\n"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&s"(wb0), "=&s"(wb1), "=&s"(wb2), "=&s"(wb3), "=&s"(m[0]), "=&s"(m[1]), "=&s"(m[2]), "=&s"(m[3]),
-          "=&s"(rec)
-        : "s"(w0), "s"(w1), "s"(w2), "s"(w3), "s"(m0p), "s"(m1p), "s"(m2p), "s"(m3p), "s"(recp)
-        : "memory");
+    c.si += 1;
+    if (c.si < hi) {
+      c.e = c.end;
+      c.end = p.seg_begin[c.si + 1];
+      c.u = p.seg_unit[c.si];
+    }
   }
-  w[0] = __uint_as_float(wb0);
-  w[1] = __uint_as_float(wb1);
-  w[2] = __uint_as_float(wb2);
-  w[3] = __uint_as_float(wb3);
+}
+
+// record of the lane's edge (lanes past the chunk take the chunk's first edge: in bounds, unused)
+__device__ __forceinline__ unsigned dx_load_rec(const DxK& p, const DxChunk& c, int lane) {
+  const unsigned n = min(c.end - c.e, 64u);
+  return p.rec[c.e + ((unsigned)lane < n ? (unsigned)lane : 0u)];
+}
+
+template <int K, int T>
+__device__ __forceinline__ void dx_gather(const DxK& p, const uint32_t* mask_tc, const DxChunk& c, unsigned rec,
+                                          DxGather<T>& g) {
+  const long long nb = (long long)(c.u / p.P) * p.S + (long long)(c.u % p.P) * US;  // first neuron of the unit
+  const unsigned woff = rec & REC_OFF_MASK;  // byte offset of W[n, k] in the unit
+  const unsigned nl = woff >> (K == 8 ? 5 : 6);
+  g.rec = rec;
+  g.w = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.W + nb * K) + woff);
+  const uint32_t* mr = mask_tc + (nb + nl) * (2 * T);
+  if constexpr (T == 1) {
+    const uint2 v = *reinterpret_cast<const uint2*>(mr);
+    g.m[0] = v.x, g.m[1] = v.y;
+  } else {
+#pragma unroll
+    for (int h = 0; h < T / 2; ++h) {
+      const uint4 v = *reinterpret_cast<const uint4*>(mr + 4 * h);
+      g.m[4 * h] = v.x, g.m[4 * h + 1] = v.y, g.m[4 * h + 2] = v.z, g.m[4 * h + 3] = v.w;
+    }
+  }
 }
 
 template <int T>
+__device__ __forceinline__ void dx_load_c1(const DxK& p, int u, int tok0, float (&c1)[T]) {
+  const float* c = p.c1t + (long long)(u / p.P) * p.cap + tok0;
+#pragma unroll
+  for (int j = 0; j < T; ++j) c1[j] = c[j * 64];
+}
+
+// Edges i in [i0, i1) of the chunk, all of feature F0 of the range: acc[F0][j] += [m_j] c1[j] w.
+template <int F0, int T>
+__device__ __forceinline__ void dx_run(const DxGather<T>& g, int i0, int i1, const float (&c1)[T],
+                                       float (&acc)[FW][T]) {
+  for (int i = i0; i < i1; ++i) {
+    const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g.w), i));
+#pragma unroll
+    for (int j = 0; j < T; ++j) {
+      const uint64_t m = (uint64_t)(unsigned)__builtin_amdgcn_readlane((int)g.m[2 * j], i) |
+                         ((uint64_t)(unsigned)__builtin_amdgcn_readlane((int)g.m[2 * j + 1], i) << 32);
+      acc[F0][j] = __builtin_fmaf(__builtin_amdgcn_inverse_ballot_w64(m) ? c1[j] : 0.f, w, acc[F0][j]);
+    }
+  }
+}
+
+// The chunk's edges are sorted by feature: ballots give every feature's edge range, and one loop
+// per feature (unrolled over the range) keeps every accumulator index a compile-time constant.
+template <int T>
+__device__ __forceinline__ void dx_compute(const DxGather<T>& g, int n, int lane, const float (&c1)[T],
+                                           float (&acc)[FW][T]) {
+  const int f = lane < n ? (int)((g.rec >> REC_F_SHIFT) & REC_F_MASK) : FW;
+  int b[FW + 1];
+  b[0] = 0;
+#pragma unroll
+  for (int x = 1; x <= FW; ++x) b[x] = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(f < x));
+#define GL_DX_RUN(X) dx_run<X, T>(g, b[X], b[X + 1], c1, acc)
+  GL_DX_RUN(0);
+  GL_DX_RUN(1);
+  GL_DX_RUN(2);
+  GL_DX_RUN(3);
+  GL_DX_RUN(4);
+  GL_DX_RUN(5);
+  GL_DX_RUN(6);
+  GL_DX_RUN(7);
+#undef GL_DX_RUN
+  static_assert(FW == 8, "dx_compute unrolls eight features");
+}
+
+template <int K, int T>
 __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
-  __shared__ float acc[FW][T][64];  // lane-private columns: no barrier needed
   const int lane = threadIdx.x;
+  // Workgroups are dispatched round-robin over the 8 XCDs.  All feature ranges of one unit range
+  // run on the same XCD, side by side (F fastest), so the unit range's weights and mask words are
+  // fetched into that XCD's L2 and shared by the waves of every feature range.
   const int bid = blockIdx.x;
-  const int tc = bid % p.n_tc;
-  const int q = (bid / p.n_tc) % p.Q;
-  const int F = bid / (p.n_tc * p.Q);
+  const int xcd = bid & 7;
+  const int loc = bid >> 3;
+  const int F = loc % p.FR;
+  const int rest = loc / p.FR;
+  const int ql = rest % p.QL;
+  const int tc = rest / p.QL;
+  const int q = ql * 8 + xcd;
   const int u_lo = q * p.UQ;
   const int u_hi = min(u_lo + p.UQ, p.U);
-  // segments of feature range F whose unit lies in [u_lo, u_hi) (units ascend within F)
   int lo = (int)p.seg_ptr[F], hi = (int)p.seg_ptr[F + 1];
   {
     int a = lo, b = hi;
     while (a < b) {
-      int m = (a + b) >> 1;
-      if (p.seg_unit[m] < u_lo) a = m + 1; else b = m;
+      int mid = (a + b) >> 1;
+      if (p.seg_unit[mid] < u_lo) a = mid + 1; else b = mid;
     }
     lo = a;
     b = hi;
     while (a < b) {
-      int m = (a + b) >> 1;
-      if (p.seg_unit[m] < u_hi) a = m + 1; else b = m;
+      int mid = (a + b) >> 1;
+      if (p.seg_unit[mid] < u_hi) a = mid + 1; else b = mid;
     }
     hi = a;
   }
+  float acc[FW][T];
 #pragma unroll
   for (int f = 0; f < FW; ++f)
 #pragma unroll
-    for (int j = 0; j < T; ++j) acc[f][j][lane] = 0.f;
+    for (int j = 0; j < T; ++j) acc[f][j] = 0.f;
 
   const int tok0 = tc * 64 * T + lane;
-  const uint32_t* mask_tc = p.mask + (long long)tc * 2 * T;  // this wave's 64-bit words of every record
-  for (int si = lo; si < hi; ++si) {
-    const int u = p.seg_unit[si];
-    const unsigned e0 = p.seg_begin[si];
-    const unsigned e1 = p.seg_begin[si + 1];
-    const long long g = u / p.P;
-    const long long nb = g * p.S + (long long)(u % p.P) * US;
+  const uint32_t* mask_tc = p.mask + (long long)tc * p.NS * (2 * T);
+  if (lo < hi) {
+    DxChunk cc{lo, p.seg_begin[lo], p.seg_begin[lo + 1], p.seg_unit[lo]};
+    DxGather<T> gc;
+    dx_gather<K, T>(p, mask_tc, cc, dx_load_rec(p, cc, lane), gc);
     float c1[T];
+    dx_load_c1<T>(p, cc.u, tok0, c1);
+    DxChunk cn = cc;
+    dx_next(p, cn, hi);
+    unsigned rn = cn.si < hi ? dx_load_rec(p, cn, lane) : 0u;
+    for (;;) {
+      // next chunk: gather (its records were requested one iteration ago), then request the
+      // records of the chunk after it; both are in flight while the current chunk is computed
+      const bool more = cn.si < hi;
+      DxGather<T> gn = gc;
+      float c1n[T];
 #pragma unroll
-    for (int j = 0; j < T; ++j) c1[j] = p.c1t[g * p.cap + tok0 + j * 64];
-    float run[T];
-#pragma unroll
-    for (int j = 0; j < T; ++j) run[j] = 0.f;
-    // records of the first batch (the record array carries DX_BATCH entries of padding)
-    const u32x4 r0 = *reinterpret_cast<const u32x4*>(p.rec + e0);
-    unsigned r[DX_BATCH] = {r0[0], r0[1], r0[2], r0[3]};
-    int fcur = (int)(r[0] >> (REC_N_BITS + REC_K_BITS));
-    for (unsigned e = e0; e < e1; e += DX_BATCH) {
-      const float* wp[DX_BATCH];
-      const void* mp[DX_BATCH];
-#pragma unroll
-      for (int i = 0; i < DX_BATCH; ++i) {
-        // past the segment end: reuse the first edge (in bounds; its contribution is skipped)
-        const unsigned ri = e + i < e1 ? r[i] : r[0];
-        const long long n = nb + (ri & ((1u << REC_N_BITS) - 1));
-        const int k = (ri >> REC_N_BITS) & ((1 << REC_K_BITS) - 1);
-        wp[i] = p.W + n * p.K + k;
-        mp[i] = mask_tc + n * p.rs;
+      for (int j = 0; j < T; ++j) c1n[j] = c1[j];
+      DxChunk cnn = cn;
+      unsigned rnn = 0u;
+      if (more) {
+        dx_gather<K, T>(p, mask_tc, cn, rn, gn);
+        if (cn.si != cc.si) dx_load_c1<T>(p, cn.u, tok0, c1n);
+        dx_next(p, cnn, hi);
+        if (cnn.si < hi) rnn = dx_load_rec(p, cnn, lane);
       }
-      float wv[DX_BATCH];
-      typename MaskWords<T>::v mv[DX_BATCH];
-      u32x4 rn;
-      dx_batch_loads<T>(wp[0], wp[1], wp[2], wp[3], mp[0], mp[1], mp[2], mp[3], p.rec + e + DX_BATCH, wv, mv, rn);
+      dx_compute<T>(gc, (int)min(cc.end - cc.e, 64u), lane, c1, acc);
+      if (!more) break;
+      cc = cn;
+      gc = gn;
 #pragma unroll
-      for (int i = 0; i < DX_BATCH; ++i) {
-        if (e + i < e1) {
-          const int f = (int)(r[i] >> (REC_N_BITS + REC_K_BITS));
-          if (f != fcur) {
-#pragma unroll
-            for (int j = 0; j < T; ++j) {
-              acc[fcur][j][lane] += run[j];
-              run[j] = 0.f;
-            }
-            fcur = f;
-          }
-#pragma unroll
-          for (int j = 0; j < T; ++j) {
-            const uint64_t mj = (uint64_t)mv[i][2 * j] | ((uint64_t)mv[i][2 * j + 1] << 32);
-            run[j] = __builtin_fmaf(__builtin_amdgcn_inverse_ballot_w64(mj) ? c1[j] : 0.f, wv[i], run[j]);
-          }
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < DX_BATCH; ++i) r[i] = rn[i];
+      for (int j = 0; j < T; ++j) c1[j] = c1n[j];
+      cn = cnn;
+      rn = rnn;
     }
-#pragma unroll
-    for (int j = 0; j < T; ++j) acc[fcur][j][lane] += run[j];
   }
   float* out = p.part + (long long)q * p.D * p.cap;
 #pragma unroll
@@ -346,7 +370,7 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
     const int d = F * FW + f;
     if (d < p.D) {
 #pragma unroll
-      for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j * 64] = acc[f][j][lane];
+      for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j * 64] = acc[f][j];
     }
   }
 }
@@ -375,7 +399,7 @@ __global__ void __launch_bounds__(256) dx_reduce_kernel(const float* __restrict_
 
 // ---- host side -------------------------------------------------------------------------------
 struct BwdPlan {
-  int bc_max, npl, waves, cpg, tiles_max, cap_max, rs_max, FR, P, U, Q, UQ;
+  int bc_max, npl, waves, cpg, tiles_max, cap_max, rs_max, FR, P, U, Q, QL, UQ;
   long long n_chunks, e_max, nseg_max;
   size_t lds, xt_bytes, c1_bytes, mask_bytes, part_bytes, edges_bytes;
 };
@@ -393,14 +417,16 @@ static BwdPlan bwd_plan(int B, int D, int G, int S, int K) {
   q.FR = ceil_div(D, FW);
   q.P = ceil_div(S, US);
   q.U = G * q.P;
+  // Q = 8 * QL unit ranges (one set of QL per XCD); enough waves to fill the chip a few times
   const int n_tc = q.cap_max / (64 * dx_slots(q.bc_max));
-  const long long waves_wanted = 8192;
-  long long Qw = (waves_wanted + (long long)q.FR * n_tc - 1) / ((long long)q.FR * n_tc);
-  if (Qw < 1) Qw = 1;
-  if (Qw > q.U) Qw = q.U;
-  if (Qw > 64) Qw = 64;
-  q.UQ = ceil_div(q.U, Qw);
-  q.Q = ceil_div(q.U, q.UQ);
+  const long long waves_wanted = 32768;
+  long long ql = (waves_wanted + 8LL * q.FR * n_tc - 1) / (8LL * q.FR * n_tc);
+  if (ql < 1) ql = 1;
+  if (ql > 8) ql = 8;
+  if (8 * ql > q.U) ql = ceil_div(q.U, 8);
+  q.QL = (int)ql;
+  q.Q = 8 * q.QL;
+  q.UQ = ceil_div(q.U, q.Q);
   q.lds = (size_t)D * 16;
   q.xt_bytes = (size_t)round_up((long long)q.tiles_max * D * 16, 256);
   q.c1_bytes = (size_t)round_up((long long)G * q.cap_max * 4, 256);
@@ -465,15 +491,21 @@ static int launch_bwd_w_any(int K, int D, int act, const BwK& k, hipStream_t s, 
                             : launch_bwd_w_act<GL_ACT_IDENTITY>(K, D, k, s, lds);
 }
 
-static int launch_dx(int T, const DxK& k, int FR, hipStream_t s) {
-  dim3 grid((unsigned)((long long)FR * k.Q * k.n_tc));
-  switch (T) {
-    case 1: GL_LAUNCH(GL_KERNEL_DX, dx_kernel<1>, grid, dim3(64), 0, s, k); break;
-    case 2: GL_LAUNCH(GL_KERNEL_DX, dx_kernel<2>, grid, dim3(64), 0, s, k); break;
-    default: GL_LAUNCH(GL_KERNEL_DX, dx_kernel<4>, grid, dim3(64), 0, s, k); break;
-  }
+template <int K, int T>
+static int launch_dx_kt(const DxK& k, hipStream_t s) {
+  auto fn = dx_kernel<K, T>;
+  GL_LAUNCH(GL_KERNEL_DX, fn, dim3((unsigned)(8LL * k.FR * k.QL * k.n_tc)), dim3(64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;
+}
+
+template <int K>
+static int launch_dx_k(int T, const DxK& k, hipStream_t s) {
+  return T == 1 ? launch_dx_kt<K, 1>(k, s) : (T == 2 ? launch_dx_kt<K, 2>(k, s) : launch_dx_kt<K, 4>(k, s));
+}
+
+static int launch_dx(int K, int T, const DxK& k, hipStream_t s) {
+  return K == 8 ? launch_dx_k<8>(T, k, s) : launch_dx_k<16>(T, k, s);
 }
 
 }  // namespace gl
@@ -512,18 +544,18 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     const int n_tiles = ceil_div(Bc, BT);
     const int T = dx_slots(Bc);
     const int cap = dx_cap(Bc);
-    const int rs = mask_stride(Bc);
     GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles, xt, s));
     GL_LAUNCH(GL_KERNEL_C1T, c1t_kernel, dim3((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(cap, 32)), dim3(256), 0, s,
                        a->g_pre, a->counts, c1t, a->G, b0, Bc, cap, a->pool);
     GL_CHECK_LAUNCH();
-    BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, q.n_chunks,
-           a->D, a->S, q.cpg, n_tiles, cap, rs};
+    const long long NS = (long long)a->G * a->S;
+    BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, q.n_chunks, NS,
+           a->D, a->S, q.cpg, n_tiles, cap, 2 * T};
     GL_TRY(launch_bwd_w_any(a->K, a->D, a->act, bk, s, q.lds));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
            (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, a->W, part,
-           a->D, a->S, a->K, q.P, q.U, q.Q, q.UQ, cap, rs, cap / (64 * T)};
-    GL_TRY(launch_dx(T, dk, q.FR, s));
+           NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * T)};
+    GL_TRY(launch_dx(a->K, T, dk, s));
     GL_LAUNCH(GL_KERNEL_DX_REDUCE, dx_reduce_kernel, dim3((unsigned)ceil_div(a->D, 32), (unsigned)ceil_div(Bc, 32)), dim3(256), 0,
                        s, part, a->dX, a->D, cap, q.Q, b0, Bc);
     GL_CHECK_LAUNCH();

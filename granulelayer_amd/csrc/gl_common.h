@@ -17,8 +17,13 @@ constexpr int BT = 4;
 constexpr int FW = 8;
 constexpr int US = 1024;
 // input-major edge record: n_local (12 bits) | k << 12 (5 bits) | f_local << 17 (5 bits)
-constexpr int REC_N_BITS = 12;
-constexpr int REC_K_BITS = 5;
+// dX edge record (32 bit): bits [0, 16) byte offset of W[n, k] inside its unit,
+// (s_local * K + k) * 4; bits [16, 24) feature inside the range; bit 31 set when the feature
+// differs from the one of the previous edge of the same segment (a new accumulation run).
+constexpr int REC_F_SHIFT = 16;
+constexpr unsigned REC_OFF_MASK = 0xffffu;
+constexpr unsigned REC_F_MASK = 0xffu;
+constexpr unsigned REC_NEWF = 1u << 31;
 // largest token chunk of one backward pass (bounds the per-neuron mask record)
 constexpr int BWD_TOKEN_CHUNK = 1024;
 

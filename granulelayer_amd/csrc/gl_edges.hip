@@ -175,11 +175,11 @@ __global__ void __launch_bounds__(EB_THREADS) edges_scatter_kernel(ScatterK p) {
     const unsigned long long key = keys[i];
     const int d = (int)(key >> 32);
     const int F = d / FW;
-    const unsigned el = (unsigned)key;
-    const unsigned s_local = el / (unsigned)p.K, k = el % (unsigned)p.K;
+    const unsigned el = (unsigned)key;  // s_local * K + k
     const unsigned long long o = p.off[(long long)F * p.U + u];
     const unsigned pos = (unsigned)o + ((unsigned)i - loc[F]);
-    p.rec[pos] = s_local | (k << REC_N_BITS) | ((unsigned)(d % FW) << (REC_N_BITS + REC_K_BITS));
+    const bool newf = (unsigned)i != loc[F] && (int)(keys[i - 1] >> 32) != d;
+    p.rec[pos] = el * 4u | ((unsigned)(d % FW) << REC_F_SHIFT) | (newf ? REC_NEWF : 0u);
     if ((unsigned)i == loc[F]) {
       const unsigned seg = (unsigned)(o >> 32);
       p.seg_unit[seg] = u;

@@ -153,7 +153,9 @@ def partition(H: int, G: int, block: int = 8):
 # ----------------------------------------------------------------------------------------------
 # transposed (input-major) edge list of the HIP dX kernel
 # ----------------------------------------------------------------------------------------------
-REC_N_BITS, REC_K_BITS = 12, 5  # record = n_local | k << 12 | f_local << 17
+# record = (n_local * K + k) * 4 | f_local << 16 | newf << 31, where n_local is the slot inside
+# the unit and newf marks an edge whose feature differs from the previous edge of its segment
+REC_F_SHIFT, REC_NEWF = 16, 1 << 31
 
 
 def xedges(idx, counts, S, D, Fw, US):
@@ -163,7 +165,8 @@ def xedges(idx, counts, S, D, Fw, US):
         (F = d // Fw, unit u, f_local = d % Fw, eid = n*K + k)
     where unit u = g * P + s // US (P = ceil(S / US) pieces per group) and n = g*S + s.
     Returns dict:
-      rec       uint32 [E]   n_local | k << 12 | f_local << 17   (n_local = s % US)
+      rec       uint32 [E]   (n_local * K + k) * 4 | f_local << 16 | newf << 31   (n_local = s % US;
+                             newf: same segment as the previous edge, different feature)
       seg_ptr   int64 [FR+1] segment range of feature range F
       seg_unit  int32 [nseg] unit of each (F, u) segment with at least one edge, ascending in u
       seg_begin int64 [nseg+1] first edge of each segment (+ total E)
@@ -185,9 +188,13 @@ def xedges(idx, counts, S, D, Fw, US):
     F = d // Fw
     fl = d % Fw
     order = np.lexsort((eid, fl, u, F))
-    rec = ((nn % S) % US)[order] | (kk[order] << REC_N_BITS) | (fl[order] << (REC_N_BITS + REC_K_BITS))
-    Fo, uo = F[order], u[order]
+    Fo, uo, flo = F[order], u[order], fl[order]
     key = Fo * (G * P) + uo
+    newf = np.zeros(len(key), bool)
+    if len(key) > 1:
+        newf[1:] = (key[1:] == key[:-1]) & (flo[1:] != flo[:-1])
+    el = ((nn % S) % US) * K + kk
+    rec = (el[order] * 4) | (flo << REC_F_SHIFT) | (newf.astype(np.int64) << 31)
     if len(key):
         starts = np.concatenate([[0], np.nonzero(np.diff(key))[0] + 1])
     else:

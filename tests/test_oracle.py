@@ -247,9 +247,14 @@ def test_xedges_matches_bruteforce(oracle, D, G, S, K, Fw, US):
         for si in range(e["seg_ptr"][F], e["seg_ptr"][F + 1]):
             u = int(e["seg_unit"][si])
             g, piece = divmod(u, P)
+            prev_f = None
             for j in range(e["seg_begin"][si], e["seg_begin"][si + 1]):
                 r = int(e["rec"][j])
-                nl, k, f = r & 4095, (r >> 12) & 31, (r >> 17) & 31
+                el, f, newf = (r & 0xFFFF) >> 2, (r >> 16) & 0xFF, r >> 31
+                assert r & 3 == 0 and (r >> 24) & 0x7F == 0
+                assert newf == (prev_f is not None and f != prev_f)
+                prev_f = f
+                nl, k = divmod(el, K)
                 n = g * S + piece * US + nl
                 got.append((F, u, f, n * K + k, n, k))
     assert got == want
