@@ -48,19 +48,38 @@ def cpu_model() -> str:
 
 
 def algorithmic(kernel: str, B: int, N: int, K: int, D: int, G: int, x_bytes: int = 4):
-    """(bytes, flops) per launch of a kernel: each input read once, each output written once."""
+    """(bytes, flops) of one training step's launches of a kernel (one launch each, except the
+    AdamW kernel: one launch for the weights, one for the bias): every input read once, every
+    output written once."""
     E = N * K
     if kernel == "fwd_kernel":
+        # idx + W + bias, X once, pooled output
         return 4 * E + 4 * E + 4 * N + B * D * x_bytes + 4 * B * G, 2 * B * E
     if kernel == "bwd_w_kernel":
-        # params + X once, dW/db read-modify-write, per-neuron {w, mask} record written
-        return 4 * E + 4 * E + 4 * N + B * D * x_bytes + 8 * E + 8 * N + 4 * E + N * B // 8, 4 * B * E
+        # idx + W + bias, X once, dW/db read-modify-write, mask bits written
+        return 4 * E + 4 * E + 4 * N + B * D * x_bytes + 8 * E + 8 * N + N * B // 8, 4 * B * E
     if kernel == "dx_kernel":
-        # edge records, each neuron's {w, mask} record once per edge, dX partials
-        return 4 * E + E * (4 + B // 8) + 4 * B * D, 2 * B * E
+        # per edge: record, weight and the neuron's B mask bits; dX written once
+        return E * (4 + 4 + B // 8) + 4 * B * D, 2 * B * E
     if kernel == "adam_kernel":
         return 32 * (E + N), 12 * (E + N)
     return None, None
+
+
+def read_traffic(path: str) -> dict:
+    """Calibrated HBM bytes per launch of each kernel from a committed rocprofv3 summary: lines
+    ``traffic <kernel> <bytes>`` (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the
+    counter reads for a device copy of known size)."""
+    out = {}
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic":
+                    out[parts[1]] = int(float(parts[2]))
+    except OSError:
+        pass
+    return out
 
 
 def cpu_baseline(groups: int, steps: int):
@@ -90,8 +109,10 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-groups", type=int, default=192, help="pools in the CPU baseline's sample")
+    ap.add_argument("--cpu-groups", type=int, default=768, help="pools in the CPU baseline's sample")
     ap.add_argument("--cpu-steps", type=int, default=5)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build measures one MI355X (--gpus {args.gpus} requested); "
@@ -103,6 +124,17 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
+    if args.copy_probe:
+        n = args.copy_probe * (1 << 20) // 4
+        a = torch.ones(n, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)  # runtime copy kernel
+        for _ in range(3):
+            torch.mul(a, 1.0, out=b)  # elementwise kernel reading and writing the same bytes
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": 4 * n, "copy_probe_bytes_written": 4 * n}), flush=True)
+        return
     from granulelayer_amd import FusedAdamW, SparsePoolingLayer
     from granulelayer_amd._native import KernelTrace
 
@@ -162,27 +194,34 @@ def main():
     E = N * K
     kernels = {}
     for name, ts in ktimes.items():
-        avg = sum(ts) / len(ts)
+        step_ms = sum(ts) / args.steps  # all launches of the kernel in one step
         by, fl = algorithmic(name, B, N, K, D, G)
-        rec = {"ms": round(avg, 4), "launches": len(ts)}
+        rec = {"ms": round(sum(ts) / len(ts), 4), "launches_per_step": len(ts) // args.steps,
+               "ms_per_step": round(step_ms, 4)}
         if by is not None:
-            rec["hbm_frac"] = round(by / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
-            rec["valu_frac"] = round(fl / (avg * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4)
+            rec["alg_GBps"] = round(by / (step_ms * 1e-3) / 1e9, 1)
+            rec["hbm_frac"] = round(by / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+            rec["fp32_frac"] = round(fl / (step_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4)
         kernels[name] = rec
-    dom = max(ktimes, key=lambda n: sum(ktimes[n]) / args.steps)
-    dom_ms = sum(ktimes[dom]) / len(ktimes[dom])
+    dom = max(ktimes, key=lambda n: sum(ktimes[n]))
+    dom_ms = sum(ktimes[dom]) / args.steps
     by, fl = algorithmic(dom, B, N, K, D, G)
+    traffic = read_traffic(os.path.join(ROOT, "profiles", "pmc_c2_train_step.txt")).get(dom)
     if dom == "adam_kernel":
         roof = {"bound": "hbm", "achieved": round(by / (dom_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s"}
     else:
-        roof = {"bound": "valu", "achieved": round(fl / (dom_ms * 1e-3) / 1e12, 2), "peak": FP32_PEAK_TFLOPS,
-                "unit": "TFLOP/s"}
+        # fp32 arithmetic on the vector ALUs (no MFMA on this gather path): the fp32 peak is the
+        # figure MI355X publishes for fp32 (157.3 TFLOP/s, packed issue); code built without
+        # packed-FP32 instructions can issue at most half of it
+        roof = {"bound": "mfma", "achieved": round(fl / (dom_ms * 1e-3) / 1e12, 2), "peak": FP32_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "compute": "fp32 VALU FMA (no MFMA; non-packed issue limit 78.65 TFLOP/s)"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["traffic"] = traffic
     roof["kernel"] = dom
     roof["ms"] = round(dom_ms, 4)
-    roof["traffic"] = None
-    roof["hbm_frac_algorithmic"] = round(by / (dom_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    roof["algorithmic_bytes"] = by
+    roof["algorithmic_flops"] = fl
 
     value = B * E / (ms_step * 1e-3) / 1e9
     out = {

@@ -260,3 +260,55 @@ def test_sampled_pools_at_scale():
     (mW, mb, _), (uW, ub, _) = bnd["mag"], bnd["unc"]
     assert_parity(dw.cpu().numpy().reshape(-1, K)[sl], wdW, mW, uW, what="dW (sampled pools)")
     assert_parity(db.cpu().numpy().reshape(-1)[sl], wdb, mb, ub, what="db (sampled pools)")
+
+
+# ---- stored known-answer vectors (tests/golden/make_golden.py) --------------------------------
+def _golden(name):
+    from pathlib import Path
+
+    with np.load(Path(__file__).resolve().parent / "golden" / "golden_small.npz") as d:
+        return {k.split("/", 1)[1]: d[k] for k in d.files if k.startswith(name + "/")}
+
+
+@pytest.mark.parametrize("name", ["mean_k8", "sum_k8", "sum_k16"])
+def test_hip_matches_golden_vectors(name):
+    """Forward and backward of the HIP library (arbitrary per-pool counts with padded slots) against
+    the stored torch float64 vectors; fp32 bar with the oracle's error scales."""
+    from types import SimpleNamespace
+
+    c = _golden(name)
+    B, D, G, S, K, pool = (int(v) for v in c["shape"])
+    pool = "mean" if pool == 0 else "sum"
+    L = SimpleNamespace(groups=G, slots_per_group=S, fan_in=K, input_dim=D, weight_shape=(G * S, K),
+                        bias_shape=(G * S,))
+    rt = SimpleNamespace(layout=L, level=LevelSpec(pool, activation="relu"), idx=torch.tensor(c["idx"]).to(DEV),
+                         counts_i32=torch.tensor(c["counts"]).to(DEV), last_info={})
+    hb = HipBackend.get()
+    x, w, b = (torch.tensor(c[k]).to(DEV) for k in ("x", "w", "b"))
+    pre = hb.forward(rt, x, w, b)["pre"].cpu().numpy()
+    _, mag = O.forward(c["x"], c["idx"], c["w"], c["b"], c["counts"], S, "relu", pool, with_mag=True)
+    assert_parity(pre, c["pre"], mag, what=f"{name} pre")
+    dW = torch.zeros(G * S, K, device=DEV)
+    db = torch.zeros(G * S, device=DEV)
+    dx = hb.backward(rt, x, w, b, torch.tensor(c["dy"]).to(DEV), {}, dW, db).cpu().numpy()
+    _, _, _, bnd = O.backward(c["x"], c["idx"], c["w"], c["b"], c["counts"], S, c["dy"], "relu", pool,
+                              with_bounds=True)
+    (mW, mb, mX), (uW, ub, uX) = bnd["mag"], bnd["unc"]
+    assert_parity(dx, c["dX"], mX, uX, what=f"{name} dX")
+    assert_parity(dW.cpu().numpy(), c["dW"], mW, uW, what=f"{name} dW")
+    assert_parity(db.cpu().numpy(), c["db"], mb, ub, what=f"{name} db")
+
+
+def test_hip_adam_matches_golden_adamw():
+    a = _golden("adam")
+    lr, b1, b2, eps, wd = (float(v) for v in a["hyper"])
+    p = torch.tensor(a["p0"]).to(DEV)
+    m = torch.zeros_like(p)
+    v = torch.zeros_like(p)
+    for t in range(1, 4):
+        g = torch.tensor(a["grads"][t - 1]).to(DEV)
+        HipBackend.get().adam(p, g, m, v, lr, b1, b2, eps, wd, 1 - b1 ** t, 1 - b2 ** t)
+    # torch.optim.AdamW forms 1 - beta in double, the reference in fp32 (see test_golden.py)
+    np.testing.assert_allclose(m.cpu().numpy(), a["m"], rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(v.cpu().numpy(), a["v"], rtol=2e-5, atol=1e-9)
+    np.testing.assert_allclose(p.cpu().numpy(), a["p"], rtol=0, atol=3 * lr * 1e-4)
