@@ -189,9 +189,9 @@ struct DxK {
 // lanes first gather, one edge each, the chunk's records, weights and mask words with vector
 // loads (64 independent requests per instruction: random scalar loads would be limited by the
 // scalar cache's miss rate); the gathers of the next chunk are issued before the current chunk is
-// computed.  The compute loop then broadcasts edge i's weight and 64-bit mask words to the token
-// lanes with v_readlane (SGPR operands: the weight feeds the FMA, each mask word is the lane mask
-// of a v_cndmask) and accumulates into acc[f] through a branch tree on the uniform feature f.
+// computed.  The chunk is staged in LDS; for edge i every token lane reads the weight (a
+// broadcast) and the mask word holding its own bit, turns the bit into an all-ones / zero mask
+// (v_bfe_i32) that selects c1, and accumulates c1 * w into the register of the edge's feature.
 template <int T>
 struct DxGather {
   unsigned rec;
@@ -253,16 +253,37 @@ __device__ __forceinline__ void dx_load_c1(const DxK& p, int u, int tok0, float 
 }
 
 // Edges i in [i0, i1) of the chunk, all of feature F0 of the range: acc[F0][j] += [m_j] c1[j] w.
+// LDS copy of one chunk: every edge's weight and its 2T mask words in [half][slot] order, so the
+// word holding token lane b's bit of slot j is m[i][b >> 5][j].
+template <int T>
+struct DxStage {
+  float w[64];
+  unsigned m[64][2][T];
+};
+
+template <int T>
+__device__ __forceinline__ void dx_stage(DxStage<T>& st, const DxGather<T>& g, int lane) {
+  st.w[lane] = g.w;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int j = 0; j < T; ++j) st.m[lane][h][j] = g.m[2 * j + h];
+}
+
+// Edges i in [i0, i1) of the chunk, all of feature F0 of the range: acc[F0][j] += [m_j] c1[j] w.
 template <int F0, int T>
-__device__ __forceinline__ void dx_run(const DxGather<T>& g, int i0, int i1, const float (&c1)[T],
+__device__ __forceinline__ void dx_run(const DxStage<T>& st, int i0, int i1, int lane, const float (&c1)[T],
                                        float (&acc)[FW][T]) {
+  // weight: an LDS broadcast; mask bit: the lane's own bit of the staged word, sign-extended to
+  // an all-ones / zero mask that selects c1
+  const int half = lane >> 5;
+  const unsigned bit = (unsigned)lane & 31u;
   for (int i = i0; i < i1; ++i) {
-    const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g.w), i));
+    const float w = st.w[i];
 #pragma unroll
     for (int j = 0; j < T; ++j) {
-      const uint64_t m = (uint64_t)(unsigned)__builtin_amdgcn_readlane((int)g.m[2 * j], i) |
-                         ((uint64_t)(unsigned)__builtin_amdgcn_readlane((int)g.m[2 * j + 1], i) << 32);
-      acc[F0][j] = __builtin_fmaf(__builtin_amdgcn_inverse_ballot_w64(m) ? c1[j] : 0.f, w, acc[F0][j]);
+      const int sel = __builtin_amdgcn_sbfe((int)st.m[i][half][j], bit, 1u);
+      acc[F0][j] = __builtin_fmaf(__builtin_bit_cast(float, sel & __builtin_bit_cast(int, c1[j])), w, acc[F0][j]);
     }
   }
 }
@@ -270,14 +291,16 @@ __device__ __forceinline__ void dx_run(const DxGather<T>& g, int i0, int i1, con
 // The chunk's edges are sorted by feature: ballots give every feature's edge range, and one loop
 // per feature (unrolled over the range) keeps every accumulator index a compile-time constant.
 template <int T>
-__device__ __forceinline__ void dx_compute(const DxGather<T>& g, int n, int lane, const float (&c1)[T],
-                                           float (&acc)[FW][T]) {
+__device__ __forceinline__ void dx_compute(const DxGather<T>& g, DxStage<T>& st, int n, int lane,
+                                           const float (&c1)[T], float (&acc)[FW][T]) {
+  dx_stage<T>(st, g, lane);
+  __syncthreads();  // one wave per workgroup: orders the staging before the broadcast reads
   const int f = lane < n ? (int)((g.rec >> REC_F_SHIFT) & REC_F_MASK) : FW;
   int b[FW + 1];
   b[0] = 0;
 #pragma unroll
   for (int x = 1; x <= FW; ++x) b[x] = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(f < x));
-#define GL_DX_RUN(X) dx_run<X, T>(g, b[X], b[X + 1], c1, acc)
+#define GL_DX_RUN(X) dx_run<X, T>(st, b[X], b[X + 1], lane, c1, acc)
   GL_DX_RUN(0);
   GL_DX_RUN(1);
   GL_DX_RUN(2);
@@ -288,6 +311,7 @@ __device__ __forceinline__ void dx_compute(const DxGather<T>& g, int n, int lane
   GL_DX_RUN(7);
 #undef GL_DX_RUN
   static_assert(FW == 8, "dx_compute unrolls eight features");
+  __syncthreads();  // the next chunk's staging overwrites st
 }
 
 template <int K, int T>
@@ -329,6 +353,7 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
 
   const int tok0 = tc * 64 * T + lane;
   const uint32_t* mask_tc = p.mask + (long long)tc * p.NS * (2 * T);
+  __shared__ DxStage<T> st;
   if (lo < hi) {
     DxChunk cc{lo, p.seg_begin[lo], p.seg_begin[lo + 1], p.seg_unit[lo]};
     DxGather<T> gc;
@@ -354,7 +379,7 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
         dx_next(p, cnn, hi);
         if (cnn.si < hi) rnn = dx_load_rec(p, cnn, lane);
       }
-      dx_compute<T>(gc, (int)min(cc.end - cc.e, 64u), lane, c1, acc);
+      dx_compute<T>(gc, st, (int)min(cc.end - cc.e, 64u), lane, c1, acc);
       if (!more) break;
       cc = cn;
       gc = gn;
