@@ -20,6 +20,7 @@ import ctypes
 import threading
 from typing import Dict, Optional
 
+import numpy as np
 import torch
 
 from . import _native as N
@@ -114,7 +115,8 @@ class HipBackend:
         if B == 0:
             return {"pre": pre}
         a = N.GlFwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=L.input_dim, G=G, S=S, K=K, act=act, pool=pool,
-                        idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32), pre=_ptr(pre))
+                        idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
+                        sched=_ptr(self.schedule(rt)), pre=_ptr(pre))
         with torch.cuda.device(x.device):
             need = self.lib.size_query("gl_fwd_workspace", a)
             ws = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)
@@ -122,6 +124,23 @@ class HipBackend:
             self.lib.call("gl_fwd", ctypes.byref(a), ctypes.c_void_p(_stream(x.device)))
         rt.last_info["workspace_bytes"] = need
         return {"pre": pre}
+
+    # ------------------------------------------------------------------ gather schedule
+    def schedule(self, rt) -> Optional[torch.Tensor]:
+        """Gather schedule of rt's index tensor for the forward / dW kernels (fan-in 8; built on the
+        host once per index tensor and cached on rt), or None for fan-in 16."""
+        L, G, S, K = self._layer(rt)
+        if K != 8:
+            return None
+        key = (rt.idx.data_ptr(), rt.idx._version)
+        cached = getattr(rt, "_hip_sched", None)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        host = self.lib.sched_build(rt.idx.reshape(-1, K).cpu().numpy(), rt.counts_i32.cpu().numpy(), L.input_dim,
+                                    G, S, K)
+        sched = torch.from_numpy(host.view(np.int32)).to(rt.idx.device)
+        rt._hip_sched = (key, sched)
+        return sched
 
     # ------------------------------------------------------------------ edges
     def edges(self, rt) -> torch.Tensor:
@@ -163,7 +182,8 @@ class HipBackend:
             return dx
         edges = self.edges(rt)
         a = N.GlBwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=D, G=G, S=S, K=K, act=act, pool=pool,
-                        idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32), g_pre=_ptr(g_pre),
+                        idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
+                        sched=_ptr(self.schedule(rt)), g_pre=_ptr(g_pre),
                         dW=_ptr(dw_buf), db=_ptr(db_buf), dX=_ptr(dx), edges=_ptr(edges),
                         edges_bytes=edges.numel())
         with torch.cuda.device(x.device):

@@ -50,8 +50,9 @@ struct BwK {
   float* dW;
   float* db;
   uint32_t* mask;  // [n_tc][G*S][mw2] activation-mask words (one slab per dX token slice)
+  const uint32_t* sched;  // gather schedule or null
   long long n_chunks, NS;
-  int D, S, cpg, n_tiles, cap, mw2;
+  int D, S, cpg, n_tiles, cap, mw2, nwin;
 };
 
 template <int K, int NPL, int WAVES, int ACT, int PF>
@@ -70,19 +71,24 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   float w[NPL][K], dw[NPL][K];
   float bias[NPL], dbv[NPL];
   unsigned mw[NPL];
+  unsigned slot2[(NPL + 1) / 2];  // slots of neurons 2i, 2i+1 within the pool (16 bits each; >= n_g: padding)
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    const int s = s_lo + j * 64 + lane;
+    uint32_t order;
+    const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, lane, order);
+    const unsigned s16 = (unsigned)(s < 0xffff ? s : 0xffff);
+    if (j % 2 == 0) slot2[j / 2] = s16; else slot2[j / 2] |= s16 << 16;
     const bool valid = s < n_g;
     const long long n = g * p.S + (s < p.S ? s : p.S - 1);  // in-bounds address; invalid slots masked
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
+    for (int ks = 0; ks < K; ++ks) {
+      const int k = sched_k<K>(order, ks);
       int d = p.idx[n * K + k];
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-      addr[j][k] = (unsigned)d * 16u;
+      addr[j][ks] = (unsigned)d * 16u;
       const float wl = p.W[n * K + k];
-      w[j][k] = valid ? wl : 0.f;
-      dw[j][k] = 0.f;
+      w[j][ks] = valid ? wl : 0.f;
+      dw[j][ks] = 0.f;
     }
     const float bl = p.bias[n];
     bias[j] = valid ? bl : 0.f;
@@ -145,23 +151,24 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    const int ln = opaque(lane);  // address math kept local (see opaque())
     const int word = t0 >> 3;
-    uint32_t* mrow = p.mask + ((long long)(word / p.mw2) * p.NS + g * p.S + s_lo + ln) * p.mw2 + word % p.mw2;
+    uint32_t* mslab = p.mask + ((long long)(word / p.mw2) * p.NS + g * p.S) * p.mw2 + word % p.mw2;
 #pragma unroll
-    for (int j = 0; j < NPL; ++j)
-      if (active && s_lo + j * 64 + ln < n_g) mrow[(long long)j * 64 * p.mw2] = mw[j];
+    for (int j = 0; j < NPL; ++j) {
+      const int s = (int)((opaque((int)slot2[j / 2]) >> (16 * (j % 2))) & 0xffff);  // address math kept local
+      if (active && s < n_g) mslab[(long long)s * p.mw2] = mw[j];
+    }
   }
   // mask words of tokens past the chunk are never written: their c1 is zero, so dX ignores them
   if (!active) return;
-  const int ln = opaque(lane);
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    const int s = s_lo + j * 64 + ln;
+    uint32_t order;
+    const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, opaque(lane), order);
     if (s >= n_g) continue;
     const long long n = g * p.S + s;
 #pragma unroll
-    for (int k = 0; k < K; ++k) p.dW[n * K + k] += dw[j][k];
+    for (int ks = 0; ks < K; ++ks) p.dW[n * K + sched_k<K>(order, ks)] += dw[j][ks];
     p.db[n] += dbv[j];
   }
 }
@@ -508,7 +515,7 @@ static int launch_bwd_w_pf(int D, const BwK& k, hipStream_t s, size_t lds) {
 template <int ACT>
 static int launch_bwd_w_act(int K, int D, const BwK& k, hipStream_t s, size_t lds) {
   if (K == 8) return launch_bwd_w_pf<ACT, 8, 6, 8>(D, k, s, lds);
-  return launch_bwd_w_pf<ACT, 16, 3, 4>(D, k, s, lds);
+  return launch_bwd_w_pf<ACT, 16, 3, 2>(D, k, s, lds);
 }
 
 static int launch_bwd_w_any(int K, int D, int act, const BwK& k, hipStream_t s, size_t lds) {
@@ -548,6 +555,7 @@ extern "C" int gl_bwd_workspace(const GlBwdArgs* a, size_t* bytes) {
 
 extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
   if (!a || !a->g_pre || !a->dW || !a->db || !a->dX || !a->edges) return GL_ERR_ARG;
+  if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;
   size_t need = 0;
   GL_TRY(gl_bwd_workspace(a, &need));
   if (!a->ws || a->ws_bytes < need) return GL_ERR_WORKSPACE;
@@ -574,8 +582,8 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
                        a->g_pre, a->counts, c1t, a->G, b0, Bc, cap, a->pool);
     GL_CHECK_LAUNCH();
     const long long NS = (long long)a->G * a->S;
-    BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, q.n_chunks, NS,
-           a->D, a->S, q.cpg, n_tiles, cap, 2 * T};
+    BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, a->sched, q.n_chunks, NS,
+           a->D, a->S, q.cpg, n_tiles, cap, 2 * T, ceil_div(a->S, SCHED_WIN)};
     GL_TRY(launch_bwd_w_any(a->K, a->D, a->act, bk, s, q.lds));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
            (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, a->W, part,

@@ -16,7 +16,6 @@ constexpr int BT = 4;
 // dX: features per range (one accumulator row each) and slots per edge-list unit.
 constexpr int FW = 8;
 constexpr int US = 1024;
-// input-major edge record: n_local (12 bits) | k << 12 (5 bits) | f_local << 17 (5 bits)
 // dX edge record (32 bit): bits [0, 16) byte offset of W[n, k] inside its unit,
 // (s_local * K + k) * 4; bits [16, 24) feature inside the range; bit 31 set when the feature
 // differs from the one of the previous edge of the same segment (a new accumulation run).
@@ -28,6 +27,45 @@ constexpr unsigned REC_NEWF = 1u << 31;
 constexpr int BWD_TOKEN_CHUNK = 1024;
 
 constexpr int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
+
+// ---- gather schedule of the neuron-stationary kernels (gl_sched.hip) --------------------------
+// Slots are scheduled in windows of 128: neuron slot j of lane `lane` in a chunk starting at slot
+// s_lo (a multiple of 128) reads record ((g * nwin + s_lo / 128 + j / 2) * 128 + ((j % 2) * 4 +
+// lane / 16) * 16 + lane % 16) = s_local | k_0 << 7 | ... | k_6 << 25 (k_7 = 28 - sum).  Without a
+// schedule the slot is s_lo + 64 j + lane and edges are visited in k order.
+constexpr int SCHED_WIN = 128;
+constexpr uint32_t SCHED_IDENTITY = 0u | 1u << 3 | 2u << 6 | 3u << 9 | 4u << 12 | 5u << 15 | 6u << 18;
+
+// slot (within the pool; >= S when the window lies past the pool) and packed visiting order
+__device__ __forceinline__ int sched_slot(const uint32_t* __restrict__ sched, int nwin, int S, long long g, int s_lo,
+                                          int j, int lane, uint32_t& order) {
+  if (sched == nullptr) {
+    order = SCHED_IDENTITY;
+    return s_lo + j * 64 + lane;
+  }
+  const int w = s_lo / SCHED_WIN + (j >> 1);
+  if (w >= nwin) {
+    order = SCHED_IDENTITY;
+    return S;
+  }
+  const uint32_t rec = sched[((long long)g * nwin + w) * SCHED_WIN + ((j & 1) * 4 + (lane >> 4)) * 16 + (lane & 15)];
+  order = rec >> 7;
+  return w * SCHED_WIN + (int)(rec & 127u);
+}
+
+// edge visited at position ks (K = 8 orders; K = 16 is never scheduled)
+template <int K>
+__device__ __forceinline__ int sched_k(uint32_t order, int ks) {
+  if constexpr (K != 8) {
+    return ks;
+  } else {
+    if (ks < 7) return (int)((order >> (3 * ks)) & 7u);
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 7; ++i) sum += (int)((order >> (3 * i)) & 7u);
+    return 28 - sum;
+  }
+}
 constexpr long long round_up(long long a, long long b) { return (a + b - 1) / b * b; }
 
 // Tokens of one dX wave: 64 lanes x T slots, T in {1, 2, 4}, for a chunk of B tokens.

@@ -50,8 +50,9 @@ struct FwdK {
   const float* bias;
   const int32_t* counts;
   float* part;            // [n_chunks][b_pad]
+  const uint32_t* sched;  // gather schedule or null
   long long n_chunks;
-  int D, S, cpg, n_tiles, b_pad;
+  int D, S, cpg, n_tiles, b_pad, nwin;
 };
 
 template <int K, int NPL, int WAVES, int ACT, int PF>
@@ -71,16 +72,18 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   float bias[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    const int s = s_lo + j * 64 + lane;
+    uint32_t order;
+    const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, lane, order);
     const bool valid = s < n_g;
     const long long n = g * p.S + (s < p.S ? s : p.S - 1);  // in-bounds address; invalid slots masked
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
+    for (int ks = 0; ks < K; ++ks) {
+      const int k = sched_k<K>(order, ks);  // the pooled sum does not depend on the visiting order
       int d = p.idx[n * K + k];
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-      addr[j][k] = (unsigned)d * 16u;
+      addr[j][ks] = (unsigned)d * 16u;
       const float wl = p.W[n * K + k];
-      w[j][k] = valid ? wl : 0.f;
+      w[j][ks] = valid ? wl : 0.f;
     }
     const float bl = p.bias[n];
     bias[j] = valid ? bl : 0.f;
@@ -252,7 +255,9 @@ extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
   float4* xt = (float4*)a->ws;
   float* part = (float*)((char*)a->ws + q.xt_bytes);
   GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, 0, q.n_tiles, xt, s));
-  FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles, q.b_pad};
+  if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;
+  FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, a->sched, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles, q.b_pad,
+         ceil_div(a->S, SCHED_WIN)};
   GL_TRY(a->act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU>(a->K, a->D, k, s, q.lds)
                                 : launch_fwd_act<GL_ACT_IDENTITY>(a->K, a->D, k, s, q.lds));
   dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(q.b_pad, 32));

@@ -1,0 +1,224 @@
+// Gather schedule of the neuron-stationary kernels (forward and dW), built on the host once per
+// index tensor.
+//
+// Those kernels read, per (neuron slot j, k), one 16-byte LDS entry X[d] (4 tokens) per lane with
+// ds_read_b128.  The LDS serves a b128 read in passes of 16 lanes; a pass is conflict-free when
+// its 16 lanes read 16 distinct 16-byte slots mod 16, i.e. distinct residues d mod 16.  With
+// random indices a 16-lane group averages ~3 passes.  The schedule lowers that by choosing
+//   * which 16 neurons of a window of 128 slots share a 16-lane group ("set"), so each set's
+//     residue histogram is flat (greedy: neurons with the most repeated residue first, each to
+//     the set whose sum of squared excess over 8 per residue grows least), and
+//   * the order in which every neuron visits its K = 8 edges: round by round, a maximum matching
+//     of the set's 16 lanes to distinct residues among their unused edges (augmenting paths,
+//     residues with more remaining edges tried first); unmatched lanes take the edge whose
+//     residue the round uses least.
+// Both only reorder a pool's neurons and each neuron's terms, so the pooled sum and every
+// gradient keep their value (fp32 rounding order aside).
+//
+// Record of lane l, neuron slot j of a chunk that starts at window w0 (chunk slots are multiples
+// of 128): window w = w0 + j / 2, set = (j % 2) * 4 + l / 16, position = set * 16 + l % 16;
+// sched[(g * nwin + w) * 128 + position] = s_local | k_0 << 7 | k_1 << 10 | ... | k_6 << 25, where
+// s_local (0..127) is the slot within the window and k_0..k_6 the first seven edges in visiting
+// order (k_7 = 28 - their sum).
+#include <algorithm>
+#include <thread>
+#include <vector>
+
+#include "gl_common.h"
+#include "gl_internal.h"
+
+namespace gl {
+namespace {
+
+constexpr int WIN = 128;
+constexpr int SETS = WIN / 16;
+constexpr int KS = 8;
+
+struct Window {
+  int res[WIN][KS];  // residue of edge k of slot p (-1: invalid slot)
+  int hist[WIN][16];
+  bool valid[WIN];
+};
+
+// greedy balance: slots with the most repeated residue first; each goes to the set (with room)
+// whose sum over residues of (count - 8)^2 for counts above 8 grows least (ties: lower set)
+void balance(const Window& W, int members[SETS][16]) {
+  int order[WIN], mx[WIN];
+  for (int p = 0; p < WIN; ++p) {
+    order[p] = p;
+    mx[p] = 0;
+    for (int r = 0; r < 16; ++r) mx[p] = std::max(mx[p], W.hist[p][r]);
+  }
+  std::stable_sort(order, order + WIN, [&](int a, int b) { return mx[a] > mx[b]; });
+  int H[SETS][16] = {};
+  int cnt[SETS] = {};
+  for (int oi = 0; oi < WIN; ++oi) {
+    const int p = order[oi];
+    int rs[KS], hs[KS], nr = 0;  // distinct residues of slot p and their multiplicities
+    for (int r = 0; r < 16; ++r)
+      if (W.hist[p][r]) rs[nr] = r, hs[nr++] = W.hist[p][r];
+    int best = -1, best_cost = 0;
+    for (int set = 0; set < SETS; ++set) {
+      if (cnt[set] == 16) continue;
+      int c = 0;
+      for (int i = 0; i < nr; ++i) {
+        const int before = H[set][rs[i]] - 8, after = before + hs[i];
+        c += (after > 0 ? after * after : 0) - (before > 0 ? before * before : 0);
+      }
+      if (best < 0 || c < best_cost) best = set, best_cost = c;
+    }
+    for (int i = 0; i < nr; ++i) H[best][rs[i]] += hs[i];
+    members[best][cnt[best]++] = p;
+  }
+}
+
+// Kuhn's augmenting paths over 16 lanes and 16 residues; cand[l] = residues of lane l's unused
+// edges, tried in the round's residue order (most remaining edges first)
+struct Matcher {
+  uint32_t cand[16];
+  int ord[16];
+  int owner[16];
+  uint32_t seen;
+
+  bool try_lane(int l) {
+    for (int i = 0; i < 16; ++i) {
+      const int r = ord[i];
+      if (!((cand[l] >> r) & 1u) || ((seen >> r) & 1u)) continue;
+      seen |= 1u << r;
+      if (owner[r] < 0 || try_lane(owner[r])) {
+        owner[r] = l;
+        return true;
+      }
+    }
+    return false;
+  }
+};
+
+// visiting order kperm[lane][round] of the set's lanes; invalid lanes keep the identity
+void match_set(const Window& W, const int mem[16], int kperm[16][KS]) {
+  int rem[16][KS];  // residue of each lane's unused edge k (-1 = used)
+  bool live[16];
+  for (int l = 0; l < 16; ++l) {
+    live[l] = W.valid[mem[l]];
+    for (int k = 0; k < KS; ++k) {
+      rem[l][k] = live[l] ? W.res[mem[l]][k] : -1;
+      kperm[l][k] = k;
+    }
+  }
+  Matcher M;
+  for (int round = 0; round < KS; ++round) {
+    int deg[16] = {};
+    int ndist[16];
+    for (int l = 0; l < 16; ++l) {
+      M.cand[l] = 0;
+      for (int k = 0; k < KS; ++k)
+        if (rem[l][k] >= 0) deg[rem[l][k]]++, M.cand[l] |= 1u << rem[l][k];
+      ndist[l] = __builtin_popcount(M.cand[l]);
+    }
+    for (int r = 0; r < 16; ++r) M.ord[r] = r, M.owner[r] = -1;
+    std::stable_sort(M.ord, M.ord + 16, [&](int a, int b) { return deg[a] > deg[b]; });
+    int order[16];
+    for (int l = 0; l < 16; ++l) order[l] = l;
+    std::stable_sort(order, order + 16, [&](int a, int b) { return ndist[a] < ndist[b]; });
+    for (int i = 0; i < 16; ++i) {
+      const int l = order[i];
+      if (!live[l]) continue;
+      M.seen = 0;
+      M.try_lane(l);
+    }
+    int lane_res[16], used[16] = {};
+    for (int l = 0; l < 16; ++l) lane_res[l] = -1;
+    for (int r = 0; r < 16; ++r)
+      if (M.owner[r] >= 0) lane_res[M.owner[r]] = r, used[r]++;
+    for (int l = 0; l < 16; ++l) {  // unmatched lanes: the residue this round uses least
+      if (!live[l] || lane_res[l] >= 0) continue;
+      int best = -1;
+      for (int k = 0; k < KS; ++k) {
+        const int r = rem[l][k];
+        if (r < 0) continue;
+        if (best < 0 || used[r] < used[best] ||
+            (used[r] == used[best] && (deg[r] > deg[best] || (deg[r] == deg[best] && r < best))))
+          best = r;
+      }
+      lane_res[l] = best;
+      used[best]++;
+    }
+    for (int l = 0; l < 16; ++l) {
+      if (!live[l]) continue;
+      for (int k = 0; k < KS; ++k)  // the lowest unused edge with that residue
+        if (rem[l][k] == lane_res[l]) {
+          kperm[l][round] = k;
+          rem[l][k] = -1;
+          break;
+        }
+    }
+  }
+}
+
+void build_range(const int32_t* idx, const int32_t* counts, int D, int G, int S, long long w_begin,
+                 long long w_end, uint32_t* sched) {
+  const int nwin = ceil_div(S, WIN);
+  Window W;
+  for (long long gw = w_begin; gw < w_end; ++gw) {
+    const long long g = gw / nwin;
+    const int w = (int)(gw % nwin);
+    const int n_g = std::min(counts[g], S);
+    for (int p = 0; p < WIN; ++p) {
+      const int s = w * WIN + p;
+      W.valid[p] = s < n_g;
+      for (int r = 0; r < 16; ++r) W.hist[p][r] = 0;
+      for (int k = 0; k < KS; ++k) {
+        int r = -1;
+        if (W.valid[p]) {
+          int d = idx[((long long)g * S + s) * KS + k];
+          d = d < 0 ? 0 : (d >= D ? D - 1 : d);
+          r = d & 15;
+          W.hist[p][r]++;
+        }
+        W.res[p][k] = r;
+      }
+    }
+    int members[SETS][16];
+    balance(W, members);
+    uint32_t* out = sched + gw * WIN;
+    for (int set = 0; set < SETS; ++set) {
+      int kperm[16][KS];
+      match_set(W, members[set], kperm);
+      for (int l = 0; l < 16; ++l) {
+        uint32_t rec = (uint32_t)members[set][l];
+        for (int ks = 0; ks < KS - 1; ++ks) rec |= (uint32_t)kperm[l][ks] << (7 + 3 * ks);
+        out[set * 16 + l] = rec;
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace gl
+
+using namespace gl;
+
+extern "C" int gl_sched_size(int32_t G, int32_t S, int32_t K, size_t* bytes) {
+  if (!bytes || G < 1 || S < 1) return GL_ERR_ARG;
+  if (K != 8) return GL_ERR_UNSUPPORTED;
+  *bytes = (size_t)G * ceil_div(S, WIN) * WIN * sizeof(uint32_t);
+  return 0;
+}
+
+extern "C" int gl_sched_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S,
+                                   int32_t K, uint32_t* sched, int32_t threads) {
+  if (!idx || !counts || !sched || D < 1 || G < 1 || S < 1) return GL_ERR_ARG;
+  if (K != 8) return GL_ERR_UNSUPPORTED;
+  const long long nw = (long long)G * ceil_div(S, WIN);
+  int nt = threads > 0 ? threads : (int)std::thread::hardware_concurrency();
+  if (nt < 1) nt = 1;
+  if (nt > 256) nt = 256;
+  if ((long long)nt > nw) nt = (int)nw;
+  std::vector<std::thread> pool;
+  for (int t = 0; t < nt; ++t) {
+    const long long b = nw * t / nt, e = nw * (t + 1) / nt;
+    pool.emplace_back(build_range, idx, counts, D, G, S, b, e, sched);
+  }
+  for (auto& th : pool) th.join();
+  return 0;
+}

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 1
+#define GL_ABI_VERSION 2
 
 enum {
   GL_OK = 0,
@@ -57,6 +57,7 @@ typedef struct GlFwdArgs {
   const float* W;         /* [G*S, K] */
   const float* bias;      /* [G*S] */
   const int32_t* counts;  /* [G] valid neurons per group, 1 <= counts[g] <= S */
+  const uint32_t* sched;  /* gather schedule from gl_sched_build_host (K = 8), or NULL */
   float* pre;             /* out [B, G]: pooled value before the (identity) out-activation */
   void* ws;               /* workspace of gl_fwd_workspace() bytes */
   size_t ws_bytes;
@@ -75,6 +76,7 @@ typedef struct GlBwdArgs {
   const float* W;
   const float* bias;
   const int32_t* counts;
+  const uint32_t* sched;  /* gather schedule from gl_sched_build_host (K = 8), or NULL */
   const float* g_pre;     /* [B, G] dL/dpre (fp32) */
   float* dW;              /* [G*S, K] ACCUMULATED (+=), e.g. W.main_grad; padded slots untouched */
   float* db;              /* [G*S] ACCUMULATED (+=) */
@@ -137,6 +139,17 @@ int gl_bwd(const GlBwdArgs* a, void* stream);
 
 /* Fused AdamW (in place). */
 int gl_adam(const GlAdamArgs* a, void* stream);
+
+/* Gather schedule of the forward and dW kernels (K = 8 only), built on the HOST once per index
+ * tensor from host copies of idx [G*S, 8] and counts [G]; upload the result and pass it as
+ * GlFwdArgs.sched / GlBwdArgs.sched.  It reorders, within windows of 128 slots, which neurons
+ * share a 16-lane LDS gather and the order of each neuron's 8 edges, so the kernels' 16-byte LDS
+ * reads hit distinct banks more often; results are unchanged up to fp32 summation order.  No
+ * reference counterpart (the reference's Triton Mode-A kernels gather from global memory,
+ * sparse_pooling/kernels/triton_fused.py:253-264).  threads <= 0: one per hardware thread. */
+int gl_sched_size(int32_t G, int32_t S, int32_t K, size_t* bytes);
+int gl_sched_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
+                        uint32_t* sched, int32_t threads);
 
 /* Kernel ids reported by the trace below. */
 enum {
