@@ -82,6 +82,72 @@ def read_traffic(path: str) -> dict:
     return out
 
 
+CONFIG_WORK = {"C1": "fwd+bwd+adam", "C2": "fwd", "C3": "fwd+bwd", "C4": "fwd+bwd+adam", "C5": "fwd+bwd"}
+
+
+def run_config(name: str, steps: int, warmup: int):
+    """One JSON line for a BASELINE config at its full size: the config's own work (forward,
+    forward + backward, or the training step) timed over ``steps`` calls after ``warmup``."""
+    import torch
+
+    from granulelayer_amd import FusedAdamW, SparsePoolingLayer
+    from granulelayer_amd._native import KernelTrace
+    from granulelayer_amd.synthetic import CONFIGS, make_problem
+
+    c = CONFIGS[name]
+    work = CONFIG_WORK[name]
+    dev = torch.device("cuda", 0)
+    N, K, D, B, pool = c["N"], c["K"], c["D"], c["B"], c["pool"]
+    G = N // pool
+    t0 = time.time()
+    lay = SparsePoolingLayer(D, N, G, fan_in=K, shared_neurons=None, pooling="sum", dtype=torch.float32, device=dev,
+                             seed=0)
+    if c["indices"] != "uniform":  # locality windows (C3) or top-16 of 64 candidates (C5)
+        pr = make_problem(name, device=dev, seed=0)
+        with torch.no_grad():
+            lay.indices.copy_(pr.idx)
+            lay.weight.copy_(pr.w)
+        del pr
+    lay.enable_main_grad()
+    opt = FusedAdamW(lay.parameters(), lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, moments="fp32")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    x = torch.randn(B, D, generator=gen, device=dev).to(c["x_dtype"])
+    dy = torch.randn(B, G, generator=gen, device=dev).to(c["x_dtype"]).float()
+    torch.cuda.synchronize()
+    log(f"{name}: layer N={N:,} K={K} D={D} B={B} pool={pool} ready in {time.time() - t0:.1f} s")
+
+    def one():
+        if work == "fwd":
+            with torch.no_grad():
+                lay(x)
+            return
+        y = lay(x)
+        y.backward(dy)
+        if work.endswith("adam"):
+            opt.step()
+        else:
+            lay.zero_main_grad()
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with KernelTrace(max_launches=32 * steps) as tr:
+        e0.record()
+        for _ in range(steps):
+            one()
+        e1.record()
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    kt = {k: round(sum(v) / len(v), 4) for k, v in tr.times_ms().items()}
+    out = {"metric": f"BASELINE config {name} ({work}) ms and G edge-MAC/s", "config": name, "work": work,
+           "value": round(B * N * K / (ms * 1e-3) / 1e9, 2), "unit": "G edge-MAC/s", "ms": round(ms, 3),
+           "steps": steps, "warmup": warmup, "neurons": N, "fan_in": K, "d_in": D, "batch": B, "pool": pool,
+           "x_dtype": str(c["x_dtype"]).replace("torch.", ""), "indices": c["indices"], "kernels_ms": kt}
+    print(json.dumps(out), flush=True)
+
+
 def cpu_baseline(groups: int, steps: int):
     import torch
 
@@ -111,6 +177,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-groups", type=int, default=768, help="pools in the CPU baseline's sample")
     ap.add_argument("--cpu-steps", type=int, default=5)
+    ap.add_argument("--config", choices=sorted(CONFIG_WORK), default=None,
+                    help="time one BASELINE config's own work at full size instead of the headline step")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -124,6 +192,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
+    if args.config:
+        run_config(args.config, args.steps, args.warmup)
+        return
     if args.copy_probe:
         n = args.copy_probe * (1 << 20) // 4
         a = torch.ones(n, device="cuda")

@@ -236,30 +236,41 @@ def test_no_hidden_activation_is_materialized():
     assert e2 < B * 4_194_304 * 4 / 10, f"peak extra {e2 / 2**20:.0f} MiB"
 
 
-def test_sampled_pools_at_scale():
-    """4M neurons (4096 pools of 1024, D=4096, B=256): the HIP result of 24 randomly chosen pools
-    against the oracle run on just those pools."""
+@pytest.mark.parametrize("cfg,groups", [("C2", 4096), ("C3", 2048), ("C4", 512), ("C5", 2048)])
+def test_configs_at_scale_on_sampled_pools(cfg, groups):
+    """BASELINE config shapes (B, D, fan-in, pool size, index structure, X dtype) with a few
+    thousand pools: the HIP forward, dW and db of 24 random pools against the oracle run on just
+    those pools, and the full-layer dX against the oracle's dX of those pools with dY zero on every
+    other pool (dX only sums pools whose dY is non-zero)."""
     from granulelayer_amd.synthetic import make_problem
 
-    pr = make_problem("C2", device="cpu", seed=0, groups=4096)
+    pr = make_problem(cfg, device="cpu", seed=0, groups=groups)
     L = pr.layout
+    S, K = L.slots_per_group, L.fan_in
     rt = Level1Runtime(L, pr.idx.to(DEV), LevelSpec("sum"), PhysicalPlan())
-    pre = rt.forward(pr.x.to(DEV), pr.w.to(DEV), pr.b.to(DEV))["pre"].cpu().numpy()
+    xd = pr.x.to(DEV)
+    pre = rt.forward(xd, pr.w.to(DEV), pr.b.to(DEV))["pre"].cpu().numpy()
+    pools = np.sort(np.random.default_rng(0).choice(L.groups, 24, replace=False))
+    dy = torch.zeros_like(pr.dy)
+    dy[:, pools] = pr.dy[:, pools]
     dw = torch.zeros(L.weight_shape, device=DEV)
     db = torch.zeros(L.bias_shape, device=DEV)
-    rt.backward(pr.x.to(DEV), pr.w.to(DEV), pr.b.to(DEV), pr.dy.to(DEV), {}, "minimal_stats", dw, db)
-    pools = np.sort(np.random.default_rng(0).choice(L.groups, 24, replace=False))
-    S, K = L.slots_per_group, L.fan_in
+    dx = rt.backward(xd, pr.w.to(DEV), pr.b.to(DEV), dy.to(DEV), {}, "minimal_stats", dw, db).cpu().numpy()
     sl = np.concatenate([np.arange(g * S, (g + 1) * S) for g in pools])
     fi, fw, fb = flat(L, pr.idx, pr.w, pr.b)
     counts = np.full(len(pools), S, np.int32)
-    want, mag = O.forward(pr.x.numpy(), fi[sl], fw[sl], fb[sl], counts, S, "relu", "sum", with_mag=True)
-    assert_parity(pre[:, pools], want, mag, what="pre (sampled pools)")
-    wdW, wdb, _, bnd = O.backward(pr.x.numpy(), fi[sl], fw[sl], fb[sl], counts, S, pr.dy.numpy()[:, pools], "relu",
-                                  "sum", with_bounds=True)
-    (mW, mb, _), (uW, ub, _) = bnd["mag"], bnd["unc"]
-    assert_parity(dw.cpu().numpy().reshape(-1, K)[sl], wdW, mW, uW, what="dW (sampled pools)")
-    assert_parity(db.cpu().numpy().reshape(-1)[sl], wdb, mb, ub, what="db (sampled pools)")
+    xn = pr.x.float().numpy()  # bf16 inputs widened exactly, as the kernels do
+    want, mag = O.forward(xn, fi[sl], fw[sl], fb[sl], counts, S, "relu", "sum", with_mag=True)
+    assert_parity(pre[:, pools], want, mag, what=f"{cfg} pre (sampled pools)")
+    wdW, wdb, wdX, bnd = O.backward(xn, fi[sl], fw[sl], fb[sl], counts, S, pr.dy.numpy()[:, pools], "relu", "sum",
+                                    with_bounds=True)
+    (mW, mb, mX), (uW, ub, uX) = bnd["mag"], bnd["unc"]
+    assert_parity(dw.cpu().numpy().reshape(-1, K)[sl], wdW, mW, uW, what=f"{cfg} dW (sampled pools)")
+    assert_parity(db.cpu().numpy().reshape(-1)[sl], wdb, mb, ub, what=f"{cfg} db (sampled pools)")
+    assert_parity(dx, wdX, mX, uX, what=f"{cfg} dX (dY on sampled pools)")
+    other = np.setdiff1d(np.arange(L.groups), pools)[:64]
+    osl = np.concatenate([np.arange(g * S, (g + 1) * S) for g in other])
+    assert float(np.abs(dw.cpu().numpy().reshape(-1, K)[osl]).max()) == 0.0, "pools with zero dY get zero dW"
 
 
 # ---- stored known-answer vectors (tests/golden/make_golden.py) --------------------------------
