@@ -55,9 +55,62 @@ struct BwK {
   int D, S, cpg, n_tiles, cap, mw2, nwin;
 };
 
-template <int K, int NPL, int WAVES, int ACT, int PF>
+// One token tile of the dW pass (LDS at xsb): recompute z, form dz = c1 * act'(z), accumulate
+// db, dW and the tile's 4 mask bits (bit 4 (t % 8) + i of word mw for token i of tile t).  The
+// first RA LDS reads of neuron j + 1 are issued before the arithmetic of neuron j.
+template <int K, int NPL, int ACT, int RA>
+__device__ __forceinline__ void bwd_w_tile(const char* xsb, int t, const float4 c1, const unsigned (&addr)[NPL][K],
+                                           const float (&w)[NPL][K], const float (&bias)[NPL], float (&dw)[NPL][K],
+                                           float (&dbv)[NPL], unsigned (&mw)[NPL]) {
+  float4 xc[K];
+#pragma unroll
+  for (int k = 0; k < RA; ++k) xc[k] = lds_x<false>(xsb, addr[0][k]);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+#pragma unroll
+    for (int k = RA; k < K; ++k) xc[k] = lds_x<false>(xsb, addr[j][k]);
+    float4 xn[RA];
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xn[k] = lds_x<false>(xsb, addr[j + 1][k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
+      z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
+      z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
+      z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
+    }
+    const bool m0 = ACT != GL_ACT_RELU || z0 > 0.f, m1 = ACT != GL_ACT_RELU || z1 > 0.f;
+    const bool m2 = ACT != GL_ACT_RELU || z2 > 0.f, m3 = ACT != GL_ACT_RELU || z3 > 0.f;
+    const float d0 = m0 ? c1.x : 0.f, d1 = m1 ? c1.y : 0.f, d2 = m2 ? c1.z : 0.f, d3 = m3 ? c1.w : 0.f;
+    dbv[j] = dbv[j] + d0 + d1 + d2 + d3;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      float a = dw[j][k];
+      a = __builtin_fmaf(d0, xc[k].x, a);
+      a = __builtin_fmaf(d1, xc[k].y, a);
+      a = __builtin_fmaf(d2, xc[k].z, a);
+      a = __builtin_fmaf(d3, xc[k].w, a);
+      dw[j][k] = a;
+    }
+    mw[j] |= ((unsigned)m0 | ((unsigned)m1 << 1) | ((unsigned)m2 << 2) | ((unsigned)m3 << 3)) << ((t & 7) * 4);
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xc[k] = xn[k];
+    }
+  }
+}
+
+// The token tile is staged by global_load_lds into one buffer (load, wait, read): with the dW
+// accumulators live, a second buffer's loop does not fit the 256 VGPRs a wave has at 2 waves per
+// SIMD.
+template <int K, int NPL, int WAVES, int ACT, int RA>
 __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
-  extern __shared__ float4 xs[];
+  __shared__ float4 xs[XTILE_SB];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   long long chunk = (long long)blockIdx.x * WAVES + wave;
@@ -70,7 +123,6 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   unsigned addr[NPL][K];
   float w[NPL][K], dw[NPL][K];
   float bias[NPL], dbv[NPL];
-  unsigned mw[NPL];
   unsigned slot2[(NPL + 1) / 2];  // slots of neurons 2i, 2i+1 within the pool (16 bits each; >= n_g: padding)
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
@@ -93,14 +145,9 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
     const float bl = p.bias[n];
     bias[j] = valid ? bl : 0.f;
     dbv[j] = 0.f;
-    mw[j] = 0u;
   }
   const float* c1row = p.c1t + g * p.cap;
-  const char* xsb = reinterpret_cast<const char*>(xs);
-  // token tiles are staged as in the forward (PF > 0: next tile prefetched into registers)
   constexpr int NT = WAVES * 64;
-  PrefetchRegs<PF> pf;
-  if constexpr (PF > 0) pf.load(p.xt, NT);
 
   // 8 token tiles (32 tokens) per mask word; the word is stored after the inner loop
   for (int t0 = 0; t0 < p.n_tiles; t0 += 8) {
@@ -109,47 +156,12 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
     for (int j = 0; j < NPL; ++j) mw[j] = 0u;
     const int t1 = t0 + 8 < p.n_tiles ? t0 + 8 : p.n_tiles;
     for (int t = t0; t < t1; ++t) {
+      __syncthreads();  // every wave is done with tile t - 1
+      stage_tile(p.xt + (long long)t * p.D, xs, p.D, NT);
+      const float4 c1 = *reinterpret_cast<const float4*>(c1row + t * BT);
+      stage_wait();
       __syncthreads();
-      if constexpr (PF > 0) {
-        pf.store(xs, NT);
-      } else {
-        const float4* src = p.xt + (long long)t * p.D;
-        for (int i = threadIdx.x; i < p.D; i += NT) xs[i] = src[i];
-      }
-      __syncthreads();
-      const float4 c1 = *reinterpret_cast<const float4*>(c1row + t * BT);  // issued before the prefetch
-      if constexpr (PF > 0) {
-        if (t + 1 < p.n_tiles) pf.load(p.xt + (long long)(t + 1) * p.D, NT);
-      }
-#pragma unroll
-      for (int j = 0; j < NPL; ++j) {
-        float4 x[K];
-        float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          x[k] = *reinterpret_cast<const float4*>(xsb + addr[j][k]);
-          z0 = __builtin_fmaf(x[k].x, w[j][k], z0);
-          z1 = __builtin_fmaf(x[k].y, w[j][k], z1);
-          z2 = __builtin_fmaf(x[k].z, w[j][k], z2);
-          z3 = __builtin_fmaf(x[k].w, w[j][k], z3);
-        }
-        const bool m0 = ACT != GL_ACT_RELU || z0 > 0.f, m1 = ACT != GL_ACT_RELU || z1 > 0.f;
-        const bool m2 = ACT != GL_ACT_RELU || z2 > 0.f, m3 = ACT != GL_ACT_RELU || z3 > 0.f;
-        const float d0 = m0 ? c1.x : 0.f, d1 = m1 ? c1.y : 0.f, d2 = m2 ? c1.z : 0.f, d3 = m3 ? c1.w : 0.f;
-        dbv[j] = dbv[j] + d0 + d1 + d2 + d3;
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          float a = dw[j][k];
-          a = __builtin_fmaf(d0, x[k].x, a);
-          a = __builtin_fmaf(d1, x[k].y, a);
-          a = __builtin_fmaf(d2, x[k].z, a);
-          a = __builtin_fmaf(d3, x[k].w, a);
-          dw[j][k] = a;
-        }
-        mw[j] |= ((unsigned)m0 | ((unsigned)m1 << 1) | ((unsigned)m2 << 2) | ((unsigned)m3 << 3)) << ((t & 7) * 4);
-        // keeps the gathers of the unrolled neuron loop from all being hoisted (register pressure)
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      bwd_w_tile<K, NPL, ACT, RA>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw, dbv, mw);
     }
     const int word = t0 >> 3;
     uint32_t* mslab = p.mask + ((long long)(word / p.mw2) * p.NS + g * p.S) * p.mw2 + word % p.mw2;
@@ -433,7 +445,7 @@ __global__ void __launch_bounds__(256) dx_reduce_kernel(const float* __restrict_
 struct BwdPlan {
   int bc_max, npl, waves, cpg, tiles_max, cap_max, rs_max, FR, P, U, Q, QL, UQ;
   long long n_chunks, e_max, nseg_max;
-  size_t lds, xt_bytes, c1_bytes, mask_bytes, part_bytes, edges_bytes;
+  size_t xt_bytes, c1_bytes, mask_bytes, part_bytes, edges_bytes;
 };
 
 static BwdPlan bwd_plan(int B, int D, int G, int S, int K) {
@@ -459,7 +471,6 @@ static BwdPlan bwd_plan(int B, int D, int G, int S, int K) {
   q.QL = (int)ql;
   q.Q = 8 * q.QL;
   q.UQ = ceil_div(q.U, q.Q);
-  q.lds = (size_t)D * 16;
   q.xt_bytes = (size_t)round_up((long long)q.tiles_max * D * 16, 256);
   q.c1_bytes = (size_t)round_up((long long)G * q.cap_max * 4, 256);
   q.mask_bytes = (size_t)round_up((long long)G * S * q.rs_max * 4, 256);
@@ -488,39 +499,23 @@ void edge_layout(int D, int G, int S, int K, EdgeHeader* h, size_t* total) {
   *total = off;
 }
 
-template <int K, int NPL, int WAVES, int ACT, int PF>
-static int launch_bwd_w(const BwK& k, hipStream_t s, size_t lds) {
-  auto fn = bwd_w_kernel<K, NPL, WAVES, ACT, PF>;
-  GL_TRY(set_lds_limit((const void*)fn, lds));
-  GL_LAUNCH(GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)), dim3(WAVES * 64), lds, s, k);
+template <int K, int NPL, int WAVES, int ACT, int RA>
+static int launch_bwd_w(const BwK& k, hipStream_t s) {
+  auto fn = bwd_w_kernel<K, NPL, WAVES, ACT, RA>;
+  GL_LAUNCH(GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)), dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;
 }
 
-// 8 waves per workgroup; next-tile register prefetch when D is a multiple of 512 and needs at
-// most MAXPF float4 per thread (the dW accumulators leave no room for more)
-template <int ACT, int K, int NPL, int MAXPF>
-static int launch_bwd_w_pf(int D, const BwK& k, hipStream_t s, size_t lds) {
-  int pf = D % 512 == 0 ? D / 512 : 0;
-  if (pf > MAXPF) pf = 0;
-  switch (pf) {
-    case 1: return launch_bwd_w<K, NPL, 8, ACT, 1>(k, s, lds);
-    case 2: return launch_bwd_w<K, NPL, 8, ACT, 2>(k, s, lds);
-    case 4: return launch_bwd_w<K, NPL, 8, ACT, 4>(k, s, lds);
-    case 8: return launch_bwd_w<K, NPL, 8, ACT, 8>(k, s, lds);
-    default: return launch_bwd_w<K, NPL, 8, ACT, 0>(k, s, lds);
-  }
-}
-
+// 8 waves per workgroup; read-ahead of 8 LDS reads at K = 8, 2 at K = 16 (more would spill)
 template <int ACT>
-static int launch_bwd_w_act(int K, int D, const BwK& k, hipStream_t s, size_t lds) {
-  if (K == 8) return launch_bwd_w_pf<ACT, 8, 6, 8>(D, k, s, lds);
-  return launch_bwd_w_pf<ACT, 16, 3, 2>(D, k, s, lds);
+static int launch_bwd_w_act(int K, const BwK& k, hipStream_t s) {
+  if (K == 8) return launch_bwd_w<8, 6, 8, ACT, 8>(k, s);
+  return launch_bwd_w<16, 3, 8, ACT, 2>(k, s);
 }
 
-static int launch_bwd_w_any(int K, int D, int act, const BwK& k, hipStream_t s, size_t lds) {
-  return act == GL_ACT_RELU ? launch_bwd_w_act<GL_ACT_RELU>(K, D, k, s, lds)
-                            : launch_bwd_w_act<GL_ACT_IDENTITY>(K, D, k, s, lds);
+static int launch_bwd_w_any(int K, int act, const BwK& k, hipStream_t s) {
+  return act == GL_ACT_RELU ? launch_bwd_w_act<GL_ACT_RELU>(K, k, s) : launch_bwd_w_act<GL_ACT_IDENTITY>(K, k, s);
 }
 
 template <int K, int T>
@@ -584,7 +579,7 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     const long long NS = (long long)a->G * a->S;
     BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, a->sched, q.n_chunks, NS,
            a->D, a->S, q.cpg, n_tiles, cap, 2 * T, ceil_div(a->S, SCHED_WIN)};
-    GL_TRY(launch_bwd_w_any(a->K, a->D, a->act, bk, s, q.lds));
+    GL_TRY(launch_bwd_w_any(a->K, a->act, bk, s));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
            (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, a->W, part,
            NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * T)};

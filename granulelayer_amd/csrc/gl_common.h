@@ -102,27 +102,31 @@ __device__ __forceinline__ int opaque(int v) {
   return v;
 }
 
-// PF float4 slots per thread kept in one register vector (a plain array of float4 is placed in
-// scratch memory by the compiler when PF > 1).
-template <int PF>
-struct PrefetchRegs {
-  typedef float vec __attribute__((ext_vector_type(PF > 0 ? 4 * PF : 4)));
-  vec r;
-  __device__ __forceinline__ void load(const float4* __restrict__ src, int stride) {
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const float4 v = src[threadIdx.x + i * stride];
-      r[4 * i] = v.x;
-      r[4 * i + 1] = v.y;
-      r[4 * i + 2] = v.z;
-      r[4 * i + 3] = v.w;
-    }
-  }
-  __device__ __forceinline__ void store(float4* dst, int stride) const {
-#pragma unroll
-    for (int i = 0; i < PF; ++i) dst[threadIdx.x + i * stride] = make_float4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
-  }
-};
+// ---- X token tiles: global -> LDS directly ----------------------------------------------------
+// A tile is D float4 slots (4 tokens per input feature).  Every lane copies 16-byte slots with
+// global_load_lds_dwordx4, which writes lane i's data to LDS at (wave-uniform base) + 16 i, so the
+// data never passes through VGPRs.  D <= XTILE_DB features: two static buffers, the next tile
+// lands while the current one is read; larger D (up to XTILE_SB): one buffer.
+constexpr int XTILE_DB = 4096;
+constexpr int XTILE_SB = 10112;
+
+__device__ __forceinline__ void stage_tile(const float4* __restrict__ src, float4* dst, int D, int nthreads) {
+  const int lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < D; i += nthreads)
+    __builtin_amdgcn_global_load_lds((const void*)(src + i),
+                                     (__attribute__((address_space(3))) void*)(dst + (i - lane)), 16, 0, 0);
+}
+// X slot at byte offset a of a tile buffer.  FAR: the buffer's base does not fit the 16-bit
+// ds_read offset, so base + a costs one v_add per read; the offset then passes through an empty
+// asm so the compiler keeps doing that add at the read instead of hoisting a second copy of every
+// address out of the tile loop (which would not fit the register file).
+template <bool FAR>
+__device__ __forceinline__ float4 lds_x(const char* buf, unsigned a) {
+  if constexpr (FAR) asm volatile("" : "+v"(a));
+  return *reinterpret_cast<const float4*>(buf + a);
+}
+// this wave's tile loads have reached LDS (vmcnt(0)); a barrier then publishes every wave's
+__device__ __forceinline__ void stage_wait() { __builtin_amdgcn_s_waitcnt(0x3f70); }
 
 // DPP move (row/quad patterns) as a float
 template <int CTRL>

@@ -55,9 +55,62 @@ struct FwdK {
   int D, S, cpg, n_tiles, b_pad, nwin;
 };
 
-template <int K, int NPL, int WAVES, int ACT, int PF>
+// One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
+// pooled over the wave's neurons and lanes.  The first RA LDS reads of neuron j + 1 are issued
+// before the arithmetic of neuron j, so up to K + RA reads are in flight per wave (the default
+// schedule keeps two).
+template <int K, int NPL, int ACT, bool FAR, int RA = (K < 8 ? K : 8)>
+__device__ __forceinline__ void fwd_tile(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+                                         const float (&bias)[NPL], float* out, bool store) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  float4 xc[K];
+#pragma unroll
+  for (int k = 0; k < RA; ++k) xc[k] = lds_x<FAR>(xsb, addr[0][k]);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+#pragma unroll
+    for (int k = RA; k < K; ++k) xc[k] = lds_x<FAR>(xsb, addr[j][k]);
+    float4 xn[RA];
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xn[k] = lds_x<FAR>(xsb, addr[j + 1][k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
+      z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
+      z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
+      z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
+    }
+    if (ACT == GL_ACT_RELU) {
+      z0 = __builtin_fmaxf(z0, 0.f);
+      z1 = __builtin_fmaxf(z1, 0.f);
+      z2 = __builtin_fmaxf(z2, 0.f);
+      z3 = __builtin_fmaxf(z3, 0.f);
+    }
+    a0 += z0;
+    a1 += z1;
+    a2 += z2;
+    a3 += z3;
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xc[k] = xn[k];
+    }
+  }
+  a0 = wave_sum(a0);
+  a1 = wave_sum(a1);
+  a2 = wave_sum(a2);
+  a3 = wave_sum(a3);
+  if (store) *reinterpret_cast<float4*>(out) = make_float4(a0, a1, a2, a3);
+}
+
+template <int K, int NPL, int WAVES, int ACT, bool DBUF>
 __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
-  extern __shared__ float4 xs[];
+  __shared__ float4 xa[DBUF ? XTILE_DB : XTILE_SB];
+  __shared__ float4 xb[DBUF ? XTILE_DB : 1];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   long long chunk = (long long)blockIdx.x * WAVES + wave;
@@ -89,57 +142,34 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
     bias[j] = valid ? bl : 0.f;
   }
 
-  const char* xsb = reinterpret_cast<const char*>(xs);
-  // Token tile t (D float4 slots) is staged into LDS.  PF > 0 (D == PF * WAVES * 64): each
-  // thread holds PF slots of the next tile in registers, loaded while the current tile is
-  // computed, so the global-load latency hides behind the gathers; PF == 0: direct copy.
+  // Token tiles are staged into LDS by global_load_lds (stage_tile).  DBUF: tile t + 1 is loaded
+  // into the other buffer while tile t is read, one barrier per tile; tiles alternate xa (even t)
+  // and xb (odd t), each buffer read through its own array.  Otherwise: load, wait, read.
   constexpr int NT = WAVES * 64;
-  PrefetchRegs<PF> pf;
-  if constexpr (PF > 0) pf.load(p.xt, NT);
-  for (int t = 0; t < p.n_tiles; ++t) {
-    __syncthreads();
-    if constexpr (PF > 0) {
-      pf.store(xs, NT);
-    } else {
-      const float4* src = p.xt + (long long)t * p.D;
-      for (int e = threadIdx.x; e < p.D; e += NT) xs[e] = src[e];
-    }
-    __syncthreads();
-    if constexpr (PF > 0) {
+  float* out = p.part + chunk * p.b_pad;
+  const bool store = active && lane == 0;
+  if constexpr (DBUF) {
+    stage_tile(p.xt, xa, p.D, NT);
+    for (int t = 0; t < p.n_tiles; t += 2) {
+      stage_wait();
+      __syncthreads();  // tile t is in xa; every wave is done with xb (tile t - 1)
+      if (t + 1 < p.n_tiles) stage_tile(p.xt + (long long)(t + 1) * p.D, xb, p.D, NT);
+      fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store);
       if (t + 1 < p.n_tiles) {
-        const float4* src = p.xt + (long long)(t + 1) * p.D;
-        pf.load(src, NT);
+        stage_wait();
+        __syncthreads();  // tile t + 1 is in xb; every wave is done with xa
+        if (t + 2 < p.n_tiles) stage_tile(p.xt + (long long)(t + 2) * p.D, xa, p.D, NT);
+        fwd_tile<K, NPL, ACT, true>(reinterpret_cast<const char*>(xb), addr, w, bias, out + (t + 1) * BT, store);
       }
     }
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-      float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const float4 xv = *reinterpret_cast<const float4*>(xsb + addr[j][k]);
-        z0 = __builtin_fmaf(xv.x, w[j][k], z0);
-        z1 = __builtin_fmaf(xv.y, w[j][k], z1);
-        z2 = __builtin_fmaf(xv.z, w[j][k], z2);
-        z3 = __builtin_fmaf(xv.w, w[j][k], z3);
-      }
-      if (ACT == GL_ACT_RELU) {
-        z0 = __builtin_fmaxf(z0, 0.f);
-        z1 = __builtin_fmaxf(z1, 0.f);
-        z2 = __builtin_fmaxf(z2, 0.f);
-        z3 = __builtin_fmaxf(z3, 0.f);
-      }
-      a0 += z0;
-      a1 += z1;
-      a2 += z2;
-      a3 += z3;
+  } else {
+    for (int t = 0; t < p.n_tiles; ++t) {
+      __syncthreads();  // every wave is done with tile t - 1
+      stage_tile(p.xt + (long long)t * p.D, xa, p.D, NT);
+      stage_wait();
+      __syncthreads();
+      fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store);
     }
-    a0 = wave_sum(a0);
-    a1 = wave_sum(a1);
-    a2 = wave_sum(a2);
-    a3 = wave_sum(a3);
-    if (active && lane == 0)
-      *reinterpret_cast<float4*>(p.part + chunk * p.b_pad + (long long)t * BT) = make_float4(a0, a1, a2, a3);
   }
 }
 
@@ -171,7 +201,7 @@ __global__ void __launch_bounds__(256) fwd_finalize_kernel(const float* __restri
 struct FwdPlan {
   int npl, waves, cpg, n_tiles, b_pad;
   long long n_chunks;
-  size_t lds, xt_bytes, part_bytes;
+  size_t xt_bytes, part_bytes;
 };
 
 static FwdPlan fwd_plan(const GlFwdArgs* a) {
@@ -182,41 +212,30 @@ static FwdPlan fwd_plan(const GlFwdArgs* a) {
   q.n_chunks = (long long)a->G * q.cpg;
   q.n_tiles = ceil_div(a->B, BT);
   q.b_pad = q.n_tiles * BT;
-  q.lds = (size_t)a->D * 16;
   q.xt_bytes = (size_t)round_up((long long)q.n_tiles * a->D * 16, 256);
   q.part_bytes = (size_t)round_up((long long)q.n_chunks * q.b_pad * 4, 256);
   return q;
 }
 
-template <int K, int NPL, int WAVES, int ACT, int PF>
-static int launch_fwd(const FwdK& k, hipStream_t s, size_t lds) {
-  auto fn = fwd_kernel<K, NPL, WAVES, ACT, PF>;
-  GL_TRY(set_lds_limit((const void*)fn, lds));
+template <int K, int NPL, int WAVES, int ACT, bool DBUF>
+static int launch_fwd(const FwdK& k, hipStream_t s) {
+  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF>;
   dim3 grid((unsigned)ceil_div(k.n_chunks, WAVES));
-  GL_LAUNCH(GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), lds, s, k);
+  GL_LAUNCH(GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;
 }
 
-// 8 waves per workgroup (one workgroup per CU at D = 4096); the next tile is prefetched into
-// registers when D is a multiple of the 512 threads and needs at most 16 float4 per thread
+// 8 waves per workgroup (one workgroup per CU); two tile buffers when D fits them
 template <int ACT, int K, int NPL>
-static int launch_fwd_pf(int D, const FwdK& k, hipStream_t s, size_t lds) {
-  const int pf = D % 512 == 0 ? D / 512 : 0;
-  switch (pf) {
-    case 1: return launch_fwd<K, NPL, 8, ACT, 1>(k, s, lds);
-    case 2: return launch_fwd<K, NPL, 8, ACT, 2>(k, s, lds);
-    case 4: return launch_fwd<K, NPL, 8, ACT, 4>(k, s, lds);
-    case 8: return launch_fwd<K, NPL, 8, ACT, 8>(k, s, lds);
-    case 16: return launch_fwd<K, NPL, 8, ACT, 16>(k, s, lds);
-    default: return launch_fwd<K, NPL, 8, ACT, 0>(k, s, lds);
-  }
+static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
+  return D <= XTILE_DB ? launch_fwd<K, NPL, 8, ACT, true>(k, s) : launch_fwd<K, NPL, 8, ACT, false>(k, s);
 }
 
 template <int ACT>
-static int launch_fwd_act(int K, int D, const FwdK& k, hipStream_t s, size_t lds) {
-  if (K == 8) return launch_fwd_pf<ACT, 8, 8>(D, k, s, lds);
-  return launch_fwd_pf<ACT, 16, 4>(D, k, s, lds);
+static int launch_fwd_act(int K, int D, const FwdK& k, hipStream_t s) {
+  if (K == 8) return launch_fwd_buf<ACT, 8, 8>(D, k, s);
+  return launch_fwd_buf<ACT, 16, 4>(D, k, s);
 }
 
 int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const float* W,
@@ -228,7 +247,7 @@ int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void
   if (pool != GL_POOL_MEAN && pool != GL_POOL_SUM) return GL_ERR_UNSUPPORTED;
   if (x_dtype != GL_DTYPE_F32 && x_dtype != GL_DTYPE_BF16) return GL_ERR_UNSUPPORTED;
   if ((long long)G * S > (1LL << 31) / 16) return GL_ERR_UNSUPPORTED;
-  if ((size_t)D * 16 > max_lds_bytes()) return GL_ERR_LDS;
+  if (D > XTILE_SB) return GL_ERR_LDS;  // one token tile (D x 16 bytes) must fit the LDS tile buffer
   return 0;
 }
 
@@ -258,8 +277,8 @@ extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
   if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;
   FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, a->sched, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles, q.b_pad,
          ceil_div(a->S, SCHED_WIN)};
-  GL_TRY(a->act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU>(a->K, a->D, k, s, q.lds)
-                                : launch_fwd_act<GL_ACT_IDENTITY>(a->K, a->D, k, s, q.lds));
+  GL_TRY(a->act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU>(a->K, a->D, k, s)
+                                : launch_fwd_act<GL_ACT_IDENTITY>(a->K, a->D, k, s));
   dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(q.b_pad, 32));
   GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_kernel, grid, dim3(256), 0, s, part, a->counts, a->pre, a->B, a->G, q.cpg, q.b_pad,
                      0, a->pool);
