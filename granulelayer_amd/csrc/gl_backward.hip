@@ -442,6 +442,11 @@ __global__ void __launch_bounds__(256) dx_reduce_kernel(const float* __restrict_
 }
 
 // ---- host side -------------------------------------------------------------------------------
+// dW pass: 4 neurons per lane in 12 waves at K = 8 (3 waves per SIMD), 3 in 8 waves at K = 16; a
+// workgroup covers 3072 neurons per staged token tile either way
+constexpr int bwd_npl(int K) { return K == 8 ? 4 : 3; }
+constexpr int bwd_waves(int K) { return K == 8 ? 12 : 8; }
+
 struct BwdPlan {
   int bc_max, npl, waves, cpg, tiles_max, cap_max, rs_max, FR, P, U, Q, QL, UQ;
   long long n_chunks, e_max, nseg_max;
@@ -451,8 +456,8 @@ struct BwdPlan {
 static BwdPlan bwd_plan(int B, int D, int G, int S, int K) {
   BwdPlan q;
   q.bc_max = B < BWD_TOKEN_CHUNK ? B : BWD_TOKEN_CHUNK;
-  q.npl = 48 / K;  // 6 neurons per lane at K = 8, 3 at K = 16
-  q.waves = 8;
+  q.npl = bwd_npl(K);
+  q.waves = bwd_waves(K);
   q.cpg = ceil_div(S, 64 * q.npl);
   q.n_chunks = (long long)G * q.cpg;
   q.tiles_max = ceil_div(q.bc_max, BT);
@@ -507,11 +512,11 @@ static int launch_bwd_w(const BwK& k, hipStream_t s) {
   return 0;
 }
 
-// 8 waves per workgroup; read-ahead of 8 LDS reads at K = 8, 2 at K = 16 (more would spill)
+// read-ahead of 2 LDS reads (more would spill)
 template <int ACT>
 static int launch_bwd_w_act(int K, const BwK& k, hipStream_t s) {
-  if (K == 8) return launch_bwd_w<8, 6, 8, ACT, 8>(k, s);
-  return launch_bwd_w<16, 3, 8, ACT, 2>(k, s);
+  if (K == 8) return launch_bwd_w<8, bwd_npl(8), bwd_waves(8), ACT, 2>(k, s);
+  return launch_bwd_w<16, bwd_npl(16), bwd_waves(16), ACT, 2>(k, s);
 }
 
 static int launch_bwd_w_any(int K, int act, const BwK& k, hipStream_t s) {

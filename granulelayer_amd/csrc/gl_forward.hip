@@ -57,9 +57,9 @@ struct FwdK {
 
 // One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
 // pooled over the wave's neurons and lanes.  The first RA LDS reads of neuron j + 1 are issued
-// before the arithmetic of neuron j, so up to K + RA reads are in flight per wave (the default
-// schedule keeps two).
-template <int K, int NPL, int ACT, bool FAR, int RA = (K < 8 ? K : 8)>
+// before the arithmetic of neuron j, so up to K + RA reads are in flight per wave (the compiler's
+// own schedule keeps two).
+template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8)>
 __device__ __forceinline__ void fwd_tile(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                          const float (&bias)[NPL], float* out, bool store) {
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
@@ -198,6 +198,11 @@ __global__ void __launch_bounds__(256) fwd_finalize_kernel(const float* __restri
 }
 
 // ---- host side -------------------------------------------------------------------------------
+// 4 neurons per lane; 16 waves per workgroup at K = 8 (4 waves per SIMD, 128 VGPRs), 8 at K = 16
+// (2 per SIMD: the parameters of 4 neurons of fan-in 16 take twice the registers)
+constexpr int FWD_NPL = 4;
+constexpr int fwd_waves(int K) { return K == 8 ? 16 : 8; }
+
 struct FwdPlan {
   int npl, waves, cpg, n_tiles, b_pad;
   long long n_chunks;
@@ -206,8 +211,8 @@ struct FwdPlan {
 
 static FwdPlan fwd_plan(const GlFwdArgs* a) {
   FwdPlan q;
-  q.npl = 64 / a->K;  // 8 neurons per lane at K = 8, 4 at K = 16 (~140 VGPRs of parameters)
-  q.waves = 8;
+  q.npl = FWD_NPL;
+  q.waves = fwd_waves(a->K);
   q.cpg = ceil_div(a->S, 64 * q.npl);
   q.n_chunks = (long long)a->G * q.cpg;
   q.n_tiles = ceil_div(a->B, BT);
@@ -226,16 +231,16 @@ static int launch_fwd(const FwdK& k, hipStream_t s) {
   return 0;
 }
 
-// 8 waves per workgroup (one workgroup per CU); two tile buffers when D fits them
-template <int ACT, int K, int NPL>
+// one workgroup per CU (the tile buffers take the LDS); two tile buffers when D fits them
+template <int ACT, int K>
 static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
-  return D <= XTILE_DB ? launch_fwd<K, NPL, 8, ACT, true>(k, s) : launch_fwd<K, NPL, 8, ACT, false>(k, s);
+  constexpr int W = fwd_waves(K);
+  return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true>(k, s) : launch_fwd<K, FWD_NPL, W, ACT, false>(k, s);
 }
 
 template <int ACT>
 static int launch_fwd_act(int K, int D, const FwdK& k, hipStream_t s) {
-  if (K == 8) return launch_fwd_buf<ACT, 8, 8>(D, k, s);
-  return launch_fwd_buf<ACT, 16, 4>(D, k, s);
+  return K == 8 ? launch_fwd_buf<ACT, 8>(D, k, s) : launch_fwd_buf<ACT, 16>(D, k, s);
 }
 
 int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const float* W,
