@@ -199,18 +199,21 @@ struct DxK {
 };
 
 // ---- dX ----------------------------------------------------------------------------------------
-// One wave owns FW consecutive features, one range of UQ units and 64*T tokens (lane = token,
-// slot j = token + 64 j).  It walks the input-major edges of its features unit by unit, in the
-// stored order, and for every edge (n, k) -> d adds c1[b, g(n)] * [mask[n, b]] * W[n, k] to the
-// register accumulator of d.
+// One wave owns FW consecutive features, one range of UQ units and a slice of 64*T tokens: lane l
+// holds tokens T*l .. T*l + T - 1 of the slice, whose activation bits are the T adjacent bits
+// (T*l) % 32 .. of the neuron's mask word (T*l) / 32.  It walks the input-major edges of its
+// features unit by unit, in the stored order, and for every edge (n, k) -> d adds
+// c1[b, g(n)] * [mask[n, b]] * W[n, k] to the register accumulator of d.
 //
 // Edges are taken in chunks of up to 64 (one segment, or a 64-edge piece of a long one).  The
 // lanes first gather, one edge each, the chunk's records, weights and mask words with vector
 // loads (64 independent requests per instruction: random scalar loads would be limited by the
 // scalar cache's miss rate); the gathers of the next chunk are issued before the current chunk is
-// computed.  The chunk is staged in LDS; for edge i every token lane reads the weight (a
-// broadcast) and the mask word holding its own bit, turns the bit into an all-ones / zero mask
-// (v_bfe_i32) that selects c1, and accumulates c1 * w into the register of the edge's feature.
+// computed.  The chunk is staged in LDS; for edge i every lane reads the weight (a broadcast) and
+// the mask word holding its bits.  At T = 4 one v_bfe_u32 takes the lane's 4 bits, a 16-entry
+// LDS table turns them into a byte mask (0x00 / 0xff per token), and an SDWA v_and_b32 with the
+// sign-extended byte selects c1: two VALU per token and edge (select, FMA).  At T <= 2 each bit
+// is sign-extended to an all-ones / zero mask by v_bfe_i32 (three VALU per token and edge).
 template <int T>
 struct DxGather {
   unsigned rec;
@@ -264,45 +267,59 @@ __device__ __forceinline__ void dx_gather(const DxK& p, const uint32_t* mask_tc,
   }
 }
 
+// c1 of the lane's T tokens (tok0 = the first of them) for the pool of unit u
 template <int T>
 __device__ __forceinline__ void dx_load_c1(const DxK& p, int u, int tok0, float (&c1)[T]) {
   const float* c = p.c1t + (long long)(u / p.P) * p.cap + tok0;
-#pragma unroll
-  for (int j = 0; j < T; ++j) c1[j] = c[j * 64];
+  if constexpr (T == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(c);
+    c1[0] = v.x, c1[1] = v.y, c1[2] = v.z, c1[3] = v.w;
+  } else if constexpr (T == 2) {
+    const float2 v = *reinterpret_cast<const float2*>(c);
+    c1[0] = v.x, c1[1] = v.y;
+  } else {
+    c1[0] = c[0];
+  }
 }
 
-// Edges i in [i0, i1) of the chunk, all of feature F0 of the range: acc[F0][j] += [m_j] c1[j] w.
-// LDS copy of one chunk: every edge's weight and its 2T mask words in [half][slot] order, so the
-// word holding token lane b's bit of slot j is m[i][b >> 5][j].
+// LDS copy of one chunk: every edge's weight and its 2T mask words (token order); nib[v] expands
+// the 4-bit value v to a byte mask (byte i = 0xff when bit i is set)
 template <int T>
 struct DxStage {
   float w[64];
-  unsigned m[64][2][T];
+  unsigned m[64][2 * T];
+  unsigned nib[16];
 };
 
 template <int T>
 __device__ __forceinline__ void dx_stage(DxStage<T>& st, const DxGather<T>& g, int lane) {
   st.w[lane] = g.w;
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int j = 0; j < T; ++j) st.m[lane][h][j] = g.m[2 * j + h];
+  for (int i = 0; i < 2 * T; ++i) st.m[lane][i] = g.m[i];
 }
 
 // Edges i in [i0, i1) of the chunk, all of feature F0 of the range: acc[F0][j] += [m_j] c1[j] w.
 template <int F0, int T>
 __device__ __forceinline__ void dx_run(const DxStage<T>& st, int i0, int i1, int lane, const float (&c1)[T],
                                        float (&acc)[FW][T]) {
-  // weight: an LDS broadcast; mask bit: the lane's own bit of the staged word, sign-extended to
-  // an all-ones / zero mask that selects c1
-  const int half = lane >> 5;
-  const unsigned bit = (unsigned)lane & 31u;
+  const int word = (T * lane) >> 5;
+  const unsigned bit = (unsigned)(T * lane) & 31u;
   for (int i = i0; i < i1; ++i) {
-    const float w = st.w[i];
+    const float w = st.w[i];  // an LDS broadcast
+    const unsigned mw = st.m[i][word];
+    if constexpr (T == 4) {
+      const unsigned bm = st.nib[__builtin_amdgcn_ubfe(mw, bit, 4u)];
 #pragma unroll
-    for (int j = 0; j < T; ++j) {
-      const int sel = __builtin_amdgcn_sbfe((int)st.m[i][half][j], bit, 1u);
-      acc[F0][j] = __builtin_fmaf(__builtin_bit_cast(float, sel & __builtin_bit_cast(int, c1[j])), w, acc[F0][j]);
+      for (int j = 0; j < 4; ++j) {
+        const int sel = (int)(signed char)(bm >> (8 * j));  // SDWA: sign-extended byte j
+        acc[F0][j] = __builtin_fmaf(__builtin_bit_cast(float, sel & __builtin_bit_cast(int, c1[j])), w, acc[F0][j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < T; ++j) {
+        const int sel = __builtin_amdgcn_sbfe((int)mw, bit + j, 1u);
+        acc[F0][j] = __builtin_fmaf(__builtin_bit_cast(float, sel & __builtin_bit_cast(int, c1[j])), w, acc[F0][j]);
+      }
     }
   }
 }
@@ -370,9 +387,15 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
 #pragma unroll
     for (int j = 0; j < T; ++j) acc[f][j] = 0.f;
 
-  const int tok0 = tc * 64 * T + lane;
+  const int tok0 = tc * 64 * T + T * lane;
   const uint32_t* mask_tc = p.mask + (long long)tc * p.NS * (2 * T);
   __shared__ DxStage<T> st;
+  if (lane < 16) {
+    unsigned v = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v |= ((unsigned)lane >> i & 1u) ? 0xffu << (8 * i) : 0u;
+    st.nib[lane] = v;
+  }
   if (lo < hi) {
     DxChunk cc{lo, p.seg_begin[lo], p.seg_begin[lo + 1], p.seg_unit[lo]};
     DxGather<T> gc;
@@ -414,7 +437,7 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
     const int d = F * FW + f;
     if (d < p.D) {
 #pragma unroll
-      for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j * 64] = acc[f][j];
+      for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j] = acc[f][j];
     }
   }
 }
