@@ -493,11 +493,13 @@ static BwdPlan bwd_plan(int B, int D, int G, int S, int K) {
   // that share a unit close together in time, so the unit's weights and mask words are still in
   // the XCD's L2 when the next of them gathers from it (measured at C2: QL 8 -> 32 cut the dX
   // kernel by 8% for 0.3 ms more partial-sum reduction).  About 256K waves in total, at most
-  // QL = 32: the [Q, D, tokens] partials then do not depend on the number of neurons.
+  // QL = 32 and at least 128 units per range, so the [Q, D, tokens] partials (and their
+  // reduction) stay small next to the layer.
   const int n_tc = q.cap_max / (64 * dx_slots(q.bc_max));
   const long long waves_wanted = 262144;
   long long ql = (waves_wanted + 8LL * q.FR * n_tc - 1) / (8LL * q.FR * n_tc);
   if (ql > 32) ql = 32;
+  if (ql > q.U / 1024) ql = q.U / 1024;
   if (ql < 1) ql = 1;
   if (8 * ql > q.U) ql = ceil_div(q.U, 8);
   q.QL = (int)ql;
