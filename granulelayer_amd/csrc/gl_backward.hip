@@ -8,7 +8,7 @@
 // and records the activation mask bit act'(z) of every token (a [neurons, tokens] bit matrix, 1/32
 // of the bytes of the fp32 hidden tensor).  At the end it adds dW/db to the caller's accumulators.
 //
-// Pass 2 (dx_kernel) owns 16 consecutive input features, one pool range and 64*T tokens per
+// Pass 2 (dx_kernel) owns FW = 8 consecutive input features, one unit range and 64*T tokens per
 // wave.  It walks the input-major edges of its features in the fixed order (unit, feature, edge
 // id); for every edge (n, k) it adds c1[b, g(n)] * W[n,k] * mask[n, b] to the register
 // accumulator of its feature.  The pool-range partials are summed in a fixed order by

@@ -1,7 +1,8 @@
 // Forward: fused sparse projection -> activation -> pool (sum / mean), neuron-stationary.
 //
 // Each wave owns a "chunk": up to 64*NPL consecutive slots of one group, NPL neurons per lane
-// (slot s_lo + j*64 + lane).  Index records, weights and bias of the chunk are loaded into VGPRs
+// (slot s_lo + j*64 + lane, or the gather schedule's permutation of the chunk's 128-slot
+// windows).  Index records, weights and bias of the chunk are loaded into VGPRs
 // once; the wave then streams every token tile of X through LDS (4 tokens per 16-byte slot,
 // feature-major), gathers one slot per (neuron, k) with ds_read_b128, accumulates z in fp32,
 // applies the activation and reduces the chunk's per-token sum across the wave.  The hidden
