@@ -282,12 +282,13 @@ __device__ __forceinline__ void dx_load_c1(const DxK& p, int u, int tok0, float 
   }
 }
 
-// LDS copy of one chunk: every edge's weight and its 2T mask words (token order); nib[v] expands
+// LDS copy of one chunk: every edge's weight and its 2T mask words (token order; rows padded to
+// an odd number of words, so the 64 lanes' row writes hit 64 different banks); nib[v] expands
 // the 4-bit value v to a byte mask (byte i = 0xff when bit i is set)
 template <int T>
 struct DxStage {
   float w[64];
-  unsigned m[64][2 * T];
+  unsigned m[64][2 * T + 1];
   unsigned nib[16];
 };
 
