@@ -58,21 +58,21 @@ struct BwK {
 // One token tile of the dW pass (LDS at xsb): recompute z, form dz = c1 * act'(z), accumulate
 // db, dW and the tile's 4 mask bits (bit 4 (t % 8) + i of word mw for token i of tile t).  The
 // first RA LDS reads of neuron j + 1 are issued before the arithmetic of neuron j.
-template <int K, int NPL, int ACT, int RA>
+template <int K, int NPL, int ACT, int RA, bool FAR>
 __device__ __forceinline__ void bwd_w_tile(const char* xsb, int t, const float4 c1, const unsigned (&addr)[NPL][K],
                                            const float (&w)[NPL][K], const float (&bias)[NPL], float (&dw)[NPL][K],
                                            float (&dbv)[NPL], unsigned (&mw)[NPL]) {
   float4 xc[K];
 #pragma unroll
-  for (int k = 0; k < RA; ++k) xc[k] = lds_x<false>(xsb, addr[0][k]);
+  for (int k = 0; k < RA; ++k) xc[k] = lds_x<FAR>(xsb, addr[0][k]);
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
 #pragma unroll
-    for (int k = RA; k < K; ++k) xc[k] = lds_x<false>(xsb, addr[j][k]);
+    for (int k = RA; k < K; ++k) xc[k] = lds_x<FAR>(xsb, addr[j][k]);
     float4 xn[RA];
     if (j + 1 < NPL) {
 #pragma unroll
-      for (int k = 0; k < RA; ++k) xn[k] = lds_x<false>(xsb, addr[j + 1][k]);
+      for (int k = 0; k < RA; ++k) xn[k] = lds_x<FAR>(xsb, addr[j + 1][k]);
     }
     __builtin_amdgcn_sched_barrier(0);
     float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
@@ -105,14 +105,17 @@ __device__ __forceinline__ void bwd_w_tile(const char* xsb, int t, const float4 
   }
 }
 
-// The token tile is staged by global_load_lds into one buffer (load, wait, read): with the dW
-// accumulators live, a second buffer's loop does not fit the 256 VGPRs a wave has at 2 waves per
-// SIMD.
-template <int K, int NPL, int WAVES, int ACT, int RA>
+// Token tiles reach LDS by LDS-DMA (dma_tile).  DBUF (D <= XTILE_DB): two buffers, tile t + 1
+// lands while tile t is read; one tile body reads buffer (t & 1) through a run-time base, so the
+// loop holds one copy of the gather code (two inlined copies, one per buffer, do not fit the 256
+// VGPRs a wave has at 2 waves per SIMD with the dW accumulators live).  Otherwise one buffer:
+// load, wait, read.  The wave index goes through readfirstlane so the chunk's parameters and the
+// c1 row are addressed with scalar registers.
+template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF>
 __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
-  __shared__ float4 xs[XTILE_SB];
+  __shared__ float4 xs[DBUF ? 2 * XTILE_DB : XTILE_SB];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   long long chunk = (long long)blockIdx.x * WAVES + wave;
   const bool active = chunk < p.n_chunks;
   if (!active) chunk = p.n_chunks - 1;  // idle waves of the last block recompute a real chunk, store nothing
@@ -149,6 +152,11 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   const float* c1row = p.c1t + g * p.cap;
   constexpr int NT = WAVES * 64;
 
+  if constexpr (DBUF) {
+    dma_tile(p.xt, xs, p.D, NT);
+    stage_wait();
+    __syncthreads();
+  }
   // 8 token tiles (32 tokens) per mask word; the word is stored after the inner loop
   for (int t0 = 0; t0 < p.n_tiles; t0 += 8) {
     unsigned mw[NPL];
@@ -156,12 +164,23 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
     for (int j = 0; j < NPL; ++j) mw[j] = 0u;
     const int t1 = t0 + 8 < p.n_tiles ? t0 + 8 : p.n_tiles;
     for (int t = t0; t < t1; ++t) {
-      __syncthreads();  // every wave is done with tile t - 1
-      stage_tile(p.xt + (long long)t * p.D, xs, p.D, NT);
-      const float4 c1 = *reinterpret_cast<const float4*>(c1row + t * BT);
-      stage_wait();
-      __syncthreads();
-      bwd_w_tile<K, NPL, ACT, RA>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw, dbv, mw);
+      if constexpr (DBUF) {
+        // buffer cur ^ 1 was last read in tile t - 1, which every wave finished before the barrier
+        const int cur = t & 1;
+        if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xs + (cur ^ 1) * XTILE_DB, p.D, NT);
+        const float4 c1 = ld_uniform4(c1row, t * BT);
+        bwd_w_tile<K, NPL, ACT, RA, true>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t, c1,
+                                          addr, w, bias, dw, dbv, mw);
+        stage_wait();  // tile t + 1 is in LDS for this wave's copies; the barrier publishes every wave's
+        __syncthreads();
+      } else {
+        __syncthreads();  // every wave is done with tile t - 1
+        dma_tile(p.xt + (long long)t * p.D, xs, p.D, NT);
+        const float4 c1 = ld_uniform4(c1row, t * BT);
+        stage_wait();
+        __syncthreads();
+        bwd_w_tile<K, NPL, ACT, RA, false>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw, dbv, mw);
+      }
     }
     const int word = t0 >> 3;
     uint32_t* mslab = p.mask + ((long long)(word / p.mw2) * p.NS + g * p.S) * p.mw2 + word % p.mw2;
@@ -545,7 +564,7 @@ void edge_layout(int D, int G, int S, int K, EdgeHeader* h, size_t* total) {
 
 template <int K, int NPL, int WAVES, int ACT, int RA>
 static int launch_bwd_w(const BwK& k, hipStream_t s) {
-  auto fn = bwd_w_kernel<K, NPL, WAVES, ACT, RA>;
+  auto fn = k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true> : bwd_w_kernel<K, NPL, WAVES, ACT, RA, false>;
   GL_LAUNCH(GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)), dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;

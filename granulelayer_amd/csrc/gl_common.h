@@ -116,6 +116,26 @@ __device__ __forceinline__ void stage_tile(const float4* __restrict__ src, float
     __builtin_amdgcn_global_load_lds((const void*)(src + i),
                                      (__attribute__((address_space(3))) void*)(dst + (i - lane)), 16, 0, 0);
 }
+// The same copy issued from inline asm: the compiler does not see these loads, so it inserts no
+// vmcnt wait for them before LDS reads of the tile buffers (the builtin makes it wait before every
+// read of the same LDS object, including the buffer the wave is reading while the other one
+// fills).  The caller waits with stage_wait() and a barrier before reading the tile.
+__device__ __forceinline__ void dma_tile(const float4* __restrict__ src, float4* dst, int D, int nthreads) {
+  const int lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < D; i += nthreads) {
+    const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(dst + (i - lane)));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(src + i), "s"(base) : "memory", "m0");
+  }
+}
+// Four consecutive floats at a wave-uniform address, read through the constant address space so
+// the load stays scalar (s_load) even after barriers and LDS-DMA, where a generic load of the
+// same address becomes a vector load the vmcnt waits then include.
+__device__ __forceinline__ float4 ld_uniform4(const float* row, int i) {
+  typedef const __attribute__((address_space(4))) float CF;
+  const CF* q = (const CF*)(row + i);
+  return make_float4(q[0], q[1], q[2], q[3]);
+}
 // X slot at byte offset a of a tile buffer.  FAR: the buffer's base does not fit the 16-bit
 // ds_read offset, so base + a costs one v_add per read; the offset then passes through an empty
 // asm so the compiler keeps doing that add at the read instead of hoisting a second copy of every
