@@ -110,22 +110,29 @@ __device__ __forceinline__ int opaque(int v) {
 constexpr int XTILE_DB = 4096;
 constexpr int XTILE_SB = 10112;
 
-__device__ __forceinline__ void stage_tile(const float4* __restrict__ src, float4* dst, int D, int nthreads) {
-  const int lane = threadIdx.x & 63;
-  for (int i = threadIdx.x; i < D; i += nthreads)
-    __builtin_amdgcn_global_load_lds((const void*)(src + i),
-                                     (__attribute__((address_space(3))) void*)(dst + (i - lane)), 16, 0, 0);
-}
-// The same copy issued from inline asm: the compiler does not see these loads, so it inserts no
-// vmcnt wait for them before LDS reads of the tile buffers (the builtin makes it wait before every
-// read of the same LDS object, including the buffer the wave is reading while the other one
-// fills).  The caller waits with stage_wait() and a barrier before reading the tile.
+// The copy is issued from inline asm: the compiler does not see these loads, so it inserts no
+// vmcnt wait for them before LDS reads of the tile buffers, and its LDS-read waits stay graded
+// (lgkmcnt(n) for the reads a use needs; the builtin global_load_lds makes it wait for every
+// outstanding LDS read, and for the copy itself before any read of the same LDS object).  The
+// caller waits with stage_wait() and a barrier before reading the tile.
 __device__ __forceinline__ void dma_tile(const float4* __restrict__ src, float4* dst, int D, int nthreads) {
-  const int lane = threadIdx.x & 63;
-  for (int i = threadIdx.x; i < D; i += nthreads) {
-    const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(dst + (i - lane)));
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-                 :: "v"(src + i), "s"(base) : "memory", "m0");
+  // Pass r copies slots [r * nthreads, (r + 1) * nthreads): the pass base is wave-uniform and
+  // goes into the scalar address and M0; the lane part is the one VGPR threadIdx.x * 16.
+  const unsigned tid = threadIdx.x;
+  const unsigned wave0 = __builtin_amdgcn_readfirstlane(tid & ~63u);  // thread index of the wave's lane 0
+  // readfirstlane is 32-bit: the 64-bit address goes through it as two halves
+  const unsigned long long sa = (unsigned long long)(size_t)src;
+  const unsigned s_lo = __builtin_amdgcn_readfirstlane((unsigned)sa);
+  const unsigned s_hi = __builtin_amdgcn_readfirstlane((unsigned)(sa >> 32));
+  const char* s0 = (const char*)(size_t)((unsigned long long)s_hi << 32 | s_lo);
+  const unsigned d0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)dst);
+  for (int b = 0; b < D; b += nthreads) {
+    if (b + (int)tid < D) {
+      const char* sb = s0 + (size_t)b * 16;
+      const unsigned m0v = d0 + (unsigned)(b + (int)wave0) * 16u;
+      asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
+                   :: "v"(tid * 16u), "s"(m0v), "s"(sb) : "memory", "m0");
+    }
   }
 }
 // Four consecutive floats at a wave-uniform address, read through the constant address space so

@@ -113,7 +113,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   __shared__ float4 xa[DBUF ? XTILE_DB : XTILE_SB];
   __shared__ float4 xb[DBUF ? XTILE_DB : 1];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar chunk addressing
   long long chunk = (long long)blockIdx.x * WAVES + wave;
   const bool active = chunk < p.n_chunks;
   if (!active) chunk = p.n_chunks - 1;  // idle waves of the last block recompute a real chunk, store nothing
@@ -143,30 +143,32 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
     bias[j] = valid ? bl : 0.f;
   }
 
-  // Token tiles are staged into LDS by global_load_lds (stage_tile).  DBUF: tile t + 1 is loaded
-  // into the other buffer while tile t is read, one barrier per tile; tiles alternate xa (even t)
-  // and xb (odd t), each buffer read through its own array.  Otherwise: load, wait, read.
+  // Token tiles reach LDS by LDS-DMA (dma_tile).  DBUF: tile t + 1 is loaded into the other
+  // buffer while tile t is read, one barrier per tile; tiles alternate xa (even t) and xb (odd t),
+  // each buffer read through its own array.  Otherwise: load, wait, read.  The copies are issued
+  // from inline asm: a copy the compiler sees in flight during the gather makes it wait for all
+  // LDS reads (lgkmcnt(0)) before each use instead of only the ones the use needs.
   constexpr int NT = WAVES * 64;
   float* out = p.part + chunk * p.b_pad;
   const bool store = active && lane == 0;
   if constexpr (DBUF) {
-    stage_tile(p.xt, xa, p.D, NT);
+    dma_tile(p.xt, xa, p.D, NT);
     for (int t = 0; t < p.n_tiles; t += 2) {
       stage_wait();
       __syncthreads();  // tile t is in xa; every wave is done with xb (tile t - 1)
-      if (t + 1 < p.n_tiles) stage_tile(p.xt + (long long)(t + 1) * p.D, xb, p.D, NT);
+      if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xb, p.D, NT);
       fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store);
       if (t + 1 < p.n_tiles) {
         stage_wait();
         __syncthreads();  // tile t + 1 is in xb; every wave is done with xa
-        if (t + 2 < p.n_tiles) stage_tile(p.xt + (long long)(t + 2) * p.D, xa, p.D, NT);
+        if (t + 2 < p.n_tiles) dma_tile(p.xt + (long long)(t + 2) * p.D, xa, p.D, NT);
         fwd_tile<K, NPL, ACT, true>(reinterpret_cast<const char*>(xb), addr, w, bias, out + (t + 1) * BT, store);
       }
     }
   } else {
     for (int t = 0; t < p.n_tiles; ++t) {
       __syncthreads();  // every wave is done with tile t - 1
-      stage_tile(p.xt + (long long)t * p.D, xa, p.D, NT);
+      dma_tile(p.xt + (long long)t * p.D, xa, p.D, NT);
       stage_wait();
       __syncthreads();
       fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store);
