@@ -155,21 +155,35 @@ __device__ __forceinline__ float4 lds_x(const char* buf, unsigned a) {
 // this wave's tile loads have reached LDS (vmcnt(0)); a barrier then publishes every wave's
 __device__ __forceinline__ void stage_wait() { __builtin_amdgcn_s_waitcnt(0x3f70); }
 
-// DPP move (row/quad patterns) as a float
+// DPP move (row/quad patterns) as a float; the source lane is always valid for the patterns used
+// here, so the move folds into the consuming v_add_f32 as a DPP operand
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
-// Sum over the 64 lanes of a wave; every lane receives the total.  Fixed reduction tree.
-__device__ __forceinline__ float wave_sum(float v) {
-  v += dpp<0xB1>(v);   // quad_perm(1,0,3,2)
-  v += dpp<0x4E>(v);   // quad_perm(2,3,0,1)
-  v += dpp<0x141>(v);  // row_half_mirror
-  v += dpp<0x140>(v);  // row_mirror
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+// Token of a tile whose total wave_sum4 leaves in lane l (l mod 4 = 0, 1, 2, 3 -> 0, 2, 1, 3).
+__device__ __forceinline__ int wave_sum4_token(int lane) { return ((lane & 1) << 1) | ((lane >> 1) & 1); }
+
+// Sums over the 64 lanes of a wave of four per-lane values (one per token of a tile), as a
+// reduce-scatter: two quad steps leave each lane one token's quad sum (lane ^ 1: even lanes keep
+// tokens 0, 1, odd lanes 2, 3; lane ^ 2: one of the two), two row rotations sum the 4 quads of a
+// row with the same token, and the two cross-row swaps of gfx950 (v_permlane16_swap rows 0<->1,
+// 2<->3, v_permlane32_swap rows 0,1<->2,3) add the rows.  Every lane ends with the total of token
+// wave_sum4_token(lane).  VALU only (no LDS round trips), fixed order: deterministic.
+__device__ __forceinline__ float wave_sum4(float a0, float a1, float a2, float a3, int lane) {
+  const bool odd = lane & 1, hi = lane & 2;
+  const float b0 = (odd ? a2 : a0) + dpp<0xB1>(odd ? a0 : a2);  // quad_perm(1,0,3,2)
+  const float b1 = (odd ? a3 : a1) + dpp<0xB1>(odd ? a1 : a3);
+  float c = (hi ? b1 : b0) + dpp<0x4E>(hi ? b0 : b1);  // quad_perm(2,3,0,1)
+  c += dpp<0x124>(c);  // row_ror:4
+  c += dpp<0x128>(c);  // row_ror:8
+  // each swap returns (first operand with its odd rows / rows 2,3 replaced, second operand with
+  // its even rows / rows 0,1 replaced); with both operands c their sum holds the row-pair sum
+  const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+  c = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+  return __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
 }
 
 }  // namespace gl

@@ -57,12 +57,12 @@ struct FwdK {
 };
 
 // One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
-// pooled over the wave's neurons and lanes.  The first RA LDS reads of neuron j + 1 are issued
-// before the arithmetic of neuron j, so up to K + RA reads are in flight per wave (the compiler's
-// own schedule keeps two).
+// pooled over the wave's neurons and lanes (wave_sum4; lanes 0-3 store the 4 token sums).  The
+// first RA LDS reads of neuron j + 1 are issued before the arithmetic of neuron j, so up to K + RA
+// reads are in flight per wave (the compiler's own schedule keeps two).
 template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8)>
 __device__ __forceinline__ void fwd_tile(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
-                                         const float (&bias)[NPL], float* out, bool store) {
+                                         const float (&bias)[NPL], float* out, bool store, int lane) {
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
   float4 xc[K];
 #pragma unroll
@@ -101,11 +101,8 @@ __device__ __forceinline__ void fwd_tile(const char* xsb, const unsigned (&addr)
       for (int k = 0; k < RA; ++k) xc[k] = xn[k];
     }
   }
-  a0 = wave_sum(a0);
-  a1 = wave_sum(a1);
-  a2 = wave_sum(a2);
-  a3 = wave_sum(a3);
-  if (store) *reinterpret_cast<float4*>(out) = make_float4(a0, a1, a2, a3);
+  const float tot = wave_sum4(a0, a1, a2, a3, lane);
+  if (store && lane < 4) out[wave_sum4_token(lane)] = tot;  // 4 lanes, 16 contiguous bytes
 }
 
 template <int K, int NPL, int WAVES, int ACT, bool DBUF>
@@ -150,19 +147,19 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   // LDS reads (lgkmcnt(0)) before each use instead of only the ones the use needs.
   constexpr int NT = WAVES * 64;
   float* out = p.part + chunk * p.b_pad;
-  const bool store = active && lane == 0;
+  const bool store = active;
   if constexpr (DBUF) {
     dma_tile(p.xt, xa, p.D, NT);
     for (int t = 0; t < p.n_tiles; t += 2) {
       stage_wait();
       __syncthreads();  // tile t is in xa; every wave is done with xb (tile t - 1)
       if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xb, p.D, NT);
-      fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store);
+      fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
       if (t + 1 < p.n_tiles) {
         stage_wait();
         __syncthreads();  // tile t + 1 is in xb; every wave is done with xa
         if (t + 2 < p.n_tiles) dma_tile(p.xt + (long long)(t + 2) * p.D, xa, p.D, NT);
-        fwd_tile<K, NPL, ACT, true>(reinterpret_cast<const char*>(xb), addr, w, bias, out + (t + 1) * BT, store);
+        fwd_tile<K, NPL, ACT, true>(reinterpret_cast<const char*>(xb), addr, w, bias, out + (t + 1) * BT, store, lane);
       }
     }
   } else {
@@ -171,7 +168,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       dma_tile(p.xt + (long long)t * p.D, xa, p.D, NT);
       stage_wait();
       __syncthreads();
-      fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store);
+      fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
     }
   }
 }
