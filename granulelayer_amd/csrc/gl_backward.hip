@@ -157,7 +157,10 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
     stage_wait();
     __syncthreads();
   }
-  // 8 token tiles (32 tokens) per mask word; the word is stored after the inner loop
+  // 8 token tiles (32 tokens) per mask word.  An even word is held in mwe until the odd word after
+  // it is done, and the pair is stored as one 8-byte write: each store writes a separate 32-byte
+  // memory sector, so pairs halve the mask's write traffic.
+  unsigned mwe[NPL];
   for (int t0 = 0; t0 < p.n_tiles; t0 += 8) {
     unsigned mw[NPL];
 #pragma unroll
@@ -183,11 +186,22 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
       }
     }
     const int word = t0 >> 3;
-    uint32_t* mslab = p.mask + ((long long)(word / p.mw2) * p.NS + g * p.S) * p.mw2 + word % p.mw2;
+    if ((word & 1) == 0 && t0 + 8 < p.n_tiles) {
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) mwe[j] = mw[j];
+      continue;
+    }
+    // odd word: (word - 1, word) in one row of one slab (mw2 is even); a last even word alone
+    const int w0 = word & ~1;
+    uint32_t* mslab = p.mask + ((long long)(w0 / p.mw2) * p.NS + g * p.S) * p.mw2 + w0 % p.mw2;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
       const int s = (int)((opaque((int)slot2[j / 2]) >> (16 * (j % 2))) & 0xffff);  // address math kept local
-      if (active && s < n_g) mslab[(long long)s * p.mw2] = mw[j];
+      if (!active || s >= n_g) continue;
+      if (word & 1)
+        *reinterpret_cast<uint2*>(mslab + (long long)s * p.mw2) = make_uint2(mwe[j], mw[j]);
+      else
+        mslab[(long long)s * p.mw2] = mw[j];
     }
   }
   // mask words of tokens past the chunk are never written: their c1 is zero, so dX ignores them
