@@ -260,15 +260,6 @@ struct DxChunk {
   int u;            // unit of the segment
 };
 
-// The segment table is read-only while the kernel runs: reading it through the constant address
-// space keeps these wave-uniform loads scalar.  As plain loads after the kernel's barriers they
-// become vector loads, and waiting for them (in-order) also waits for every gather in flight.
-template <typename V>
-__device__ __forceinline__ V ld_const(const V* p, long long i) {
-  typedef const __attribute__((address_space(4))) V CV;
-  return ((CV*)p)[i];
-}
-
 __device__ __forceinline__ void dx_next(const DxK& p, DxChunk& c, int hi) {
   if (c.e + 64 < c.end) {
     c.e += 64;
@@ -276,8 +267,8 @@ __device__ __forceinline__ void dx_next(const DxK& p, DxChunk& c, int hi) {
     c.si += 1;
     if (c.si < hi) {
       c.e = c.end;
-      c.end = ld_const(p.seg_begin, c.si + 1);
-      c.u = ld_const(p.seg_unit, c.si);
+      c.end = p.seg_begin[c.si + 1];
+      c.u = p.seg_unit[c.si];
     }
   }
 }
@@ -409,18 +400,18 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
   const int q = ql * 8 + xcd;
   const int u_lo = q * p.UQ;
   const int u_hi = min(u_lo + p.UQ, p.U);
-  int lo = (int)ld_const(p.seg_ptr, F), hi = (int)ld_const(p.seg_ptr, F + 1);
+  int lo = (int)p.seg_ptr[F], hi = (int)p.seg_ptr[F + 1];
   {
     int a = lo, b = hi;
     while (a < b) {
       int mid = (a + b) >> 1;
-      if (ld_const(p.seg_unit, mid) < u_lo) a = mid + 1; else b = mid;
+      if (p.seg_unit[mid] < u_lo) a = mid + 1; else b = mid;
     }
     lo = a;
     b = hi;
     while (a < b) {
       int mid = (a + b) >> 1;
-      if (ld_const(p.seg_unit, mid) < u_hi) a = mid + 1; else b = mid;
+      if (p.seg_unit[mid] < u_hi) a = mid + 1; else b = mid;
     }
     hi = a;
   }
@@ -440,7 +431,7 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
     st.nib[lane] = v;
   }
   if (lo < hi) {
-    DxChunk cc{lo, ld_const(p.seg_begin, lo), ld_const(p.seg_begin, lo + 1), ld_const(p.seg_unit, lo)};
+    DxChunk cc{lo, p.seg_begin[lo], p.seg_begin[lo + 1], p.seg_unit[lo]};
     DxGather<T> gc;
     dx_gather<K, T>(p, mask_tc, cc, dx_load_rec(p, cc, lane), gc);
     float c1[T];
