@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgranulelayer_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 GL_ACT = {"identity": 0, "relu": 1}
 GL_POOL = {"mean": 0, "sum": 1}
@@ -25,13 +25,13 @@ _P, _I32, _I64, _SZ, _F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctype
 class GlFwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
                 ("K", _I32), ("act", _I32), ("pool", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
-                ("sched", _P), ("pre", _P), ("ws", _P), ("ws_bytes", _SZ)]
+                ("sched", _P), ("win", _P), ("win_width", _I32), ("pre", _P), ("ws", _P), ("ws_bytes", _SZ)]
 
 
 class GlBwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
                 ("K", _I32), ("act", _I32), ("pool", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
-                ("sched", _P), ("g_pre", _P), ("dW", _P), ("db", _P), ("dX", _P), ("edges", _P), ("edges_bytes", _SZ),
+                ("sched", _P), ("win", _P), ("win_width", _I32), ("g_pre", _P), ("dW", _P), ("db", _P), ("dX", _P), ("edges", _P), ("edges_bytes", _SZ),
                 ("ws", _P), ("ws_bytes", _SZ)]
 
 
@@ -49,9 +49,10 @@ STRUCTS = (GlFwdArgs, GlBwdArgs, GlEdgeArgs, GlAdamArgs)  # gl_struct_layout ids
 # every symbol include/granulelayer_amd.h declares
 EXPORTS = ("gl_abi_version", "gl_struct_layout", "gl_error_string", "gl_fwd_workspace", "gl_fwd", "gl_edges_size",
            "gl_edges_build", "gl_bwd_workspace", "gl_bwd", "gl_adam", "gl_sched_size", "gl_sched_build_host",
-           "gl_trace_begin", "gl_trace_end")
+           "gl_window_build_host", "gl_trace_begin", "gl_trace_end")
 KERNEL_NAMES = {1: "tile_x_kernel", 2: "fwd_kernel", 3: "fwd_finalize_kernel", 4: "c1t_kernel", 5: "bwd_w_kernel",
-                6: "dx_kernel", 7: "dx_reduce_kernel", 8: "adam_kernel", 9: "edges_build"}
+                6: "dx_kernel", 7: "dx_reduce_kernel", 8: "adam_kernel", 9: "edges_build", 10: "fwd_kernel_win",
+                11: "bwd_w_kernel_win"}
 
 
 class NativeError(RuntimeError):
@@ -94,6 +95,8 @@ class Library:
         L.gl_sched_size.argtypes = [_I32, _I32, _I32, ctypes.POINTER(_SZ)]
         L.gl_sched_build_host.restype = ctypes.c_int
         L.gl_sched_build_host.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _P, _I32]
+        L.gl_window_build_host.restype = ctypes.c_int
+        L.gl_window_build_host.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(_I32)]
         self.check_abi()
 
     def check_abi(self):
@@ -140,6 +143,21 @@ class Library:
         out = np.empty(int(n.value) // 4, dtype=np.uint32)
         self.call("gl_sched_build_host", idx.ctypes.data, counts.ctypes.data, D, G, S, K, out.ctypes.data, threads)
         return out
+
+    def window_build(self, idx, counts, D: int, G: int, S: int, K: int):
+        """Per-pool input windows from host int32 arrays idx [G*S, K] and counts [G]: (lo uint32 [G],
+        widest window width)."""
+        import numpy as np
+
+        idx = np.ascontiguousarray(idx, dtype=np.int32)
+        counts = np.ascontiguousarray(counts, dtype=np.int32)
+        if idx.size != G * S * K or counts.size != G:
+            raise ValueError("idx must hold G*S*K and counts G entries")
+        lo = np.empty(G, dtype=np.uint32)
+        width = _I32(0)
+        self.call("gl_window_build_host", idx.ctypes.data, counts.ctypes.data, D, G, S, K, lo.ctypes.data,
+                  ctypes.byref(width))
+        return lo, int(width.value)
 
 
 class KernelTrace:

@@ -61,8 +61,10 @@ class HipBackend:
     _instance = None
     _lock = threading.Lock()
 
-    def __init__(self, lib: Optional[N.Library] = None):
+    def __init__(self, lib: Optional[N.Library] = None, window_staging: bool = True):
         self.lib = lib or N.library()
+        # stage only each pool's input window in LDS when the windows are narrow (same results)
+        self.window_staging = window_staging
 
     @classmethod
     def get(cls) -> "HipBackend":
@@ -114,9 +116,10 @@ class HipBackend:
         pre = torch.empty((B, G), device=x.device, dtype=torch.float32)
         if B == 0:
             return {"pre": pre}
+        win_lo, win_width = self.windows(rt)
         a = N.GlFwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=L.input_dim, G=G, S=S, K=K, act=act, pool=pool,
                         idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
-                        sched=_ptr(self.schedule(rt)), pre=_ptr(pre))
+                        sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, pre=_ptr(pre))
         with torch.cuda.device(x.device):
             need = self.lib.size_query("gl_fwd_workspace", a)
             ws = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)
@@ -141,6 +144,24 @@ class HipBackend:
         sched = torch.from_numpy(host.view(np.int32)).to(rt.idx.device)
         rt._hip_sched = (key, sched)
         return sched
+
+    # ------------------------------------------------------------------ pool windows
+    def windows(self, rt):
+        """Per-pool input windows of rt's index tensor (first input per pool on the device, widest
+        width), built on the host once per index tensor and cached on rt; (None, 0) when
+        ``window_staging`` is off.  The library stages only the windows when they are narrow."""
+        if not self.window_staging:
+            return None, 0
+        L, G, S, K = self._layer(rt)
+        key = (rt.idx.data_ptr(), rt.idx._version)
+        cached = getattr(rt, "_hip_win", None)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        lo, width = self.lib.window_build(rt.idx.reshape(-1, K).cpu().numpy(), rt.counts_i32.cpu().numpy(),
+                                          L.input_dim, G, S, K)
+        out = (torch.from_numpy(lo.view(np.int32)).to(rt.idx.device), width)
+        rt._hip_win = (key, out)
+        return out
 
     # ------------------------------------------------------------------ edges
     def edges(self, rt) -> torch.Tensor:
@@ -180,10 +201,11 @@ class HipBackend:
         dx = torch.empty((B, D), device=x.device, dtype=torch.float32)
         if B == 0:
             return dx
+        win_lo, win_width = self.windows(rt)
         edges = self.edges(rt)
         a = N.GlBwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=D, G=G, S=S, K=K, act=act, pool=pool,
                         idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
-                        sched=_ptr(self.schedule(rt)), g_pre=_ptr(g_pre),
+                        sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, g_pre=_ptr(g_pre),
                         dW=_ptr(dw_buf), db=_ptr(db_buf), dX=_ptr(dx), edges=_ptr(edges),
                         edges_bytes=edges.numel())
         with torch.cuda.device(x.device):

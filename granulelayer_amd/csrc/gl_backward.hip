@@ -51,8 +51,10 @@ struct BwK {
   float* db;
   uint32_t* mask;  // [n_tc][G*S][mw2] activation-mask words (one slab per dX token slice)
   const uint32_t* sched;  // gather schedule or null
+  const uint32_t* win;    // per-pool window starts (window staging) or null
   long long n_chunks, NS;
   int D, S, cpg, n_tiles, cap, mw2, nwin;
+  int G, ww, npw;         // window staging: pools, padded window width, pools per workgroup
 };
 
 // One token tile of the dW pass (LDS at xsb): recompute z, form dz = c1 * act'(z), accumulate
@@ -111,9 +113,9 @@ __device__ __forceinline__ void bwd_w_tile(const char* xsb, int t, const float4 
 // VGPRs a wave has at 2 waves per SIMD with the dW accumulators live).  Otherwise one buffer:
 // load, wait, read.  The wave index goes through readfirstlane so the chunk's parameters and the
 // c1 row are addressed with scalar registers.
-template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF>
+template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF, bool WS = false>
 __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
-  __shared__ float4 xs[DBUF ? 2 * XTILE_DB : XTILE_SB];
+  __shared__ float4 xs[DBUF || WS ? 2 * XTILE_DB : XTILE_SB];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   long long chunk = (long long)blockIdx.x * WAVES + wave;
@@ -127,6 +129,10 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   float w[NPL][K], dw[NPL][K];
   float bias[NPL], dbv[NPL];
   unsigned slot2[(NPL + 1) / 2];  // slots of neurons 2i, 2i+1 within the pool (16 bits each; >= n_g: padding)
+  // window staging: this wave's pool is slot pk of the workgroup's staged pools, window start lo
+  const int g_first = (int)((long long)blockIdx.x * WAVES / p.cpg);
+  const int pk = WS ? (int)(g - g_first) : 0;
+  const int lo = WS ? (int)__builtin_amdgcn_readfirstlane(p.win[g]) : 0;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     uint32_t order;
@@ -140,7 +146,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
       const int k = sched_k<K>(order, ks);
       int d = p.idx[n * K + k];
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-      addr[j][ks] = (unsigned)d * 16u;
+      addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * 16u;
       const float wl = p.W[n * K + k];
       w[j][ks] = valid ? wl : 0.f;
       dw[j][ks] = 0.f;
@@ -152,7 +158,15 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   const float* c1row = p.c1t + g * p.cap;
   constexpr int NT = WAVES * 64;
 
-  if constexpr (DBUF) {
+  // window staging: WS_TILES tiles per stage and barrier; tile t at slot (t mod 2 WS_TILES) * nsl
+  const WinLayout L{p.win, p.ww, p.npw, g_first, p.G};
+  const int nsl = p.npw * p.ww;
+  const unsigned tstep = (unsigned)nsl * 16u;
+  if constexpr (WS) {
+    dma_window_stage(p.xt, xs, 0, p.n_tiles, p.D, L, WAVES);
+    stage_wait();
+    __syncthreads();
+  } else if constexpr (DBUF) {
     dma_tile(p.xt, xs, p.D, NT);
     stage_wait();
     __syncthreads();
@@ -166,7 +180,29 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
 #pragma unroll
     for (int j = 0; j < NPL; ++j) mw[j] = 0u;
     const int t1 = t0 + 8 < p.n_tiles ? t0 + 8 : p.n_tiles;
-    for (int t = t0; t < t1; ++t) {
+    if constexpr (WS) {
+      for (int ts0 = t0; ts0 < t1; ts0 += WS_TILES) {
+        const int r = (ts0 / WS_TILES) & 1;
+        // region r ^ 1 was last read in the previous stage, which every wave finished before the barrier
+        if (ts0 + WS_TILES < p.n_tiles)
+          dma_window_stage(p.xt, xs + (r ^ 1) * WS_TILES * nsl, ts0 + WS_TILES, p.n_tiles, p.D, L, WAVES);
+        const int tn = p.n_tiles - ts0 < WS_TILES ? p.n_tiles - ts0 : WS_TILES;
+        for (int tt = 0; tt < tn; ++tt) {
+          const int t = ts0 + tt;
+          const float4 c1 = ld_uniform4(c1row, t * BT);
+          bwd_w_tile<K, NPL, ACT, RA, false>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw, dbv, mw);
+          // next tile's slot; after the last tile of region 1 back to region 0 (uniform step, no branch)
+          const unsigned step = (t & (2 * WS_TILES - 1)) == 2 * WS_TILES - 1 ? tstep - 2u * WS_TILES * tstep : tstep;
+#pragma unroll
+          for (int j = 0; j < NPL; ++j)
+#pragma unroll
+            for (int k = 0; k < K; ++k) addr[j][k] += step;
+        }
+        stage_wait();
+        __syncthreads();
+      }
+    }
+    for (int t = t0; t < t1 && !WS; ++t) {
       if constexpr (DBUF) {
         // buffer cur ^ 1 was last read in tile t - 1, which every wave finished before the barrier
         const int cur = t & 1;
@@ -569,8 +605,10 @@ void edge_layout(int D, int G, int S, int K, EdgeHeader* h, size_t* total) {
 
 template <int K, int NPL, int WAVES, int ACT, int RA>
 static int launch_bwd_w(const BwK& k, hipStream_t s) {
-  auto fn = k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true> : bwd_w_kernel<K, NPL, WAVES, ACT, RA, false>;
-  GL_LAUNCH(GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)), dim3(WAVES * 64), 0, s, k);
+  auto fn = k.win ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, true>
+                  : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true> : bwd_w_kernel<K, NPL, WAVES, ACT, RA, false>);
+  GL_LAUNCH(k.win ? GL_KERNEL_BWD_W_WIN : GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)),
+            dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;
 }
@@ -645,8 +683,9 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
                        a->g_pre, a->counts, c1t, a->G, b0, Bc, cap, a->pool);
     GL_CHECK_LAUNCH();
     const long long NS = (long long)a->G * a->S;
-    BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, a->sched, q.n_chunks, NS,
-           a->D, a->S, q.cpg, n_tiles, cap, 2 * T, ceil_div(a->S, SCHED_WIN)};
+    BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, a->sched, nullptr, q.n_chunks, NS,
+           a->D, a->S, q.cpg, n_tiles, cap, 2 * T, ceil_div(a->S, SCHED_WIN), a->G, 0, 0};
+    if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &bk.ww, &bk.npw)) bk.win = a->win;
     GL_TRY(launch_bwd_w_any(a->K, a->act, bk, s));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
            (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, a->W, part,

@@ -115,16 +115,21 @@ constexpr int XTILE_SB = 10112;
 // (lgkmcnt(n) for the reads a use needs; the builtin global_load_lds makes it wait for every
 // outstanding LDS read, and for the copy itself before any read of the same LDS object).  The
 // caller waits with stage_wait() and a barrier before reading the tile.
+// A wave-uniform global address in scalar registers.  readfirstlane is 32-bit and returns int:
+// the halves go through it separately and are widened as unsigned (a sign-extended low half would
+// set every bit of the high half whenever bit 31 of the address is set).
+__device__ __forceinline__ const char* uniform_ptr(const void* p) {
+  const unsigned long long a = (unsigned long long)(size_t)p;
+  const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((unsigned)a);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+  return (const char*)(size_t)((unsigned long long)hi << 32 | (unsigned long long)lo);
+}
 __device__ __forceinline__ void dma_tile(const float4* __restrict__ src, float4* dst, int D, int nthreads) {
   // Pass r copies slots [r * nthreads, (r + 1) * nthreads): the pass base is wave-uniform and
   // goes into the scalar address and M0; the lane part is the one VGPR threadIdx.x * 16.
   const unsigned tid = threadIdx.x;
   const unsigned wave0 = __builtin_amdgcn_readfirstlane(tid & ~63u);  // thread index of the wave's lane 0
-  // readfirstlane is 32-bit: the 64-bit address goes through it as two halves
-  const unsigned long long sa = (unsigned long long)(size_t)src;
-  const unsigned s_lo = __builtin_amdgcn_readfirstlane((unsigned)sa);
-  const unsigned s_hi = __builtin_amdgcn_readfirstlane((unsigned)(sa >> 32));
-  const char* s0 = (const char*)(size_t)((unsigned long long)s_hi << 32 | s_lo);
+  const char* s0 = uniform_ptr(src);
   const unsigned d0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)dst);
   for (int b = 0; b < D; b += nthreads) {
     if (b + (int)tid < D) {
@@ -135,6 +140,53 @@ __device__ __forceinline__ void dma_tile(const float4* __restrict__ src, float4*
     }
   }
 }
+// ---- pool-window staging -----------------------------------------------------------------------
+// When the pools of every workgroup draw their inputs from narrow windows (gl_window_build_host),
+// the forward and dW kernels stage only those windows: a stage is WS_TILES token tiles, each
+// [pool k of the workgroup][window slot i] with nsl = npw * ww slots of 16 bytes (npw pools per
+// workgroup, ww the widest window rounded up to 64), slot (k, i) = X[tile][lo_k + i].  Two stage
+// regions of WS_TILES * nsl slots alternate; tile t sits at slot (t mod 2 WS_TILES) * nsl, so the
+// kernels step their LDS addresses by nsl * 16 bytes per tile.  nsl <= WS_SLOTS keeps a region in
+// 64 KiB; one barrier serves WS_TILES tiles.
+constexpr int WS_TILES = 4;
+constexpr int WS_SLOTS = XTILE_DB / WS_TILES;
+
+struct WinLayout {
+  const uint32_t* win;  // [G] first input of each pool's window
+  int ww, npw, g_first, G;
+};
+
+// region <- the WS_TILES tiles from t0 (tiles past n_tiles repeat the last one: in bounds, unread).
+// A stage is WS_TILES * npw runs (one tile's window of one pool, ww slots); wave w copies runs
+// w, w + waves, ...  (taking its own runs directly: walking every 64-slot group of the stage in
+// each wave cost ~25% of the kernel in scalar instructions)
+__device__ __forceinline__ void dma_window_stage(const float4* __restrict__ xt, float4* region, int t0, int n_tiles,
+                                                 int D, const WinLayout& L, int waves) {
+  const unsigned lane = threadIdx.x & 63u;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const char* xb = uniform_ptr(xt);
+  const unsigned r0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)region);
+  for (int run = wave; run < WS_TILES * L.npw; run += waves) {
+    const int tt = run / L.npw, k = run - tt * L.npw;
+    const int t = t0 + tt < n_tiles ? t0 + tt : n_tiles - 1;
+    const int g = L.g_first + k < L.G ? L.g_first + k : L.G - 1;
+    const int lo = (int)__builtin_amdgcn_readfirstlane(L.win[g]);
+    const char* sb = xb + (size_t)t * D * 16;
+    for (int i0 = 0; i0 < L.ww; i0 += 64) {
+      const int col = lo + i0 + (int)lane < D - 1 ? lo + i0 + (int)lane : D - 1;
+      const unsigned m0v = r0 + (unsigned)(run * L.ww + i0) * 16u;
+      asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
+                   :: "v"((unsigned)col * 16u), "s"(m0v), "s"(sb) : "memory", "m0");
+    }
+  }
+}
+// LDS byte address of input d of a neuron in pool slot k of the workgroup whose window starts at lo
+__device__ __forceinline__ unsigned win_addr(int d, int k, int lo, int ww) {
+  int i = d - lo;
+  i = i < 0 ? 0 : (i >= ww ? ww - 1 : i);  // the host validated the widths; clamp keeps LDS reads in bounds
+  return (unsigned)(k * ww + i) * 16u;
+}
+
 // Four consecutive floats at a wave-uniform address, read through the constant address space so
 // the load stays scalar (s_load) even after barriers and LDS-DMA, where a generic load of the
 // same address becomes a vector load the vmcnt waits then include.

@@ -52,8 +52,10 @@ struct FwdK {
   const int32_t* counts;
   float* part;            // [n_chunks][b_pad]
   const uint32_t* sched;  // gather schedule or null
+  const uint32_t* win;    // per-pool window starts (window staging) or null
   long long n_chunks;
   int D, S, cpg, n_tiles, b_pad, nwin;
+  int G, ww, npw;         // window staging: pools, padded window width, pools per workgroup
 };
 
 // One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
@@ -105,9 +107,10 @@ __device__ __forceinline__ void fwd_tile(const char* xsb, const unsigned (&addr)
   if (store && lane < 4) out[wave_sum4_token(lane)] = tot;  // 4 lanes, 16 contiguous bytes
 }
 
-template <int K, int NPL, int WAVES, int ACT, bool DBUF>
+template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false>
 __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
-  __shared__ float4 xa[DBUF ? XTILE_DB : XTILE_SB];
+  // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots)
+  __shared__ float4 xa[WS ? 2 * XTILE_DB : (DBUF ? XTILE_DB : XTILE_SB)];
   __shared__ float4 xb[DBUF ? XTILE_DB : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar chunk addressing
@@ -121,6 +124,10 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   unsigned addr[NPL][K];
   float w[NPL][K];
   float bias[NPL];
+  // window staging: this wave's pool is slot pk of the workgroup's staged pools, window start lo
+  const int g_first = (int)((long long)blockIdx.x * WAVES / p.cpg);
+  const int pk = WS ? (int)(g - g_first) : 0;
+  const int lo = WS ? (int)__builtin_amdgcn_readfirstlane(p.win[g]) : 0;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     uint32_t order;
@@ -132,7 +139,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       const int k = sched_k<K>(order, ks);  // the pooled sum does not depend on the visiting order
       int d = p.idx[n * K + k];
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-      addr[j][ks] = (unsigned)d * 16u;
+      addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * 16u;
       const float wl = p.W[n * K + k];
       w[j][ks] = valid ? wl : 0.f;
     }
@@ -148,7 +155,33 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   constexpr int NT = WAVES * 64;
   float* out = p.part + chunk * p.b_pad;
   const bool store = active;
-  if constexpr (DBUF) {
+  if constexpr (WS) {
+    // window staging: WS_TILES tiles per stage and barrier; tile t at slot (t mod 2 WS_TILES) * nsl
+    const WinLayout L{p.win, p.ww, p.npw, g_first, p.G};
+    const int nsl = p.npw * p.ww;
+    const unsigned tstep = (unsigned)nsl * 16u;
+    dma_window_stage(p.xt, xa, 0, p.n_tiles, p.D, L, WAVES);
+    stage_wait();
+    __syncthreads();
+    for (int t0 = 0; t0 < p.n_tiles; t0 += WS_TILES) {
+      const int r = (t0 / WS_TILES) & 1;
+      // region r ^ 1 was last read in the previous stage, which every wave finished before the barrier
+      if (t0 + WS_TILES < p.n_tiles) dma_window_stage(p.xt, xa + (r ^ 1) * WS_TILES * nsl, t0 + WS_TILES, p.n_tiles, p.D, L, WAVES);
+      const int tn = p.n_tiles - t0 < WS_TILES ? p.n_tiles - t0 : WS_TILES;
+      for (int tt = 0; tt < tn; ++tt) {
+        const int t = t0 + tt;
+        fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
+        // next tile's slot; after the last tile of region 1 back to region 0
+        const unsigned step = (t & (2 * WS_TILES - 1)) == 2 * WS_TILES - 1 ? tstep - 2u * WS_TILES * tstep : tstep;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j)
+#pragma unroll
+          for (int k = 0; k < K; ++k) addr[j][k] += step;
+      }
+      stage_wait();
+      __syncthreads();
+    }
+  } else if constexpr (DBUF) {
     dma_tile(p.xt, xa, p.D, NT);
     for (int t = 0; t < p.n_tiles; t += 2) {
       stage_wait();
@@ -222,25 +255,41 @@ static FwdPlan fwd_plan(const GlFwdArgs* a) {
   return q;
 }
 
-template <int K, int NPL, int WAVES, int ACT, bool DBUF>
+template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false>
 static int launch_fwd(const FwdK& k, hipStream_t s) {
-  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF>;
+  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS>;
   dim3 grid((unsigned)ceil_div(k.n_chunks, WAVES));
-  GL_LAUNCH(GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), 0, s, k);
+  GL_LAUNCH(WS ? GL_KERNEL_FWD_WIN : GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;
 }
 
-// one workgroup per CU (the tile buffers take the LDS); two tile buffers when D fits them
+// one workgroup per CU (the tile buffers take the LDS); pool windows when they fit, else two tile
+// buffers when D fits them, else one
 template <int ACT, int K>
 static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
   constexpr int W = fwd_waves(K);
+  if (k.win) return launch_fwd<K, FWD_NPL, W, ACT, false, true>(k, s);
   return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true>(k, s) : launch_fwd<K, FWD_NPL, W, ACT, false>(k, s);
 }
 
 template <int ACT>
 static int launch_fwd_act(int K, int D, const FwdK& k, hipStream_t s) {
   return K == 8 ? launch_fwd_buf<ACT, 8>(D, k, s) : launch_fwd_buf<ACT, 16>(D, k, s);
+}
+
+// Window staging applies when the staged windows of a workgroup's pools (npw of them, each ww
+// inputs) fit a stage tile (<= WS_SLOTS) and are narrower than the full input width.
+bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, int G, int* ww, int* npw) {
+  if (!win || width < 1) return false;
+  const int w = (int)round_up(width, 64);
+  // pools spanned by `waves` consecutive chunks (cpg chunks per pool)
+  int n = waves % cpg == 0 ? waves / cpg : (waves - 1) / cpg + 2;
+  if (n > G) n = G;
+  if ((long long)n * w > WS_SLOTS || (long long)n * w >= D) return false;
+  *ww = w;
+  *npw = n;
+  return true;
 }
 
 int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const float* W,
@@ -280,8 +329,9 @@ extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
   float* part = (float*)((char*)a->ws + q.xt_bytes);
   GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, 0, q.n_tiles, xt, s));
   if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;
-  FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, a->sched, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles, q.b_pad,
-         ceil_div(a->S, SCHED_WIN)};
+  FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, a->sched, nullptr, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles,
+         q.b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0};
+  if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) k.win = a->win;
   GL_TRY(a->act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU>(a->K, a->D, k, s)
                                 : launch_fwd_act<GL_ACT_IDENTITY>(a->K, a->D, k, s));
   dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(q.b_pad, 32));

@@ -13,6 +13,10 @@ int set_lds_limit(const void* kernel, size_t bytes);
 int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const float* W,
                 const float* bias, const int32_t* counts, int x_dtype);
 
+// Window staging for a kernel whose workgroups hold `waves` chunks of cpg per pool: true (with the
+// padded width *ww and pools per workgroup *npw) when the pools' windows fit a stage tile.
+bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, int G, int* ww, int* npw);
+
 // X rows [b0, b0 + n_tiles*BT) -> token tiles [n_tiles][D] float4 (zero past B).
 int launch_tile_x(const void* X, long long sxb, int x_dtype, int B, int D, int b0, int n_tiles, float4* xt,
                   hipStream_t s);

@@ -222,3 +222,29 @@ extern "C" int gl_sched_build_host(const int32_t* idx, const int32_t* counts, in
   for (auto& th : pool) th.join();
   return 0;
 }
+
+// Per-pool input windows (no reference counterpart; the per-pool analogue of the reference's
+// per-supergroup feature sets, sparse_pooling/supergroups.py:1-40): lo[g] = the smallest index
+// of pool g's valid neurons, *width = max over pools of (largest - smallest + 1).  With narrow
+// windows the forward and dW kernels stage only each pool's window of X in LDS.
+extern "C" int gl_window_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S,
+                                    int32_t K, uint32_t* lo, int32_t* width) {
+  if (!idx || !counts || !lo || !width || D < 1 || G < 1 || S < 1 || K < 1) return GL_ERR_ARG;
+  int32_t wmax = 0;
+  for (long long g = 0; g < G; ++g) {
+    const int n_g = counts[g] < S ? counts[g] : S;
+    int32_t mn = D, mx = -1;
+    const int32_t* r = idx + g * (long long)S * K;
+    for (long long e = 0; e < (long long)n_g * K; ++e) {
+      int32_t d = r[e];
+      d = d < 0 ? 0 : (d >= D ? D - 1 : d);
+      mn = d < mn ? d : mn;
+      mx = d > mx ? d : mx;
+    }
+    if (mx < 0) mn = mx = 0;
+    lo[g] = (uint32_t)mn;
+    wmax = mx - mn + 1 > wmax ? mx - mn + 1 : wmax;
+  }
+  *width = wmax;
+  return 0;
+}

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 2
+#define GL_ABI_VERSION 3
 
 enum {
   GL_OK = 0,
@@ -58,6 +58,8 @@ typedef struct GlFwdArgs {
   const float* bias;      /* [G*S] */
   const int32_t* counts;  /* [G] valid neurons per group, 1 <= counts[g] <= S */
   const uint32_t* sched;  /* gather schedule from gl_sched_build_host (K = 8), or NULL */
+  const uint32_t* win;    /* [G] first input of each pool's window (gl_window_build_host), or NULL */
+  int32_t win_width;      /* widest pool window; the kernels stage only the windows when narrow */
   float* pre;             /* out [B, G]: pooled value before the (identity) out-activation */
   void* ws;               /* workspace of gl_fwd_workspace() bytes */
   size_t ws_bytes;
@@ -77,6 +79,8 @@ typedef struct GlBwdArgs {
   const float* bias;
   const int32_t* counts;
   const uint32_t* sched;  /* gather schedule from gl_sched_build_host (K = 8), or NULL */
+  const uint32_t* win;    /* as GlFwdArgs.win / win_width */
+  int32_t win_width;
   const float* g_pre;     /* [B, G] dL/dpre (fp32) */
   float* dW;              /* [G*S, K] ACCUMULATED (+=), e.g. W.main_grad; padded slots untouched */
   float* db;              /* [G*S] ACCUMULATED (+=) */
@@ -151,10 +155,22 @@ int gl_sched_size(int32_t G, int32_t S, int32_t K, size_t* bytes);
 int gl_sched_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
                         uint32_t* sched, int32_t threads);
 
+/* Per-pool input windows, built on the HOST once per index tensor: lo[g] = the smallest input
+ * index of pool g's valid neurons, *width = the widest window (largest - smallest + 1) over all
+ * pools.  Pass lo as GlFwdArgs.win / GlBwdArgs.win and *width as win_width: when every workgroup's
+ * pools fit (pools per workgroup x width rounded up to 64 <= 1024 inputs, and fewer than D) the
+ * forward and dW kernels stage only those windows of X in LDS, 16 tokens per stage instead of 4.
+ * Results are unchanged (same arithmetic, same order).  No reference counterpart in Mode A
+ * (the reference stages per-supergroup feature sets in its Mode-B grouped kernels,
+ * sparse_pooling/supergroups.py:1-40, kernels/cuda/sparse_pool_sg.cuh). */
+int gl_window_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
+                         uint32_t* lo, int32_t* width);
+
 /* Kernel ids reported by the trace below. */
 enum {
   GL_KERNEL_TILE_X = 1, GL_KERNEL_FWD = 2, GL_KERNEL_FWD_FINALIZE = 3, GL_KERNEL_C1T = 4, GL_KERNEL_BWD_W = 5,
-  GL_KERNEL_DX = 6, GL_KERNEL_DX_REDUCE = 7, GL_KERNEL_ADAM = 8, GL_KERNEL_EDGES = 9
+  GL_KERNEL_DX = 6, GL_KERNEL_DX_REDUCE = 7, GL_KERNEL_ADAM = 8, GL_KERNEL_EDGES = 9,
+  GL_KERNEL_FWD_WIN = 10, GL_KERNEL_BWD_W_WIN = 11  /* forward / dW with pool-window staging */
 };
 
 /* Launch trace for benchmarks and tests (process-wide, not for concurrent callers): after

@@ -97,6 +97,64 @@ def test_backward_matches_oracle(case, pool, act):
     assert not dw.cpu().numpy().reshape(-1, K)[~valid].any()
 
 
+def make_window_case(D, H, G, K, B, width, seed=0):
+    """The C3 index structure: every pool draws its inputs from one contiguous window of `width`
+    inputs at a seeded offset (padded slots keep index 0)."""
+    from granulelayer_amd.layout import sample_distinct
+
+    L, idx, w, b, x, dy = make_case(D, H, G, K, B, seed=seed)
+    S = L.slots_per_group
+    gen = torch.Generator().manual_seed(seed + 7)
+    off = torch.randint(0, D - width + 1, (G,), generator=gen)
+    rec = sample_distinct(G * S, width, K, gen, "cpu").to(torch.int32) + off.repeat_interleave(S)[:, None].to(torch.int32)
+    rec[~L.valid_mask("cpu").reshape(-1)] = 0
+    return L, rec.view(L.index_shape).to(idx.dtype), w, b, x, dy
+
+
+# (D, H, G, K, B, window): pools of 1024 (4 per forward workgroup), of 300 (8 per workgroup), K = 16
+WIN_CASES = [(2048, 8192, 8, 8, 37, 256), (1536, 4800, 16, 8, 70, 120), (2048, 2048, 4, 16, 33, 200)]
+
+
+@pytest.mark.parametrize("case", WIN_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}w{c[5]}")
+def test_window_staging_matches_full_staging_and_oracle(case):
+    """Pool-window staging (gl_window_build_host) runs the window kernels and gives bit-identical
+    results to full-width staging, within the oracle's bar."""
+    from granulelayer_amd import _native as N
+
+    D, H, G, K, B, width = case
+    L, idx, w, b, x, dy = make_window_case(D, H, G, K, B, width)
+    be = HipBackend.get()
+    outs = {}
+    try:
+        for ws in (True, False):
+            be.window_staging = ws
+            rt = runtime(L, idx, "sum", "relu")
+            dw = torch.zeros(L.weight_shape, device=DEV)
+            db = torch.zeros(L.bias_shape, device=DEV)
+            with N.KernelTrace() as tr:
+                pre = rt.forward(x.to(DEV), w.to(DEV), b.to(DEV))["pre"]
+                dx = rt.backward(x.to(DEV), w.to(DEV), b.to(DEV), dy.to(DEV), {}, "minimal_stats", dw, db)
+            names = set(tr.times_ms())
+            want = {"fwd_kernel_win", "bwd_w_kernel_win"} if ws else {"fwd_kernel", "bwd_w_kernel"}
+            assert want <= names, f"window_staging={ws}: ran {sorted(names)}"
+            outs[ws] = [t.cpu() for t in (pre, dw, db, dx)]
+    finally:
+        be.window_staging = True
+    for name, a, c in zip(("pre", "dW", "db", "dX"), outs[True], outs[False]):
+        assert torch.equal(a, c), f"{name} differs between window and full staging"
+    pre, dw, db, dx = (t.numpy() for t in outs[True])
+    fi, fw, fb = flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    want, mag = O.forward(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, "relu", "sum", with_mag=True)
+    assert_parity(pre, want, mag, what="pre")
+    wdW, wdb, wdX, bnd = O.backward(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, dy.numpy(), "relu", "sum",
+                                    with_bounds=True)
+    (mW, mb, mX), (uW, ub, uX) = bnd["mag"], bnd["unc"]
+    assert_parity(dx, wdX, mX, uX, what="dX")
+    assert_parity(dw.reshape(-1, K), wdW, mW, uW, what="dW")
+    assert_parity(db.reshape(-1), wdb, mb, ub, what="db")
+
+
 def _read_edges(edges: torch.Tensor):
     raw = edges.cpu().numpy()
     h = np.frombuffer(raw[:48].tobytes(), dtype=np.int32)

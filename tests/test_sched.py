@@ -88,3 +88,23 @@ def test_schedule_refuses_fan_in_16_and_bad_arguments(lib):
         lib.sched_build(np.zeros((2 * 128, 16), np.int32), counts, 64, 2, 128, 16)
     with pytest.raises(ValueError):
         lib.sched_build(idx[:-1], counts, 64, 2, 128, 8)
+
+
+def test_window_build_matches_numpy(lib):
+    """gl_window_build_host: per-pool smallest input of the valid neurons and the widest window."""
+    rng = np.random.default_rng(6)
+    G, S, D, K = 7, 96, 700, 8
+    counts = np.array([96, 1, 50, 96, 17, 80, 3], np.int32)
+    idx = np.zeros((G * S, K), np.int32)
+    for g in range(G):
+        off = rng.integers(0, D - 120)
+        for s in range(counts[g]):
+            idx[g * S + s] = np.sort(off + rng.choice(120, K, replace=False))
+        # padded slots hold far-away inputs the windows must ignore
+        idx[g * S + counts[g]:(g + 1) * S] = D - 1 if g % 2 else 0
+    lo, width = lib.window_build(idx, counts, D, G, S, K)
+    want_lo = [idx[g * S:g * S + counts[g]].min() for g in range(G)]
+    want_w = max(idx[g * S:g * S + counts[g]].max() - want_lo[g] + 1 for g in range(G))
+    assert lo.tolist() == want_lo and width == want_w
+    with pytest.raises(_native.NativeError):
+        lib.window_build(idx, counts, 0, G, S, K)
