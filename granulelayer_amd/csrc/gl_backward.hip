@@ -278,11 +278,13 @@ struct DxK {
 // lanes first gather, one edge each, the chunk's records, weights and mask words with vector
 // loads (64 independent requests per instruction: random scalar loads would be limited by the
 // scalar cache's miss rate); the gathers of the next chunk are issued before the current chunk is
-// computed.  The chunk is staged in LDS; for edge i every lane reads the weight (a broadcast) and
-// the mask word holding its bits.  At T = 4 one v_bfe_u32 takes the lane's 4 bits, a 16-entry
-// LDS table turns them into a byte mask (0x00 / 0xff per token), and an SDWA v_and_b32 with the
-// sign-extended byte selects c1: two VALU per token and edge (select, FMA).  At T <= 2 each bit
-// is sign-extended to an all-ones / zero mask by v_bfe_i32 (three VALU per token and edge).
+// computed.  The chunk is staged in LDS as (mask word, weight) pairs, so for edge i every lane
+// reads the word holding its bits and the weight with one ds_read_b64.  One v_bfe_u32 takes the
+// lane's T bits, and a 2^T-entry LDS table turns them into T floats 0.0 / 1.0.
+//
+// A chunk belongs to one unit, so c1 is the same for all its edges: per run of edges into one
+// feature the lanes sum S[j] = sum [mask] * W (one FMA per token and edge) and then add
+// c1[j] * S[j] to the feature's accumulator (one FMA per token and run).
 template <int T>
 struct DxGather {
   unsigned rec;
@@ -351,72 +353,76 @@ __device__ __forceinline__ void dx_load_c1(const DxK& p, int u, int tok0, float 
   }
 }
 
-// LDS copy of one chunk: every edge's weight and its 2T mask words (token order; rows padded to
-// an odd number of words, so the 64 lanes' row writes hit 64 different banks); nib[v] expands
-// the 4-bit value v to a byte mask (byte i = 0xff when bit i is set)
+// LDS copy of one chunk: per edge its 2T (mask word, weight) pairs, rows padded by one pair to
+// 4T + 2 words (row e starts at bank 2 (2T + 1) e mod 64: the 32 lanes of each half of a 64-bit
+// row write hit 32 different bank pairs); lut[v][j] = 1.0f when bit j of v is set, else 0.0f
 template <int T>
-struct DxStage {
-  float w[64];
-  unsigned m[64][2 * T + 1];
-  unsigned nib[16];
+struct __align__(16) DxStage {
+  uint2 e[64][2 * T + 1];
+  float lut[1 << T][T];
 };
 
+// the lane's T mask bits of word mw as floats 0.0 / 1.0
 template <int T>
-__device__ __forceinline__ void dx_stage(DxStage<T>& st, const DxGather<T>& g, int lane) {
-  st.w[lane] = g.w;
-#pragma unroll
-  for (int i = 0; i < 2 * T; ++i) st.m[lane][i] = g.m[i];
+__device__ __forceinline__ void dx_bits(const DxStage<T>& st, unsigned mw, unsigned bit, float (&mf)[T]) {
+  const unsigned v = __builtin_amdgcn_ubfe(mw, bit, (unsigned)T);
+  if constexpr (T == 4) {
+    const float4 t = *reinterpret_cast<const float4*>(&st.lut[v][0]);
+    mf[0] = t.x, mf[1] = t.y, mf[2] = t.z, mf[3] = t.w;
+  } else if constexpr (T == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(&st.lut[v][0]);
+    mf[0] = t.x, mf[1] = t.y;
+  } else {
+    mf[0] = st.lut[v][0];
+  }
 }
 
-// Edges i in [i0, i1) of the chunk, all of feature F0 of the range: acc[F0][j] += [m_j] c1[j] w.
-template <int F0, int T>
-__device__ __forceinline__ void dx_run(const DxStage<T>& st, int i0, int i1, int lane, const float (&c1)[T],
-                                       float (&acc)[FW][T]) {
-  const int word = (T * lane) >> 5;
-  const unsigned bit = (unsigned)(T * lane) & 31u;
-  for (int i = i0; i < i1; ++i) {
-    const float w = st.w[i];  // an LDS broadcast
-    const unsigned mw = st.m[i][word];
-    if constexpr (T == 4) {
-      const unsigned bm = st.nib[__builtin_amdgcn_ubfe(mw, bit, 4u)];
+// Edges i in [i0, i1) of the chunk, all into feature X of the range:
+// acc[X][j] += c1[j] * sum_i [m_ij] w_i.
+template <int X, int T>
+__device__ __forceinline__ void dx_run(const DxStage<T>& st, int i0, int i1, int word, unsigned bit,
+                                       const float (&c1)[T], float (&acc)[FW][T]) {
+  if (i0 >= i1) return;
+  const uint2* e = &st.e[i0][word];
+  float s[T], mf[T];
+  uint2 mw = *e;
+  dx_bits<T>(st, mw.x, bit, mf);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int sel = (int)(signed char)(bm >> (8 * j));  // SDWA: sign-extended byte j
-        acc[F0][j] = __builtin_fmaf(__builtin_bit_cast(float, sel & __builtin_bit_cast(int, c1[j])), w, acc[F0][j]);
-      }
-    } else {
+  for (int j = 0; j < T; ++j) s[j] = mf[j] * __uint_as_float(mw.y);
+  for (int n = i1 - i0 - 1; n > 0; --n) {
+    e += 2 * T + 1;
+    mw = *e;
+    dx_bits<T>(st, mw.x, bit, mf);
 #pragma unroll
-      for (int j = 0; j < T; ++j) {
-        const int sel = __builtin_amdgcn_sbfe((int)mw, bit + j, 1u);
-        acc[F0][j] = __builtin_fmaf(__builtin_bit_cast(float, sel & __builtin_bit_cast(int, c1[j])), w, acc[F0][j]);
-      }
-    }
+    for (int j = 0; j < T; ++j) s[j] = __builtin_fmaf(mf[j], __uint_as_float(mw.y), s[j]);
   }
+#pragma unroll
+  for (int j = 0; j < T; ++j) acc[X][j] = __builtin_fmaf(c1[j], s[j], acc[X][j]);
+}
+
+template <int X, int T>
+__device__ __forceinline__ void dx_runs(const DxStage<T>& st, const int (&b)[FW + 1], int word, unsigned bit,
+                                        const float (&c1)[T], float (&acc)[FW][T]) {
+  dx_run<X, T>(st, b[X], b[X + 1], word, bit, c1, acc);
+  if constexpr (X + 1 < FW) dx_runs<X + 1, T>(st, b, word, bit, c1, acc);
 }
 
 // The chunk's edges are sorted by feature: ballots give every feature's edge range, and one loop
 // per feature (unrolled over the range) keeps every accumulator index a compile-time constant.
 template <int T>
-__device__ __forceinline__ void dx_compute(const DxGather<T>& g, DxStage<T>& st, int n, int lane,
-                                           const float (&c1)[T], float (&acc)[FW][T]) {
-  dx_stage<T>(st, g, lane);
+__device__ __forceinline__ void dx_compute(const DxGather<T>& g, DxStage<T>& st, int n, int lane, int word,
+                                           unsigned bit, const float (&c1)[T], float (&acc)[FW][T]) {
+  const unsigned wb = __float_as_uint(g.w);
+#pragma unroll
+  for (int i = 0; i < 2 * T; ++i) st.e[lane][i] = make_uint2(g.m[i], wb);
   __syncthreads();  // one wave per workgroup: orders the staging before the broadcast reads
   const int f = lane < n ? (int)((g.rec >> REC_F_SHIFT) & REC_F_MASK) : FW;
   int b[FW + 1];
   b[0] = 0;
 #pragma unroll
-  for (int x = 1; x <= FW; ++x) b[x] = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(f < x));
-#define GL_DX_RUN(X) dx_run<X, T>(st, b[X], b[X + 1], lane, c1, acc)
-  GL_DX_RUN(0);
-  GL_DX_RUN(1);
-  GL_DX_RUN(2);
-  GL_DX_RUN(3);
-  GL_DX_RUN(4);
-  GL_DX_RUN(5);
-  GL_DX_RUN(6);
-  GL_DX_RUN(7);
-#undef GL_DX_RUN
-  static_assert(FW == 8, "dx_compute unrolls eight features");
+  for (int x = 1; x <= FW; ++x)  // (readfirstlane keeps the bounds 32-bit: 64-bit compares are VALU)
+    b[x] = __builtin_amdgcn_readfirstlane((int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(f < x)));
+  dx_runs<0, T>(st, b, word, bit, c1, acc);
   __syncthreads();  // the next chunk's staging overwrites st
 }
 
@@ -458,13 +464,13 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
     for (int j = 0; j < T; ++j) acc[f][j] = 0.f;
 
   const int tok0 = tc * 64 * T + T * lane;
+  const int word = (T * lane) >> 5;
+  const unsigned bit = (unsigned)(T * lane) & 31u;
   const uint32_t* mask_tc = p.mask + (long long)tc * p.NS * (2 * T);
   __shared__ DxStage<T> st;
-  if (lane < 16) {
-    unsigned v = 0u;
+  if (lane < (1 << T)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v |= ((unsigned)lane >> i & 1u) ? 0xffu << (8 * i) : 0u;
-    st.nib[lane] = v;
+    for (int j = 0; j < T; ++j) st.lut[lane][j] = (lane >> j) & 1 ? 1.0f : 0.0f;
   }
   if (lo < hi) {
     DxChunk cc{lo, p.seg_begin[lo], p.seg_begin[lo + 1], p.seg_unit[lo]};
@@ -491,7 +497,7 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
         dx_next(p, cnn, hi);
         if (cnn.si < hi) rnn = dx_load_rec(p, cnn, lane);
       }
-      dx_compute<T>(gc, st, (int)min(cc.end - cc.e, 64u), lane, c1, acc);
+      dx_compute<T>(gc, st, (int)min(cc.end - cc.e, 64u), lane, word, bit, c1, acc);
       if (!more) break;
       cc = cn;
       gc = gn;
