@@ -129,7 +129,7 @@ class Level1Runtime:
         self.check_devices(x, w, b)
         self._require_backend()
         self.resolve_reduction(x.shape[0])
-        out = self.backend.forward(self, x, w, b, False)
+        out = self.backend.forward(self, x, w, b, track_ids)
         self.last_info["forward_backend"] = "hip"
         return out
 
@@ -174,9 +174,14 @@ def _grad_buffers(w, b):
 
 
 def _saved_stats(level: LevelSpec, out: Dict[str, torch.Tensor], policy: str) -> Dict[str, torch.Tensor]:
+    """What the forward keeps for backward (autograd.py:366-377): pre, and with save_winners the
+    max-pooling winner ids."""
     if policy == "recompute_stats":
         return {}
-    return {"pre": out["pre"]}
+    keep = {"pre": out["pre"]}
+    if policy == "save_winners" and "winner" in out:
+        keep["winner"] = out["winner"]
+    return keep
 
 
 class SparsePoolFunction(torch.autograd.Function):
@@ -187,7 +192,7 @@ class SparsePoolFunction(torch.autograd.Function):
         policy = fit_policy(rt, policy, x.shape[0])
         xc, wc, bc = _compute_operands(x, w, b, compute_dtype)
         lv = rt.level
-        out = rt.forward(xc, wc, bc, track_ids=False)
+        out = rt.forward(xc, wc, bc, track_ids=(policy == "save_winners"))
         pre = out["pre"]
         y = act_torch(pre, lv.out_activation)
         saved = _saved_stats(lv, out, policy)
@@ -204,7 +209,9 @@ class SparsePoolFunction(torch.autograd.Function):
         rt: Level1Runtime = ctx.rt
         lv = rt.level
         xc, wc, bc = _compute_operands(x, w, b, ctx.compute_dtype)
-        recomputed = "pre" not in saved
+        # statistics the backward needs and the policy did not save (autograd.py:246-258): max
+        # pooling needs the winners, so minimal_stats recomputes the forward with track_ids
+        recomputed = "pre" not in saved or (lv.type == "max" and "winner" not in saved)
         if recomputed:
             saved.update(rt.forward(xc, wc, bc, track_ids=True))
         g_pre = dy.float() * dact_torch(saved["pre"], lv.out_activation)

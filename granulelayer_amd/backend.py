@@ -4,7 +4,7 @@
 backend (sparse_pooling/autograd.py:220-223 and :265-267; implemented for CUDA at
 sparse_pooling/backends/cuda/runtime.py:339-712):
 
-    forward(rt, x, w, b, track_ids)                     -> {"pre": [B, U] fp32}
+    forward(rt, x, w, b, track_ids)                     -> {"pre": [B, U] fp32[, "winner": [B, U] int32]}
     backward(rt, x, w, b, g_pre, stats, dw_buf, db_buf) -> dX [B, D] fp32 (dW/db accumulated)
 
 plus ``adam`` (the FusedAdamW launch, sparse_pooling/optim.py:116-123) and ``edges`` (the
@@ -114,19 +114,24 @@ class HipBackend:
         w, b = _f32(w, "weight"), _f32(b, "bias")
         B = x.shape[0]
         pre = torch.empty((B, G), device=x.device, dtype=torch.float32)
+        # max pooling with track_ids: the winner slot of every (token, pool), the reference's
+        # "winner" statistic (kernels/ops.py:189-195)
+        winner = torch.empty((B, G), device=x.device, dtype=torch.int32) if (track_ids and pool == N.GL_POOL["max"]) else None
+        out = {"pre": pre} if winner is None else {"pre": pre, "winner": winner}
         if B == 0:
-            return {"pre": pre}
+            return out
         win_lo, win_width = self.windows(rt)
         a = N.GlFwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=L.input_dim, G=G, S=S, K=K, act=act, pool=pool,
                         idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
-                        sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, pre=_ptr(pre))
+                        sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, pre=_ptr(pre),
+                        winner=_ptr(winner))
         with torch.cuda.device(x.device):
             need = self.lib.size_query("gl_fwd_workspace", a)
             ws = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)
             a.ws, a.ws_bytes = _ptr(ws), need
             self.lib.call("gl_fwd", ctypes.byref(a), ctypes.c_void_p(_stream(x.device)))
         rt.last_info["workspace_bytes"] = need
-        return {"pre": pre}
+        return out
 
     # ------------------------------------------------------------------ gather schedule
     def schedule(self, rt) -> Optional[torch.Tensor]:
@@ -198,6 +203,14 @@ class HipBackend:
         for name, t, shape in (("dw_buf", dw_buf, L.weight_shape), ("db_buf", db_buf, L.bias_shape)):
             if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != tuple(shape):
                 raise ValueError(f"{name} must be a contiguous float32 tensor of shape {tuple(shape)}")
+        winner = None
+        if pool == N.GL_POOL["max"]:  # the only neuron of a (token, pool) with a gradient
+            winner = stats.get("winner")
+            if winner is None:
+                raise ValueError("max pooling backward needs the forward's winner ids (stats['winner'])")
+            if winner.dtype != torch.int32 or tuple(winner.shape) != (B, G) or winner.device != x.device:
+                raise ValueError(f"winner must be an int32 [{B}, {G}] tensor on {x.device}")
+            winner = winner.contiguous()
         dx = torch.empty((B, D), device=x.device, dtype=torch.float32)
         if B == 0:
             return dx
@@ -206,6 +219,7 @@ class HipBackend:
         a = N.GlBwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=D, G=G, S=S, K=K, act=act, pool=pool,
                         idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, g_pre=_ptr(g_pre),
+                        winner=_ptr(winner),
                         dW=_ptr(dw_buf), db=_ptr(db_buf), dX=_ptr(dx), edges=_ptr(edges),
                         edges_bytes=edges.numel())
         with torch.cuda.device(x.device):

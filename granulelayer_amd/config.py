@@ -20,7 +20,7 @@ POOL_ID = {name: i for i, name in enumerate(POOL_TYPES)}
 ACT_ID = {name: i for i, name in enumerate(ACTIVATIONS)}
 
 # operators executed by the HIP path (everything else parses but is refused at run time)
-HIP_POOLS = ("mean", "sum")
+HIP_POOLS = ("mean", "sum", "max")
 HIP_ACTIVATIONS = ("identity", "relu")
 
 _DEFAULT_ACT = {"max": "identity", "topk_mean": "identity", "mean": "relu", "logmeanexp": "identity",
@@ -93,8 +93,8 @@ class LevelSpec:
             return f"pooling {self.type!r} is not on the MI355X path (supported: {', '.join(HIP_POOLS)})"
         if self.activation not in HIP_ACTIVATIONS:
             return f"activation {self.activation!r} is not on the MI355X path (supported: relu, identity)"
-        if self.out_activation != "identity":
-            return f"out_activation {self.out_activation!r} is not on the MI355X path"
+        if self.out_activation not in HIP_ACTIVATIONS:  # applied to pre by the autograd layer (torch)
+            return f"out_activation {self.out_activation!r} is not on the MI355X path (supported: relu, identity)"
         if self.neurons_per_shard is not None:
             return "semantic two-level pooling is not on the MI355X path"
         return ""

@@ -195,6 +195,11 @@ __device__ __forceinline__ float4 ld_uniform4(const float* row, int i) {
   const CF* q = (const CF*)(row + i);
   return make_float4(q[0], q[1], q[2], q[3]);
 }
+__device__ __forceinline__ int4 ld_uniform4i(const int32_t* row, int i) {
+  typedef const __attribute__((address_space(4))) int32_t CI;
+  const CI* q = (const CI*)(row + i);
+  return make_int4(q[0], q[1], q[2], q[3]);
+}
 // X slot at byte offset a of a tile buffer.  FAR: the buffer's base does not fit the 16-bit
 // ds_read offset, so base + a costs one v_add per read; the offset then passes through an empty
 // asm so the compiler keeps doing that add at the read instead of hoisting a second copy of every
@@ -236,6 +241,46 @@ __device__ __forceinline__ float wave_sum4(float a0, float a1, float a2, float a
   c = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
   const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
   return __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+}
+
+// Max pooling keeps (value, slot) pairs ordered by value, then by the smaller slot: the maximum
+// of act(z) and the first slot reaching it (torch.argmax).  The order is total (for non-NaN
+// values), so any combination order gives the same pair.
+__device__ __forceinline__ void vmax_pair(float& m, int& s, float m2, int s2) {
+  const bool take = m2 > m || (m2 == m && s2 < s);
+  m = take ? m2 : m;
+  s = take ? s2 : s;
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dppi(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
+// wave_sum4's reduce-scatter for (value, slot) pairs: every lane ends with the wave's maximum
+// pair of token wave_sum4_token(lane).
+__device__ __forceinline__ void wave_max4(float a0, float a1, float a2, float a3, int s0, int s1, int s2, int s3,
+                                          int lane, float& m, int& s) {
+  const bool odd = lane & 1, hi = lane & 2;
+  float b0 = odd ? a2 : a0, b1 = odd ? a3 : a1;
+  int t0 = odd ? s2 : s0, t1 = odd ? s3 : s1;
+  vmax_pair(b0, t0, dpp<0xB1>(odd ? a0 : a2), dppi<0xB1>(odd ? s0 : s2));  // quad_perm(1,0,3,2)
+  vmax_pair(b1, t1, dpp<0xB1>(odd ? a1 : a3), dppi<0xB1>(odd ? s1 : s3));
+  float c = hi ? b1 : b0;
+  int u = hi ? t1 : t0;
+  vmax_pair(c, u, dpp<0x4E>(hi ? b0 : b1), dppi<0x4E>(hi ? t0 : t1));  // quad_perm(2,3,0,1)
+  vmax_pair(c, u, dpp<0x124>(c), dppi<0x124>(u));                      // row_ror:4
+  vmax_pair(c, u, dpp<0x128>(c), dppi<0x128>(u));                      // row_ror:8
+  const auto c16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+  const auto u16 = __builtin_amdgcn_permlane16_swap((unsigned)u, (unsigned)u, false, false);
+  c = __uint_as_float(c16[0]);
+  u = (int)u16[0];
+  vmax_pair(c, u, __uint_as_float(c16[1]), (int)u16[1]);
+  const auto c32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+  const auto u32 = __builtin_amdgcn_permlane32_swap((unsigned)u, (unsigned)u, false, false);
+  m = __uint_as_float(c32[0]);
+  s = (int)u32[0];
+  vmax_pair(m, s, __uint_as_float(c32[1]), (int)u32[1]);
 }
 
 }  // namespace gl

@@ -51,6 +51,7 @@ struct FwdK {
   const float* bias;
   const int32_t* counts;
   float* part;            // [n_chunks][b_pad]
+  int* pslot;             // max pooling: [n_chunks][b_pad] slot of each partial maximum
   const uint32_t* sched;  // gather schedule or null
   const uint32_t* win;    // per-pool window starts (window staging) or null
   long long n_chunks;
@@ -107,7 +108,72 @@ __device__ __forceinline__ void fwd_tile(const char* xsb, const unsigned (&addr)
   if (store && lane < 4) out[wave_sum4_token(lane)] = tot;  // 4 lanes, 16 contiguous bytes
 }
 
-template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false>
+// Max pooling tile: per token the largest act(z) of the wave's neurons and its pool slot (the
+// smaller slot on ties), reduced over the lanes by wave_max4; lanes 0-3 store value and slot.
+// Padded slots carry z = -inf (bias -inf, weights 0) and slots >= n_g, so they never win: with
+// relu they tie at 0 with a valid slot and lose on the slot.
+template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8)>
+__device__ __forceinline__ void fwd_tile_max(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+                                             const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
+                                             bool store, int lane) {
+  float m0 = -__builtin_inff(), m1 = m0, m2 = m0, m3 = m0;
+  int s0 = 0x7fffffff, s1 = s0, s2 = s0, s3 = s0;
+  float4 xc[K];
+#pragma unroll
+  for (int k = 0; k < RA; ++k) xc[k] = lds_x<FAR>(xsb, addr[0][k]);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+#pragma unroll
+    for (int k = RA; k < K; ++k) xc[k] = lds_x<FAR>(xsb, addr[j][k]);
+    float4 xn[RA];
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xn[k] = lds_x<FAR>(xsb, addr[j + 1][k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
+      z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
+      z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
+      z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
+    }
+    if (ACT == GL_ACT_RELU) {
+      z0 = __builtin_fmaxf(z0, 0.f);
+      z1 = __builtin_fmaxf(z1, 0.f);
+      z2 = __builtin_fmaxf(z2, 0.f);
+      z3 = __builtin_fmaxf(z3, 0.f);
+    }
+    vmax_pair(m0, s0, z0, slot[j]);
+    vmax_pair(m1, s1, z1, slot[j]);
+    vmax_pair(m2, s2, z2, slot[j]);
+    vmax_pair(m3, s3, z3, slot[j]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xc[k] = xn[k];
+    }
+  }
+  float m;
+  int sl;
+  wave_max4(m0, m1, m2, m3, s0, s1, s2, s3, lane, m, sl);
+  if (store && lane < 4) {
+    out[wave_sum4_token(lane)] = m;
+    oslot[wave_sum4_token(lane)] = sl;
+  }
+}
+
+// sum / mean tile or max tile
+template <int K, int NPL, int ACT, bool FAR, bool MAXP>
+__device__ __forceinline__ void fwd_tile_any(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+                                             const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
+                                             bool store, int lane) {
+  if constexpr (MAXP) fwd_tile_max<K, NPL, ACT, FAR>(xsb, addr, w, bias, slot, out, oslot, store, lane);
+  else fwd_tile<K, NPL, ACT, FAR>(xsb, addr, w, bias, out, store, lane);
+}
+
+template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, bool MAXP = false>
 __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots)
   __shared__ float4 xa[WS ? 2 * XTILE_DB : (DBUF ? XTILE_DB : XTILE_SB)];
@@ -124,6 +190,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   unsigned addr[NPL][K];
   float w[NPL][K];
   float bias[NPL];
+  int slot[NPL];  // max pooling: pool slot of each neuron
   // window staging: this wave's pool is slot pk of the workgroup's staged pools, window start lo
   const int g_first = (int)((long long)blockIdx.x * WAVES / p.cpg);
   const int pk = WS ? (int)(g - g_first) : 0;
@@ -144,7 +211,8 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       w[j][ks] = valid ? wl : 0.f;
     }
     const float bl = p.bias[n];
-    bias[j] = valid ? bl : 0.f;
+    bias[j] = valid ? bl : (MAXP ? -__builtin_inff() : 0.f);
+    slot[j] = s;
   }
 
   // Token tiles reach LDS by LDS-DMA (dma_tile).  DBUF: tile t + 1 is loaded into the other
@@ -154,6 +222,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   // LDS reads (lgkmcnt(0)) before each use instead of only the ones the use needs.
   constexpr int NT = WAVES * 64;
   float* out = p.part + chunk * p.b_pad;
+  int* oslot = MAXP ? p.pslot + chunk * p.b_pad : nullptr;
   const bool store = active;
   if constexpr (WS) {
     // window staging: WS_TILES tiles per stage and barrier; tile t at slot (t mod 2 WS_TILES) * nsl
@@ -170,7 +239,8 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       const int tn = p.n_tiles - t0 < WS_TILES ? p.n_tiles - t0 : WS_TILES;
       for (int tt = 0; tt < tn; ++tt) {
         const int t = t0 + tt;
-        fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
+        fwd_tile_any<K, NPL, ACT, false, MAXP>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT,
+                                               oslot + t * BT, store, lane);
         // next tile's slot; after the last tile of region 1 back to region 0
         const unsigned step = (t & (2 * WS_TILES - 1)) == 2 * WS_TILES - 1 ? tstep - 2u * WS_TILES * tstep : tstep;
 #pragma unroll
@@ -187,12 +257,14 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       stage_wait();
       __syncthreads();  // tile t is in xa; every wave is done with xb (tile t - 1)
       if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xb, p.D, NT);
-      fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
+      fwd_tile_any<K, NPL, ACT, false, MAXP>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT,
+                                             oslot + t * BT, store, lane);
       if (t + 1 < p.n_tiles) {
         stage_wait();
         __syncthreads();  // tile t + 1 is in xb; every wave is done with xa
         if (t + 2 < p.n_tiles) dma_tile(p.xt + (long long)(t + 2) * p.D, xa, p.D, NT);
-        fwd_tile<K, NPL, ACT, true>(reinterpret_cast<const char*>(xb), addr, w, bias, out + (t + 1) * BT, store, lane);
+        fwd_tile_any<K, NPL, ACT, true, MAXP>(reinterpret_cast<const char*>(xb), addr, w, bias, slot,
+                                              out + (t + 1) * BT, oslot + (t + 1) * BT, store, lane);
       }
     }
   } else {
@@ -201,7 +273,8 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       dma_tile(p.xt + (long long)t * p.D, xa, p.D, NT);
       stage_wait();
       __syncthreads();
-      fwd_tile<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
+      fwd_tile_any<K, NPL, ACT, false, MAXP>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT,
+                                             oslot + t * BT, store, lane);
     }
   }
 }
@@ -230,34 +303,66 @@ __global__ void __launch_bounds__(256) fwd_finalize_kernel(const float* __restri
   }
 }
 
+// Max pooling: pre[b, g] = the largest partial maximum over the pool's cpg chunks, winner[b, g] its
+// slot (the smaller slot on ties, as merge_finalize, kernels/ops.py:189-195); tiled transpose.
+__global__ void __launch_bounds__(256) fwd_finalize_max_kernel(const float* __restrict__ part, const int* __restrict__ pslot,
+                                                               float* __restrict__ pre, int32_t* __restrict__ winner, int B,
+                                                               int G, int cpg, int b_pad) {
+  __shared__ float tile[32][33];
+  __shared__ int tslot[32][33];
+  const int g0 = blockIdx.x * 32, bb0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int r = ty; r < 32; r += 8) {
+    const int g = g0 + r, b = bb0 + tx;
+    float m = -__builtin_inff();
+    int sl = 0x7fffffff;
+    if (g < G && b < b_pad) {
+      const long long o = (long long)g * cpg * b_pad + b;
+      for (int c = 0; c < cpg; ++c) vmax_pair(m, sl, part[o + (long long)c * b_pad], pslot[o + (long long)c * b_pad]);
+    }
+    tile[r][tx] = m;
+    tslot[r][tx] = sl;
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const int b = bb0 + r, g = g0 + tx;
+    if (g < G && b < B && b < b_pad) {
+      pre[(long long)b * G + g] = tile[tx][r];
+      if (winner) winner[(long long)b * G + g] = tslot[tx][r];
+    }
+  }
+}
+
 // ---- host side -------------------------------------------------------------------------------
 // 4 neurons per lane; 16 waves per workgroup at K = 8 (4 waves per SIMD, 128 VGPRs), 8 at K = 16
-// (2 per SIMD: the parameters of 4 neurons of fan-in 16 take twice the registers)
+// (2 per SIMD: the parameters of 4 neurons of fan-in 16 take twice the registers).  Max pooling
+// keeps a slot per neuron and a (value, slot) pair per token: 12 waves at K = 8, 4 at K = 16.
 constexpr int FWD_NPL = 4;
-constexpr int fwd_waves(int K) { return K == 8 ? 16 : 8; }
+constexpr int fwd_waves(int K, bool maxp = false) { return K == 8 ? (maxp ? 12 : 16) : (maxp ? 4 : 8); }
 
 struct FwdPlan {
   int npl, waves, cpg, n_tiles, b_pad;
   long long n_chunks;
-  size_t xt_bytes, part_bytes;
+  size_t xt_bytes, part_bytes, slot_bytes;
 };
 
 static FwdPlan fwd_plan(const GlFwdArgs* a) {
   FwdPlan q;
   q.npl = FWD_NPL;
-  q.waves = fwd_waves(a->K);
+  q.waves = fwd_waves(a->K, a->pool == GL_POOL_MAX);
   q.cpg = ceil_div(a->S, 64 * q.npl);
   q.n_chunks = (long long)a->G * q.cpg;
   q.n_tiles = ceil_div(a->B, BT);
   q.b_pad = q.n_tiles * BT;
   q.xt_bytes = (size_t)round_up((long long)q.n_tiles * a->D * 16, 256);
   q.part_bytes = (size_t)round_up((long long)q.n_chunks * q.b_pad * 4, 256);
+  q.slot_bytes = a->pool == GL_POOL_MAX ? q.part_bytes : 0;  // slot of every partial maximum
   return q;
 }
 
-template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false>
+template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS, bool MAXP>
 static int launch_fwd(const FwdK& k, hipStream_t s) {
-  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS>;
+  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, MAXP>;
   dim3 grid((unsigned)ceil_div(k.n_chunks, WAVES));
   GL_LAUNCH(WS ? GL_KERNEL_FWD_WIN : GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
@@ -266,16 +371,22 @@ static int launch_fwd(const FwdK& k, hipStream_t s) {
 
 // one workgroup per CU (the tile buffers take the LDS); pool windows when they fit, else two tile
 // buffers when D fits them, else one
-template <int ACT, int K>
+template <int ACT, int K, bool MAXP>
 static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
-  constexpr int W = fwd_waves(K);
-  if (k.win) return launch_fwd<K, FWD_NPL, W, ACT, false, true>(k, s);
-  return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true>(k, s) : launch_fwd<K, FWD_NPL, W, ACT, false>(k, s);
+  constexpr int W = fwd_waves(K, MAXP);
+  if (k.win) return launch_fwd<K, FWD_NPL, W, ACT, false, true, MAXP>(k, s);
+  return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true, false, MAXP>(k, s)
+                       : launch_fwd<K, FWD_NPL, W, ACT, false, false, MAXP>(k, s);
 }
 
-template <int ACT>
+template <int ACT, bool MAXP>
 static int launch_fwd_act(int K, int D, const FwdK& k, hipStream_t s) {
-  return K == 8 ? launch_fwd_buf<ACT, 8>(D, k, s) : launch_fwd_buf<ACT, 16>(D, k, s);
+  return K == 8 ? launch_fwd_buf<ACT, 8, MAXP>(D, k, s) : launch_fwd_buf<ACT, 16, MAXP>(D, k, s);
+}
+
+template <bool MAXP>
+static int launch_fwd_any(int act, int K, int D, const FwdK& k, hipStream_t s) {
+  return act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU, MAXP>(K, D, k, s) : launch_fwd_act<GL_ACT_IDENTITY, MAXP>(K, D, k, s);
 }
 
 // Window staging applies when the staged windows of a workgroup's pools (npw of them, each ww
@@ -298,7 +409,7 @@ int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void
   if (B < 1 || D < 1 || G < 1 || S < 1) return GL_ERR_ARG;
   if (K != 8 && K != 16) return GL_ERR_UNSUPPORTED;
   if (act != GL_ACT_IDENTITY && act != GL_ACT_RELU) return GL_ERR_UNSUPPORTED;
-  if (pool != GL_POOL_MEAN && pool != GL_POOL_SUM) return GL_ERR_UNSUPPORTED;
+  if (pool != GL_POOL_MEAN && pool != GL_POOL_SUM && pool != GL_POOL_MAX) return GL_ERR_UNSUPPORTED;
   if (x_dtype != GL_DTYPE_F32 && x_dtype != GL_DTYPE_BF16) return GL_ERR_UNSUPPORTED;
   if ((long long)G * S > (1LL << 31) / 16) return GL_ERR_UNSUPPORTED;
   if (D > XTILE_SB) return GL_ERR_LDS;  // one token tile (D x 16 bytes) must fit the LDS tile buffer
@@ -314,7 +425,7 @@ extern "C" int gl_fwd_workspace(const GlFwdArgs* a, size_t* bytes) {
   GL_TRY(check_layer(a->B, a->D, a->G, a->S, a->K, a->act, a->pool, a->X, a->idx, a->W, a->bias, a->counts,
                      a->x_dtype));
   FwdPlan q = fwd_plan(a);
-  *bytes = q.xt_bytes + q.part_bytes;
+  *bytes = q.xt_bytes + q.part_bytes + q.slot_bytes;
   return 0;
 }
 
@@ -327,16 +438,22 @@ extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
   FwdPlan q = fwd_plan(a);
   float4* xt = (float4*)a->ws;
   float* part = (float*)((char*)a->ws + q.xt_bytes);
+  int* pslot = a->pool == GL_POOL_MAX ? (int*)((char*)a->ws + q.xt_bytes + q.part_bytes) : nullptr;
   GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, 0, q.n_tiles, xt, s));
   if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;
-  FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, a->sched, nullptr, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles,
+  FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, pslot, a->sched, nullptr, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles,
          q.b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0};
   if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) k.win = a->win;
-  GL_TRY(a->act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU>(a->K, a->D, k, s)
-                                : launch_fwd_act<GL_ACT_IDENTITY>(a->K, a->D, k, s));
   dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(q.b_pad, 32));
-  GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_kernel, grid, dim3(256), 0, s, part, a->counts, a->pre, a->B, a->G, q.cpg, q.b_pad,
-                     0, a->pool);
+  if (a->pool == GL_POOL_MAX) {
+    GL_TRY(launch_fwd_any<true>(a->act, a->K, a->D, k, s));
+    GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_max_kernel, grid, dim3(256), 0, s, part, pslot, a->pre, a->winner,
+              a->B, a->G, q.cpg, q.b_pad);
+  } else {
+    GL_TRY(launch_fwd_any<false>(a->act, a->K, a->D, k, s));
+    GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_kernel, grid, dim3(256), 0, s, part, a->counts, a->pre, a->B, a->G,
+              q.cpg, q.b_pad, 0, a->pool);
+  }
   GL_CHECK_LAUNCH();
   return 0;
 }

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 3
+#define GL_ABI_VERSION 4
 
 enum {
   GL_OK = 0,
@@ -40,7 +40,9 @@ enum {
   GL_ERR_DEVICE = -7        /* no current HIP device or attribute query failed */
 };
 enum { GL_ACT_IDENTITY = 0, GL_ACT_RELU = 1 };
-enum { GL_POOL_MEAN = 0, GL_POOL_SUM = 1 };
+/* max: pytorch_reference.py:61-67 (winner = first maximum of act(z) over the pool's valid
+ * slots), merged as kernels/ops.py:189-195 */
+enum { GL_POOL_MEAN = 0, GL_POOL_SUM = 1, GL_POOL_MAX = 2 };
 enum { GL_DTYPE_F32 = 0, GL_DTYPE_BF16 = 1 };
 
 /* Forward arguments.  Replaces the reference's FwdArgs + sp_fwd
@@ -61,6 +63,8 @@ typedef struct GlFwdArgs {
   const uint32_t* win;    /* [G] first input of each pool's window (gl_window_build_host), or NULL */
   int32_t win_width;      /* widest pool window; the kernels stage only the windows when narrow */
   float* pre;             /* out [B, G]: pooled value before the (identity) out-activation */
+  int32_t* winner;        /* out [B, G] (GL_POOL_MAX, or NULL): pool-local slot of the maximum, the
+                             reference's track_ids / "winner" statistic (ops.py:192-195) */
   void* ws;               /* workspace of gl_fwd_workspace() bytes */
   size_t ws_bytes;
 } GlFwdArgs;
@@ -82,6 +86,7 @@ typedef struct GlBwdArgs {
   const uint32_t* win;    /* as GlFwdArgs.win / win_width */
   int32_t win_width;
   const float* g_pre;     /* [B, G] dL/dpre (fp32) */
+  const int32_t* winner;  /* [B, G] GL_POOL_MAX: the forward's winner slots (required); else NULL */
   float* dW;              /* [G*S, K] ACCUMULATED (+=), e.g. W.main_grad; padded slots untouched */
   float* db;              /* [G*S] ACCUMULATED (+=) */
   float* dX;              /* out [B, D] fp32, overwritten */

@@ -20,6 +20,12 @@
  *     db[n]  += sum_b dz ;  dW[n,k] += sum_b dz * x[b, idx[n,k]] ;  dX[b, idx[n,k]] += dz * w[n,k]
  *   padded slots (s >= n_g) are masked out of every sum (triton_fused.py:330-338, 428-431).
  *
+ *   max pooling (pool 2; pytorch_reference.py:61-67, merge_finalize kernels/ops.py:189-195,
+ *   triton_fused.py:129-139 _update max):
+ *     pre[b,g] = max_{s < n_g} a[b, g*S+s];  winner[b,g] = the smallest slot s attaining it
+ *     backward (autograd of the gather, the event backward autograd.py:284-289): only the winner
+ *     gets a gradient:  dz[b, winner] = dy[b,g] * act'(z[b, winner])
+ *
  *   Adam (sparse_pooling/optim.py:26-64, fp32 parameters: HAS_MASTER=False, STOCH=False):
  *     m = b1*m + (1-b1)*g ; v = b2*v + (1-b2)*g*g ; upd = (m/bc1) / (sqrt(v/bc2) + eps)
  *     p = p*(1 - lr*wd) - lr*upd ; g = 0        evaluated in fp32, in this order, unfused.
@@ -50,7 +56,7 @@ static inline double neuron_z(const float* xb, const int32_t* idx, const float* 
 
 /*
  * Forward.  x [B, D] fp32 (bf16 inputs are widened exactly by the caller); idx/w [G*S, K];
- * bias [G*S]; counts [G]; pool 0 = mean, 1 = sum; act 0 = identity, 1 = relu.
+ * bias [G*S]; counts [G]; pool 0 = mean, 1 = sum (max: glo_forward_max_f64); act 0 = identity, 1 = relu.
  * pre [B, G] float64.  mag (optional, [B, G]): scale_g * sum_s (sum_k |x w| + |bias|), the
  * magnitude the rounding error of an fp32 evaluation of pre is proportional to.
  */
@@ -67,6 +73,40 @@ void glo_forward_f64(int B, int D, int G, int S, int K, const float* x, const in
       }
       pre[(size_t)b * G + g] = pool == 0 ? s / (double)n_g : s;
       if (mag) mag[(size_t)b * G + g] = pool == 0 ? m / (double)n_g : m;
+    }
+  }
+}
+
+/*
+ * Max pooling forward (pool 2).  pre [B, G] float64, winner [B, G] int32 (pool-local slot), and
+ * gap [B, G] (optional): (best - second best) / (scale of the fp32 rounding of z), the margin by
+ * which an fp32 evaluation of the two leading values could swap them (+inf for a single neuron).
+ * Ties go to the smaller slot, as torch.argmax returns the first maximum.
+ */
+void glo_forward_max_f64(int B, int D, int G, int S, int K, const float* x, const int32_t* idx, const float* w,
+                         const float* bias, const int32_t* counts, int act, double* pre, int32_t* winner,
+                         double* gap) {
+  for (int b = 0; b < B; ++b) {
+    const float* xb = x + (size_t)b * D;
+    for (int g = 0; g < G; ++g) {
+      const int n_g = counts[g];
+      double best = -INFINITY, second = -INFINITY, mag = 0.0;
+      int win = 0;
+      for (int sl = 0; sl < n_g; ++sl) {
+        double zm;
+        const double a = act_f(neuron_z(xb, idx, w, bias, (long)g * S + sl, K, &zm), act);
+        if (zm > mag) mag = zm;
+        if (a > best) {
+          second = best;
+          best = a;
+          win = sl;
+        } else if (a > second) {
+          second = a;
+        }
+      }
+      pre[(size_t)b * G + g] = best;
+      winner[(size_t)b * G + g] = win;
+      if (gap) gap[(size_t)b * G + g] = n_g < 2 ? INFINITY : (best - second) / (mag > 0.0 ? mag : 1.0);
     }
   }
 }
@@ -91,7 +131,16 @@ void glo_backward_f64(int B, int D, int G, int S, int K, const float* x, const i
     for (int g = 0; g < G; ++g) {
       int n_g = counts[g];
       double c1 = (double)dy[(size_t)b * G + g] * (pool == 0 ? 1.0 / (double)n_g : 1.0);
+      int win = -1;  /* max pooling: the winner (first maximum of act(z)) is the only neuron with a gradient */
+      if (pool == 2) {
+        double best = -INFINITY;
+        for (int sl = 0; sl < n_g; ++sl) {
+          const double a = act_f(neuron_z(xb, idx, w, bias, (long)g * S + sl, K, NULL), act);
+          if (a > best) best = a, win = sl;
+        }
+      }
       for (int sl = 0; sl < n_g; ++sl) {
+        if (pool == 2 && sl != win) continue;
         long n = (long)g * S + sl;
         double zm;
         double z = neuron_z(xb, idx, w, bias, n, K, &zm);

@@ -5,7 +5,7 @@ module, and only as the checker.  The product package ``granulelayer_amd`` never
 
 Contents (each restates the reference; file:line citations are relative to the reference root):
 
-* ``forward`` / ``backward`` -- float64 C restatement (``gl_oracle.c``) of
+* ``forward`` / ``forward_max`` / ``backward`` -- float64 C restatement (``gl_oracle.c``) of
   ``sparse_pooling/reference/pytorch_reference.py:29-79`` (Mode A) and of the recompute backward
   ``sparse_pooling/kernels/triton_fused.py:364-445`` + ``kernels/ops.py:242-249``.
 * ``adam`` -- fp32 restatement of ``sparse_pooling/optim.py:26-64`` (fp32 parameters).
@@ -17,7 +17,10 @@ Contents (each restates the reference; file:line citations are relative to the r
 Parity status (what pins each function; see tests/test_oracle.py):
   forward   pinned: dense-GEMM restatement via torch.matmul, one-hot inputs (closed form),
             mean = sum / n_g, padded-slot masking, hand-computed known answer.
-  backward  pinned: torch autograd of the dense-GEMM forward, float64 central differences.
+  forward_max pinned: dense-GEMM z with torch.max / torch.argmax (first maximum), hand-built
+            ties (smaller slot wins, padded slots never win, relu all-zero pools).
+  backward  pinned: torch autograd of the dense-GEMM forward, float64 central differences; max
+            pooling: autograd of the winner gather (pytorch_reference.py:61-67).
   adam      pinned: torch.optim.Adam / AdamW (library), step-1 closed form.
   partition pinned: invariants of test_sparse_projection.py:14-27 (enumerates range(H)).
   xedges    pinned: brute force per feature on tiny inputs; invariants (permutation of the valid
@@ -55,7 +58,8 @@ def _load():
         lib.glo_backward_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, i, P, P, P, P, ctypes.c_double,
                                          P, P, P, P, P, P]
         lib.glo_adam_f32.argtypes = [ctypes.c_long, P, P, P, P, f, f, f, f, f, f, f, i]
-        for fn in (lib.glo_forward_f64, lib.glo_backward_f64, lib.glo_adam_f32):
+        lib.glo_forward_max_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, P, P, P]
+        for fn in (lib.glo_forward_f64, lib.glo_backward_f64, lib.glo_adam_f32, lib.glo_forward_max_f64):
             fn.restype = None
         _lib = lib
     return _lib
@@ -93,6 +97,23 @@ def forward(x, idx, w, bias, counts, S, act="relu", pool="mean", with_mag=False)
     mag = np.zeros((B, G), np.float64) if with_mag else None
     _load().glo_forward_f64(B, D, G, S, K, px, pi, pw, pb, pc, _ACT[act], _POOL[pool], _p(pre), _p(mag))
     return (pre, mag) if with_mag else pre
+
+
+def forward_max(x, idx, w, bias, counts, S, act="identity"):
+    """Max pooling: (pre [B, G] float64, winner [B, G] int32 pool-local slot, gap [B, G]).  gap is
+    the lead of the maximum over the runner-up relative to the rounding scale of z; pairs with a
+    gap below ~1e-6 may pick another winner in fp32."""
+    B, D, G, K = _shapes(x, idx, counts, S)
+    x, px = _c(x, np.float32)
+    idx, pi = _c(idx, np.int32)
+    w, pw = _c(np.asarray(w).reshape(G * S, K), np.float32)
+    bias, pb = _c(np.asarray(bias).reshape(G * S), np.float32)
+    counts, pc = _c(counts, np.int32)
+    pre = np.zeros((B, G), np.float64)
+    win = np.zeros((B, G), np.int32)
+    gap = np.zeros((B, G), np.float64)
+    _load().glo_forward_max_f64(B, D, G, S, K, px, pi, pw, pb, pc, _ACT[act], _p(pre), _p(win), _p(gap))
+    return pre, win, gap
 
 
 # relu masks decided within this relative distance of z = 0 may differ in fp32 (z is a sum of
@@ -134,7 +155,7 @@ def adam(p, g, m, v, lr, b1, b2, eps, wd, step, moments_bf16=False):
 
 
 _ACT = {"identity": 0, "relu": 1}
-_POOL = {"mean": 0, "sum": 1}
+_POOL = {"mean": 0, "sum": 1, "max": 2}
 
 
 def partition(H: int, G: int, block: int = 8):

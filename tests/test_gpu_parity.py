@@ -381,3 +381,99 @@ def test_hip_adam_matches_golden_adamw():
     np.testing.assert_allclose(m.cpu().numpy(), a["m"], rtol=1e-6, atol=1e-7)
     np.testing.assert_allclose(v.cpu().numpy(), a["v"], rtol=2e-5, atol=1e-9)
     np.testing.assert_allclose(p.cpu().numpy(), a["p"], rtol=0, atol=3 * lr * 1e-4)
+
+
+# ---- max pooling (pytorch_reference.py:61-67; winner = first maximum, ties to the smaller slot) ----
+MAX_CASES = [
+    # D, H, G, K, B, x dtype: ragged pools (padded slots must never win), bf16 X, K = 16, D > 4096
+    (64, 3000, 8, 8, 37, torch.float32),
+    (1024, 20011, 16, 8, 64, torch.bfloat16),
+    (96, 5000, 7, 16, 33, torch.float32),
+    (1024, 65536, 64, 8, 260, torch.float32),
+    (6000, 9000, 9, 8, 20, torch.float32),
+]
+
+
+def _max_oracle(L, idx, w, b, x, act):
+    fi, fw, fb = flat(L, idx, w, b)
+    return O.forward_max(x.float().numpy(), fi, fw, fb, L.counts_tensor("cpu").numpy(), L.slots_per_group, act)
+
+
+@pytest.mark.parametrize("case", MAX_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
+@pytest.mark.parametrize("act", ["identity", "relu"])
+def test_max_forward_matches_oracle(case, act):
+    D, H, G, K, B, xdt = case
+    L, idx, w, b, x, _ = make_case(D, H, G, K, B, x_dtype=xdt)
+    rt = runtime(L, idx, "max", act)
+    out = rt.forward(x.to(DEV), w.to(DEV), b.to(DEV), track_ids=True)
+    pre, win = out["pre"].cpu().numpy(), out["winner"].cpu().numpy()
+    want, wwin, gap = _max_oracle(L, idx, w, b, x, act)
+    # the maximum of fp32 z values: within fp32 rounding of the float64 maximum
+    assert_close(pre, want, rtol=1e-5, atol=1e-6, what=f"max pre/{act}")
+    # winners bit-exact wherever fp32 cannot swap the two leading neurons
+    # fp32 z carries at most ~(K + 1) 2^-24 of its scale: leads above 2e-6 cannot swap
+    clear = gap > 2e-6
+    assert clear.mean() > 0.99
+    assert (win[clear] == wwin[clear]).all(), f"{(win[clear] != wwin[clear]).sum()} winners differ"
+    counts = L.counts_tensor("cpu").numpy()
+    assert ((win >= 0) & (win < counts[None, :])).all()  # never a padded slot
+    # without track_ids only pre is returned, with the same values
+    pre2 = rt.forward(x.to(DEV), w.to(DEV), b.to(DEV))
+    assert set(pre2) == {"pre"} and torch.equal(pre2["pre"].cpu(), out["pre"].cpu())
+
+
+@pytest.mark.parametrize("case", MAX_CASES[:4], ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
+@pytest.mark.parametrize("act", ["identity", "relu"])
+def test_max_backward_matches_oracle(case, act):
+    D, H, G, K, B, xdt = case
+    L, idx, w, b, x, dy = make_case(D, H, G, K, B, x_dtype=xdt)
+    _, _, gap = _max_oracle(L, idx, w, b, x, act)
+    assert gap.min() > 2e-6, "seeded case has a near-tie; the float64 and fp32 winners could differ"
+    rt = runtime(L, idx, "max", act)
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    stats = rt.forward(xd, wd, bd, track_ids=True)
+    dw = torch.zeros(L.weight_shape, device=DEV)
+    db = torch.zeros(L.bias_shape, device=DEV)
+    dx = rt.backward(xd, wd, bd, dy.to(DEV), stats, "save_winners", dw, db).cpu().numpy()
+    fi, fw, fb = flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    wdW, wdb, wdX, bnd = O.backward(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, dy.numpy(), act, "max",
+                                    with_bounds=True)
+    (mW, mb, mX), (uW, ub, uX) = bnd["mag"], bnd["unc"]
+    assert_parity(dx, wdX, mX, uX, what="max dX")
+    assert_parity(dw.cpu().numpy().reshape(-1, K), wdW, mW, uW, what="max dW")
+    assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, ub, what="max db")
+    # at most one neuron per (token, pool) has a gradient: db is non-zero on at most B slots per pool
+    assert (np.count_nonzero(db.cpu().numpy().reshape(G, -1), axis=1) <= B).all()
+    # the ABI refuses a max backward without winners
+    with pytest.raises(Exception):
+        rt.backward(xd, wd, bd, dy.to(DEV), {}, "save_winners", dw, db)
+
+
+@pytest.mark.parametrize("policy", ["save_winners", "minimal_stats"])
+def test_max_layer_autograd_policies(policy):
+    """SparsePoolingLayer with max pooling (defaults: identity activation, relu out-activation, so
+    y = relu(max z)): save_winners keeps the forward's winners, minimal_stats recomputes them in
+    backward (autograd.py:246-258); both give the oracle's gradients."""
+    D, H, G, K, B = 256, 12000, 12, 8, 40
+    lay = SparsePoolingLayer(D, H, G, fan_in=K, shared_neurons=None, pooling="max", checkpoint_policy=policy,
+                             dtype=torch.float32, device=DEV, seed=6, bias_std=0.2)
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(B, D, generator=gen).to(DEV).requires_grad_(True)
+    dy = torch.randn(B, G, generator=gen).to(DEV)
+    y = lay(x)
+    (y * dy).sum().backward()
+    L = lay.layout
+    fi, fw, fb = flat(L, lay.indices.cpu(), lay.weight.detach().cpu(), lay.bias.detach().cpu())
+    counts = L.counts_tensor("cpu").numpy()
+    want_pre, _, gap = O.forward_max(x.detach().cpu().numpy(), fi, fw, fb, counts, L.slots_per_group, "identity")
+    assert gap.min() > 2e-6 and np.abs(want_pre).min() > 1e-5  # no near-ties, no pre near the relu kink
+    g_pre = (dy.cpu().numpy() * (want_pre > 0)).astype(np.float32)  # dL/dpre through the relu out-activation
+    wdW, wdb, wdX, bnd = O.backward(x.detach().cpu().numpy(), fi, fw, fb, counts, L.slots_per_group, g_pre,
+                                    "identity", "max", with_bounds=True)
+    (mW, mb, mX), (uW, ub, uX) = bnd["mag"], bnd["unc"]
+    assert_close(y.detach().cpu().numpy(), np.maximum(want_pre, 0.0), rtol=1e-5, atol=1e-6, what="y")
+    assert_parity(x.grad.cpu().numpy(), wdX, mX, uX, what="dx")
+    assert_parity(lay.weight.grad.cpu().numpy().reshape(-1, K), wdW, mW, uW, what="dW")
+    assert_parity(lay.bias.grad.cpu().numpy().reshape(-1), wdb, mb, ub, what="db")
+    assert lay.last_info["recomputed_stats"] == (policy == "minimal_stats")

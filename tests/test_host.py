@@ -82,7 +82,9 @@ def test_config_parsing_matches_reference_semantics():
     assert PoolingConfig.parse("sum").levels[0].activation == "relu"
     assert PoolingConfig.parse({"type": "mean", "activation": "identity"}).levels[0].hip_reason() == ""
     assert LevelSpec("max").out_activation == "relu"
-    assert LevelSpec("max").hip_reason()
+    assert LevelSpec("max").hip_reason() == ""  # max pooling with winner ids is on the HIP path
+    assert LevelSpec("logmeanexp").hip_reason()
+    assert LevelSpec("mean", out_activation="gelu").hip_reason()
     assert LevelSpec("mean", activation="gelu").hip_reason()
     with pytest.raises(ValueError):
         LevelSpec("topk_mean", k=3)
@@ -93,7 +95,7 @@ def test_config_parsing_matches_reference_semantics():
 
 @pytest.mark.parametrize("kwargs,exc", [
     (dict(shared_neurons=8, pooling="mean"), NotImplementedError),
-    (dict(shared_neurons=None, pooling="max"), NotImplementedError),
+    (dict(shared_neurons=None, pooling="topk_mean"), NotImplementedError),
     (dict(shared_neurons=None, pooling={"type": "mean", "activation": "gelu"}), NotImplementedError),
     (dict(shared_neurons=None, pooling="mean", backend="triton"), ValueError),
     (dict(shared_neurons=None, pooling="mean", weight_layout="packed"), ValueError),

@@ -132,6 +132,74 @@ def test_backward_matches_autograd(oracle, act, pool):
     assert_close(db, (bt.grad * valid).numpy(), rtol=1e-12, atol=1e-12, what="db")
 
 
+def dense_z(x, idx, w, b, counts, S):
+    """float64 z [B, G, S] and slot validity [G, S] through a dense weight matrix (torch.matmul)."""
+    x = torch.as_tensor(x, dtype=torch.float64)
+    G = len(counts)
+    N, K = idx.shape
+    valid = torch.arange(S)[None, :] < torch.as_tensor(counts)[:, None]
+    Wd = torch.zeros(N, x.shape[1], dtype=torch.float64)
+    Wd.scatter_(1, torch.as_tensor(idx, dtype=torch.int64), torch.as_tensor(w, dtype=torch.float64))
+    z = torch.matmul(x, Wd.T) + torch.as_tensor(b, dtype=torch.float64)
+    return z.reshape(x.shape[0], G, S), valid
+
+
+@pytest.mark.parametrize("act", ["identity", "relu"])
+@pytest.mark.parametrize("B,D,G,S,K", [(4, 16, 3, 32, 8), (3, 40, 2, 64, 16)])
+def test_forward_max_matches_torch_argmax(oracle, act, B, D, G, S, K):
+    # pytorch_reference.py:61-67: am = where(mask, act(z), -inf); winner = argmax (first maximum)
+    rng = np.random.default_rng(11)
+    x, idx, w, b, counts = random_problem(rng, B, D, G, S, K)
+    z, valid = dense_z(x, idx, w, b, counts, S)
+    a = torch.relu(z) if act == "relu" else z
+    am = torch.where(valid[None], a, torch.tensor(float("-inf"), dtype=torch.float64))
+    want_pre, want_win = am.max(-1).values.numpy(), am.argmax(-1).numpy()
+    pre, win, gap = oracle.forward_max(x, idx, w, b, counts, S, act)
+    assert_close(pre, want_pre, rtol=1e-12, atol=1e-12, what="max pre")
+    assert (win == want_win).all()
+    assert (gap > 0).all() or act == "relu"  # relu: several zeros tie at the maximum 0
+
+
+def test_forward_max_ties_go_to_the_smaller_slot(oracle):
+    # slots 1 and 3 both reach z = 2 (x = [1, 1]); slot 0 reaches 1; slot 2 is padded away (n_g = 4
+    # but its z = 5 would win if it counted) -- winner 1, the first maximum
+    x = np.array([[1.0, 1.0]], np.float32)
+    idx = np.array([[0, 1], [0, 1], [0, 1], [0, 1], [0, 1]], np.int32)
+    w = np.array([[0.5, 0.5], [1.0, 1.0], [2.5, 2.5], [1.0, 1.0], [9.0, 9.0]], np.float32)
+    b = np.zeros(5, np.float32)
+    pre, win, gap = oracle.forward_max(x, idx, w, b, np.array([4], np.int32), 5, "identity")
+    assert pre[0, 0] == 5.0 and win[0, 0] == 2  # slot 2 counts (n_g = 4): z = 5
+    pre, win, gap = oracle.forward_max(x, idx, w[[0, 1, 3, 2, 4]], b, np.array([3], np.int32), 5, "identity")
+    assert pre[0, 0] == 2.0 and win[0, 0] == 1 and gap[0, 0] == 0.0  # slots 1, 2 tie at 2; slot 3 (z 5) padded
+    # relu with every z <= 0: all activations are 0, the first slot wins
+    pre, win, _ = oracle.forward_max(-x, idx, w, b, np.array([4], np.int32), 5, "relu")
+    assert pre[0, 0] == 0.0 and win[0, 0] == 0
+
+
+@pytest.mark.parametrize("act", ["identity", "relu"])
+def test_backward_max_matches_autograd(oracle, act):
+    # the gradient reaches only the winner (autograd of am.gather(winner), pytorch_reference.py:61-67)
+    rng = np.random.default_rng(12)
+    B, D, G, S, K = 5, 24, 3, 32, 8
+    x, idx, w, b, counts = random_problem(rng, B, D, G, S, K)
+    dy = rng.standard_normal((B, G)).astype(np.float32)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
+    bt = torch.tensor(b, dtype=torch.float64, requires_grad=True)
+    z = (xt[:, torch.as_tensor(idx, dtype=torch.int64)] * wt).sum(-1) + bt  # [B, N]
+    a = torch.relu(z) if act == "relu" else z
+    valid = (torch.arange(S)[None, :] < torch.as_tensor(counts)[:, None]).reshape(-1)
+    am = torch.where(valid[None], a, torch.tensor(float("-inf"), dtype=torch.float64)).reshape(B, G, S)
+    win = am.detach().argmax(-1, keepdim=True)
+    pooled = am.gather(-1, win).squeeze(-1)
+    (pooled * torch.as_tensor(dy, dtype=torch.float64)).sum().backward()
+    dW, db, dX = oracle.backward(x, idx, w, b, counts, S, dy, act, "max")
+    assert_close(dW, wt.grad.numpy(), rtol=1e-12, atol=1e-12, what="dW")
+    assert_close(db, bt.grad.numpy(), rtol=1e-12, atol=1e-12, what="db")
+    assert_close(dX, xt.grad.numpy(), rtol=1e-12, atol=1e-12, what="dX")
+    assert (np.count_nonzero(db.reshape(G, S), axis=1) <= B).all()  # at most one winner per token
+
+
 def test_backward_accumulates_and_finite_differences(oracle):
     rng = np.random.default_rng(5)
     B, D, G, S, K = 3, 20, 2, 32, 8
