@@ -54,7 +54,7 @@ EXPORTS = ("gl_abi_version", "gl_struct_layout", "gl_error_string", "gl_fwd_work
            "gl_window_build_host", "gl_trace_begin", "gl_trace_end")
 KERNEL_NAMES = {1: "tile_x_kernel", 2: "fwd_kernel", 3: "fwd_finalize_kernel", 4: "c1t_kernel", 5: "bwd_w_kernel",
                 6: "dx_kernel", 7: "dx_reduce_kernel", 8: "adam_kernel", 9: "edges_build", 10: "fwd_kernel_win",
-                11: "bwd_w_kernel_win"}
+                11: "bwd_w_kernel_win", 12: "max_events_dw_kernel", 13: "max_events_dx_kernel"}
 
 
 class NativeError(RuntimeError):

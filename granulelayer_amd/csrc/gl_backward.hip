@@ -691,6 +691,7 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
   if (!a || !a->g_pre || !a->dW || !a->db || !a->dX || !a->edges) return GL_ERR_ARG;
   if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;
   if ((a->pool == GL_POOL_MAX) != (a->winner != nullptr)) return GL_ERR_ARG;  // winners exactly for max
+  if (a->winner && a->S >= (1 << 21)) return GL_ERR_UNSUPPORTED;  // the event sort keys hold slot << 11
   size_t need = 0;
   GL_TRY(gl_bwd_workspace(a, &need));
   if (!a->ws || a->ws_bytes < need) return GL_ERR_WORKSPACE;
@@ -717,6 +718,12 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     GL_LAUNCH(GL_KERNEL_C1T, c1t_kernel, dim3((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(cap, 32)), dim3(256), 0, s,
                        a->g_pre, a->counts, c1t, a->G, b0, Bc, cap, a->pool, a->winner, wint);
     GL_CHECK_LAUNCH();
+    if (a->winner) {  // max pooling: winner events (gl_max_bwd.hip), no dense pass
+      const MaxEvKArgs ev{xt, a->idx, a->W, a->bias, c1t, wint, a->g_pre, a->winner, a->dW, a->db, a->dX,
+                          a->D, a->G, a->S, cap, Bc, b0};
+      GL_TRY(launch_max_events(a->K, a->act, ev, s));
+      continue;
+    }
     const long long NS = (long long)a->G * a->S;
     BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, wint, a->dW, a->db, mask, a->sched, nullptr, q.n_chunks, NS,
            a->D, a->S, q.cpg, n_tiles, cap, 2 * T, ceil_div(a->S, SCHED_WIN), a->G, 0, 0};

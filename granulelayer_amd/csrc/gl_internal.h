@@ -21,6 +21,25 @@ bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, i
 int launch_tile_x(const void* X, long long sxb, int x_dtype, int B, int D, int b0, int n_tiles, float4* xt,
                   hipStream_t s);
 
+// Max-pooling backward as winner events (gl_max_bwd.hip): dW / db / dX of one token chunk
+// [b0, b0 + Bc) from the chunk's token tiles, transposed g_pre / winners (c1t_kernel) and the
+// row-major g_pre / winners.
+struct MaxEvKArgs {
+  const float4* xt;
+  const int32_t* idx;
+  const float* W;
+  const float* bias;
+  const float* c1t;
+  const int32_t* wint;
+  const float* g_pre;
+  const int32_t* winner;
+  float* dW;
+  float* db;
+  float* dX;
+  int D, G, S, cap, Bc, b0;
+};
+int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s);
+
 // Launch trace (gl_trace_begin): record an event pair around one kernel launch.
 void trace_before(hipStream_t s, int kernel_id);
 void trace_after(hipStream_t s);

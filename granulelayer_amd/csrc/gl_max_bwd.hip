@@ -1,0 +1,208 @@
+// Max-pooling backward as winner events, without floating-point atomics.
+//
+// With max pooling only the winner neuron n* = g*S + winner[b, g] of each (token, pool) receives a
+// gradient: dz = g_pre[b, g] * act'(z[b, n*]) (pytorch_reference.py:61-67 through autograd).  The
+// reference runs this as an event kernel with fp32 atomics (sparse_pooling/kernels/triton_fused.py
+// :478-520 bwd_events_kernel, launched from autograd.py:284-289), touching the winner's K edges
+// only.  Here the same events are summed in a fixed order:
+//   * max_events_dw_kernel, one workgroup per pool: each token's event recomputes z (K MACs, as
+//     the reference does for act'), the pool's events are sorted by (slot, token) in LDS, and the
+//     first event of every slot sums that slot's events in token order and adds them to dW and db
+//     (one writer per neuron);
+//   * max_events_dx_kernel, one workgroup per token: the events' dz * W[n*, k] are summed into
+//     dX[b, idx[n*, k]] as 64-bit fixed-point integers (LDS atomics: integer sums do not depend on
+//     their order).  A first pass bounds every term by |g_pre| * max_k |W[n*, k]| and picks a
+//     power-of-two scale under which the sum of all G * K terms stays below 2^62; the result is
+//     converted back once per input.
+#include "gl_common.h"
+#include "gl_internal.h"
+
+namespace gl {
+
+struct MaxEvK {
+  const float4* __restrict__ xt;      // [n_tiles][D] token tiles of the chunk (fp32)
+  const int32_t* __restrict__ idx;    // [G*S, K]
+  const float* __restrict__ W;        // [G*S, K]
+  const float* __restrict__ bias;     // [G*S]
+  const float* __restrict__ c1t;      // [G][cap] g_pre of the chunk's tokens
+  const int32_t* __restrict__ wint;   // [G][cap] winner slots of the chunk's tokens
+  const float* __restrict__ g_pre;    // [B, G]
+  const int32_t* __restrict__ winner; // [B, G]
+  float* dW;                          // [G*S, K] accumulated
+  float* db;                          // [G*S] accumulated
+  float* dX;                          // [B, D] overwritten
+  int D, G, S, cap, Bc, b0, npow2;
+};
+
+// x[b, d] of the chunk's token b from the token tiles
+__device__ __forceinline__ float tile_x(const float4* xt, int D, int b, int d) {
+  const float* e = reinterpret_cast<const float*>(xt + (long long)(b >> 2) * D + d);
+  return e[b & 3];
+}
+
+// dz of the event (token b, pool g, slot s): g_pre * act'(z), z = bias + sum_k x[idx] w in k order
+template <int K, int ACT, typename XF>
+__device__ __forceinline__ float event_dz(const MaxEvK& p, long long n, float c1, XF xat, float (&xk)[K],
+                                          float (&wk)[K], int (&dk)[K]) {
+  float z = p.bias[n];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    int d = p.idx[n * K + k];
+    d = d < 0 ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps reads in bounds
+    dk[k] = d;
+    wk[k] = p.W[n * K + k];
+    xk[k] = xat(d);
+    z = __builtin_fmaf(xk[k], wk[k], z);
+  }
+  return ACT == GL_ACT_RELU ? (z > 0.f ? c1 : 0.f) : c1;
+}
+
+// dW / db of one pool's events.  LDS: npow2 sort keys, then per token its dz and K products.
+template <int K, int ACT>
+__global__ void __launch_bounds__(256) max_events_dw_kernel(MaxEvK p) {
+  extern __shared__ unsigned lds[];
+  unsigned* keys = lds;
+  float* ev = reinterpret_cast<float*>(lds + p.npow2);  // [Bc][K + 1]: dz, dz * x_k
+  const int g = blockIdx.x;
+  for (int i = threadIdx.x; i < p.npow2; i += blockDim.x) {
+    unsigned key = ~0u;
+    if (i < p.Bc) {
+      int s = p.wint[(long long)g * p.cap + i];
+      const bool ok = s >= 0 && s < p.S;
+      s = ok ? s : 0;
+      const long long n = (long long)g * p.S + s;
+      float xk[K], wk[K];
+      int dk[K];
+      const float dz = ok ? event_dz<K, ACT>(p, n, p.c1t[(long long)g * p.cap + i],
+                                             [&](int d) { return tile_x(p.xt, p.D, i, d); }, xk, wk, dk)
+                          : 0.f;
+      float* e = ev + (long long)i * (K + 1);
+      e[0] = dz;
+#pragma unroll
+      for (int k = 0; k < K; ++k) e[1 + k] = dz * xk[k];
+      key = ((unsigned)s << 11) | (unsigned)i;  // slot, then token (Bc <= 1024 < 2^11)
+    }
+    keys[i] = key;
+  }
+  __syncthreads();
+  for (int size = 2; size <= p.npow2; size <<= 1) {  // bitonic sort, ascending
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < p.npow2 / 2; i += blockDim.x) {
+        const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+        const bool asc = (lo & size) == 0;
+        const unsigned a = keys[lo], b = keys[hi];
+        if ((a > b) == asc) keys[lo] = b, keys[hi] = a;
+      }
+      __syncthreads();
+    }
+  }
+  // the first event of each slot sums the slot's events in token order
+  for (int i = threadIdx.x; i < p.Bc; i += blockDim.x) {
+    const unsigned s = keys[i] >> 11;
+    if (i > 0 && (keys[i - 1] >> 11) == s) continue;
+    float acc[K + 1];
+#pragma unroll
+    for (int k = 0; k <= K; ++k) acc[k] = 0.f;
+    for (int j = i; j < p.Bc && (keys[j] >> 11) == s; ++j) {
+      const float* e = ev + (long long)(keys[j] & 2047u) * (K + 1);
+#pragma unroll
+      for (int k = 0; k <= K; ++k) acc[k] += e[k];
+    }
+    const long long n = (long long)g * p.S + s;
+    p.db[n] += acc[0];
+#pragma unroll
+    for (int k = 0; k < K; ++k) p.dW[n * K + k] += acc[1 + k];
+  }
+}
+
+// dX of one token.  LDS: the token's X row (D floats), then D 64-bit fixed-point accumulators.
+template <int K, int ACT>
+__global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
+  extern __shared__ unsigned long long ldsq[];
+  unsigned long long* acc = ldsq;                               // [D]
+  float* xrow = reinterpret_cast<float*>(ldsq + p.D);            // [D]
+  __shared__ float wmax[16];
+  __shared__ double scale_s;
+  const int b = blockIdx.x;
+  const long long row = (long long)(p.b0 + b) * p.G;
+  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
+    xrow[d] = tile_x(p.xt, p.D, b, d);
+    acc[d] = 0ull;
+  }
+  // pass 1: every term |dz * W[n*, k]| is at most |g_pre| * max_k |W[n*, k]|
+  float m = 0.f;
+  for (int g = threadIdx.x; g < p.G; g += blockDim.x) {
+    int s = p.winner[row + g];
+    s = s < 0 ? 0 : (s >= p.S ? p.S - 1 : s);
+    const long long n = (long long)g * p.S + s;
+    float wm = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) wm = __builtin_fmaxf(wm, __builtin_fabsf(p.W[n * K + k]));
+    m = __builtin_fmaxf(m, __builtin_fabsf(p.g_pre[row + g]) * wm);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t = __builtin_fmaxf(t, wmax[w]);
+    const double total = (double)t * (double)p.G * (double)K;  // bound of |sum| over all terms
+    // |sum| * scale < 2^62 (and no term's scaled value exceeds it): scale = 2^(61 - floor(log2 total)),
+    // floor(log2) read from the (normal) double's exponent field, the power kept in the normal range
+    double sc = 1.0;
+    if (total > 0.0) {
+      const int e2 = (int)((__double_as_longlong(total) >> 52) & 0x7ff) - 1023;
+      int e = 61 - e2;
+      e = e > 1000 ? 1000 : (e < -1000 ? -1000 : e);
+      sc = __longlong_as_double((long long)(1023 + e) << 52);
+    }
+    scale_s = sc;
+  }
+  __syncthreads();
+  const double scale = scale_s;
+  // pass 2: the events' dz * W[n*, k] as fixed-point integers
+  for (int g = threadIdx.x; g < p.G; g += blockDim.x) {
+    int s = p.winner[row + g];
+    const bool ok = s >= 0 && s < p.S;
+    s = ok ? s : 0;
+    const long long n = (long long)g * p.S + s;
+    float xk[K], wk[K];
+    int dk[K];
+    const float dz = event_dz<K, ACT>(p, n, p.g_pre[row + g], [&](int d) { return xrow[d]; }, xk, wk, dk);
+    if (!ok || dz == 0.f) continue;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const long long q = __double2ll_rn((double)(dz * wk[k]) * scale);
+      atomicAdd(&acc[dk[k]], (unsigned long long)q);
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < p.D; d += blockDim.x)
+    p.dX[(long long)(p.b0 + b) * p.D + d] = (float)((double)(long long)acc[d] / scale);
+}
+
+template <int K, int ACT>
+static int launch_max_events_k(const MaxEvK& k, hipStream_t s) {
+  const size_t dw_lds = (size_t)k.npow2 * 4 + (size_t)k.Bc * (K + 1) * 4;
+  const size_t dx_lds = (size_t)k.D * 12;
+  if (dw_lds > max_lds_bytes() || dx_lds > max_lds_bytes()) return GL_ERR_LDS;
+  GL_TRY(set_lds_limit((const void*)max_events_dw_kernel<K, ACT>, dw_lds));
+  GL_TRY(set_lds_limit((const void*)max_events_dx_kernel<K, ACT>, dx_lds));
+  GL_LAUNCH(GL_KERNEL_MAX_EV_DW, (max_events_dw_kernel<K, ACT>), dim3((unsigned)k.G), dim3(256), dw_lds, s, k);
+  GL_CHECK_LAUNCH();
+  GL_LAUNCH(GL_KERNEL_MAX_EV_DX, (max_events_dx_kernel<K, ACT>), dim3((unsigned)k.Bc), dim3(1024), dx_lds, s, k);
+  GL_CHECK_LAUNCH();
+  return 0;
+}
+
+int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s) {
+  int npow2 = 1;
+  while (npow2 < a.Bc) npow2 <<= 1;
+  const MaxEvK k{a.xt, a.idx, a.W, a.bias, a.c1t, a.wint, a.g_pre, a.winner, a.dW, a.db, a.dX,
+                 a.D, a.G, a.S, a.cap, a.Bc, a.b0, npow2};
+  if (K == 8) return act == GL_ACT_RELU ? launch_max_events_k<8, GL_ACT_RELU>(k, s) : launch_max_events_k<8, GL_ACT_IDENTITY>(k, s);
+  return act == GL_ACT_RELU ? launch_max_events_k<16, GL_ACT_RELU>(k, s) : launch_max_events_k<16, GL_ACT_IDENTITY>(k, s);
+}
+
+}  // namespace gl

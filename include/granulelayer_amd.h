@@ -175,7 +175,8 @@ int gl_window_build_host(const int32_t* idx, const int32_t* counts, int32_t D, i
 enum {
   GL_KERNEL_TILE_X = 1, GL_KERNEL_FWD = 2, GL_KERNEL_FWD_FINALIZE = 3, GL_KERNEL_C1T = 4, GL_KERNEL_BWD_W = 5,
   GL_KERNEL_DX = 6, GL_KERNEL_DX_REDUCE = 7, GL_KERNEL_ADAM = 8, GL_KERNEL_EDGES = 9,
-  GL_KERNEL_FWD_WIN = 10, GL_KERNEL_BWD_W_WIN = 11  /* forward / dW with pool-window staging */
+  GL_KERNEL_FWD_WIN = 10, GL_KERNEL_BWD_W_WIN = 11, /* forward / dW with pool-window staging */
+  GL_KERNEL_MAX_EV_DW = 12, GL_KERNEL_MAX_EV_DX = 13  /* max-pooling backward: winner events */
 };
 
 /* Launch trace for benchmarks and tests (process-wide, not for concurrent callers): after

@@ -432,9 +432,19 @@ def test_max_backward_matches_oracle(case, act):
     rt = runtime(L, idx, "max", act)
     xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
     stats = rt.forward(xd, wd, bd, track_ids=True)
+    from granulelayer_amd import _native as N
+
     dw = torch.zeros(L.weight_shape, device=DEV)
     db = torch.zeros(L.bias_shape, device=DEV)
-    dx = rt.backward(xd, wd, bd, dy.to(DEV), stats, "save_winners", dw, db).cpu().numpy()
+    with N.KernelTrace() as tr:
+        dx = rt.backward(xd, wd, bd, dy.to(DEV), stats, "save_winners", dw, db).cpu().numpy()
+    # the winner-event kernels ran, not the dense dW / dX passes
+    names = set(tr.times_ms())
+    assert {"max_events_dw_kernel", "max_events_dx_kernel"} <= names and "dx_kernel" not in names, sorted(names)
+    # deterministic: a second backward gives the same bits
+    dw2, db2 = torch.zeros_like(dw), torch.zeros_like(db)
+    dx2 = rt.backward(xd, wd, bd, dy.to(DEV), stats, "save_winners", dw2, db2).cpu().numpy()
+    assert np.array_equal(dx, dx2) and torch.equal(dw, dw2) and torch.equal(db, db2)
     fi, fw, fb = flat(L, idx, w, b)
     counts = L.counts_tensor("cpu").numpy()
     wdW, wdb, wdX, bnd = O.backward(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, dy.numpy(), act, "max",
