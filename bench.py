@@ -179,9 +179,10 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--config", choices=sorted(CONFIG_WORK), default=None,
                     help="time one BASELINE config's own work at full size instead of the headline step")
-    ap.add_argument("--pooling", choices=("sum", "mean", "max"), default="sum",
+    ap.add_argument("--pooling", choices=("sum", "mean", "max", "topk"), default="sum",
                     help="pooling of the train-step layer (default: the headline's sum of relu; max: the "
-                         "reference's defaults, relu(max z), winners saved for backward)")
+                         "reference's defaults, relu(max z), winners saved for backward; topk: top-8 mean, "
+                         "slots saved)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -217,7 +218,8 @@ def main():
     dev = torch.device("cuda", 0)
     t0 = time.time()
     log(f"building layer N={N:,} K={K} D={D} G={G:,} on {torch.cuda.get_device_name(0)}")
-    lay = SparsePoolingLayer(D, N, G, fan_in=K, shared_neurons=None, pooling=args.pooling, dtype=torch.float32,
+    pooling = {"type": "topk_mean", "k": 8} if args.pooling == "topk" else args.pooling
+    lay = SparsePoolingLayer(D, N, G, fan_in=K, shared_neurons=None, pooling=pooling, dtype=torch.float32,
                              device=dev, seed=0)
     lay.enable_main_grad()
     opt = FusedAdamW(lay.parameters(), lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, moments="fp32")
@@ -313,7 +315,8 @@ def main():
         "data": "synthetic (seeded: uniform distinct indices, W~N(0,1/8), bias 0, X and dY ~N(0,1))",
         "config": {"workload": "C2-shaped train step: fwd + recompute bwd (dX, dW, db) + fused AdamW",
                    "neurons": N, "fan_in": K, "d_in": D, "batch": B, "pool": pool, "groups": G,
-                   "pooling": {"sum": "sum(relu)", "mean": "mean(relu)", "max": "relu(max z)"}[args.pooling], "x_dtype": "f32", "moments": "f32", "parallelism": "single GPU"},
+                   "pooling": {"sum": "sum(relu)", "mean": "mean(relu)", "max": "relu(max z)",
+                               "topk": "top-8 mean(z)"}[args.pooling], "x_dtype": "f32", "moments": "f32", "parallelism": "single GPU"},
         "fwd_ms": round(fwd_ms, 3),
         "fwd_G_edge_macs_per_s": round(B * E / (fwd_ms * 1e-3) / 1e9, 2),
         "kernels": kernels,

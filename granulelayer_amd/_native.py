@@ -13,10 +13,10 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgranulelayer_amd.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 GL_ACT = {"identity": 0, "relu": 1}
-GL_POOL = {"mean": 0, "sum": 1, "max": 2}
+GL_POOL = {"mean": 0, "sum": 1, "max": 2, "topk_mean": 3}
 GL_DTYPE_F32, GL_DTYPE_BF16 = 0, 1
 
 _P, _I32, _I64, _SZ, _F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
@@ -24,14 +24,14 @@ _P, _I32, _I64, _SZ, _F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctype
 
 class GlFwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
-                ("K", _I32), ("act", _I32), ("pool", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
+                ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("pre", _P), ("winner", _P), ("ws", _P),
                 ("ws_bytes", _SZ)]
 
 
 class GlBwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
-                ("K", _I32), ("act", _I32), ("pool", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
+                ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("g_pre", _P), ("winner", _P), ("dW", _P), ("db", _P),
                 ("dX", _P), ("edges", _P), ("edges_bytes", _SZ),
                 ("ws", _P), ("ws_bytes", _SZ)]

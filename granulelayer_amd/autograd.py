@@ -175,12 +175,13 @@ def _grad_buffers(w, b):
 
 def _saved_stats(level: LevelSpec, out: Dict[str, torch.Tensor], policy: str) -> Dict[str, torch.Tensor]:
     """What the forward keeps for backward (autograd.py:366-377): pre, and with save_winners the
-    max-pooling winner ids."""
+    max-pooling winner ids or the top-k slots."""
     if policy == "recompute_stats":
         return {}
     keep = {"pre": out["pre"]}
-    if policy == "save_winners" and "winner" in out:
-        keep["winner"] = out["winner"]
+    for key in ("winner", "topk_slot"):
+        if policy == "save_winners" and key in out:
+            keep[key] = out[key]
     return keep
 
 
@@ -211,7 +212,8 @@ class SparsePoolFunction(torch.autograd.Function):
         xc, wc, bc = _compute_operands(x, w, b, ctx.compute_dtype)
         # statistics the backward needs and the policy did not save (autograd.py:246-258): max
         # pooling needs the winners, so minimal_stats recomputes the forward with track_ids
-        recomputed = "pre" not in saved or (lv.type == "max" and "winner" not in saved)
+        need = {"max": "winner", "topk_mean": "topk_slot"}.get(lv.type)
+        recomputed = "pre" not in saved or (need is not None and need not in saved)
         if recomputed:
             saved.update(rt.forward(xc, wc, bc, track_ids=True))
         g_pre = dy.float() * dact_torch(saved["pre"], lv.out_activation)

@@ -4,7 +4,7 @@
 backend (sparse_pooling/autograd.py:220-223 and :265-267; implemented for CUDA at
 sparse_pooling/backends/cuda/runtime.py:339-712):
 
-    forward(rt, x, w, b, track_ids)                     -> {"pre": [B, U] fp32[, "winner": [B, U] int32]}
+    forward(rt, x, w, b, track_ids)                     -> {"pre": [B, U] fp32[, "winner" | "topk_slot"]}
     backward(rt, x, w, b, g_pre, stats, dw_buf, db_buf) -> dX [B, D] fp32 (dW/db accumulated)
 
 plus ``adam`` (the FusedAdamW launch, sparse_pooling/optim.py:116-123) and ``edges`` (the
@@ -114,15 +114,21 @@ class HipBackend:
         w, b = _f32(w, "weight"), _f32(b, "bias")
         B = x.shape[0]
         pre = torch.empty((B, G), device=x.device, dtype=torch.float32)
-        # max pooling with track_ids: the winner slot of every (token, pool), the reference's
-        # "winner" statistic (kernels/ops.py:189-195)
-        winner = torch.empty((B, G), device=x.device, dtype=torch.int32) if (track_ids and pool == N.GL_POOL["max"]) else None
-        out = {"pre": pre} if winner is None else {"pre": pre, "winner": winner}
+        # with track_ids, the selected slots: max pooling's "winner" [B, U] and top-k mean's
+        # "topk_slot" [B, U, k] (best first, -1 past min(n_g, k)), the reference's statistics
+        # (kernels/ops.py:189-195, 212-228)
+        topk = rt.level.k if pool == N.GL_POOL["topk_mean"] else 0
+        winner, key = None, None
+        if track_ids and pool == N.GL_POOL["max"]:
+            winner, key = torch.empty((B, G), device=x.device, dtype=torch.int32), "winner"
+        elif track_ids and topk:
+            winner, key = torch.empty((B, G, topk), device=x.device, dtype=torch.int32), "topk_slot"
+        out = {"pre": pre} if winner is None else {"pre": pre, key: winner}
         if B == 0:
             return out
         win_lo, win_width = self.windows(rt)
         a = N.GlFwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=L.input_dim, G=G, S=S, K=K, act=act, pool=pool,
-                        idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
+                        topk=topk, idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, pre=_ptr(pre),
                         winner=_ptr(winner))
         with torch.cuda.device(x.device):
@@ -203,13 +209,16 @@ class HipBackend:
         for name, t, shape in (("dw_buf", dw_buf, L.weight_shape), ("db_buf", db_buf, L.bias_shape)):
             if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != tuple(shape):
                 raise ValueError(f"{name} must be a contiguous float32 tensor of shape {tuple(shape)}")
-        winner = None
-        if pool == N.GL_POOL["max"]:  # the only neuron of a (token, pool) with a gradient
-            winner = stats.get("winner")
+        # max / top-k mean: the selected neurons are the only ones with a gradient
+        winner, topk = None, 0
+        if pool in (N.GL_POOL["max"], N.GL_POOL["topk_mean"]):
+            key, shape = ("winner", (B, G)) if pool == N.GL_POOL["max"] else ("topk_slot", (B, G, rt.level.k))
+            topk = rt.level.k if pool == N.GL_POOL["topk_mean"] else 0
+            winner = stats.get(key)
             if winner is None:
-                raise ValueError("max pooling backward needs the forward's winner ids (stats['winner'])")
-            if winner.dtype != torch.int32 or tuple(winner.shape) != (B, G) or winner.device != x.device:
-                raise ValueError(f"winner must be an int32 [{B}, {G}] tensor on {x.device}")
+                raise ValueError(f"{rt.level.type} backward needs the forward's selected slots (stats[{key!r}])")
+            if winner.dtype != torch.int32 or tuple(winner.shape) != shape or winner.device != x.device:
+                raise ValueError(f"{key} must be an int32 {list(shape)} tensor on {x.device}")
             winner = winner.contiguous()
         dx = torch.empty((B, D), device=x.device, dtype=torch.float32)
         if B == 0:
@@ -217,7 +226,7 @@ class HipBackend:
         win_lo, win_width = self.windows(rt)
         edges = self.edges(rt)
         a = N.GlBwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=D, G=G, S=S, K=K, act=act, pool=pool,
-                        idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
+                        topk=topk, idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, g_pre=_ptr(g_pre),
                         winner=_ptr(winner),
                         dW=_ptr(dw_buf), db=_ptr(db_buf), dX=_ptr(dx), edges=_ptr(edges),

@@ -20,7 +20,7 @@ POOL_ID = {name: i for i, name in enumerate(POOL_TYPES)}
 ACT_ID = {name: i for i, name in enumerate(ACTIVATIONS)}
 
 # operators executed by the HIP path (everything else parses but is refused at run time)
-HIP_POOLS = ("mean", "sum", "max")
+HIP_POOLS = ("mean", "sum", "max", "topk_mean")
 HIP_ACTIVATIONS = ("identity", "relu")
 
 _DEFAULT_ACT = {"max": "identity", "topk_mean": "identity", "mean": "relu", "logmeanexp": "identity",

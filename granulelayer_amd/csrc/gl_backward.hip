@@ -19,12 +19,13 @@
 
 namespace gl {
 
-// c1t[g, b] = g_pre[b0 + b, g] * scale_g for b < Bc, zero up to cap (tiled transpose).  Max
-// pooling (winner != null) also transposes the winner slots: wint[g, b] = winner[b0 + b, g], -1 up
-// to cap.
+// c1t[g, b] = g_pre[b0 + b, g] * scale_g for b < Bc, zero up to cap (tiled transpose); scale_g =
+// 1 / n_g (mean), 1 / min(n_g, k) (top-k mean), else 1.  Max pooling (winner != null) also
+// transposes the winner slots: wint[g, b] = winner[b0 + b, g], -1 up to cap.
 __global__ void __launch_bounds__(256) c1t_kernel(const float* __restrict__ g_pre, const int32_t* __restrict__ counts,
                                                   float* __restrict__ c1t, int G, int b0, int Bc, int cap, int pool,
-                                                  const int32_t* __restrict__ winner, int32_t* __restrict__ wint) {
+                                                  int topk, const int32_t* __restrict__ winner,
+                                                  int32_t* __restrict__ wint) {
   __shared__ float tile[32][33];
   __shared__ int tw[32][33];
   const int g0 = blockIdx.x * 32, bb = blockIdx.y * 32;
@@ -41,10 +42,23 @@ __global__ void __launch_bounds__(256) c1t_kernel(const float* __restrict__ g_pr
     if (g < G && b < cap) {
       float v = tile[tx][r];
       if (pool == GL_POOL_MEAN) v = v / (float)counts[g];
+      if (pool == GL_POOL_TOPK_MEAN) v = v / (float)(counts[g] < topk ? counts[g] : topk);
       c1t[(long long)g * cap + b] = v;
       if (winner) wint[(long long)g * cap + b] = tw[tx][r];
     }
   }
+}
+
+// Top-k slots of the chunk's tokens, pool-major: wint[g, b, j] = slots[b0 + b, g, j] (-1 past Bc).
+__global__ void __launch_bounds__(256) events_transpose_kernel(const int32_t* __restrict__ slots,
+                                                               int32_t* __restrict__ wint, int G, int b0, int Bc,
+                                                               int cap, int kpe) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;  // (g, b, j), j fastest
+  if (i >= (long long)G * cap * kpe) return;
+  const int j = (int)(i % kpe);
+  const long long gb = i / kpe;
+  const int b = (int)(gb % cap), g = (int)(gb / cap);
+  wint[i] = b < Bc ? slots[((long long)(b0 + b) * G + g) * kpe + j] : -1;
 }
 
 struct BwK {
@@ -54,7 +68,6 @@ struct BwK {
   const float* __restrict__ bias;
   const int32_t* __restrict__ counts;
   const float* __restrict__ c1t;
-  const int32_t* __restrict__ wint;  // max pooling: [G][cap] winner slot of each token, else null
   float* dW;
   float* db;
   uint32_t* mask;  // [n_tc][G*S][mw2] activation-mask words (one slab per dX token slice)
@@ -67,12 +80,9 @@ struct BwK {
 
 // One token tile of the dW pass (LDS at xsb): recompute z, form dz = c1 * act'(z), accumulate
 // db, dW and the tile's 4 mask bits (bit 4 (t % 8) + i of word mw for token i of tile t).  The
-// first RA LDS reads of neuron j + 1 are issued before the arithmetic of neuron j.  Max pooling
-// (MAXP): only the token's winner slot gets dz (the event backward, autograd.py:284-289), so the
-// mask bit is act'(z) and slot == winner.
-template <int K, int NPL, int ACT, int RA, bool FAR, bool MAXP>
-__device__ __forceinline__ void bwd_w_tile(const char* xsb, int t, const float4 c1, const int4 wn,
-                                           const unsigned (&slot2)[(NPL + 1) / 2], const unsigned (&addr)[NPL][K],
+// first RA LDS reads of neuron j + 1 are issued before the arithmetic of neuron j.
+template <int K, int NPL, int ACT, int RA, bool FAR>
+__device__ __forceinline__ void bwd_w_tile(const char* xsb, int t, const float4 c1, const unsigned (&addr)[NPL][K],
                                            const float (&w)[NPL][K], const float (&bias)[NPL], float (&dw)[NPL][K],
                                            float (&dbv)[NPL], unsigned (&mw)[NPL]) {
   float4 xc[K];
@@ -96,12 +106,8 @@ __device__ __forceinline__ void bwd_w_tile(const char* xsb, int t, const float4 
       z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
       z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
     }
-    bool m0 = ACT != GL_ACT_RELU || z0 > 0.f, m1 = ACT != GL_ACT_RELU || z1 > 0.f;
-    bool m2 = ACT != GL_ACT_RELU || z2 > 0.f, m3 = ACT != GL_ACT_RELU || z3 > 0.f;
-    if constexpr (MAXP) {
-      const int sj = (int)((slot2[j / 2] >> (16 * (j % 2))) & 0xffffu);
-      m0 = m0 && sj == wn.x, m1 = m1 && sj == wn.y, m2 = m2 && sj == wn.z, m3 = m3 && sj == wn.w;
-    }
+    const bool m0 = ACT != GL_ACT_RELU || z0 > 0.f, m1 = ACT != GL_ACT_RELU || z1 > 0.f;
+    const bool m2 = ACT != GL_ACT_RELU || z2 > 0.f, m3 = ACT != GL_ACT_RELU || z3 > 0.f;
     const float d0 = m0 ? c1.x : 0.f, d1 = m1 ? c1.y : 0.f, d2 = m2 ? c1.z : 0.f, d3 = m3 ? c1.w : 0.f;
     dbv[j] = dbv[j] + d0 + d1 + d2 + d3;
 #pragma unroll
@@ -128,7 +134,7 @@ __device__ __forceinline__ void bwd_w_tile(const char* xsb, int t, const float4 
 // VGPRs a wave has at 2 waves per SIMD with the dW accumulators live).  Otherwise one buffer:
 // load, wait, read.  The wave index goes through readfirstlane so the chunk's parameters and the
 // c1 row are addressed with scalar registers.
-template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF, bool WS = false, bool MAXP = false>
+template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF, bool WS = false>
 __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   __shared__ float4 xs[DBUF || WS ? 2 * XTILE_DB : XTILE_SB];
   const int lane = threadIdx.x & 63;
@@ -171,7 +177,6 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
     dbv[j] = 0.f;
   }
   const float* c1row = p.c1t + g * p.cap;
-  const int32_t* wrow = MAXP ? p.wint + g * p.cap : nullptr;
   constexpr int NT = WAVES * 64;
 
   // window staging: WS_TILES tiles per stage and barrier; tile t at slot (t mod 2 WS_TILES) * nsl
@@ -206,9 +211,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
         for (int tt = 0; tt < tn; ++tt) {
           const int t = ts0 + tt;
           const float4 c1 = ld_uniform4(c1row, t * BT);
-          const int4 wn = MAXP ? ld_uniform4i(wrow, t * BT) : int4{};
-          bwd_w_tile<K, NPL, ACT, RA, false, MAXP>(reinterpret_cast<const char*>(xs), t, c1, wn, slot2, addr, w, bias,
-                                                   dw, dbv, mw);
+          bwd_w_tile<K, NPL, ACT, RA, false>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw, dbv, mw);
           // next tile's slot; after the last tile of region 1 back to region 0 (uniform step, no branch)
           const unsigned step = (t & (2 * WS_TILES - 1)) == 2 * WS_TILES - 1 ? tstep - 2u * WS_TILES * tstep : tstep;
 #pragma unroll
@@ -226,20 +229,17 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
         const int cur = t & 1;
         if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xs + (cur ^ 1) * XTILE_DB, p.D, NT);
         const float4 c1 = ld_uniform4(c1row, t * BT);
-        const int4 wn = MAXP ? ld_uniform4i(wrow, t * BT) : int4{};
-        bwd_w_tile<K, NPL, ACT, RA, true, MAXP>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t,
-                                                c1, wn, slot2, addr, w, bias, dw, dbv, mw);
+        bwd_w_tile<K, NPL, ACT, RA, true>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t, c1,
+                                          addr, w, bias, dw, dbv, mw);
         stage_wait();  // tile t + 1 is in LDS for this wave's copies; the barrier publishes every wave's
         __syncthreads();
       } else {
         __syncthreads();  // every wave is done with tile t - 1
         dma_tile(p.xt + (long long)t * p.D, xs, p.D, NT);
         const float4 c1 = ld_uniform4(c1row, t * BT);
-        const int4 wn = MAXP ? ld_uniform4i(wrow, t * BT) : int4{};
         stage_wait();
         __syncthreads();
-        bwd_w_tile<K, NPL, ACT, RA, false, MAXP>(reinterpret_cast<const char*>(xs), t, c1, wn, slot2, addr, w, bias, dw,
-                                                 dbv, mw);
+        bwd_w_tile<K, NPL, ACT, RA, false>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw, dbv, mw);
       }
     }
     const int word = t0 >> 3;
@@ -630,11 +630,10 @@ void edge_layout(int D, int G, int S, int K, EdgeHeader* h, size_t* total) {
   *total = off;
 }
 
-template <int K, int NPL, int WAVES, int ACT, int RA, bool MAXP>
+template <int K, int NPL, int WAVES, int ACT, int RA>
 static int launch_bwd_w(const BwK& k, hipStream_t s) {
-  auto fn = k.win ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, true, MAXP>
-                  : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true, false, MAXP>
-                                     : bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, false, MAXP>);
+  auto fn = k.win ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, true>
+                  : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true> : bwd_w_kernel<K, NPL, WAVES, ACT, RA, false>);
   GL_LAUNCH(k.win ? GL_KERNEL_BWD_W_WIN : GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)),
             dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
@@ -642,18 +641,14 @@ static int launch_bwd_w(const BwK& k, hipStream_t s) {
 }
 
 // read-ahead of 2 LDS reads (more would spill)
-template <int ACT, bool MAXP>
+template <int ACT>
 static int launch_bwd_w_act(int K, const BwK& k, hipStream_t s) {
-  if (K == 8) return launch_bwd_w<8, bwd_npl(8), bwd_waves(8), ACT, 2, MAXP>(k, s);
-  return launch_bwd_w<16, bwd_npl(16), bwd_waves(16), ACT, 2, MAXP>(k, s);
+  if (K == 8) return launch_bwd_w<8, bwd_npl(8), bwd_waves(8), ACT, 2>(k, s);
+  return launch_bwd_w<16, bwd_npl(16), bwd_waves(16), ACT, 2>(k, s);
 }
 
-static int launch_bwd_w_any(int K, int act, bool maxp, const BwK& k, hipStream_t s) {
-  if (maxp)
-    return act == GL_ACT_RELU ? launch_bwd_w_act<GL_ACT_RELU, true>(K, k, s)
-                              : launch_bwd_w_act<GL_ACT_IDENTITY, true>(K, k, s);
-  return act == GL_ACT_RELU ? launch_bwd_w_act<GL_ACT_RELU, false>(K, k, s)
-                            : launch_bwd_w_act<GL_ACT_IDENTITY, false>(K, k, s);
+static int launch_bwd_w_any(int K, int act, const BwK& k, hipStream_t s) {
+  return act == GL_ACT_RELU ? launch_bwd_w_act<GL_ACT_RELU>(K, k, s) : launch_bwd_w_act<GL_ACT_IDENTITY>(K, k, s);
 }
 
 template <int K, int T>
@@ -682,15 +677,18 @@ extern "C" int gl_bwd_workspace(const GlBwdArgs* a, size_t* bytes) {
   GL_TRY(check_layer(a->B, a->D, a->G, a->S, a->K, a->act, a->pool, a->X, a->idx, a->W, a->bias, a->counts,
                      a->x_dtype));
   BwdPlan q = bwd_plan(a->B, a->D, a->G, a->S, a->K);
-  // max pooling: the transposed winner slots, laid out like c1t
-  *bytes = q.xt_bytes + q.c1_bytes + q.mask_bytes + q.part_bytes + (a->pool == GL_POOL_MAX ? q.c1_bytes : 0);
+  GL_TRY(check_topk(a->pool, a->topk, a->S));
+  // max / top-k pooling: the transposed selected slots, laid out like c1t (times k for top-k)
+  const size_t kpe = a->pool == GL_POOL_TOPK_MEAN ? (size_t)a->topk : (a->pool == GL_POOL_MAX ? 1 : 0);
+  *bytes = q.xt_bytes + q.c1_bytes + q.mask_bytes + q.part_bytes + kpe * q.c1_bytes;
   return 0;
 }
 
 extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
   if (!a || !a->g_pre || !a->dW || !a->db || !a->dX || !a->edges) return GL_ERR_ARG;
   if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;
-  if ((a->pool == GL_POOL_MAX) != (a->winner != nullptr)) return GL_ERR_ARG;  // winners exactly for max
+  const bool sel = a->pool == GL_POOL_MAX || a->pool == GL_POOL_TOPK_MEAN;
+  if (sel != (a->winner != nullptr)) return GL_ERR_ARG;  // selected slots exactly for max / top-k
   if (a->winner && a->S >= (1 << 21)) return GL_ERR_UNSUPPORTED;  // the event sort keys hold slot << 11
   size_t need = 0;
   GL_TRY(gl_bwd_workspace(a, &need));
@@ -715,20 +713,27 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     const int T = dx_slots(Bc);
     const int cap = dx_cap(Bc);
     GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles, xt, s));
+    const int kpe = a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1;
     GL_LAUNCH(GL_KERNEL_C1T, c1t_kernel, dim3((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(cap, 32)), dim3(256), 0, s,
-                       a->g_pre, a->counts, c1t, a->G, b0, Bc, cap, a->pool, a->winner, wint);
+                       a->g_pre, a->counts, c1t, a->G, b0, Bc, cap, a->pool, a->topk, kpe == 1 ? a->winner : nullptr,
+                       wint);
     GL_CHECK_LAUNCH();
-    if (a->winner) {  // max pooling: winner events (gl_max_bwd.hip), no dense pass
-      const MaxEvKArgs ev{xt, a->idx, a->W, a->bias, c1t, wint, a->g_pre, a->winner, a->dW, a->db, a->dX,
-                          a->D, a->G, a->S, cap, Bc, b0};
+    if (a->winner) {  // max / top-k pooling: selection events (gl_max_bwd.hip), no dense pass
+      if (kpe > 1) {
+        GL_LAUNCH(GL_KERNEL_C1T, events_transpose_kernel, dim3((unsigned)ceil_div((long long)a->G * cap * kpe, 256)),
+                  dim3(256), 0, s, a->winner, wint, a->G, b0, Bc, cap, kpe);
+        GL_CHECK_LAUNCH();
+      }
+      const MaxEvKArgs ev{xt, a->idx, a->W, a->bias, a->counts, c1t, wint, a->g_pre, a->winner, a->dW, a->db, a->dX,
+                          a->D, a->G, a->S, cap, Bc, b0, kpe, a->pool == GL_POOL_TOPK_MEAN};
       GL_TRY(launch_max_events(a->K, a->act, ev, s));
       continue;
     }
     const long long NS = (long long)a->G * a->S;
-    BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, wint, a->dW, a->db, mask, a->sched, nullptr, q.n_chunks, NS,
+    BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, a->sched, nullptr, q.n_chunks, NS,
            a->D, a->S, q.cpg, n_tiles, cap, 2 * T, ceil_div(a->S, SCHED_WIN), a->G, 0, 0};
     if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &bk.ww, &bk.npw)) bk.win = a->win;
-    GL_TRY(launch_bwd_w_any(a->K, a->act, a->winner != nullptr, bk, s));
+    GL_TRY(launch_bwd_w_any(a->K, a->act, bk, s));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
            (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, a->W, part,
            NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * T)};

@@ -195,11 +195,6 @@ __device__ __forceinline__ float4 ld_uniform4(const float* row, int i) {
   const CF* q = (const CF*)(row + i);
   return make_float4(q[0], q[1], q[2], q[3]);
 }
-__device__ __forceinline__ int4 ld_uniform4i(const int32_t* row, int i) {
-  typedef const __attribute__((address_space(4))) int32_t CI;
-  const CI* q = (const CI*)(row + i);
-  return make_int4(q[0], q[1], q[2], q[3]);
-}
 // X slot at byte offset a of a tile buffer.  FAR: the buffer's base does not fit the 16-bit
 // ds_read offset, so base + a costs one v_add per read; the offset then passes through an empty
 // asm so the compiler keeps doing that add at the read instead of hoisting a second copy of every

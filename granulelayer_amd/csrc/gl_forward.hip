@@ -51,7 +51,8 @@ struct FwdK {
   const float* bias;
   const int32_t* counts;
   float* part;            // [n_chunks][b_pad]
-  int* pslot;             // max pooling: [n_chunks][b_pad] slot of each partial maximum
+  int* pslot;             // max / top-k pooling: [n_chunks][b_pad][kp] slot of each partial candidate
+  int topk;               // top-k pooling: k (candidates per chunk and token)
   const uint32_t* sched;  // gather schedule or null
   const uint32_t* win;    // per-pool window starts (window staging) or null
   long long n_chunks;
@@ -164,16 +165,103 @@ __device__ __forceinline__ void fwd_tile_max(const char* xsb, const unsigned (&a
   }
 }
 
-// sum / mean tile or max tile
-template <int K, int NPL, int ACT, bool FAR, bool MAXP>
+// (value, slot) list of one token, best first (value descending, then the smaller slot)
+__device__ __forceinline__ void cand_cmpex(float& va, int& sa, float& vb, int& sb) {
+  const bool swap = vb > va || (vb == va && sb < sa);
+  const float tv = va;
+  const int ts = sa;
+  va = swap ? vb : va, sa = swap ? sb : sa;
+  vb = swap ? tv : vb, sb = swap ? ts : sb;
+}
+
+// drop the list's head when it is the round's winner w
+__device__ __forceinline__ void cand_pop(float (&v)[4], int (&sl)[4], int w) {
+  const bool take = sl[0] == w;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) v[i] = take ? v[i + 1] : v[i], sl[i] = take ? sl[i + 1] : sl[i];
+  v[3] = take ? -__builtin_inff() : v[3];
+  sl[3] = take ? 0x7fffffff : sl[3];
+}
+
+// Top-k tile (top-k mean pooling, pytorch_reference.py:68-77): per token the k largest raw z of the
+// wave's neurons with their slots (ties to the smaller slot), best first.  Every lane sorts its 4
+// candidates per token; then k rounds take the wave's best head (wave_max4) and drop it from the
+// lane that holds it.  Lanes 0-3 store each round's pair; the finalize merges the pool's chunks.
+template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8)>
+__device__ __forceinline__ void fwd_tile_topk(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+                                              const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
+                                              int k, bool store, int lane) {
+  static_assert(NPL == 4, "per-lane candidate lists of 4");
+  float v[4][4];  // [token][position]
+  int sv[4][4];
+  float4 xc[K];
+#pragma unroll
+  for (int k0 = 0; k0 < RA; ++k0) xc[k0] = lds_x<FAR>(xsb, addr[0][k0]);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+#pragma unroll
+    for (int kk = RA; kk < K; ++kk) xc[kk] = lds_x<FAR>(xsb, addr[j][kk]);
+    float4 xn[RA];
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int kk = 0; kk < RA; ++kk) xn[kk] = lds_x<FAR>(xsb, addr[j + 1][kk]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+#pragma unroll
+    for (int kk = 0; kk < K; ++kk) {
+      z0 = __builtin_fmaf(xc[kk].x, w[j][kk], z0);
+      z1 = __builtin_fmaf(xc[kk].y, w[j][kk], z1);
+      z2 = __builtin_fmaf(xc[kk].z, w[j][kk], z2);
+      z3 = __builtin_fmaf(xc[kk].w, w[j][kk], z3);
+    }
+    v[0][j] = z0, v[1][j] = z1, v[2][j] = z2, v[3][j] = z3;  // raw z ranks (the activation is the finalize's)
+    sv[0][j] = sv[1][j] = sv[2][j] = sv[3][j] = slot[j];
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int kk = 0; kk < RA; ++kk) xc[kk] = xn[kk];
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {  // sorting network for 4
+    cand_cmpex(v[t][0], sv[t][0], v[t][1], sv[t][1]);
+    cand_cmpex(v[t][2], sv[t][2], v[t][3], sv[t][3]);
+    cand_cmpex(v[t][0], sv[t][0], v[t][2], sv[t][2]);
+    cand_cmpex(v[t][1], sv[t][1], v[t][3], sv[t][3]);
+    cand_cmpex(v[t][1], sv[t][1], v[t][2], sv[t][2]);
+  }
+  const int tok = wave_sum4_token(lane);
+  for (int r = 0; r < k; ++r) {
+    float m;
+    int sl;
+    wave_max4(v[0][0], v[1][0], v[2][0], v[3][0], sv[0][0], sv[1][0], sv[2][0], sv[3][0], lane, m, sl);
+    if (store && lane < 4) {
+      out[tok * k + r] = m;
+      oslot[tok * k + r] = sl;
+    }
+    // lanes 0, 2, 1, 3 hold the winners of tokens 0, 1, 2, 3
+    cand_pop(v[0], sv[0], __builtin_amdgcn_readlane(sl, 0));
+    cand_pop(v[1], sv[1], __builtin_amdgcn_readlane(sl, 2));
+    cand_pop(v[2], sv[2], __builtin_amdgcn_readlane(sl, 1));
+    cand_pop(v[3], sv[3], __builtin_amdgcn_readlane(sl, 3));
+  }
+}
+
+// pool kinds of the forward tile
+constexpr int PK_SUM = 0, PK_MAX = 1, PK_TOPK = 2;
+
+// sum / mean, max or top-k tile
+template <int K, int NPL, int ACT, bool FAR, int PK>
 __device__ __forceinline__ void fwd_tile_any(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                              const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
-                                             bool store, int lane) {
-  if constexpr (MAXP) fwd_tile_max<K, NPL, ACT, FAR>(xsb, addr, w, bias, slot, out, oslot, store, lane);
+                                             int k, bool store, int lane) {
+  if constexpr (PK == PK_MAX) fwd_tile_max<K, NPL, ACT, FAR>(xsb, addr, w, bias, slot, out, oslot, store, lane);
+  else if constexpr (PK == PK_TOPK) fwd_tile_topk<K, NPL, ACT, FAR>(xsb, addr, w, bias, slot, out, oslot, k, store, lane);
   else fwd_tile<K, NPL, ACT, FAR>(xsb, addr, w, bias, out, store, lane);
 }
 
-template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, bool MAXP = false>
+template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, int PK = PK_SUM>
 __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots)
   __shared__ float4 xa[WS ? 2 * XTILE_DB : (DBUF ? XTILE_DB : XTILE_SB)];
@@ -190,7 +278,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   unsigned addr[NPL][K];
   float w[NPL][K];
   float bias[NPL];
-  int slot[NPL];  // max pooling: pool slot of each neuron
+  int slot[NPL];  // max / top-k pooling: pool slot of each neuron
   // window staging: this wave's pool is slot pk of the workgroup's staged pools, window start lo
   const int g_first = (int)((long long)blockIdx.x * WAVES / p.cpg);
   const int pk = WS ? (int)(g - g_first) : 0;
@@ -211,7 +299,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       w[j][ks] = valid ? wl : 0.f;
     }
     const float bl = p.bias[n];
-    bias[j] = valid ? bl : (MAXP ? -__builtin_inff() : 0.f);
+    bias[j] = valid ? bl : (PK != PK_SUM ? -__builtin_inff() : 0.f);
     slot[j] = s;
   }
 
@@ -221,8 +309,9 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   // from inline asm: a copy the compiler sees in flight during the gather makes it wait for all
   // LDS reads (lgkmcnt(0)) before each use instead of only the ones the use needs.
   constexpr int NT = WAVES * 64;
-  float* out = p.part + chunk * p.b_pad;
-  int* oslot = MAXP ? p.pslot + chunk * p.b_pad : nullptr;
+  const int kp = PK == PK_TOPK ? p.topk : 1;  // candidates per token
+  float* out = p.part + chunk * p.b_pad * kp;
+  int* oslot = PK != PK_SUM ? p.pslot + chunk * p.b_pad * kp : nullptr;
   const bool store = active;
   if constexpr (WS) {
     // window staging: WS_TILES tiles per stage and barrier; tile t at slot (t mod 2 WS_TILES) * nsl
@@ -239,8 +328,8 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       const int tn = p.n_tiles - t0 < WS_TILES ? p.n_tiles - t0 : WS_TILES;
       for (int tt = 0; tt < tn; ++tt) {
         const int t = t0 + tt;
-        fwd_tile_any<K, NPL, ACT, false, MAXP>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT,
-                                               oslot + t * BT, store, lane);
+        fwd_tile_any<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT * kp,
+                                             oslot + t * BT * kp, kp, store, lane);
         // next tile's slot; after the last tile of region 1 back to region 0
         const unsigned step = (t & (2 * WS_TILES - 1)) == 2 * WS_TILES - 1 ? tstep - 2u * WS_TILES * tstep : tstep;
 #pragma unroll
@@ -257,14 +346,14 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       stage_wait();
       __syncthreads();  // tile t is in xa; every wave is done with xb (tile t - 1)
       if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xb, p.D, NT);
-      fwd_tile_any<K, NPL, ACT, false, MAXP>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT,
-                                             oslot + t * BT, store, lane);
+      fwd_tile_any<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT * kp,
+                                           oslot + t * BT * kp, kp, store, lane);
       if (t + 1 < p.n_tiles) {
         stage_wait();
         __syncthreads();  // tile t + 1 is in xb; every wave is done with xa
         if (t + 2 < p.n_tiles) dma_tile(p.xt + (long long)(t + 2) * p.D, xa, p.D, NT);
-        fwd_tile_any<K, NPL, ACT, true, MAXP>(reinterpret_cast<const char*>(xb), addr, w, bias, slot,
-                                              out + (t + 1) * BT, oslot + (t + 1) * BT, store, lane);
+        fwd_tile_any<K, NPL, ACT, true, PK>(reinterpret_cast<const char*>(xb), addr, w, bias, slot,
+                                            out + (t + 1) * BT * kp, oslot + (t + 1) * BT * kp, kp, store, lane);
       }
     }
   } else {
@@ -273,8 +362,8 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       dma_tile(p.xt + (long long)t * p.D, xa, p.D, NT);
       stage_wait();
       __syncthreads();
-      fwd_tile_any<K, NPL, ACT, false, MAXP>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT,
-                                             oslot + t * BT, store, lane);
+      fwd_tile_any<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT * kp,
+                                           oslot + t * BT * kp, kp, store, lane);
     }
   }
 }
@@ -333,12 +422,61 @@ __global__ void __launch_bounds__(256) fwd_finalize_max_kernel(const float* __re
   }
 }
 
+// Top-k mean pooling: the k largest raw z over the pool's cpg chunk lists (each sorted best first,
+// k long), ties to the smaller slot (the reference's stable descending sort); pre[b, g] = the mean
+// of act(z) over the first kk = min(n_g, k) of them, topk_slot[b, g, j] their slots (-1 past kk).
+// One thread per (token, pool) merges the lists (at most FWD_TOPK_CPG of them); consecutive threads
+// take consecutive tokens, so each candidate load of a wave reads 64 adjacent k-entry rows.
+constexpr int FWD_TOPK_CPG = 16;
+
+template <int ACT>
+__global__ void __launch_bounds__(256) fwd_finalize_topk_kernel(const float* __restrict__ part, const int* __restrict__ pslot,
+                                                                const int32_t* __restrict__ counts, float* __restrict__ pre,
+                                                                int32_t* __restrict__ topk_slot, int B, int G, int cpg,
+                                                                int b_pad, int k) {
+  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long long)B * G) return;
+  const int b = (int)(t % B), g = (int)(t / B);
+  const long long i = (long long)b * G + g;  // [B, G] output element
+  int ptr[FWD_TOPK_CPG];
+#pragma unroll
+  for (int c = 0; c < FWD_TOPK_CPG; ++c) ptr[c] = 0;
+  const int n_g = counts[g];
+  const int kk = n_g < k ? n_g : k;
+  float sum = 0.f;
+  for (int j = 0; j < kk; ++j) {
+    int best = -1;
+    float bv = 0.f;
+    int bs = 0;
+#pragma unroll
+    for (int c = 0; c < FWD_TOPK_CPG; ++c) {
+      if (c < cpg && ptr[c] < k) {
+        const long long o = (((long long)g * cpg + c) * b_pad + b) * k + ptr[c];
+        const float v = part[o];
+        const int sl = pslot[o];
+        if (best < 0 || v > bv || (v == bv && sl < bs)) best = c, bv = v, bs = sl;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < FWD_TOPK_CPG; ++c) ptr[c] += c == best;
+    sum += ACT == GL_ACT_RELU ? __builtin_fmaxf(bv, 0.f) : bv;
+    if (topk_slot) topk_slot[i * k + j] = bs;
+  }
+  if (topk_slot)
+    for (int j = kk; j < k; ++j) topk_slot[i * k + j] = -1;
+  pre[i] = sum / (float)kk;
+}
+
 // ---- host side -------------------------------------------------------------------------------
 // 4 neurons per lane; 16 waves per workgroup at K = 8 (4 waves per SIMD, 128 VGPRs), 8 at K = 16
 // (2 per SIMD: the parameters of 4 neurons of fan-in 16 take twice the registers).  Max pooling
-// keeps a slot per neuron and a (value, slot) pair per token: 12 waves at K = 8, 4 at K = 16.
+// keeps a slot per neuron and a (value, slot) pair per token: 12 waves at K = 8, 4 at K = 16;
+// top-k keeps a sorted list of 4 pairs per token: 8 waves at K = 8, 4 at K = 16.
 constexpr int FWD_NPL = 4;
-constexpr int fwd_waves(int K, bool maxp = false) { return K == 8 ? (maxp ? 12 : 16) : (maxp ? 4 : 8); }
+constexpr int fwd_waves(int K, int pk = PK_SUM) {
+  return K == 8 ? (pk == PK_SUM ? 16 : (pk == PK_MAX ? 12 : 8)) : (pk == PK_SUM ? 8 : 4);
+}
+static int pool_kind(int pool) { return pool == GL_POOL_MAX ? PK_MAX : (pool == GL_POOL_TOPK_MEAN ? PK_TOPK : PK_SUM); }
 
 struct FwdPlan {
   int npl, waves, cpg, n_tiles, b_pad;
@@ -349,20 +487,21 @@ struct FwdPlan {
 static FwdPlan fwd_plan(const GlFwdArgs* a) {
   FwdPlan q;
   q.npl = FWD_NPL;
-  q.waves = fwd_waves(a->K, a->pool == GL_POOL_MAX);
+  q.waves = fwd_waves(a->K, pool_kind(a->pool));
   q.cpg = ceil_div(a->S, 64 * q.npl);
   q.n_chunks = (long long)a->G * q.cpg;
   q.n_tiles = ceil_div(a->B, BT);
   q.b_pad = q.n_tiles * BT;
   q.xt_bytes = (size_t)round_up((long long)q.n_tiles * a->D * 16, 256);
-  q.part_bytes = (size_t)round_up((long long)q.n_chunks * q.b_pad * 4, 256);
-  q.slot_bytes = a->pool == GL_POOL_MAX ? q.part_bytes : 0;  // slot of every partial maximum
+  const long long kp = a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1;  // candidates per chunk and token
+  q.part_bytes = (size_t)round_up((long long)q.n_chunks * q.b_pad * kp * 4, 256);
+  q.slot_bytes = a->pool == GL_POOL_MAX || a->pool == GL_POOL_TOPK_MEAN ? q.part_bytes : 0;  // candidate slots
   return q;
 }
 
-template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS, bool MAXP>
+template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS, int PK>
 static int launch_fwd(const FwdK& k, hipStream_t s) {
-  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, MAXP>;
+  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, PK>;
   dim3 grid((unsigned)ceil_div(k.n_chunks, WAVES));
   GL_LAUNCH(WS ? GL_KERNEL_FWD_WIN : GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
@@ -371,22 +510,22 @@ static int launch_fwd(const FwdK& k, hipStream_t s) {
 
 // one workgroup per CU (the tile buffers take the LDS); pool windows when they fit, else two tile
 // buffers when D fits them, else one
-template <int ACT, int K, bool MAXP>
+template <int ACT, int K, int PK>
 static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
-  constexpr int W = fwd_waves(K, MAXP);
-  if (k.win) return launch_fwd<K, FWD_NPL, W, ACT, false, true, MAXP>(k, s);
-  return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true, false, MAXP>(k, s)
-                       : launch_fwd<K, FWD_NPL, W, ACT, false, false, MAXP>(k, s);
+  constexpr int W = fwd_waves(K, PK);
+  if (k.win) return launch_fwd<K, FWD_NPL, W, ACT, false, true, PK>(k, s);
+  return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true, false, PK>(k, s)
+                       : launch_fwd<K, FWD_NPL, W, ACT, false, false, PK>(k, s);
 }
 
-template <int ACT, bool MAXP>
+template <int ACT, int PK>
 static int launch_fwd_act(int K, int D, const FwdK& k, hipStream_t s) {
-  return K == 8 ? launch_fwd_buf<ACT, 8, MAXP>(D, k, s) : launch_fwd_buf<ACT, 16, MAXP>(D, k, s);
+  return K == 8 ? launch_fwd_buf<ACT, 8, PK>(D, k, s) : launch_fwd_buf<ACT, 16, PK>(D, k, s);
 }
 
-template <bool MAXP>
+template <int PK>
 static int launch_fwd_any(int act, int K, int D, const FwdK& k, hipStream_t s) {
-  return act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU, MAXP>(K, D, k, s) : launch_fwd_act<GL_ACT_IDENTITY, MAXP>(K, D, k, s);
+  return act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU, PK>(K, D, k, s) : launch_fwd_act<GL_ACT_IDENTITY, PK>(K, D, k, s);
 }
 
 // Window staging applies when the staged windows of a workgroup's pools (npw of them, each ww
@@ -409,10 +548,20 @@ int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void
   if (B < 1 || D < 1 || G < 1 || S < 1) return GL_ERR_ARG;
   if (K != 8 && K != 16) return GL_ERR_UNSUPPORTED;
   if (act != GL_ACT_IDENTITY && act != GL_ACT_RELU) return GL_ERR_UNSUPPORTED;
-  if (pool != GL_POOL_MEAN && pool != GL_POOL_SUM && pool != GL_POOL_MAX) return GL_ERR_UNSUPPORTED;
+  if (pool != GL_POOL_MEAN && pool != GL_POOL_SUM && pool != GL_POOL_MAX && pool != GL_POOL_TOPK_MEAN)
+    return GL_ERR_UNSUPPORTED;
   if (x_dtype != GL_DTYPE_F32 && x_dtype != GL_DTYPE_BF16) return GL_ERR_UNSUPPORTED;
   if ((long long)G * S > (1LL << 31) / 16) return GL_ERR_UNSUPPORTED;
   if (D > XTILE_SB) return GL_ERR_LDS;  // one token tile (D x 16 bytes) must fit the LDS tile buffer
+  return 0;
+}
+
+// top-k mean: k a power of two in [1, 64] (the reference's LevelSpec check) and pools that the
+// finalize's merge covers (cpg <= FWD_TOPK_CPG chunks of 256 slots)
+int check_topk(int pool, int topk, int S) {
+  if (pool != GL_POOL_TOPK_MEAN) return 0;
+  if (topk < 1 || topk > 64 || (topk & (topk - 1)) != 0) return GL_ERR_ARG;
+  if (ceil_div(S, 64 * FWD_NPL) > FWD_TOPK_CPG) return GL_ERR_UNSUPPORTED;
   return 0;
 }
 
@@ -424,6 +573,7 @@ extern "C" int gl_fwd_workspace(const GlFwdArgs* a, size_t* bytes) {
   if (!a || !bytes) return GL_ERR_ARG;
   GL_TRY(check_layer(a->B, a->D, a->G, a->S, a->K, a->act, a->pool, a->X, a->idx, a->W, a->bias, a->counts,
                      a->x_dtype));
+  GL_TRY(check_topk(a->pool, a->topk, a->S));
   FwdPlan q = fwd_plan(a);
   *bytes = q.xt_bytes + q.part_bytes + q.slot_bytes;
   return 0;
@@ -438,19 +588,28 @@ extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
   FwdPlan q = fwd_plan(a);
   float4* xt = (float4*)a->ws;
   float* part = (float*)((char*)a->ws + q.xt_bytes);
-  int* pslot = a->pool == GL_POOL_MAX ? (int*)((char*)a->ws + q.xt_bytes + q.part_bytes) : nullptr;
+  int* pslot = q.slot_bytes ? (int*)((char*)a->ws + q.xt_bytes + q.part_bytes) : nullptr;
   GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, 0, q.n_tiles, xt, s));
   if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;
-  FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, pslot, a->sched, nullptr, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles,
-         q.b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0};
+  FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, pslot, a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1, a->sched,
+         nullptr, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles, q.b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0};
   if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) k.win = a->win;
   dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(q.b_pad, 32));
   if (a->pool == GL_POOL_MAX) {
-    GL_TRY(launch_fwd_any<true>(a->act, a->K, a->D, k, s));
+    GL_TRY(launch_fwd_any<PK_MAX>(a->act, a->K, a->D, k, s));
     GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_max_kernel, grid, dim3(256), 0, s, part, pslot, a->pre, a->winner,
               a->B, a->G, q.cpg, q.b_pad);
+  } else if (a->pool == GL_POOL_TOPK_MEAN) {
+    GL_TRY(launch_fwd_any<PK_TOPK>(a->act, a->K, a->D, k, s));
+    const dim3 g1((unsigned)ceil_div((long long)a->B * a->G, 256));
+    if (a->act == GL_ACT_RELU)
+      GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_topk_kernel<GL_ACT_RELU>, g1, dim3(256), 0, s, part, pslot,
+                a->counts, a->pre, a->winner, a->B, a->G, q.cpg, q.b_pad, a->topk);
+    else
+      GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_topk_kernel<GL_ACT_IDENTITY>, g1, dim3(256), 0, s, part, pslot,
+                a->counts, a->pre, a->winner, a->B, a->G, q.cpg, q.b_pad, a->topk);
   } else {
-    GL_TRY(launch_fwd_any<false>(a->act, a->K, a->D, k, s));
+    GL_TRY(launch_fwd_any<PK_SUM>(a->act, a->K, a->D, k, s));
     GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_kernel, grid, dim3(256), 0, s, part, a->counts, a->pre, a->B, a->G,
               q.cpg, q.b_pad, 0, a->pool);
   }

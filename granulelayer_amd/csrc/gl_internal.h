@@ -13,6 +13,9 @@ int set_lds_limit(const void* kernel, size_t bytes);
 int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const float* W,
                 const float* bias, const int32_t* counts, int x_dtype);
 
+// GL_POOL_TOPK_MEAN arguments (k, pool size); 0 for other pools
+int check_topk(int pool, int topk, int S);
+
 // Window staging for a kernel whose workgroups hold `waves` chunks of cpg per pool: true (with the
 // padded width *ww and pools per workgroup *npw) when the pools' windows fit a stage tile.
 bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, int G, int* ww, int* npw);
@@ -21,14 +24,15 @@ bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, i
 int launch_tile_x(const void* X, long long sxb, int x_dtype, int B, int D, int b0, int n_tiles, float4* xt,
                   hipStream_t s);
 
-// Max-pooling backward as winner events (gl_max_bwd.hip): dW / db / dX of one token chunk
-// [b0, b0 + Bc) from the chunk's token tiles, transposed g_pre / winners (c1t_kernel) and the
-// row-major g_pre / winners.
+// Max / top-k pooling backward as selection events (gl_max_bwd.hip): dW / db / dX of one token
+// chunk [b0, b0 + Bc) from the chunk's token tiles, transposed coef / slots (c1t_kernel,
+// events_transpose_kernel) and the row-major g_pre / selected slots.
 struct MaxEvKArgs {
   const float4* xt;
   const int32_t* idx;
   const float* W;
   const float* bias;
+  const int32_t* counts;
   const float* c1t;
   const int32_t* wint;
   const float* g_pre;
@@ -37,6 +41,8 @@ struct MaxEvKArgs {
   float* db;
   float* dX;
   int D, G, S, cap, Bc, b0;
+  int kpe;    // selected slots per (token, pool): 1 (max) or k (top-k mean)
+  bool topk;  // coef = g_pre / min(n_g, kpe) (top-k mean) instead of g_pre
 };
 int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s);
 

@@ -1,10 +1,12 @@
-// Max-pooling backward as winner events, without floating-point atomics.
+// Max / top-k mean pooling backward as selection events, without floating-point atomics.
 //
-// With max pooling only the winner neuron n* = g*S + winner[b, g] of each (token, pool) receives a
-// gradient: dz = g_pre[b, g] * act'(z[b, n*]) (pytorch_reference.py:61-67 through autograd).  The
-// reference runs this as an event kernel with fp32 atomics (sparse_pooling/kernels/triton_fused.py
-// :478-520 bwd_events_kernel, launched from autograd.py:284-289), touching the winner's K edges
-// only.  Here the same events are summed in a fixed order:
+// Max pooling gives a gradient only to the winner of each (token, pool), top-k mean to its kk =
+// min(n_g, k) selected neurons: each selected neuron n* = g*S + slot gets dz = coef * act'(z[b, n*])
+// with coef = g_pre[b, g] (max) or g_pre[b, g] / kk (top-k), pytorch_reference.py:61-77 through
+// autograd.  The reference runs these as an event kernel with fp32 atomics
+// (sparse_pooling/kernels/triton_fused.py:478-520 bwd_events_kernel, launched from
+// autograd.py:284-295), touching the selected neurons' K edges only.  Here the same events (KPE
+// per (token, pool): 1 or k; slot -1 = none) are summed in a fixed order:
 //   * max_events_dw_kernel, one workgroup per pool: each token's event recomputes z (K MACs, as
 //     the reference does for act'), the pool's events are sorted by (slot, token) in LDS, and the
 //     first event of every slot sums that slot's events in token order and adds them to dW and db
@@ -24,14 +26,16 @@ struct MaxEvK {
   const int32_t* __restrict__ idx;    // [G*S, K]
   const float* __restrict__ W;        // [G*S, K]
   const float* __restrict__ bias;     // [G*S]
-  const float* __restrict__ c1t;      // [G][cap] g_pre of the chunk's tokens
-  const int32_t* __restrict__ wint;   // [G][cap] winner slots of the chunk's tokens
+  const int32_t* __restrict__ counts; // [G]
+  const float* __restrict__ c1t;      // [G][cap] coef of the chunk's tokens (g_pre, / kk for top-k)
+  const int32_t* __restrict__ wint;   // [G][cap][kpe] selected slots of the chunk's tokens
   const float* __restrict__ g_pre;    // [B, G]
-  const int32_t* __restrict__ winner; // [B, G]
+  const int32_t* __restrict__ winner; // [B, G, kpe]
   float* dW;                          // [G*S, K] accumulated
   float* db;                          // [G*S] accumulated
   float* dX;                          // [B, D] overwritten
-  int D, G, S, cap, Bc, b0, npow2;
+  int D, G, S, cap, Bc, b0, npow2, kpe, tsub;
+  bool topk;  // coef = g_pre / min(n_g, kpe)
 };
 
 // x[b, d] of the chunk's token b from the token tiles
@@ -57,61 +61,68 @@ __device__ __forceinline__ float event_dz(const MaxEvK& p, long long n, float c1
   return ACT == GL_ACT_RELU ? (z > 0.f ? c1 : 0.f) : c1;
 }
 
-// dW / db of one pool's events.  LDS: npow2 sort keys, then per token its dz and K products.
+// dW / db of one pool's events, tsub tokens (tsub * kpe <= 1024 events) at a time.  LDS: npow2
+// sort keys, then per event its dz and K products.
 template <int K, int ACT>
 __global__ void __launch_bounds__(256) max_events_dw_kernel(MaxEvK p) {
   extern __shared__ unsigned lds[];
   unsigned* keys = lds;
-  float* ev = reinterpret_cast<float*>(lds + p.npow2);  // [Bc][K + 1]: dz, dz * x_k
+  float* ev = reinterpret_cast<float*>(lds + p.npow2);  // [tsub * kpe][K + 1]: dz, dz * x_k
   const int g = blockIdx.x;
-  for (int i = threadIdx.x; i < p.npow2; i += blockDim.x) {
-    unsigned key = ~0u;
-    if (i < p.Bc) {
-      int s = p.wint[(long long)g * p.cap + i];
-      const bool ok = s >= 0 && s < p.S;
-      s = ok ? s : 0;
-      const long long n = (long long)g * p.S + s;
-      float xk[K], wk[K];
-      int dk[K];
-      const float dz = ok ? event_dz<K, ACT>(p, n, p.c1t[(long long)g * p.cap + i],
-                                             [&](int d) { return tile_x(p.xt, p.D, i, d); }, xk, wk, dk)
-                          : 0.f;
-      float* e = ev + (long long)i * (K + 1);
-      e[0] = dz;
+  for (int t0 = 0; t0 < p.Bc; t0 += p.tsub) {
+    const int nev = (p.Bc - t0 < p.tsub ? p.Bc - t0 : p.tsub) * p.kpe;
+    for (int i = threadIdx.x; i < p.npow2; i += blockDim.x) {
+      unsigned key = ~0u;  // no event
+      if (i < nev) {
+        const int bl = t0 + i / p.kpe;  // token of the chunk
+        const int s = p.wint[((long long)g * p.cap + bl) * p.kpe + i % p.kpe];
+        if (s >= 0 && s < p.S) {
+          const long long n = (long long)g * p.S + s;
+          float xk[K], wk[K];
+          int dk[K];
+          const float dz = event_dz<K, ACT>(p, n, p.c1t[(long long)g * p.cap + bl],
+                                            [&](int d) { return tile_x(p.xt, p.D, bl, d); }, xk, wk, dk);
+          float* e = ev + (long long)i * (K + 1);
+          e[0] = dz;
 #pragma unroll
-      for (int k = 0; k < K; ++k) e[1 + k] = dz * xk[k];
-      key = ((unsigned)s << 11) | (unsigned)i;  // slot, then token (Bc <= 1024 < 2^11)
-    }
-    keys[i] = key;
-  }
-  __syncthreads();
-  for (int size = 2; size <= p.npow2; size <<= 1) {  // bitonic sort, ascending
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < p.npow2 / 2; i += blockDim.x) {
-        const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
-        const bool asc = (lo & size) == 0;
-        const unsigned a = keys[lo], b = keys[hi];
-        if ((a > b) == asc) keys[lo] = b, keys[hi] = a;
+          for (int k = 0; k < K; ++k) e[1 + k] = dz * xk[k];
+          key = ((unsigned)s << 11) | (unsigned)i;  // slot, then event (token-major; i < 1024 < 2^11)
+        }
       }
-      __syncthreads();
+      keys[i] = key;
     }
-  }
-  // the first event of each slot sums the slot's events in token order
-  for (int i = threadIdx.x; i < p.Bc; i += blockDim.x) {
-    const unsigned s = keys[i] >> 11;
-    if (i > 0 && (keys[i - 1] >> 11) == s) continue;
-    float acc[K + 1];
-#pragma unroll
-    for (int k = 0; k <= K; ++k) acc[k] = 0.f;
-    for (int j = i; j < p.Bc && (keys[j] >> 11) == s; ++j) {
-      const float* e = ev + (long long)(keys[j] & 2047u) * (K + 1);
-#pragma unroll
-      for (int k = 0; k <= K; ++k) acc[k] += e[k];
+    __syncthreads();
+    for (int size = 2; size <= p.npow2; size <<= 1) {  // bitonic sort, ascending
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = threadIdx.x; i < p.npow2 / 2; i += blockDim.x) {
+          const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+          const bool asc = (lo & size) == 0;
+          const unsigned a = keys[lo], b = keys[hi];
+          if ((a > b) == asc) keys[lo] = b, keys[hi] = a;
+        }
+        __syncthreads();
+      }
     }
-    const long long n = (long long)g * p.S + s;
-    p.db[n] += acc[0];
+    // the first event of each slot sums the slot's events in token order (a neuron is selected at
+    // most once per token)
+    for (int i = threadIdx.x; i < nev; i += blockDim.x) {
+      const unsigned key = keys[i];
+      const unsigned s = key >> 11;
+      if (key == ~0u || (i > 0 && (keys[i - 1] >> 11) == s)) continue;
+      float acc[K + 1];
 #pragma unroll
-    for (int k = 0; k < K; ++k) p.dW[n * K + k] += acc[1 + k];
+      for (int k = 0; k <= K; ++k) acc[k] = 0.f;
+      for (int j = i; j < nev && keys[j] != ~0u && (keys[j] >> 11) == s; ++j) {
+        const float* e = ev + (long long)(keys[j] & 2047u) * (K + 1);
+#pragma unroll
+        for (int k = 0; k <= K; ++k) acc[k] += e[k];
+      }
+      const long long n = (long long)g * p.S + s;
+      p.db[n] += acc[0];
+#pragma unroll
+      for (int k = 0; k < K; ++k) p.dW[n * K + k] += acc[1 + k];
+    }
+    __syncthreads();  // the next token group reuses the LDS
   }
 }
 
@@ -124,15 +135,16 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
   __shared__ float wmax[16];
   __shared__ double scale_s;
   const int b = blockIdx.x;
-  const long long row = (long long)(p.b0 + b) * p.G;
+  const long long row = (long long)(p.b0 + b) * p.G;  // [B, G] row of the token; winners: row * kpe
   for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
     xrow[d] = tile_x(p.xt, p.D, b, d);
     acc[d] = 0ull;
   }
   // pass 1: every term |dz * W[n*, k]| is at most |g_pre| * max_k |W[n*, k]|
   float m = 0.f;
-  for (int g = threadIdx.x; g < p.G; g += blockDim.x) {
-    int s = p.winner[row + g];
+  for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
+    const int g = e / p.kpe;
+    int s = p.winner[row * p.kpe + e];
     s = s < 0 ? 0 : (s >= p.S ? p.S - 1 : s);
     const long long n = (long long)g * p.S + s;
     float wm = 0.f;
@@ -147,7 +159,7 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
   if (threadIdx.x == 0) {
     float t = 0.f;
     for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t = __builtin_fmaxf(t, wmax[w]);
-    const double total = (double)t * (double)p.G * (double)K;  // bound of |sum| over all terms
+    const double total = (double)t * (double)p.G * (double)p.kpe * (double)K;  // bound of |sum| over all terms
     // |sum| * scale < 2^62 (and no term's scaled value exceeds it): scale = 2^(61 - floor(log2 total)),
     // floor(log2) read from the (normal) double's exponent field, the power kept in the normal range
     double sc = 1.0;
@@ -162,14 +174,20 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
   __syncthreads();
   const double scale = scale_s;
   // pass 2: the events' dz * W[n*, k] as fixed-point integers
-  for (int g = threadIdx.x; g < p.G; g += blockDim.x) {
-    int s = p.winner[row + g];
+  for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
+    const int g = e / p.kpe;
+    int s = p.winner[row * p.kpe + e];
     const bool ok = s >= 0 && s < p.S;
     s = ok ? s : 0;
     const long long n = (long long)g * p.S + s;
     float xk[K], wk[K];
     int dk[K];
-    const float dz = event_dz<K, ACT>(p, n, p.g_pre[row + g], [&](int d) { return xrow[d]; }, xk, wk, dk);
+    float coef = p.g_pre[row + g];
+    if (p.topk) {  // the same expression as c1t_kernel's
+      const int n_g = p.counts[g];
+      coef = coef / (float)(n_g < p.kpe ? n_g : p.kpe);
+    }
+    const float dz = event_dz<K, ACT>(p, n, coef, [&](int d) { return xrow[d]; }, xk, wk, dk);
     if (!ok || dz == 0.f) continue;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -184,7 +202,7 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
 
 template <int K, int ACT>
 static int launch_max_events_k(const MaxEvK& k, hipStream_t s) {
-  const size_t dw_lds = (size_t)k.npow2 * 4 + (size_t)k.Bc * (K + 1) * 4;
+  const size_t dw_lds = (size_t)k.npow2 * 4 + (size_t)k.tsub * k.kpe * (K + 1) * 4;
   const size_t dx_lds = (size_t)k.D * 12;
   if (dw_lds > max_lds_bytes() || dx_lds > max_lds_bytes()) return GL_ERR_LDS;
   GL_TRY(set_lds_limit((const void*)max_events_dw_kernel<K, ACT>, dw_lds));
@@ -197,10 +215,12 @@ static int launch_max_events_k(const MaxEvK& k, hipStream_t s) {
 }
 
 int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s) {
+  // tokens per dW sort: at most 1024 events (the sort keys hold the event index in 11 bits)
+  const int tsub = a.Bc < 1024 / a.kpe ? a.Bc : 1024 / a.kpe;
   int npow2 = 1;
-  while (npow2 < a.Bc) npow2 <<= 1;
-  const MaxEvK k{a.xt, a.idx, a.W, a.bias, a.c1t, a.wint, a.g_pre, a.winner, a.dW, a.db, a.dX,
-                 a.D, a.G, a.S, a.cap, a.Bc, a.b0, npow2};
+  while (npow2 < tsub * a.kpe) npow2 <<= 1;
+  const MaxEvK k{a.xt, a.idx, a.W, a.bias, a.counts, a.c1t, a.wint, a.g_pre, a.winner, a.dW, a.db, a.dX,
+                 a.D, a.G, a.S, a.cap, a.Bc, a.b0, npow2, a.kpe, tsub, a.topk};
   if (K == 8) return act == GL_ACT_RELU ? launch_max_events_k<8, GL_ACT_RELU>(k, s) : launch_max_events_k<8, GL_ACT_IDENTITY>(k, s);
   return act == GL_ACT_RELU ? launch_max_events_k<16, GL_ACT_RELU>(k, s) : launch_max_events_k<16, GL_ACT_IDENTITY>(k, s);
 }

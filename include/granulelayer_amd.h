@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 4
+#define GL_ABI_VERSION 5
 
 enum {
   GL_OK = 0,
@@ -41,8 +41,9 @@ enum {
 };
 enum { GL_ACT_IDENTITY = 0, GL_ACT_RELU = 1 };
 /* max: pytorch_reference.py:61-67 (winner = first maximum of act(z) over the pool's valid
- * slots), merged as kernels/ops.py:189-195 */
-enum { GL_POOL_MEAN = 0, GL_POOL_SUM = 1, GL_POOL_MAX = 2 };
+ * slots), merged as kernels/ops.py:189-195; top-k mean: pytorch_reference.py:68-77 (the k largest
+ * raw z, ties to the smaller slot, mean of act(z) over min(n_g, k) of them), ops.py:212-228 */
+enum { GL_POOL_MEAN = 0, GL_POOL_SUM = 1, GL_POOL_MAX = 2, GL_POOL_TOPK_MEAN = 3 };
 enum { GL_DTYPE_F32 = 0, GL_DTYPE_BF16 = 1 };
 
 /* Forward arguments.  Replaces the reference's FwdArgs + sp_fwd
@@ -55,6 +56,7 @@ typedef struct GlFwdArgs {
   int32_t x_dtype;        /* GL_DTYPE_F32 | GL_DTYPE_BF16 */
   int32_t B, D, G, S, K;  /* tokens, inputs, groups, padded slots per group, fan-in (8 | 16) */
   int32_t act, pool;      /* GL_ACT_*, GL_POOL_* */
+  int32_t topk;           /* GL_POOL_TOPK_MEAN: k, a power of two in [1, 64] (pools of <= 4096 slots) */
   const int32_t* idx;     /* [G*S, K] input indices in [0, D) */
   const float* W;         /* [G*S, K] */
   const float* bias;      /* [G*S] */
@@ -63,8 +65,9 @@ typedef struct GlFwdArgs {
   const uint32_t* win;    /* [G] first input of each pool's window (gl_window_build_host), or NULL */
   int32_t win_width;      /* widest pool window; the kernels stage only the windows when narrow */
   float* pre;             /* out [B, G]: pooled value before the (identity) out-activation */
-  int32_t* winner;        /* out [B, G] (GL_POOL_MAX, or NULL): pool-local slot of the maximum, the
-                             reference's track_ids / "winner" statistic (ops.py:192-195) */
+  int32_t* winner;        /* out [B, G, KPE] or NULL: the selected pool-local slots, KPE = 1 for
+                             GL_POOL_MAX (the reference's "winner", ops.py:192-195), k for
+                             GL_POOL_TOPK_MEAN ("topk_slot", best first, -1 past min(n_g, k)) */
   void* ws;               /* workspace of gl_fwd_workspace() bytes */
   size_t ws_bytes;
 } GlFwdArgs;
@@ -78,6 +81,7 @@ typedef struct GlBwdArgs {
   int32_t x_dtype;
   int32_t B, D, G, S, K;
   int32_t act, pool;
+  int32_t topk;           /* as GlFwdArgs.topk */
   const int32_t* idx;
   const float* W;
   const float* bias;
@@ -86,7 +90,8 @@ typedef struct GlBwdArgs {
   const uint32_t* win;    /* as GlFwdArgs.win / win_width */
   int32_t win_width;
   const float* g_pre;     /* [B, G] dL/dpre (fp32) */
-  const int32_t* winner;  /* [B, G] GL_POOL_MAX: the forward's winner slots (required); else NULL */
+  const int32_t* winner;  /* [B, G, KPE] the forward's selected slots: required for GL_POOL_MAX and
+                             GL_POOL_TOPK_MEAN, NULL otherwise */
   float* dW;              /* [G*S, K] ACCUMULATED (+=), e.g. W.main_grad; padded slots untouched */
   float* db;              /* [G*S] ACCUMULATED (+=) */
   float* dX;              /* out [B, D] fp32, overwritten */

@@ -26,6 +26,11 @@
  *     backward (autograd of the gather, the event backward autograd.py:284-289): only the winner
  *     gets a gradient:  dz[b, winner] = dy[b,g] * act'(z[b, winner])
  *
+ *   top-k mean pooling (pool 3; pytorch_reference.py:68-77): the slots of the k largest raw z
+ *   (stable descending sort: ties to the smaller slot), kk = min(n_g, k);
+ *     pre[b,g] = sum of act(z) over the first kk of them / kk
+ *     backward (autograd.py:290-295): dz = dy[b,g] / kk * act'(z) for the kk selected neurons
+ *
  *   Adam (sparse_pooling/optim.py:26-64, fp32 parameters: HAS_MASTER=False, STOCH=False):
  *     m = b1*m + (1-b1)*g ; v = b2*v + (1-b2)*g*g ; upd = (m/bc1) / (sqrt(v/bc2) + eps)
  *     p = p*(1 - lr*wd) - lr*upd ; g = 0        evaluated in fp32, in this order, unfused.
@@ -111,6 +116,61 @@ void glo_forward_max_f64(int B, int D, int G, int S, int K, const float* x, cons
   }
 }
 
+/* slots of the kk = min(n_g, k) largest z of pool g for token row xb, best first (ties: smaller
+ * slot); returns kk.  z[s] for s < n_g must hold the pool's pre-activations. */
+static int topk_select(const double* z, int n_g, int k, int* sel) {
+  const int kk = n_g < k ? n_g : k;
+  for (int j = 0; j < kk; ++j) {
+    int best = -1;
+    for (int s = 0; s < n_g; ++s) {
+      int taken = 0;
+      for (int i = 0; i < j; ++i) taken |= sel[i] == s;
+      if (taken) continue;
+      if (best < 0 || z[s] > z[best]) best = s;  /* strict: the first (smaller) slot keeps ties */
+    }
+    sel[j] = best;
+  }
+  return kk;
+}
+
+/*
+ * Top-k mean pooling forward (pool 3).  pre [B, G] float64; slots [B, G, k] int32 (the selected
+ * pool slots, best first, -1 past kk = min(n_g, k)); gap [B, G] (optional): (z of the kk-th
+ * selected - the best unselected z) / (scale of the fp32 rounding of z), the margin by which an
+ * fp32 evaluation could change the selected set (+inf when every neuron is selected).
+ */
+void glo_forward_topk_f64(int B, int D, int G, int S, int K, const float* x, const int32_t* idx, const float* w,
+                          const float* bias, const int32_t* counts, int act, int k, double* pre, int32_t* slots,
+                          double* gap) {
+  double* z = (double*)malloc(sizeof(double) * (size_t)S);
+  int* sel = (int*)malloc(sizeof(int) * (size_t)(k > 0 ? k : 1));
+  for (int b = 0; b < B; ++b) {
+    const float* xb = x + (size_t)b * D;
+    for (int g = 0; g < G; ++g) {
+      const int n_g = counts[g];
+      double mag = 0.0;
+      for (int sl = 0; sl < n_g; ++sl) {
+        double zm;
+        z[sl] = neuron_z(xb, idx, w, bias, (long)g * S + sl, K, &zm);
+        if (zm > mag) mag = zm;
+      }
+      const int kk = topk_select(z, n_g, k, sel);
+      double sum = 0.0, rest = -INFINITY;
+      for (int j = 0; j < kk; ++j) sum += act_f(z[sel[j]], act);
+      for (int sl = 0; sl < n_g; ++sl) {
+        int taken = 0;
+        for (int j = 0; j < kk; ++j) taken |= sel[j] == sl;
+        if (!taken && z[sl] > rest) rest = z[sl];
+      }
+      pre[(size_t)b * G + g] = sum / (double)kk;
+      for (int j = 0; j < k; ++j) slots[((size_t)b * G + g) * k + j] = j < kk ? sel[j] : -1;
+      if (gap) gap[(size_t)b * G + g] = kk == n_g ? INFINITY : (z[sel[kk - 1]] - rest) / (mag > 0.0 ? mag : 1.0);
+    }
+  }
+  free(z);
+  free(sel);
+}
+
 /*
  * Backward.  dy [B, G] fp32 is dL/dpre (the out-activation of mean/sum is identity).
  * dW [G*S, K], db [G*S], dX [B, D] are float64 and ACCUMULATED (+=), like main_grad.
@@ -121,16 +181,18 @@ void glo_forward_max_f64(int B, int D, int G, int S, int K, const float* x, cons
  *         decide differently: |z| <= amb * (sum_k |x w| + |bias|).  Their terms use the float64
  *         mask in dW/db/dX and are added as |term| to unc*.
  */
-void glo_backward_f64(int B, int D, int G, int S, int K, const float* x, const int32_t* idx, const float* w,
-                      const float* bias, const int32_t* counts, int act, int pool, const float* dy, double* dW,
-                      double* db, double* dX, double amb, double* magW, double* magb, double* magX, double* uncW,
-                      double* uncb, double* uncX) {
+static void backward_impl(int B, int D, int G, int S, int K, const float* x, const int32_t* idx, const float* w,
+                          const float* bias, const int32_t* counts, int act, int pool, int topk, const float* dy,
+                          double* dW, double* db, double* dX, double amb, double* magW, double* magb, double* magX,
+                          double* uncW, double* uncb, double* uncX) {
+  double* zb = pool == 3 ? (double*)malloc(sizeof(double) * (size_t)S) : NULL;
+  int* sel = pool == 3 ? (int*)malloc(sizeof(int) * (size_t)topk) : NULL;
   for (int b = 0; b < B; ++b) {
     const float* xb = x + (size_t)b * D;
     double* dxb = dX + (size_t)b * D;
     for (int g = 0; g < G; ++g) {
       int n_g = counts[g];
-      double c1 = (double)dy[(size_t)b * G + g] * (pool == 0 ? 1.0 / (double)n_g : 1.0);
+      double c1 = (double)dy[(size_t)b * G + g] * (pool == 0 ? 1.0 / (double)n_g : 1.0);  /* pool 3: below */
       int win = -1;  /* max pooling: the winner (first maximum of act(z)) is the only neuron with a gradient */
       if (pool == 2) {
         double best = -INFINITY;
@@ -139,8 +201,19 @@ void glo_backward_f64(int B, int D, int G, int S, int K, const float* x, const i
           if (a > best) best = a, win = sl;
         }
       }
+      int kk = 0;  /* top-k mean: the kk selected neurons, each with dy / kk */
+      if (pool == 3) {
+        for (int sl = 0; sl < n_g; ++sl) zb[sl] = neuron_z(xb, idx, w, bias, (long)g * S + sl, K, NULL);
+        kk = topk_select(zb, n_g, topk, sel);
+        c1 = (double)dy[(size_t)b * G + g] / (double)kk;
+      }
       for (int sl = 0; sl < n_g; ++sl) {
         if (pool == 2 && sl != win) continue;
+        if (pool == 3) {
+          int taken = 0;
+          for (int j = 0; j < kk; ++j) taken |= sel[j] == sl;
+          if (!taken) continue;
+        }
         long n = (long)g * S + sl;
         double zm;
         double z = neuron_z(xb, idx, w, bias, n, K, &zm);
@@ -161,6 +234,60 @@ void glo_backward_f64(int B, int D, int G, int S, int K, const float* x, const i
       }
     }
   }
+  free(zb);
+  free(sel);
+}
+
+void glo_backward_f64(int B, int D, int G, int S, int K, const float* x, const int32_t* idx, const float* w,
+                      const float* bias, const int32_t* counts, int act, int pool, const float* dy, double* dW,
+                      double* db, double* dX, double amb, double* magW, double* magb, double* magX, double* uncW,
+                      double* uncb, double* uncX) {
+  backward_impl(B, D, G, S, K, x, idx, w, bias, counts, act, pool, 0, dy, dW, db, dX, amb, magW, magb, magX, uncW,
+                uncb, uncX);
+}
+
+/*
+ * Backward of a given selection (max: kpe = 1, coef = dy; top-k mean: kpe = k, coef = dy / kk with
+ * kk = min(n_g, k)): slots [B, G, kpe] (-1 = none).  dz = coef * act'(z) for every listed slot,
+ * accumulated into dW, db, dX (float64) with the mag* error scales.  Equal to the max / top-k
+ * backward when slots is that pooling's own selection.
+ */
+void glo_backward_events_f64(int B, int D, int G, int S, int K, const float* x, const int32_t* idx, const float* w,
+                             const float* bias, const int32_t* counts, int act, int topk_mode, int kpe,
+                             const int32_t* slots, const float* dy, double* dW, double* db, double* dX, double* magW,
+                             double* magb, double* magX) {
+  for (int b = 0; b < B; ++b) {
+    const float* xb = x + (size_t)b * D;
+    for (int g = 0; g < G; ++g) {
+      const int n_g = counts[g];
+      const int kk = n_g < kpe ? n_g : kpe;
+      const double coef = (double)dy[(size_t)b * G + g] / (topk_mode ? (double)kk : 1.0);
+      for (int j = 0; j < kpe; ++j) {
+        const int sl = slots[((size_t)b * G + g) * kpe + j];
+        if (sl < 0 || sl >= n_g) continue;
+        const long n = (long)g * S + sl;
+        const double dz = coef * dact_f(neuron_z(xb, idx, w, bias, n, K, NULL), act);
+        db[n] += dz;
+        if (magb) magb[n] += fabs(dz);
+        for (int k = 0; k < K; ++k) {
+          const int d = idx[n * K + k];
+          dW[n * K + k] += dz * (double)xb[d];
+          dX[(size_t)b * D + d] += dz * (double)w[n * K + k];
+          if (magW) magW[n * K + k] += fabs(dz * (double)xb[d]);
+          if (magX) magX[(size_t)b * D + d] += fabs(dz * (double)w[n * K + k]);
+        }
+      }
+    }
+  }
+}
+
+/* top-k mean backward (pool 3) with k selected per (token, pool) */
+void glo_backward_topk_f64(int B, int D, int G, int S, int K, const float* x, const int32_t* idx, const float* w,
+                           const float* bias, const int32_t* counts, int act, int k, const float* dy, double* dW,
+                           double* db, double* dX, double amb, double* magW, double* magb, double* magX,
+                           double* uncW, double* uncb, double* uncX) {
+  backward_impl(B, D, G, S, K, x, idx, w, bias, counts, act, 3, k, dy, dW, db, dX, amb, magW, magb, magX, uncW, uncb,
+                uncX);
 }
 
 /* round-to-nearest-even fp32 -> bf16 -> fp32 (torch's .to(torch.bfloat16) for finite values) */

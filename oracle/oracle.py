@@ -5,7 +5,8 @@ module, and only as the checker.  The product package ``granulelayer_amd`` never
 
 Contents (each restates the reference; file:line citations are relative to the reference root):
 
-* ``forward`` / ``forward_max`` / ``backward`` -- float64 C restatement (``gl_oracle.c``) of
+* ``forward`` / ``forward_max`` / ``forward_topk`` / ``backward`` / ``backward_topk`` -- float64 C
+  restatement (``gl_oracle.c``) of
   ``sparse_pooling/reference/pytorch_reference.py:29-79`` (Mode A) and of the recompute backward
   ``sparse_pooling/kernels/triton_fused.py:364-445`` + ``kernels/ops.py:242-249``.
 * ``adam`` -- fp32 restatement of ``sparse_pooling/optim.py:26-64`` (fp32 parameters).
@@ -19,8 +20,11 @@ Parity status (what pins each function; see tests/test_oracle.py):
             mean = sum / n_g, padded-slot masking, hand-computed known answer.
   forward_max pinned: dense-GEMM z with torch.max / torch.argmax (first maximum), hand-built
             ties (smaller slot wins, padded slots never win, relu all-zero pools).
+  forward_topk pinned: dense-GEMM z with torch.sort(descending, stable) (the reference's own
+            formula, pytorch_reference.py:68-77), hand-built ties and short pools (n_g < k).
   backward  pinned: torch autograd of the dense-GEMM forward, float64 central differences; max
-            pooling: autograd of the winner gather (pytorch_reference.py:61-67).
+            pooling: autograd of the winner gather (pytorch_reference.py:61-67); top-k mean:
+            autograd of the selected-value mean.
   adam      pinned: torch.optim.Adam / AdamW (library), step-1 closed form.
   partition pinned: invariants of test_sparse_projection.py:14-27 (enumerates range(H)).
   xedges    pinned: brute force per feature on tiny inputs; invariants (permutation of the valid
@@ -59,7 +63,12 @@ def _load():
                                          P, P, P, P, P, P]
         lib.glo_adam_f32.argtypes = [ctypes.c_long, P, P, P, P, f, f, f, f, f, f, f, i]
         lib.glo_forward_max_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, P, P, P]
-        for fn in (lib.glo_forward_f64, lib.glo_backward_f64, lib.glo_adam_f32, lib.glo_forward_max_f64):
+        lib.glo_forward_topk_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, i, P, P, P]
+        lib.glo_backward_topk_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, i, P, P, P, P, ctypes.c_double,
+                                              P, P, P, P, P, P]
+        lib.glo_backward_events_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, i, i, P, P, P, P, P, P, P, P]
+        for fn in (lib.glo_forward_f64, lib.glo_backward_f64, lib.glo_adam_f32, lib.glo_forward_max_f64,
+                   lib.glo_forward_topk_f64, lib.glo_backward_topk_f64, lib.glo_backward_events_f64):
             fn.restype = None
         _lib = lib
     return _lib
@@ -114,6 +123,65 @@ def forward_max(x, idx, w, bias, counts, S, act="identity"):
     gap = np.zeros((B, G), np.float64)
     _load().glo_forward_max_f64(B, D, G, S, K, px, pi, pw, pb, pc, _ACT[act], _p(pre), _p(win), _p(gap))
     return pre, win, gap
+
+
+def forward_topk(x, idx, w, bias, counts, S, k, act="identity"):
+    """Top-k mean pooling: (pre [B, G] float64, slots [B, G, k] int32 best first, -1 past
+    min(n_g, k), gap [B, G]).  gap is the lead of the last selected z over the best unselected one,
+    relative to the rounding scale of z; pairs with a gap below ~1e-6 may select another set in fp32."""
+    B, D, G, K = _shapes(x, idx, counts, S)
+    x, px = _c(x, np.float32)
+    idx, pi = _c(idx, np.int32)
+    w, pw = _c(np.asarray(w).reshape(G * S, K), np.float32)
+    bias, pb = _c(np.asarray(bias).reshape(G * S), np.float32)
+    counts, pc = _c(counts, np.int32)
+    pre = np.zeros((B, G), np.float64)
+    slots = np.zeros((B, G, k), np.int32)
+    gap = np.zeros((B, G), np.float64)
+    _load().glo_forward_topk_f64(B, D, G, S, K, px, pi, pw, pb, pc, _ACT[act], k, _p(pre), _p(slots), _p(gap))
+    return pre, slots, gap
+
+
+def backward_topk(x, idx, w, bias, counts, S, dy, k, act="identity", with_bounds=False):
+    """(dW, db, dX) float64 of top-k mean pooling (the kk selected neurons get dy / kk)."""
+    B, D, G, K = _shapes(x, idx, counts, S)
+    x, px = _c(x, np.float32)
+    idx, pi = _c(idx, np.int32)
+    w, pw = _c(np.asarray(w).reshape(G * S, K), np.float32)
+    bias, pb = _c(np.asarray(bias).reshape(G * S), np.float32)
+    counts, pc = _c(counts, np.int32)
+    dy, pdy = _c(dy, np.float32)
+    shapes = ((G * S, K), (G * S,), (B, D))
+    dW, db, dX = (np.zeros(s, np.float64) for s in shapes)
+    mag = tuple(np.zeros(s, np.float64) for s in shapes) if with_bounds else (None,) * 3
+    unc = tuple(np.zeros(s, np.float64) for s in shapes) if with_bounds else (None,) * 3
+    _load().glo_backward_topk_f64(B, D, G, S, K, px, pi, pw, pb, pc, _ACT[act], k, pdy, _p(dW), _p(db), _p(dX),
+                                  AMBIGUOUS_Z, *map(_p, mag), *map(_p, unc))
+    if with_bounds:
+        return dW, db, dX, {"mag": mag, "unc": unc}
+    return dW, db, dX
+
+
+def backward_events(x, idx, w, bias, counts, S, dy, slots, act="identity", topk=False):
+    """(dW, db, dX, (magW, magb, magX)) float64 of a given selection: slots [B, G] (max pooling) or
+    [B, G, k] (top-k mean, coef dy / min(n_g, k)); -1 = none.  With the pooling's own selection it
+    equals backward(pool="max") / backward_topk."""
+    B, D, G, K = _shapes(x, idx, counts, S)
+    x, px = _c(x, np.float32)
+    idx, pi = _c(idx, np.int32)
+    w, pw = _c(np.asarray(w).reshape(G * S, K), np.float32)
+    bias, pb = _c(np.asarray(bias).reshape(G * S), np.float32)
+    counts, pc = _c(counts, np.int32)
+    dy, pdy = _c(dy, np.float32)
+    slots = np.asarray(slots, np.int32).reshape(B, G, -1)
+    kpe = slots.shape[2]
+    slots, ps = _c(slots, np.int32)
+    shapes = ((G * S, K), (G * S,), (B, D))
+    dW, db, dX = (np.zeros(s, np.float64) for s in shapes)
+    mag = tuple(np.zeros(s, np.float64) for s in shapes)
+    _load().glo_backward_events_f64(B, D, G, S, K, px, pi, pw, pb, pc, _ACT[act], int(topk), kpe, ps, pdy, _p(dW),
+                                    _p(db), _p(dX), *map(_p, mag))
+    return dW, db, dX, mag
 
 
 # relu masks decided within this relative distance of z = 0 may differ in fp32 (z is a sum of

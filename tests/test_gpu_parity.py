@@ -487,3 +487,90 @@ def test_max_layer_autograd_policies(policy):
     assert_parity(lay.weight.grad.cpu().numpy().reshape(-1, K), wdW, mW, uW, what="dW")
     assert_parity(lay.bias.grad.cpu().numpy().reshape(-1), wdb, mb, ub, what="db")
     assert lay.last_info["recomputed_stats"] == (policy == "minimal_stats")
+
+
+# ---- top-k mean pooling (pytorch_reference.py:68-77: the k largest raw z, ties to the smaller slot) ----
+TOPK_CASES = MAX_CASES[:4]
+
+
+def _runtime_topk(L, idx, act, k):
+    return Level1Runtime(L, idx.to(DEV), LevelSpec("topk_mean", activation=act, k=k), PhysicalPlan())
+
+
+@pytest.mark.parametrize("case", TOPK_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
+@pytest.mark.parametrize("act,k", [("identity", 1), ("identity", 8), ("relu", 8), ("identity", 64)])
+def test_topk_forward_matches_oracle(case, act, k):
+    D, H, G, K, B, xdt = case
+    L, idx, w, b, x, _ = make_case(D, H, G, K, B, x_dtype=xdt)
+    rt = _runtime_topk(L, idx, act, k)
+    out = rt.forward(x.to(DEV), w.to(DEV), b.to(DEV), track_ids=True)
+    pre, slots = out["pre"].cpu().numpy(), out["topk_slot"].cpu().numpy()
+    fi, fw, fb = flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    want, wslots, gap = O.forward_topk(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, k, act)
+    assert_close(pre, want, rtol=1e-5, atol=1e-6, what=f"top-{k} pre/{act}")
+    # the selected set is bit-exact wherever fp32 cannot move the boundary (lead > 2e-6 of the scale);
+    # within the set, near-equal values may be listed in either order
+    clear = gap > 2e-6
+    assert clear.mean() > 0.99
+    assert (np.sort(slots, -1)[clear] == np.sort(wslots, -1)[clear]).all()
+    kk = np.minimum(counts, k)
+    assert ((slots >= 0).sum(-1) == kk[None, :]).all() and (slots < counts[None, :, None]).all()
+    pre2 = rt.forward(x.to(DEV), w.to(DEV), b.to(DEV))
+    assert set(pre2) == {"pre"} and torch.equal(pre2["pre"].cpu(), out["pre"].cpu())
+
+
+@pytest.mark.parametrize("case", TOPK_CASES[:3], ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
+@pytest.mark.parametrize("act,k", [("identity", 8), ("relu", 4), ("identity", 64)])
+def test_topk_backward_matches_oracle(case, act, k):
+    """The selection events of the HIP forward, checked against the oracle's backward of the same
+    selection (which equals its top-k backward, test_oracle.py), plus determinism."""
+    from granulelayer_amd import _native as N
+
+    D, H, G, K, B, xdt = case
+    L, idx, w, b, x, dy = make_case(D, H, G, K, B, x_dtype=xdt)
+    rt = _runtime_topk(L, idx, act, k)
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    stats = rt.forward(xd, wd, bd, track_ids=True)
+    dw = torch.zeros(L.weight_shape, device=DEV)
+    db = torch.zeros(L.bias_shape, device=DEV)
+    with N.KernelTrace() as tr:
+        dx = rt.backward(xd, wd, bd, dy.to(DEV), stats, "save_winners", dw, db).cpu().numpy()
+    names = set(tr.times_ms())
+    assert {"max_events_dw_kernel", "max_events_dx_kernel"} <= names and "dx_kernel" not in names, sorted(names)
+    dw2, db2 = torch.zeros_like(dw), torch.zeros_like(db)
+    dx2 = rt.backward(xd, wd, bd, dy.to(DEV), stats, "save_winners", dw2, db2).cpu().numpy()
+    assert np.array_equal(dx, dx2) and torch.equal(dw, dw2) and torch.equal(db, db2)
+    fi, fw, fb = flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    wdW, wdb, wdX, (mW, mb, mX) = O.backward_events(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group,
+                                                    dy.numpy(), stats["topk_slot"].cpu().numpy(), act, topk=True)
+    assert_parity(dx, wdX, mX, what=f"top-{k} dX")
+    assert_parity(dw.cpu().numpy().reshape(-1, K), wdW, mW, what=f"top-{k} dW")
+    assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, what=f"top-{k} db")
+
+
+@pytest.mark.parametrize("policy", ["save_winners", "minimal_stats"])
+def test_topk_layer_autograd_policies(policy):
+    """SparsePoolingLayer with top-k mean (k = 8, identity activations): the gradients equal the
+    oracle's backward of the layer's own selection, with the slots saved or recomputed."""
+    D, H, G, K, B = 256, 12000, 12, 8, 40
+    lay = SparsePoolingLayer(D, H, G, fan_in=K, shared_neurons=None, pooling={"type": "topk_mean", "k": 8},
+                             checkpoint_policy=policy, dtype=torch.float32, device=DEV, seed=8, bias_std=0.2)
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn(B, D, generator=gen).to(DEV).requires_grad_(True)
+    dy = torch.randn(B, G, generator=gen).to(DEV)
+    y = lay(x)
+    (y * dy).sum().backward()
+    L = lay.layout
+    fi, fw, fb = flat(L, lay.indices.cpu(), lay.weight.detach().cpu(), lay.bias.detach().cpu())
+    counts = L.counts_tensor("cpu").numpy()
+    want, slots, gap = O.forward_topk(x.detach().cpu().numpy(), fi, fw, fb, counts, L.slots_per_group, 8)
+    assert gap.min() > 2e-6  # the seeded case has no near-tie at the selection boundary
+    assert_close(y.detach().cpu().numpy(), want, rtol=1e-5, atol=1e-6, what="y")
+    wdW, wdb, wdX, (mW, mb, mX) = O.backward_events(x.detach().cpu().numpy(), fi, fw, fb, counts, L.slots_per_group,
+                                                    dy.cpu().numpy(), slots, "identity", topk=True)
+    assert_parity(x.grad.cpu().numpy(), wdX, mX, what="dx")
+    assert_parity(lay.weight.grad.cpu().numpy().reshape(-1, K), wdW, mW, what="dW")
+    assert_parity(lay.bias.grad.cpu().numpy().reshape(-1), wdb, mb, what="db")
+    assert lay.last_info["recomputed_stats"] == (policy == "minimal_stats")

@@ -95,7 +95,7 @@ def test_config_parsing_matches_reference_semantics():
 
 @pytest.mark.parametrize("kwargs,exc", [
     (dict(shared_neurons=8, pooling="mean"), NotImplementedError),
-    (dict(shared_neurons=None, pooling="topk_mean"), NotImplementedError),
+    (dict(shared_neurons=None, pooling="logmeanexp"), NotImplementedError),
     (dict(shared_neurons=None, pooling={"type": "mean", "activation": "gelu"}), NotImplementedError),
     (dict(shared_neurons=None, pooling="mean", backend="triton"), ValueError),
     (dict(shared_neurons=None, pooling="mean", weight_layout="packed"), ValueError),

@@ -200,6 +200,87 @@ def test_backward_max_matches_autograd(oracle, act):
     assert (np.count_nonzero(db.reshape(G, S), axis=1) <= B).all()  # at most one winner per token
 
 
+def _topk_reference(x, idx, w, b, counts, S, k, act):
+    """The reference's formula (pytorch_reference.py:68-77) on float64 tensors with autograd."""
+    B, G = x.shape[0], len(counts)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
+    bt = torch.tensor(b, dtype=torch.float64, requires_grad=True)
+    z = ((xt[:, torch.as_tensor(idx, dtype=torch.int64)] * wt).sum(-1) + bt).reshape(B, G, S)
+    a = torch.relu(z) if act == "relu" else z
+    mask = (torch.arange(S)[None, :] < torch.as_tensor(counts)[:, None])[None].expand_as(z)
+    count = mask.sum(-1).to(z.dtype)
+    zm = torch.where(mask, z, torch.tensor(float("-inf"), dtype=torch.float64))
+    order = torch.sort(zm.detach(), dim=-1, descending=True, stable=True).indices[..., :k]
+    sel_valid = torch.arange(k)[None, None, :] < count[..., None]
+    vals = a.gather(-1, order)
+    kk = torch.clamp(count, max=k)
+    pooled = torch.where(sel_valid, vals, torch.zeros_like(vals)).sum(-1) / kk
+    return pooled, torch.where(sel_valid, order, torch.full_like(order, -1)), (xt, wt, bt)
+
+
+@pytest.mark.parametrize("act", ["identity", "relu"])
+@pytest.mark.parametrize("k", [1, 4, 16, 64])
+def test_forward_topk_matches_reference_formula(oracle, act, k):
+    rng = np.random.default_rng(13)
+    B, D, G, S, K = 4, 40, 3, 64, 8  # ragged pools of 32-64 slots (k <= S, as the reference assumes)
+    x, idx, w, b, counts = random_problem(rng, B, D, G, S, K)
+    want_pre, want_slots, _ = _topk_reference(x, idx, w, b, counts, S, k, act)
+    pre, slots, gap = oracle.forward_topk(x, idx, w, b, counts, S, k, act)
+    assert_close(pre, want_pre.detach().numpy(), rtol=1e-12, atol=1e-12, what="topk pre")
+    assert (slots == want_slots.numpy()).all()
+    assert (gap > 0).all()
+
+
+def test_forward_topk_ties_go_to_the_smaller_slot(oracle):
+    # z = 3, 5, 5, 3, 9 (slot 4 padded away): k = 2 takes slots 1, 2; k = 3 takes 1, 2, 0 (0 before 3)
+    x = np.array([[1.0, 1.0]], np.float32)
+    idx = np.array([[0, 1]] * 5, np.int32)
+    w = np.array([[1.5, 1.5], [2.5, 2.5], [2.5, 2.5], [1.5, 1.5], [4.5, 4.5]], np.float32)
+    b = np.zeros(5, np.float32)
+    c4 = np.array([4], np.int32)
+    pre, slots, gap = oracle.forward_topk(x, idx, w, b, c4, 5, 2)
+    assert pre[0, 0] == 5.0 and slots[0, 0].tolist() == [1, 2]
+    pre, slots, gap = oracle.forward_topk(x, idx, w, b, c4, 5, 4)
+    assert pre[0, 0] == 4.0 and slots[0, 0].tolist() == [1, 2, 0, 3] and gap[0, 0] == np.inf
+    pre, slots, _ = oracle.forward_topk(x, idx, w, b, c4, 5, 8)  # short pool: kk = 4, the rest -1
+    assert pre[0, 0] == 4.0 and slots[0, 0].tolist() == [1, 2, 0, 3, -1, -1, -1, -1]
+    _, _, gap = oracle.forward_topk(x, idx, w, b, c4, 5, 3)
+    assert gap[0, 0] == 0.0  # slot 0 and slot 3 tie at the boundary
+
+
+@pytest.mark.parametrize("act", ["identity", "relu"])
+@pytest.mark.parametrize("k", [2, 8])
+def test_backward_topk_matches_autograd(oracle, act, k):
+    rng = np.random.default_rng(14)
+    B, D, G, S, K = 5, 24, 3, 32, 8
+    x, idx, w, b, counts = random_problem(rng, B, D, G, S, K)
+    dy = rng.standard_normal((B, G)).astype(np.float32)
+    pooled, _, (xt, wt, bt) = _topk_reference(x, idx, w, b, counts, S, k, act)
+    (pooled * torch.as_tensor(dy, dtype=torch.float64)).sum().backward()
+    dW, db, dX = oracle.backward_topk(x, idx, w, b, counts, S, dy, k, act)
+    assert_close(dW, wt.grad.numpy(), rtol=1e-12, atol=1e-12, what="dW")
+    assert_close(db, bt.grad.numpy(), rtol=1e-12, atol=1e-12, what="db")
+    assert_close(dX, xt.grad.numpy(), rtol=1e-12, atol=1e-12, what="dX")
+
+
+@pytest.mark.parametrize("act", ["identity", "relu"])
+def test_backward_events_of_the_own_selection_is_the_pooling_backward(oracle, act):
+    rng = np.random.default_rng(15)
+    B, D, G, S, K = 4, 32, 3, 40, 8
+    x, idx, w, b, counts = random_problem(rng, B, D, G, S, K)
+    dy = rng.standard_normal((B, G)).astype(np.float32)
+    _, win, _ = oracle.forward_max(x, idx, w, b, counts, S, act)
+    got = oracle.backward_events(x, idx, w, b, counts, S, dy, win, act)[:3]
+    for g_, w_ in zip(got, oracle.backward(x, idx, w, b, counts, S, dy, act, "max")):
+        assert_close(g_, w_, rtol=1e-14, atol=1e-14, what="events == max backward")
+    for k in (2, 8, 64):
+        _, sl, _ = oracle.forward_topk(x, idx, w, b, counts, S, k, act)
+        got = oracle.backward_events(x, idx, w, b, counts, S, dy, sl, act, topk=True)[:3]
+        for g_, w_ in zip(got, oracle.backward_topk(x, idx, w, b, counts, S, dy, k, act)):
+            assert_close(g_, w_, rtol=1e-14, atol=1e-14, what=f"events == top-{k} backward")
+
+
 def test_backward_accumulates_and_finite_differences(oracle):
     rng = np.random.default_rng(5)
     B, D, G, S, K = 3, 20, 2, 32, 8
