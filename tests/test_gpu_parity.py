@@ -574,3 +574,35 @@ def test_topk_layer_autograd_policies(policy):
     assert_parity(lay.weight.grad.cpu().numpy().reshape(-1, K), wdW, mW, what="dW")
     assert_parity(lay.bias.grad.cpu().numpy().reshape(-1), wdb, mb, what="db")
     assert lay.last_info["recomputed_stats"] == (policy == "minimal_stats")
+
+
+# two backward token chunks (B > 1024: the event kernels' b0 > 0) and D = 8192 (dX event LDS of 96 KiB)
+SEL_EDGE_CASES = [(2048, 8000, 8, 8, 1100, torch.float32), (8192, 6000, 6, 8, 70, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("case", SEL_EDGE_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
+@pytest.mark.parametrize("pool,k", [("max", 1), ("topk_mean", 8)])
+def test_selection_backward_chunks_and_wide_inputs(case, pool, k):
+    D, H, G, K, B, xdt = case
+    L, idx, w, b, x, dy = make_case(D, H, G, K, B, x_dtype=xdt)
+    spec = LevelSpec(pool, activation="relu", k=k) if pool == "topk_mean" else LevelSpec(pool, activation="relu")
+    rt = Level1Runtime(L, idx.to(DEV), spec, PhysicalPlan())
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    stats = rt.forward(xd, wd, bd, track_ids=True)
+    key = "winner" if pool == "max" else "topk_slot"
+    dw = torch.zeros(L.weight_shape, device=DEV)
+    db = torch.zeros(L.bias_shape, device=DEV)
+    dx = rt.backward(xd, wd, bd, dy.to(DEV), stats, "save_winners", dw, db).cpu().numpy()
+    fi, fw, fb = flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    xn = x.float().numpy()
+    if pool == "max":
+        want, _, _ = O.forward_max(xn, fi, fw, fb, counts, L.slots_per_group, "relu")
+    else:
+        want, _, _ = O.forward_topk(xn, fi, fw, fb, counts, L.slots_per_group, k, "relu")
+    assert_close(stats["pre"].cpu().numpy(), want, rtol=1e-5, atol=1e-6, what=f"{pool} pre")
+    wdW, wdb, wdX, (mW, mb, mX) = O.backward_events(xn, fi, fw, fb, counts, L.slots_per_group, dy.numpy(),
+                                                    stats[key].cpu().numpy(), "relu", topk=pool == "topk_mean")
+    assert_parity(dx, wdX, mX, what=f"{pool} dX")
+    assert_parity(dw.cpu().numpy().reshape(-1, K), wdW, mW, what=f"{pool} dW")
+    assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, what=f"{pool} db")
