@@ -606,3 +606,30 @@ def test_selection_backward_chunks_and_wide_inputs(case, pool, k):
     assert_parity(dx, wdX, mX, what=f"{pool} dX")
     assert_parity(dw.cpu().numpy().reshape(-1, K), wdW, mW, what=f"{pool} dW")
     assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, what=f"{pool} db")
+
+
+@pytest.mark.parametrize("k", [16, 64])
+def test_topk_pools_shorter_than_k(k):
+    """Pools of 12-13 neurons with k = 16 / 64: every valid neuron is selected (kk = n_g), the padded
+    list entries never are, and the slots past kk are -1 (pytorch_reference.py:68-77)."""
+    D, H, G, K, B = 64, 100, 8, 8, 21
+    L, idx, w, b, x, dy = make_case(D, H, G, K, B)
+    rt = _runtime_topk(L, idx, "identity", k)
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    out = rt.forward(xd, wd, bd, track_ids=True)
+    fi, fw, fb = flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    want, wslots, _ = O.forward_topk(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, k)
+    assert (counts < k).all()
+    assert_close(out["pre"].cpu().numpy(), want, rtol=1e-5, atol=1e-6, what="pre")
+    slots = out["topk_slot"].cpu().numpy()
+    assert (np.sort(slots, -1) == np.sort(wslots, -1)).all()  # the whole pool, -1 padding
+    dw = torch.zeros(L.weight_shape, device=DEV)
+    db = torch.zeros(L.bias_shape, device=DEV)
+    dx = rt.backward(xd, wd, bd, dy.to(DEV), out, "save_winners", dw, db).cpu().numpy()
+    wdW, wdb, wdX, bnd = O.backward_topk(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, dy.numpy(), k,
+                                         "identity", with_bounds=True)
+    (mW, mb, mX), (uW, ub, uX) = bnd["mag"], bnd["unc"]
+    assert_parity(dx, wdX, mX, uX, what="dX")
+    assert_parity(dw.cpu().numpy().reshape(-1, K), wdW, mW, uW, what="dW")
+    assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, ub, what="db")
