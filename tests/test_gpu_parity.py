@@ -633,3 +633,19 @@ def test_topk_pools_shorter_than_k(k):
     assert_parity(dx, wdX, mX, uX, what="dX")
     assert_parity(dw.cpu().numpy().reshape(-1, K), wdW, mW, uW, what="dW")
     assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, ub, what="db")
+
+
+@pytest.mark.parametrize("pooling", ["sum", "mean", "max", {"type": "topk_mean", "k": 8}],
+                         ids=["sum", "mean", "max", "topk8"])
+def test_empty_batch(pooling):
+    """B = 0 through the layer: an empty [0, G] output, an empty dX and zero parameter gradients
+    (the C-ABI refuses B < 1; the backend answers an empty batch without launching)."""
+    D, H, G, K = 128, 3000, 6, 8
+    lay = SparsePoolingLayer(D, H, G, fan_in=K, shared_neurons=None, pooling=pooling,
+                             checkpoint_policy="save_winners", dtype=torch.float32, device=DEV, seed=3)
+    x = torch.zeros(0, D, device=DEV, requires_grad=True)
+    y = lay(x)
+    assert tuple(y.shape) == (0, G)
+    y.sum().backward()
+    assert tuple(x.grad.shape) == (0, D)
+    assert not lay.weight.grad.any() and not lay.bias.grad.any()
