@@ -165,35 +165,80 @@ __device__ __forceinline__ void fwd_tile_max(const char* xsb, const unsigned (&a
   }
 }
 
-// (value, slot) list of one token, best first (value descending, then the smaller slot)
-__device__ __forceinline__ void cand_cmpex(float& va, int& sa, float& vb, int& sb) {
-  const bool swap = vb > va || (vb == va && sb < sa);
-  const float tv = va;
-  const int ts = sa;
-  va = swap ? vb : va, sa = swap ? sb : sa;
-  vb = swap ? tv : vb, sb = swap ? ts : sb;
+// Top-k candidates as 64-bit keys, one unsigned compare per ordering decision.  The high word
+// maps the fp32 value to an unsigned integer of the same order (negative values bit-inverted,
+// the others with the sign bit set; -0 is first made +0, so equal values compare equal); the low
+// word is ~slot, so that of two equal values the smaller slot ranks higher.  Slots are distinct
+// within a wave, so keys never tie.
+using cand_t = unsigned long long;
+__device__ __forceinline__ cand_t cand_key(float v, unsigned nslot) {
+  const unsigned b = __float_as_uint(v + 0.f);
+  const unsigned o = b ^ ((unsigned)((int)b >> 31) | 0x80000000u);
+  return ((cand_t)o << 32) | nslot;
+}
+__device__ __forceinline__ float cand_value(cand_t c) {
+  const unsigned o = (unsigned)(c >> 32);
+  return __uint_as_float((o & 0x80000000u) ? (o ^ 0x80000000u) : ~o);
+}
+__device__ __forceinline__ int cand_slot(cand_t c) { return (int)~(unsigned)c; }
+// the key of (-inf, slot 0x7fffffff): below every candidate a wave holds
+constexpr cand_t CAND_NONE = (0x007fffffull << 32) | 0x80000000u;
+
+// a before b in the best-first order
+__device__ __forceinline__ void cand_cmpex(cand_t& a, cand_t& b) {
+  const bool swap = b > a;
+  const cand_t t = a;
+  a = swap ? b : a;
+  b = swap ? t : b;
 }
 
 // drop the list's head when it is the round's winner w
-__device__ __forceinline__ void cand_pop(float (&v)[4], int (&sl)[4], int w) {
-  const bool take = sl[0] == w;
+__device__ __forceinline__ void cand_pop(cand_t (&c)[4], cand_t w) {
+  const bool take = c[0] == w;
 #pragma unroll
-  for (int i = 0; i < 3; ++i) v[i] = take ? v[i + 1] : v[i], sl[i] = take ? sl[i + 1] : sl[i];
-  v[3] = take ? -__builtin_inff() : v[3];
-  sl[3] = take ? 0x7fffffff : sl[3];
+  for (int i = 0; i < 3; ++i) c[i] = take ? c[i + 1] : c[i];
+  c[3] = take ? CAND_NONE : c[3];
+}
+
+template <int CTRL>
+__device__ __forceinline__ cand_t dppk(cand_t v) {
+  const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)v, CTRL, 0xf, 0xf, false);
+  const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(v >> 32), CTRL, 0xf, 0xf, false);
+  return ((cand_t)hi << 32) | lo;
+}
+__device__ __forceinline__ cand_t kmax(cand_t a, cand_t b) { return b > a ? b : a; }
+__device__ __forceinline__ cand_t permlane16_max(cand_t c) {
+  const auto l = __builtin_amdgcn_permlane16_swap((unsigned)c, (unsigned)c, false, false);
+  const auto h = __builtin_amdgcn_permlane16_swap((unsigned)(c >> 32), (unsigned)(c >> 32), false, false);
+  return kmax(((cand_t)h[0] << 32) | l[0], ((cand_t)h[1] << 32) | l[1]);
+}
+__device__ __forceinline__ cand_t permlane32_max(cand_t c) {
+  const auto l = __builtin_amdgcn_permlane32_swap((unsigned)c, (unsigned)c, false, false);
+  const auto h = __builtin_amdgcn_permlane32_swap((unsigned)(c >> 32), (unsigned)(c >> 32), false, false);
+  return kmax(((cand_t)h[0] << 32) | l[0], ((cand_t)h[1] << 32) | l[1]);
+}
+
+// wave_max4 over keys: the same reduce-scatter (lanes 0, 2, 1, 3 end with tokens 0, 1, 2, 3)
+__device__ __forceinline__ cand_t wave_max4_key(cand_t a0, cand_t a1, cand_t a2, cand_t a3, int lane) {
+  const bool odd = lane & 1, hi = lane & 2;
+  const cand_t b0 = kmax(odd ? a2 : a0, dppk<0xB1>(odd ? a0 : a2));  // quad_perm(1,0,3,2)
+  const cand_t b1 = kmax(odd ? a3 : a1, dppk<0xB1>(odd ? a1 : a3));
+  cand_t c = kmax(hi ? b1 : b0, dppk<0x4E>(hi ? b0 : b1));           // quad_perm(2,3,0,1)
+  c = kmax(c, dppk<0x124>(c));                                          // row_ror:4
+  c = kmax(c, dppk<0x128>(c));                                          // row_ror:8
+  return permlane32_max(permlane16_max(c));
 }
 
 // Top-k tile (top-k mean pooling, pytorch_reference.py:68-77): per token the k largest raw z of the
 // wave's neurons with their slots (ties to the smaller slot), best first.  Every lane sorts its 4
-// candidates per token; then k rounds take the wave's best head (wave_max4) and drop it from the
-// lane that holds it.  Lanes 0-3 store each round's pair; the finalize merges the pool's chunks.
+// candidates per token; then k rounds take the wave's best head (wave_max4_key) and drop it from
+// the lane that holds it.  Lanes 0-3 store each round's pair; the finalize merges the pool's chunks.
 template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8)>
 __device__ __forceinline__ void fwd_tile_topk(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                               const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
                                               int k, bool store, int lane) {
   static_assert(NPL == 4, "per-lane candidate lists of 4");
-  float v[4][4];  // [token][position]
-  int sv[4][4];
+  cand_t c[4][4];  // [token][position]
   float4 xc[K];
 #pragma unroll
   for (int k0 = 0; k0 < RA; ++k0) xc[k0] = lds_x<FAR>(xsb, addr[0][k0]);
@@ -215,8 +260,8 @@ __device__ __forceinline__ void fwd_tile_topk(const char* xsb, const unsigned (&
       z2 = __builtin_fmaf(xc[kk].z, w[j][kk], z2);
       z3 = __builtin_fmaf(xc[kk].w, w[j][kk], z3);
     }
-    v[0][j] = z0, v[1][j] = z1, v[2][j] = z2, v[3][j] = z3;  // raw z ranks (the activation is the finalize's)
-    sv[0][j] = sv[1][j] = sv[2][j] = sv[3][j] = slot[j];
+    const unsigned ns = ~(unsigned)slot[j];  // raw z ranks (the activation is the finalize's)
+    c[0][j] = cand_key(z0, ns), c[1][j] = cand_key(z1, ns), c[2][j] = cand_key(z2, ns), c[3][j] = cand_key(z3, ns);
     __builtin_amdgcn_sched_barrier(0);
     if (j + 1 < NPL) {
 #pragma unroll
@@ -225,26 +270,28 @@ __device__ __forceinline__ void fwd_tile_topk(const char* xsb, const unsigned (&
   }
 #pragma unroll
   for (int t = 0; t < 4; ++t) {  // sorting network for 4
-    cand_cmpex(v[t][0], sv[t][0], v[t][1], sv[t][1]);
-    cand_cmpex(v[t][2], sv[t][2], v[t][3], sv[t][3]);
-    cand_cmpex(v[t][0], sv[t][0], v[t][2], sv[t][2]);
-    cand_cmpex(v[t][1], sv[t][1], v[t][3], sv[t][3]);
-    cand_cmpex(v[t][1], sv[t][1], v[t][2], sv[t][2]);
+    cand_cmpex(c[t][0], c[t][1]);
+    cand_cmpex(c[t][2], c[t][3]);
+    cand_cmpex(c[t][0], c[t][2]);
+    cand_cmpex(c[t][1], c[t][3]);
+    cand_cmpex(c[t][1], c[t][2]);
   }
   const int tok = wave_sum4_token(lane);
   for (int r = 0; r < k; ++r) {
-    float m;
-    int sl;
-    wave_max4(v[0][0], v[1][0], v[2][0], v[3][0], sv[0][0], sv[1][0], sv[2][0], sv[3][0], lane, m, sl);
+    const cand_t m = wave_max4_key(c[0][0], c[1][0], c[2][0], c[3][0], lane);
     if (store && lane < 4) {
-      out[tok * k + r] = m;
-      oslot[tok * k + r] = sl;
+      out[tok * k + r] = cand_value(m);
+      oslot[tok * k + r] = cand_slot(m);
     }
     // lanes 0, 2, 1, 3 hold the winners of tokens 0, 1, 2, 3
-    cand_pop(v[0], sv[0], __builtin_amdgcn_readlane(sl, 0));
-    cand_pop(v[1], sv[1], __builtin_amdgcn_readlane(sl, 2));
-    cand_pop(v[2], sv[2], __builtin_amdgcn_readlane(sl, 1));
-    cand_pop(v[3], sv[3], __builtin_amdgcn_readlane(sl, 3));
+    const unsigned mlo = (unsigned)m, mhi = (unsigned)(m >> 32);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int src = (t == 1) ? 2 : (t == 2) ? 1 : t;
+      const cand_t wt = ((cand_t)(unsigned)__builtin_amdgcn_readlane((int)mhi, src) << 32) |
+                        (unsigned)__builtin_amdgcn_readlane((int)mlo, src);
+      cand_pop(c[t], wt);
+    }
   }
 }
 
