@@ -514,6 +514,72 @@ __global__ void __launch_bounds__(256) fwd_finalize_topk_kernel(const float* __r
   pre[i] = sum / (float)kk;
 }
 
+// k = 8 with at most 4 chunks per pool (pools of up to 1024 slots): the same merge with the lists
+// in registers.  Every thread loads its 4 lists with 16-byte loads (the lanes of a wave read
+// consecutive tokens' lists, 2 KiB in a row) instead of re-reading every head per pick, and
+// writes its 8 slots with two 16-byte stores.  Picks and summation order are those of
+// fwd_finalize_topk_kernel, so the results are bit-identical.
+constexpr int FWD_TOP8_CPG = 4;
+
+template <int ACT>
+__global__ void __launch_bounds__(256) fwd_finalize_top8_kernel(const float* __restrict__ part, const int* __restrict__ pslot,
+                                                                const int32_t* __restrict__ counts, float* __restrict__ pre,
+                                                                int32_t* __restrict__ topk_slot, int B, int G, int cpg,
+                                                                int b_pad) {
+  constexpr int KP = 8, CP = FWD_TOP8_CPG;
+  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long long)B * G) return;
+  const int b = (int)(t % B), g = (int)(t / B);
+  const long long i = (long long)b * G + g;
+  float v[CP][KP];
+  int s[CP][KP];
+#pragma unroll
+  for (int c = 0; c < CP; ++c) {
+    if (c < cpg) {
+      const long long o = (((long long)g * cpg + c) * b_pad + b) * KP;
+      const float4 a0 = *reinterpret_cast<const float4*>(part + o), a1 = *reinterpret_cast<const float4*>(part + o + 4);
+      const int4 q0 = *reinterpret_cast<const int4*>(pslot + o), q1 = *reinterpret_cast<const int4*>(pslot + o + 4);
+      v[c][0] = a0.x, v[c][1] = a0.y, v[c][2] = a0.z, v[c][3] = a0.w;
+      v[c][4] = a1.x, v[c][5] = a1.y, v[c][6] = a1.z, v[c][7] = a1.w;
+      s[c][0] = q0.x, s[c][1] = q0.y, s[c][2] = q0.z, s[c][3] = q0.w;
+      s[c][4] = q1.x, s[c][5] = q1.y, s[c][6] = q1.z, s[c][7] = q1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < KP; ++e) v[c][e] = -__builtin_inff(), s[c][e] = 0x7fffffff;
+    }
+  }
+  const int n_g = counts[g];
+  const int kk = n_g < KP ? n_g : KP;
+  float sum = 0.f;
+  int out[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    int bc = 0;
+    float bv = v[0][0];
+    int bs = s[0][0];
+#pragma unroll
+    for (int c = 1; c < CP; ++c) {
+      const bool tk = v[c][0] > bv || (v[c][0] == bv && s[c][0] < bs);
+      bc = tk ? c : bc, bv = tk ? v[c][0] : bv, bs = tk ? s[c][0] : bs;
+    }
+    out[j] = j < kk ? bs : -1;
+    if (j < kk) sum += ACT == GL_ACT_RELU ? __builtin_fmaxf(bv, 0.f) : bv;
+    // drop the head of the list it came from; after j + 1 picks a list is read at most up to
+    // position KP - 2 - j, and a list popped p <= j times still holds valid entries to KP - 1 - p
+#pragma unroll
+    for (int c = 0; c < CP; ++c) {
+      const bool take = c == bc;
+#pragma unroll
+      for (int e = 0; e + 1 < KP - j; ++e) v[c][e] = take ? v[c][e + 1] : v[c][e], s[c][e] = take ? s[c][e + 1] : s[c][e];
+    }
+  }
+  if (topk_slot) {
+    *reinterpret_cast<int4*>(topk_slot + i * KP) = make_int4(out[0], out[1], out[2], out[3]);
+    *reinterpret_cast<int4*>(topk_slot + i * KP + 4) = make_int4(out[4], out[5], out[6], out[7]);
+  }
+  pre[i] = sum / (float)kk;
+}
+
 // ---- host side -------------------------------------------------------------------------------
 // 4 neurons per lane; 16 waves per workgroup at K = 8 (4 waves per SIMD, 128 VGPRs), 8 at K = 16
 // (2 per SIMD: the parameters of 4 neurons of fan-in 16 take twice the registers).  Max pooling
@@ -649,7 +715,14 @@ extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
   } else if (a->pool == GL_POOL_TOPK_MEAN) {
     GL_TRY(launch_fwd_any<PK_TOPK>(a->act, a->K, a->D, k, s));
     const dim3 g1((unsigned)ceil_div((long long)a->B * a->G, 256));
-    if (a->act == GL_ACT_RELU)
+    const bool top8 = a->topk == 8 && q.cpg <= FWD_TOP8_CPG && ((uintptr_t)a->winner & 15) == 0;
+    if (top8 && a->act == GL_ACT_RELU)
+      GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_top8_kernel<GL_ACT_RELU>, g1, dim3(256), 0, s, part, pslot,
+                a->counts, a->pre, a->winner, a->B, a->G, q.cpg, q.b_pad);
+    else if (top8)
+      GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_top8_kernel<GL_ACT_IDENTITY>, g1, dim3(256), 0, s, part, pslot,
+                a->counts, a->pre, a->winner, a->B, a->G, q.cpg, q.b_pad);
+    else if (a->act == GL_ACT_RELU)
       GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_topk_kernel<GL_ACT_RELU>, g1, dim3(256), 0, s, part, pslot,
                 a->counts, a->pre, a->winner, a->B, a->G, q.cpg, q.b_pad, a->topk);
     else
