@@ -84,6 +84,10 @@ class SparsePoolingLayer(nn.Module):
         return self._rt
 
     def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        # a checkpoint of an input-supergroup layer carries its plan as `sg_plan` (layer.py:133-142);
+        # this layer has no connectivity, so such a checkpoint is refused as the reference refuses it
+        if prefix + "sg_plan" in state_dict:
+            raise ValueError("checkpoint and layer disagree on input-supergroup connectivity")
         key = prefix + "indices"
         if key in state_dict and state_dict[key].dtype == torch.int16:  # reference checkpoint
             state_dict[key] = state_dict[key].to(torch.int32)

@@ -165,3 +165,19 @@ def test_c5_keeps_top16_of_64_candidates():
         assert ki[r].tolist() == keep
         assert all(float(kw[r, i]) == float(wenv[r, (cand[r] == ki[r, i]).nonzero()[0, 0]]) for i in range(16))
     assert int(cand[1, 5]) in ki[1].tolist() and int(cand[1, 9]) not in ki[1].tolist()
+
+
+def test_state_dict_formats():
+    """Checkpoint formats (layer.py:82-88, 133-142): the state-dict keys are the reference's, int16
+    indices of a reference checkpoint are widened on load, and a checkpoint that carries an
+    input-supergroup plan (`sg_plan`) is refused, since this layer has no connectivity."""
+    src = SparsePoolingLayer(64, 3000, 8, shared_neurons=None, pooling="mean", dtype=torch.float32, seed=4)
+    sd = src.state_dict()
+    assert set(sd) == {"indices", "weight", "bias"}
+    dst = SparsePoolingLayer(64, 3000, 8, shared_neurons=None, pooling="mean", dtype=torch.float32, seed=5)
+    dst.load_state_dict({**sd, "indices": sd["indices"].to(torch.int16)})
+    assert dst.indices.dtype == torch.int32 and torch.equal(dst.indices, sd["indices"])
+    assert torch.equal(dst.weight, src.weight) and torch.equal(dst.bias, src.bias)
+    plan = torch.frombuffer(bytearray(b'{"kind": "supergroups"}'), dtype=torch.uint8).clone()
+    with pytest.raises(ValueError, match="supergroup"):
+        dst.load_state_dict({**sd, "sg_plan": plan})
