@@ -146,10 +146,24 @@ __device__ __forceinline__ void fwd_tile_max(const char* xsb, const unsigned (&a
       z2 = __builtin_fmaxf(z2, 0.f);
       z3 = __builtin_fmaxf(z3, 0.f);
     }
-    vmax_pair(m0, s0, z0, slot[j]);
-    vmax_pair(m1, s1, z1, slot[j]);
-    vmax_pair(m2, s2, z2, slot[j]);
-    vmax_pair(m3, s3, z3, slot[j]);
+    // A lane's neurons 2i and 2i + 1 share a 128-slot window (sched_slot), later pairs lie in later
+    // windows: slot[2i] exceeds every slot before it, so a strict compare keeps ties on the
+    // smaller slot there; inside a pair the order is free and the full pair compare decides.
+    if (j == 0) {
+      m0 = z0, m1 = z1, m2 = z2, m3 = z3;
+      s0 = s1 = s2 = s3 = slot[0];
+    } else if (j % 2 == 0) {
+      const bool t0 = z0 > m0, t1 = z1 > m1, t2 = z2 > m2, t3 = z3 > m3;
+      m0 = t0 ? z0 : m0, s0 = t0 ? slot[j] : s0;
+      m1 = t1 ? z1 : m1, s1 = t1 ? slot[j] : s1;
+      m2 = t2 ? z2 : m2, s2 = t2 ? slot[j] : s2;
+      m3 = t3 ? z3 : m3, s3 = t3 ? slot[j] : s3;
+    } else {
+      vmax_pair(m0, s0, z0, slot[j]);
+      vmax_pair(m1, s1, z1, slot[j]);
+      vmax_pair(m2, s2, z2, slot[j]);
+      vmax_pair(m3, s3, z3, slot[j]);
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (j + 1 < NPL) {
 #pragma unroll
