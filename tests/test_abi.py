@@ -74,3 +74,25 @@ def test_arguments_are_refused_before_device_use():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(N.NativeError, match="not found"):
         N.Library(tmp_path / "nope.so")
+
+
+def test_pool_limits_are_refused_by_the_size_query():
+    """Top-k mean takes k a power of two in [1, 64] (the reference's LevelSpec check) and pools of
+    up to 4096 slots; other pool codes are refused.  Host-side checks only: the pointers are
+    placeholders that the size query never dereferences."""
+    lib = N.library()
+    out = ctypes.c_size_t()
+
+    def query(pool, topk, S):
+        a = N.GlFwdArgs(X=16, idx=16, W=16, bias=16, counts=16, B=8, D=64, G=2, S=S, K=8,
+                        act=N.GL_ACT["identity"], pool=pool, topk=topk)
+        return lib.lib.gl_fwd_workspace(ctypes.byref(a), ctypes.byref(out))
+
+    tk = N.GL_POOL["topk_mean"]
+    for k in (1, 2, 8, 64):
+        assert query(tk, k, 4096) == 0 and out.value > 0
+    for k in (0, 3, 12, 128):
+        assert query(tk, k, 256) == -1
+    assert query(tk, 8, 4097) == -2
+    assert query(N.GL_POOL["max"], 0, 100000) == 0
+    assert query(7, 0, 256) == -2

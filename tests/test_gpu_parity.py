@@ -649,3 +649,31 @@ def test_empty_batch(pooling):
     y.sum().backward()
     assert tuple(x.grad.shape) == (0, D)
     assert not lay.weight.grad.any() and not lay.bias.grad.any()
+
+
+@pytest.mark.parametrize("k", [8, 64])
+def test_topk_largest_pools(k):
+    """Pools of 4000 slots: 16 chunks per pool, the most the top-k finalize merges (larger pools
+    are refused), through the generic finalize; forward and the event backward against the oracle."""
+    D, H, G, K, B = 64, 12000, 3, 8, 9
+    L, idx, w, b, x, dy = make_case(D, H, G, K, B)
+    assert L.slots_per_group > 15 * 256
+    rt = _runtime_topk(L, idx, "identity", k)
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    out = rt.forward(xd, wd, bd, track_ids=True)
+    fi, fw, fb = flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    want, wslots, gap = O.forward_topk(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, k)
+    assert_close(out["pre"].cpu().numpy(), want, rtol=1e-5, atol=1e-6, what=f"top-{k} pre")
+    slots = out["topk_slot"].cpu().numpy()
+    clear = gap > 2e-6
+    assert clear.mean() > 0.9
+    assert (np.sort(slots, -1)[clear] == np.sort(wslots, -1)[clear]).all()
+    dw = torch.zeros(L.weight_shape, device=DEV)
+    db = torch.zeros(L.bias_shape, device=DEV)
+    dx = rt.backward(xd, wd, bd, dy.to(DEV), out, "save_winners", dw, db).cpu().numpy()
+    wdW, wdb, wdX, (mW, mb, mX) = O.backward_events(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group,
+                                                    dy.numpy(), slots, "identity", topk=True)
+    assert_parity(dx, wdX, mX, what="dX")
+    assert_parity(dw.cpu().numpy().reshape(-1, K), wdW, mW, what="dW")
+    assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, what="db")
