@@ -1,4 +1,4 @@
-// Forward: fused sparse projection -> activation -> pool (sum / mean), neuron-stationary.
+// Forward: fused sparse projection -> activation -> pool (sum / mean, max, top-k mean), neuron-stationary.
 //
 // Each wave owns a "chunk": up to 64*NPL consecutive slots of one group, NPL neurons per lane
 // (slot s_lo + j*64 + lane, or the gather schedule's permutation of the chunk's 128-slot
