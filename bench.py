@@ -11,7 +11,11 @@ same layer (the headline forward) is reported beside it.
 value = useful edge-MACs per second of the whole step (B * N * 8 / step time, one pass, as the
 reference's useful_tflops(passes=1), sparse_pooling/benchmarks/common.py:80-82).
 
-Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--no-extra]
+
+Beside the headline the line carries: the C1 train step on the GPU, the C4
+full training step (configs[3], 3 timed steps), the one-time layer setup, and cpu_baseline = the
+reference's CPU path on C1 timed on the host cores.
 """
 from __future__ import annotations
 
@@ -64,22 +68,6 @@ def algorithmic(kernel: str, B: int, N: int, K: int, D: int, G: int, x_bytes: in
     if kernel == "adam_kernel":
         return 32 * (E + N), 12 * (E + N)
     return None, None
-
-
-def read_traffic(path: str) -> dict:
-    """Calibrated HBM bytes per launch of each kernel from a committed rocprofv3 summary: lines
-    ``traffic <kernel> <bytes>`` (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the
-    counter reads for a device copy of known size)."""
-    out = {}
-    try:
-        with open(path) as f:
-            for line in f:
-                parts = line.split()
-                if len(parts) == 3 and parts[0] == "traffic":
-                    out[parts[1]] = int(float(parts[2]))
-    except OSError:
-        pass
-    return out
 
 
 CONFIG_WORK = {"C1": "fwd+bwd+adam", "C2": "fwd", "C3": "fwd+bwd", "C4": "fwd+bwd+adam", "C5": "fwd+bwd"}
@@ -148,25 +136,184 @@ def run_config(name: str, steps: int, warmup: int):
     print(json.dumps(out), flush=True)
 
 
-def cpu_baseline(groups: int, steps: int):
+def _med_iqr(v):
+    import numpy as np
+
+    q1, q2, q3 = np.percentile(np.asarray(v, dtype=np.float64), [25, 50, 75])
+    return round(q2 * 1e3, 2), round((q3 - q1) * 1e3, 2)
+
+
+def c1_problem():
+    """BASELINE configs[0] (the reference's CPU-runnable case): B=64, D=1024, N=1,048,576, fan-in 8,
+    pools of 256, seed 0, generated on the CPU so the GPU and the CPU path see the same bits."""
+    from granulelayer_amd.synthetic import make_problem
+
+    return make_problem("C1", device="cpu", seed=0)
+
+
+def c1_gpu(pr, steps: int, warmup: int):
+    """The C1 training step (forward, recompute backward into main_grad, FusedAdamW) on the GPU,
+    with the layer's first output and input gradient for the CPU comparison."""
     import torch
 
-    from granulelayer_amd.synthetic import make_problem
+    from granulelayer_amd import FusedAdamW, SparsePoolingLayer
+
+    L = pr.layout
+    dev = torch.device("cuda", 0)
+    lay = SparsePoolingLayer(L.input_dim, L.hidden_dim, L.groups, fan_in=L.fan_in, shared_neurons=None,
+                             pooling="sum", dtype=torch.float32, device=dev, seed=0)
+    with torch.no_grad():
+        lay.indices.copy_(pr.idx.to(dev))
+        lay.weight.copy_(pr.w.to(dev))
+        lay.bias.copy_(pr.b.to(dev))
+    lay.enable_main_grad()
+    opt = FusedAdamW(lay.parameters(), lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, moments="fp32")
+    x = pr.x.to(dev).requires_grad_(True)
+    dy = pr.dy.to(dev)
+    y = lay(x)
+    y.backward(dy)
+    first = (y.detach().cpu(), x.grad.detach().cpu())
+    opt.step()
+
+    def step():
+        y = lay(x)
+        y.backward(dy)
+        opt.step()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    del lay, opt
+    return ms, first
+
+
+def cpu_baseline(pr, steps: int, gpu_first):
+    """The reference's CPU path on BASELINE configs[0] (C1): the materialising torch restatement of
+    sparse_pooling/reference (oracle/reference_port.py) with torch.optim.Adam, timed on the host
+    cores; its first output and input gradient are compared with the GPU's on the same inputs."""
+    import torch
+
     from oracle.reference_port import PortStep
 
-    pr = make_problem("C2", device="cpu", seed=0, groups=groups)
     st = PortStep(pr.idx, pr.w, pr.b, pr.layout.counts_tensor("cpu"), pr.layout.slots_per_group, pool="sum")
-    x = pr.x.float()
-    st.step(x, pr.dy)  # warm-up
-    times = [st.step(x, pr.dy)["step"] for _ in range(steps)]
-    t = sorted(times)[len(times) // 2]
+    x = pr.x.float().detach().requires_grad_(True)
+    y = st.forward(x)
+    (y * pr.dy).sum().backward()
+    gy, gdx = gpu_first
+    rel = lambda a, b: float((a.double() - b.double()).norm() / b.double().norm())  # noqa: E731
+    parity = {"y_rel_err": rel(gy, y.detach()), "dx_rel_err": rel(gdx, x.grad)}
+    st.w.grad = None
+    st.b.grad = None
+    times = [st.step(pr.x.float(), pr.dy) for _ in range(steps)]
     macs = pr.B * pr.edges
-    return {"value": round(macs / t / 1e9, 4), "unit": "G edge-MAC/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": (f"C2 train step (fwd+bwd+torch.optim.Adam) on {groups} of 98,304 pools "
-                       f"({groups * 1024:,} neurons, B=256, D=4096), materialising torch restatement of "
-                       f"sparse_pooling/reference on the host; median of {steps} steps = {t * 1e3:.1f} ms; "
-                       f"cpu: {cpu_model()}, os.cpu_count()={os.cpu_count()}")}
+    step_med, step_iqr = _med_iqr([t["step"] for t in times])
+    out = {"value": round(macs / (step_med * 1e-3) / 1e9, 4), "unit": "G edge-MAC/s",
+           "cores": torch.get_num_threads(), "kind": "port",
+           "sample": (f"BASELINE configs[0] (C1) whole: train step (fwd + bwd + torch.optim.Adam) of B=64, D=1024, "
+                      f"N=1,048,576, fan-in 8, pools of 256, seed 0, in the materialising torch restatement of "
+                      f"sparse_pooling/reference on the host; {steps} timed steps after one untimed step; "
+                      f"cpu: {cpu_model()}, os.cpu_count()={os.cpu_count()}"),
+           "ms_step_median": step_med, "ms_step_iqr": step_iqr, "parity_vs_gpu": parity}
+    for k in ("fwd", "bwd", "adam"):
+        out[f"ms_{k}_median"], out[f"ms_{k}_iqr"] = _med_iqr([t[k] for t in times])
+    return out
+
+
+def c4_step(steps: int, warmup: int):
+    """BASELINE configs[3] (C4): the full training step at N=100,663,296, D=8192, B=1024, bf16 X,
+    uniform indices, fwd + recompute bwd + FusedAdamW (fp32 moments), with per-kernel times."""
+    import torch
+
+    from granulelayer_amd import FusedAdamW, SparsePoolingLayer
+    from granulelayer_amd._native import KernelTrace
+    from granulelayer_amd.synthetic import CONFIGS
+
+    c = CONFIGS["C4"]
+    N, K, D, B, pool = c["N"], c["K"], c["D"], c["B"], c["pool"]
+    G = N // pool
+    dev = torch.device("cuda", 0)
+    lay = SparsePoolingLayer(D, N, G, fan_in=K, shared_neurons=None, pooling="sum", dtype=torch.float32, device=dev,
+                             seed=0)
+    lay.enable_main_grad()
+    opt = FusedAdamW(lay.parameters(), lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, moments="fp32")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    x = torch.randn(B, D, generator=gen, device=dev).to(torch.bfloat16)
+    dy = torch.randn(B, G, generator=gen, device=dev).to(torch.bfloat16).float()
+    setup = setup_times(lay, x)
+
+    def step():
+        y = lay(x)
+        y.backward(dy)
+        opt.step()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with KernelTrace(max_launches=32 * steps) as tr:
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    kt = {k: round(sum(v) / steps, 3) for k, v in tr.times_ms().items()}
+    del lay, opt
+    torch.cuda.empty_cache()
+    return {"workload": "BASELINE configs[3] (C4): fwd + recompute bwd (dX, dW, db) + FusedAdamW, N=100,663,296, "
+                        "fan-in 8, D=8192, B=1024, pools of 1024, bf16 X, fp32 W and moments",
+            "ms_per_step": round(ms, 3), "steps": steps, "warmup": warmup,
+            "G_edge_macs_per_s": round(B * N * K / (ms * 1e-3) / 1e9, 2), "kernels_ms_per_step": kt, "setup": setup}
+
+
+def setup_times(lay, x):
+    """One-time layer setup the first training step pays, timed explicitly: the gather schedule
+    (host build from a device-to-host copy of the indices, then upload), the pool windows (host),
+    and the input-major edge list (GPU)."""
+    import torch
+
+    from granulelayer_amd.backend import HipBackend
+
+    be = HipBackend.get()
+    rt = lay._runtime()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    be.schedule(rt)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    be.windows(rt)
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    be.edges(rt)
+    torch.cuda.synchronize()
+    t3 = time.perf_counter()
+    return {"gather_schedule_ms": round((t1 - t0) * 1e3, 1), "pool_windows_ms": round((t2 - t1) * 1e3, 1),
+            "edge_list_ms": round((t3 - t2) * 1e3, 1), "total_ms": round((t3 - t0) * 1e3, 1)}
+
+
+def read_profile(path: str) -> dict:
+    """Per kernel, from a committed rocprofv3 summary: ``traffic <kernel> <bytes>`` (calibrated HBM
+    bytes per dispatch: FETCH_SIZE and WRITE_SIZE, each scaled by what the counter reads for a device
+    copy of known size) and ``profile_ms <kernel> <ms>`` (the kernel's average duration in the same
+    profiled command)."""
+    out = {}
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] in ("traffic", "profile_ms"):
+                    out.setdefault(parts[1], {})[parts[0]] = float(parts[2])
+    except OSError:
+        pass
+    return out
 
 
 def main():
@@ -175,8 +322,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-groups", type=int, default=768, help="pools in the CPU baseline's sample")
-    ap.add_argument("--cpu-steps", type=int, default=5)
+    ap.add_argument("--cpu-steps", type=int, default=4, help="timed steps of the C1 CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C1 and C4 extra measurements")
     ap.add_argument("--config", choices=sorted(CONFIG_WORK), default=None,
                     help="time one BASELINE config's own work at full size instead of the headline step")
     ap.add_argument("--pooling", choices=("sum", "mean", "max", "topk"), default="sum",
@@ -188,7 +335,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build measures one MI355X (--gpus {args.gpus} requested); "
-              "multi-GPU sharding is described in DESIGN.md but not implemented", file=sys.stderr)
+              "nothing in it shards across GPUs", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -229,6 +376,8 @@ def main():
     dy = torch.randn(B, G, generator=gen, device=dev)
     torch.cuda.synchronize()
     log(f"layer ready in {time.time() - t0:.1f} s")
+    setup = setup_times(lay, x)
+    log(f"layer setup (gather schedule, windows, edge list): {setup}")
 
     def step():
         y = lay(x)
@@ -266,6 +415,8 @@ def main():
         torch.cuda.synchronize()
     fwd_ms = e0.elapsed_time(e1) / args.steps
     log(f"forward only: {fwd_ms:.3f} ms")
+    del lay, opt, x, dy
+    torch.cuda.empty_cache()
 
     E = N * K
     kernels = {}
@@ -281,21 +432,27 @@ def main():
         kernels[name] = rec
     dom = max(ktimes, key=lambda n: sum(ktimes[n]))
     dom_ms = sum(ktimes[dom]) / args.steps
+    dom_launch_ms = sum(ktimes[dom]) / len(ktimes[dom])
     by, fl = algorithmic(dom, B, N, K, D, G)
-    traffic = read_traffic(os.path.join(ROOT, "profiles", "pmc_c2_train_step.txt")).get(dom)
+    prof = read_profile(os.path.join(ROOT, "profiles", "pmc_c2_train_step.txt")).get(dom, {})
     if dom == "adam_kernel":
         roof = {"bound": "hbm", "achieved": round(by / (dom_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s"}
     else:
-        # fp32 arithmetic on the vector ALUs (no MFMA on this gather path): the fp32 peak is the
-        # figure MI355X publishes for fp32 (157.3 TFLOP/s, packed issue); code built without
-        # packed-FP32 instructions can issue at most half of it
-        roof = {"bound": "mfma", "achieved": round(fl / (dom_ms * 1e-3) / 1e12, 2), "peak": FP32_PEAK_TFLOPS,
+        # fp32 FMA on the vector ALUs: a gather path, no MFMA (north star).  The peak is MI355X's
+        # published fp32 figure (157.3 TFLOP/s, packed issue); code built without packed-FP32
+        # instructions can issue at most half of it
+        roof = {"bound": "valu", "achieved": round(fl / (dom_ms * 1e-3) / 1e12, 2), "peak": FP32_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "compute": "fp32 VALU FMA (no MFMA; non-packed issue limit 78.65 TFLOP/s)"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    roof["traffic"] = traffic
+    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes; withheld when
+    # the profiled kernel's duration is more than 10% from this run's (the kernel has changed since)
+    traffic, pms = prof.get("traffic"), prof.get("profile_ms")
+    fresh = traffic is not None and pms is not None and abs(pms - dom_launch_ms) <= 0.1 * dom_launch_ms
+    roof["traffic"] = int(traffic) if fresh else None
+    roof["traffic_profile_ms"] = pms
     roof["kernel"] = dom
-    roof["ms"] = round(dom_ms, 4)
+    roof["ms"] = round(dom_launch_ms, 4)
     roof["algorithmic_bytes"] = by
     roof["algorithmic_flops"] = fl
 
@@ -316,15 +473,30 @@ def main():
         "config": {"workload": "C2-shaped train step: fwd + recompute bwd (dX, dW, db) + fused AdamW",
                    "neurons": N, "fan_in": K, "d_in": D, "batch": B, "pool": pool, "groups": G,
                    "pooling": {"sum": "sum(relu)", "mean": "mean(relu)", "max": "relu(max z)",
-                               "topk": "top-8 mean(z)"}[args.pooling], "x_dtype": "f32", "moments": "f32", "parallelism": "single GPU"},
+                               "topk": "top-8 mean(z)"}[args.pooling], "x_dtype": "f32", "moments": "f32",
+                   "parallelism": "single GPU"},
         "fwd_ms": round(fwd_ms, 3),
         "fwd_G_edge_macs_per_s": round(B * E / (fwd_ms * 1e-3) / 1e9, 2),
+        "setup": setup,
         "kernels": kernels,
         "roofline": roof,
     }
+    pr1, first = None, None
+    if not args.no_extra or not args.no_cpu_baseline:
+        pr1 = c1_problem()
+        c1_ms, first = c1_gpu(pr1, max(args.steps, 20), 3)
+        out["c1_gpu"] = {"workload": "BASELINE configs[0] (C1) train step on the GPU: B=64, D=1024, N=1,048,576, "
+                                     "fan-in 8, pools of 256, fp32",
+                         "ms_per_step": round(c1_ms, 4),
+                         "G_edge_macs_per_s": round(pr1.B * pr1.edges / (c1_ms * 1e-3) / 1e9, 2)}
+        log(f"C1 on the GPU: {c1_ms:.3f} ms/step")
+    if not args.no_extra:
+        log("C4 full training step")
+        out["c4"] = c4_step(3, 1)
+        log(f"C4: {out['c4']['ms_per_step']} ms/step")
     if not args.no_cpu_baseline:
-        log(f"cpu baseline: {args.cpu_groups} pools x {args.cpu_steps} steps")
-        out["cpu_baseline"] = cpu_baseline(args.cpu_groups, args.cpu_steps)
+        log(f"cpu baseline: C1 x {args.cpu_steps} steps")
+        out["cpu_baseline"] = cpu_baseline(pr1, args.cpu_steps, first)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgranulelayer_amd.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 GL_ACT = {"identity": 0, "relu": 1}
 GL_POOL = {"mean": 0, "sum": 1, "max": 2, "topk_mean": 3}
@@ -26,7 +26,7 @@ class GlFwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
                 ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("pre", _P), ("winner", _P), ("ws", _P),
-                ("ws_bytes", _SZ)]
+                ("ws_bytes", _SZ), ("part_budget", _SZ)]
 
 
 class GlBwdArgs(ctypes.Structure):

@@ -34,9 +34,39 @@ def resolve_policy(level: LevelSpec, requested: str) -> str:
     return requested
 
 
+# bytes of saved selection ids (max winners, top-k slots) above which save_winners falls back to
+# recomputing them in backward, and the id-tensor size per token chunk of that recomputation
+# (the reference's CHECKPOINT_BUDGET / RECOMPUTE_CHUNK_BYTES, sparse_pooling/autograd.py:41-42)
+CHECKPOINT_BUDGET = 2 << 30
+RECOMPUTE_CHUNK_BYTES = 512 << 20
+
+
+def _ids_per_token(rt: "Level1Runtime") -> int:
+    """int32 selection ids one token keeps: U units x k (top-k mean) or x 1 (max); 0 otherwise."""
+    lv = rt.level
+    if lv.type not in ("max", "topk_mean"):
+        return 0
+    return rt.units.U * (lv.k if lv.type == "topk_mean" else 1)
+
+
 def fit_policy(rt: "Level1Runtime", policy: str, batch: int) -> str:
+    """save_winners keeps B x U x k int32 ids; above CHECKPOINT_BUDGET the backward recomputes them
+    instead and ``last_info['policy_fallback']`` says so (sparse_pooling/autograd.py:45-56)."""
+    if policy == "save_winners":
+        need = batch * _ids_per_token(rt) * 4
+        if need > CHECKPOINT_BUDGET:
+            rt.last_info["policy_fallback"] = f"save_winners needs {need / 2**30:.1f} GiB of ids -> minimal_stats"
+            return "minimal_stats"
     rt.last_info.pop("policy_fallback", None)
     return policy
+
+
+def recompute_chunk(rt: "Level1Runtime") -> int:
+    """Tokens per chunk when selection ids are recomputed in backward: the [b, U, k] id tensor of a
+    chunk stays within RECOMPUTE_CHUNK_BYTES, at least 32 tokens, a multiple of 32
+    (sparse_pooling/autograd.py:335)."""
+    per = max(_ids_per_token(rt) * 4, 1)
+    return max(32, (min(RECOMPUTE_CHUNK_BYTES, CHECKPOINT_BUDGET) // per) // 32 * 32)
 
 
 def act_torch(x: torch.Tensor, name: str) -> torch.Tensor:
@@ -185,6 +215,24 @@ def _saved_stats(level: LevelSpec, out: Dict[str, torch.Tensor], policy: str) ->
     return keep
 
 
+def _chunked_selection_backward(rt: Level1Runtime, xc, wc, bc, dy, pre, policy, dw_buf, db_buf):
+    """Max / top-k backward with the selection ids recomputed per token chunk, so the [b, U, k] id
+    tensor of one chunk stays within RECOMPUTE_CHUNK_BYTES; dW / db accumulate over the chunks.
+    The total extra work is one forward (sparse_pooling/autograd.py:329-343)."""
+    B, D = xc.shape
+    bc_tok = recompute_chunk(rt)
+    dx = torch.empty((B, D), device=xc.device, dtype=torch.float32)
+    for s0 in range(0, B, bc_tok):
+        xs = xc[s0:s0 + bc_tok]
+        st = rt.forward(xs, wc, bc, track_ids=True)
+        p = st["pre"] if pre is None else pre[s0:s0 + bc_tok]
+        g = (dy[s0:s0 + bc_tok].float() * dact_torch(p, rt.level.out_activation)).contiguous()
+        dx[s0:s0 + bc_tok] = rt.backward(xs, wc, bc, g, st, policy, dw_buf, db_buf, True)
+        del st
+    rt.last_info["backward_token_chunks"] = -(-B // bc_tok)
+    return dx
+
+
 class SparsePoolFunction(torch.autograd.Function):
     """Single level: y [B, G] = out_act(pool(sparse_projection(x)))."""
 
@@ -214,11 +262,17 @@ class SparsePoolFunction(torch.autograd.Function):
         # pooling needs the winners, so minimal_stats recomputes the forward with track_ids
         need = {"max": "winner", "topk_mean": "topk_slot"}.get(lv.type)
         recomputed = "pre" not in saved or (need is not None and need not in saved)
-        if recomputed:
-            saved.update(rt.forward(xc, wc, bc, track_ids=True))
-        g_pre = dy.float() * dact_torch(saved["pre"], lv.out_activation)
         dw_buf, db_buf, use_main = _grad_buffers(w, b)
-        dx = rt.backward(xc, wc, bc, g_pre.contiguous(), saved, ctx.policy, dw_buf, db_buf, recomputed)
+        B = x.shape[0]
+        if need is not None and need not in saved and B * _ids_per_token(rt) * 4 > CHECKPOINT_BUDGET:
+            # the ids of the whole batch would exceed the budget: recompute and consume them one
+            # token chunk at a time (sparse_pooling/autograd.py:255-259, 329-343)
+            dx = _chunked_selection_backward(rt, xc, wc, bc, dy, saved.get("pre"), ctx.policy, dw_buf, db_buf)
+        else:
+            if recomputed:
+                saved.update(rt.forward(xc, wc, bc, track_ids=True))
+            g_pre = dy.float() * dact_torch(saved["pre"], lv.out_activation)
+            dx = rt.backward(xc, wc, bc, g_pre.contiguous(), saved, ctx.policy, dw_buf, db_buf, recomputed)
         gw = None if use_main else dw_buf.to(w.dtype)
         gb = None if use_main else db_buf.to(b.dtype)
         return dx.to(x.dtype, memory_format=torch.contiguous_format), gw, gb, None, None, None

@@ -130,7 +130,7 @@ class HipBackend:
         a = N.GlFwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=L.input_dim, G=G, S=S, K=K, act=act, pool=pool,
                         topk=topk, idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, pre=_ptr(pre),
-                        winner=_ptr(winner))
+                        winner=_ptr(winner), part_budget=self.part_budget(rt))
         with torch.cuda.device(x.device):
             need = self.lib.size_query("gl_fwd_workspace", a)
             ws = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)
@@ -138,6 +138,16 @@ class HipBackend:
             self.lib.call("gl_fwd", ctypes.byref(a), ctypes.c_void_p(_stream(x.device)))
         rt.last_info["workspace_bytes"] = need
         return out
+
+    @staticmethod
+    def part_budget(rt) -> int:
+        """Bytes of per-chunk forward partials one pass may hold: the layer's ``workspace_budget``
+        when the caller set one, else 0 (the library's default of 4 GiB, which runs the BASELINE
+        shapes' sum / mean forward in one pass).  The forward runs token chunks within it."""
+        from .config import DEFAULT_WORKSPACE_BUDGET
+
+        wb = getattr(rt, "workspace_budget", DEFAULT_WORKSPACE_BUDGET)
+        return 0 if wb == DEFAULT_WORKSPACE_BUDGET else int(wb)
 
     # ------------------------------------------------------------------ gather schedule
     def schedule(self, rt) -> Optional[torch.Tensor]:

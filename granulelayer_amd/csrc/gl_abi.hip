@@ -95,7 +95,7 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
       long long t[] = {(long long)sizeof(S), OFF(S, X), OFF(S, sxb), OFF(S, x_dtype), OFF(S, B), OFF(S, D), OFF(S, G),
                        OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, idx), OFF(S, W), OFF(S, bias),
                        OFF(S, counts), OFF(S, sched), OFF(S, win), OFF(S, win_width), OFF(S, pre), OFF(S, winner), OFF(S, ws),
-                       OFF(S, ws_bytes)};
+                       OFF(S, ws_bytes), OFF(S, part_budget)};
       for (long long x : t) v[c++] = x;
       break;
     }

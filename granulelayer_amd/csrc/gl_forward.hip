@@ -605,24 +605,46 @@ constexpr int fwd_waves(int K, int pk = PK_SUM) {
 }
 static int pool_kind(int pool) { return pool == GL_POOL_MAX ? PK_MAX : (pool == GL_POOL_TOPK_MEAN ? PK_TOPK : PK_SUM); }
 
+// Forward plan: the forward runs over token chunks of bf tokens (a multiple of BT) whose per-chunk
+// partials (part_bytes + slot_bytes) fit the caller's part budget; every pass reloads the chunk
+// parameters once and streams its own token tiles.  The per-token results do not depend on the
+// chunking (same waves, same order), so any budget gives the same bits.
+constexpr size_t FWD_PART_BUDGET_DEFAULT = 4ull << 30;
+
 struct FwdPlan {
-  int npl, waves, cpg, n_tiles, b_pad;
+  int npl, waves, cpg, bf, n_passes;
   long long n_chunks;
   size_t xt_bytes, part_bytes, slot_bytes;
 };
 
-static FwdPlan fwd_plan(const GlFwdArgs* a) {
+// bytes of partial results (values, plus slots for max / top-k) one token of a pass holds
+static long long fwd_part_per_token(const GlFwdArgs* a, long long n_chunks) {
+  const long long kp = a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1;  // candidates per chunk and token
+  const bool sel = a->pool == GL_POOL_MAX || a->pool == GL_POOL_TOPK_MEAN;
+  return n_chunks * kp * 4 * (sel ? 2 : 1);
+}
+
+// plan with token chunks of at most bf_cap tokens (<= 0: no cap beyond the part budget)
+static FwdPlan fwd_plan(const GlFwdArgs* a, long long bf_cap = 0) {
   FwdPlan q;
   q.npl = FWD_NPL;
   q.waves = fwd_waves(a->K, pool_kind(a->pool));
   q.cpg = ceil_div(a->S, 64 * q.npl);
   q.n_chunks = (long long)a->G * q.cpg;
-  q.n_tiles = ceil_div(a->B, BT);
-  q.b_pad = q.n_tiles * BT;
-  q.xt_bytes = (size_t)round_up((long long)q.n_tiles * a->D * 16, 256);
-  const long long kp = a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1;  // candidates per chunk and token
-  q.part_bytes = (size_t)round_up((long long)q.n_chunks * q.b_pad * kp * 4, 256);
-  q.slot_bytes = a->pool == GL_POOL_MAX || a->pool == GL_POOL_TOPK_MEAN ? q.part_bytes : 0;  // candidate slots
+  const long long kp = a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1;
+  const bool sel = a->pool == GL_POOL_MAX || a->pool == GL_POOL_TOPK_MEAN;
+  const long long per_token = fwd_part_per_token(a, q.n_chunks);
+  const size_t budget = a->part_budget ? a->part_budget : FWD_PART_BUDGET_DEFAULT;
+  const long long b_all = round_up(a->B, BT);
+  long long bf = (long long)(budget / (size_t)per_token) / BT * BT;
+  if (bf < BT) bf = BT;
+  if (bf_cap > 0 && bf > bf_cap) bf = bf_cap;
+  if (bf > b_all) bf = b_all;
+  q.bf = (int)bf;
+  q.n_passes = ceil_div(a->B, q.bf);
+  q.xt_bytes = (size_t)round_up((long long)q.bf * a->D * 4, 256);
+  q.part_bytes = (size_t)round_up(q.n_chunks * q.bf * kp * 4, 256);
+  q.slot_bytes = sel ? q.part_bytes : 0;  // candidate slots
   return q;
 }
 
@@ -692,6 +714,53 @@ int check_topk(int pool, int topk, int S) {
   return 0;
 }
 
+// The forward passes over token chunks of q.bf tokens with the workspace at ws (q's layout).
+static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s) {
+  float4* xt = (float4*)ws;
+  float* part = (float*)((char*)ws + q.xt_bytes);
+  int* pslot = q.slot_bytes ? (int*)((char*)ws + q.xt_bytes + q.part_bytes) : nullptr;
+  const int kpe = a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1;
+  for (int b0 = 0; b0 < a->B; b0 += q.bf) {
+    // one pass: tokens [b0, b0 + Bc), written to rows b0.. of pre / winner
+    const int Bc = a->B - b0 < q.bf ? a->B - b0 : q.bf;
+    const int n_tiles = ceil_div(Bc, BT), b_pad = n_tiles * BT;
+    float* pre = a->pre + (long long)b0 * a->G;
+    int32_t* winner = a->winner ? a->winner + (long long)b0 * a->G * kpe : nullptr;
+    GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles, xt, s));
+    FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, pslot, kpe, a->sched, nullptr, q.n_chunks, a->D, a->S, q.cpg,
+           n_tiles, b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0};
+    if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) k.win = a->win;
+    dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(b_pad, 32));
+    if (a->pool == GL_POOL_MAX) {
+      GL_TRY(launch_fwd_any<PK_MAX>(a->act, a->K, a->D, k, s));
+      GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_max_kernel, grid, dim3(256), 0, s, part, pslot, pre, winner, Bc,
+                a->G, q.cpg, b_pad);
+    } else if (a->pool == GL_POOL_TOPK_MEAN) {
+      GL_TRY(launch_fwd_any<PK_TOPK>(a->act, a->K, a->D, k, s));
+      const dim3 g1((unsigned)ceil_div((long long)Bc * a->G, 256));
+      const bool top8 = a->topk == 8 && q.cpg <= FWD_TOP8_CPG && ((uintptr_t)winner & 15) == 0;
+      if (top8 && a->act == GL_ACT_RELU)
+        GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_top8_kernel<GL_ACT_RELU>, g1, dim3(256), 0, s, part, pslot,
+                  a->counts, pre, winner, Bc, a->G, q.cpg, b_pad);
+      else if (top8)
+        GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_top8_kernel<GL_ACT_IDENTITY>, g1, dim3(256), 0, s, part, pslot,
+                  a->counts, pre, winner, Bc, a->G, q.cpg, b_pad);
+      else if (a->act == GL_ACT_RELU)
+        GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_topk_kernel<GL_ACT_RELU>, g1, dim3(256), 0, s, part, pslot,
+                  a->counts, pre, winner, Bc, a->G, q.cpg, b_pad, a->topk);
+      else
+        GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_topk_kernel<GL_ACT_IDENTITY>, g1, dim3(256), 0, s, part, pslot,
+                  a->counts, pre, winner, Bc, a->G, q.cpg, b_pad, a->topk);
+    } else {
+      GL_TRY(launch_fwd_any<PK_SUM>(a->act, a->K, a->D, k, s));
+      GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_kernel, grid, dim3(256), 0, s, part, a->counts, pre, Bc, a->G,
+                q.cpg, b_pad, 0, a->pool);
+    }
+    GL_CHECK_LAUNCH();
+  }
+  return 0;
+}
+
 }  // namespace gl
 
 using namespace gl;
@@ -711,42 +780,6 @@ extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
   size_t need = 0;
   GL_TRY(gl_fwd_workspace(a, &need));
   if (!a->ws || a->ws_bytes < need) return GL_ERR_WORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
-  FwdPlan q = fwd_plan(a);
-  float4* xt = (float4*)a->ws;
-  float* part = (float*)((char*)a->ws + q.xt_bytes);
-  int* pslot = q.slot_bytes ? (int*)((char*)a->ws + q.xt_bytes + q.part_bytes) : nullptr;
-  GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, 0, q.n_tiles, xt, s));
   if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;
-  FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, pslot, a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1, a->sched,
-         nullptr, q.n_chunks, a->D, a->S, q.cpg, q.n_tiles, q.b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0};
-  if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) k.win = a->win;
-  dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(q.b_pad, 32));
-  if (a->pool == GL_POOL_MAX) {
-    GL_TRY(launch_fwd_any<PK_MAX>(a->act, a->K, a->D, k, s));
-    GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_max_kernel, grid, dim3(256), 0, s, part, pslot, a->pre, a->winner,
-              a->B, a->G, q.cpg, q.b_pad);
-  } else if (a->pool == GL_POOL_TOPK_MEAN) {
-    GL_TRY(launch_fwd_any<PK_TOPK>(a->act, a->K, a->D, k, s));
-    const dim3 g1((unsigned)ceil_div((long long)a->B * a->G, 256));
-    const bool top8 = a->topk == 8 && q.cpg <= FWD_TOP8_CPG && ((uintptr_t)a->winner & 15) == 0;
-    if (top8 && a->act == GL_ACT_RELU)
-      GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_top8_kernel<GL_ACT_RELU>, g1, dim3(256), 0, s, part, pslot,
-                a->counts, a->pre, a->winner, a->B, a->G, q.cpg, q.b_pad);
-    else if (top8)
-      GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_top8_kernel<GL_ACT_IDENTITY>, g1, dim3(256), 0, s, part, pslot,
-                a->counts, a->pre, a->winner, a->B, a->G, q.cpg, q.b_pad);
-    else if (a->act == GL_ACT_RELU)
-      GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_topk_kernel<GL_ACT_RELU>, g1, dim3(256), 0, s, part, pslot,
-                a->counts, a->pre, a->winner, a->B, a->G, q.cpg, q.b_pad, a->topk);
-    else
-      GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_topk_kernel<GL_ACT_IDENTITY>, g1, dim3(256), 0, s, part, pslot,
-                a->counts, a->pre, a->winner, a->B, a->G, q.cpg, q.b_pad, a->topk);
-  } else {
-    GL_TRY(launch_fwd_any<PK_SUM>(a->act, a->K, a->D, k, s));
-    GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_kernel, grid, dim3(256), 0, s, part, a->counts, a->pre, a->B, a->G,
-              q.cpg, q.b_pad, 0, a->pool);
-  }
-  GL_CHECK_LAUNCH();
-  return 0;
+  return fwd_run(a, a->ws, fwd_plan(a), (hipStream_t)stream);
 }

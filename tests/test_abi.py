@@ -96,3 +96,27 @@ def test_pool_limits_are_refused_by_the_size_query():
     assert query(tk, 8, 4097) == -2
     assert query(N.GL_POOL["max"], 0, 100000) == 0
     assert query(7, 0, 256) == -2
+
+
+def test_forward_workspace_is_bounded_as_the_batch_grows():
+    """The forward runs token chunks whose partial results fit part_budget (default 4 GiB), so its
+    workspace stops growing with B: at the C2 shape with top-16 mean, B = 8192 needs no more than
+    B = 1024; sum pooling at B = 256 (the headline) still runs as one pass.  Host-side size query
+    only (placeholder pointers, never dereferenced)."""
+    lib = N.library()
+    out = ctypes.c_size_t()
+
+    def ws(B, pool, topk=0, budget=0, D=4096):
+        a = N.GlFwdArgs(X=16, idx=16, W=16, bias=16, counts=16, B=B, D=D, G=98_304, S=1024, K=8,
+                        act=N.GL_ACT["relu"], pool=N.GL_POOL[pool], topk=topk, part_budget=budget)
+        assert lib.lib.gl_fwd_workspace(ctypes.byref(a), ctypes.byref(out)) == 0
+        return out.value
+
+    tk = [ws(B, "topk_mean", 16) for B in (1024, 8192, 65536)]
+    assert tk[0] == tk[1] == tk[2] <= (4 << 30) + 1024 * 4096 * 4 + 512
+    assert ws(256, "sum") == 256 * 4096 * 4 + 98_304 * 4 * 256 * 4  # X tiles + one pass of partials
+    assert ws(1 << 20, "max") <= (4 << 30) + (1 << 20) * 4096 * 4
+    small = ws(1 << 16, "sum", budget=64 << 20)
+    assert small <= (64 << 20) + (1 << 16) * 4096 * 4
+    # a budget below one token tile's partials still runs (one tile per pass)
+    assert ws(64, "topk_mean", 64, budget=1) == 4 * 4096 * 4 + 2 * 98_304 * 4 * 4 * 64 * 4

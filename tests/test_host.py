@@ -181,3 +181,29 @@ def test_state_dict_formats():
     plan = torch.frombuffer(bytearray(b'{"kind": "supergroups"}'), dtype=torch.uint8).clone()
     with pytest.raises(ValueError, match="supergroup"):
         dst.load_state_dict({**sd, "sg_plan": plan})
+
+
+def test_save_winners_over_the_checkpoint_budget_falls_back_to_minimal_stats():
+    """save_winners keeps B x U x k int32 ids; above 2 GiB the policy resolves to minimal_stats and
+    last_info says why (sparse_pooling/autograd.py:45-56); the recompute chunk keeps one chunk's ids
+    within 512 MiB (autograd.py:335)."""
+    from types import SimpleNamespace
+
+    from granulelayer_amd.autograd import CHECKPOINT_BUDGET, RECOMPUTE_CHUNK_BYTES, fit_policy, recompute_chunk
+
+    def rt(kind, U, **kw):
+        return SimpleNamespace(level=LevelSpec(kind, **kw), units=SimpleNamespace(U=U), last_info={})
+
+    r = rt("topk_mean", 98_304, k=8)
+    assert 1024 * 98_304 * 8 * 4 > CHECKPOINT_BUDGET
+    assert fit_policy(r, "save_winners", 1024) == "minimal_stats"
+    assert "GiB of ids" in r.last_info["policy_fallback"]
+    assert fit_policy(r, "save_winners", 256) == "save_winners"  # 0.8 GB fits
+    assert "policy_fallback" not in r.last_info
+    r = rt("max", 98_304)
+    assert fit_policy(r, "save_winners", 5461) == "save_winners"  # 2.15e9 bytes > 2 GiB only from 5462
+    assert fit_policy(r, "save_winners", 5462) == "minimal_stats"
+    assert fit_policy(rt("mean", 98_304), "minimal_stats", 10**6) == "minimal_stats"
+    c = recompute_chunk(rt("topk_mean", 98_304, k=8))
+    assert c % 32 == 0 and c * 98_304 * 8 * 4 <= RECOMPUTE_CHUNK_BYTES
+    assert recompute_chunk(rt("topk_mean", 10**7, k=64)) == 32  # never below 32 tokens
