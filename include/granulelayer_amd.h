@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 5
+#define GL_ABI_VERSION 6
 
 enum {
   GL_OK = 0,
@@ -70,6 +70,10 @@ typedef struct GlFwdArgs {
                              GL_POOL_TOPK_MEAN ("topk_slot", best first, -1 past min(n_g, k)) */
   void* ws;               /* workspace of gl_fwd_workspace() bytes */
   size_t ws_bytes;
+  size_t part_budget;     /* bytes of per-chunk partial results one pass may hold (0: 4 GiB).  The
+                             forward runs over token chunks whose partials fit it, so the workspace
+                             stays bounded as B grows (the reference keeps its split states within
+                             workspace_budget, sparse_pooling/kernels/ops.py:82-98) */
 } GlFwdArgs;
 
 /* Backward arguments.  Replaces the reference's BwdArgs + sp_bwd (sparse_pool_bwd.cuh:45-66,
