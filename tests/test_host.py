@@ -207,3 +207,28 @@ def test_save_winners_over_the_checkpoint_budget_falls_back_to_minimal_stats():
     c = recompute_chunk(rt("topk_mean", 98_304, k=8))
     assert c % 32 == 0 and c * 98_304 * 8 * 4 <= RECOMPUTE_CHUNK_BYTES
     assert recompute_chunk(rt("topk_mean", 10**7, k=64)) == 32  # never below 32 tokens
+
+
+def test_seeded_init_equals_the_reference_bit_for_bit():
+    """init_parameters(layout, seed=s) reproduces the reference's parameters exactly: the same
+    indices (widened from the reference's int16), weights and bias, for ragged layouts, a bias std,
+    chunked generation and bf16 parameters (fixture written by tests/golden/make_init_golden.py from
+    sparse_pooling/layout.py:191-251)."""
+    from pathlib import Path
+
+    path = Path(__file__).resolve().parent / "golden" / "init_reference.npz"
+    with np.load(path) as z:
+        d = {k: z[k] for k in z.files}
+    names = sorted({k.split("/")[0] for k in d})
+    assert len(names) == 4
+    for name in names:
+        D, H, G, seed, chunk = (int(v) for v in d[f"{name}/shape"])
+        dtype = getattr(torch, str(d[f"{name}/dtype"]))
+        L = SparseLayout(D, H, G, 8, 8, False)
+        idx, w, b = init_parameters(L, "cpu", dtype=dtype, seed=seed, bias_std=float(d[f"{name}/bias_std"]),
+                                    chunk_records=chunk)
+        assert L.padding_fraction() > 0, name
+        assert np.array_equal(idx.numpy(), d[f"{name}/idx"].astype(np.int32)), f"{name}: indices"
+        assert np.array_equal(w.float().numpy(), d[f"{name}/w"]), f"{name}: weights"
+        assert np.array_equal(b.float().numpy(), d[f"{name}/b"]), f"{name}: bias"
+        assert w.dtype == dtype and b.dtype == dtype and idx.dtype == torch.int32
