@@ -18,6 +18,8 @@ ABI_VERSION = 6
 GL_ACT = {"identity": 0, "relu": 1}
 GL_POOL = {"mean": 0, "sum": 1, "max": 2, "topk_mean": 3}
 GL_DTYPE_F32, GL_DTYPE_BF16 = 0, 1
+GL_ERR_SCRATCH = -8
+FWD_STATIC_SCRATCH_BYTES = 64 << 20  # GL_FWD_STATIC_SCRATCH_BYTES
 
 _P, _I32, _I64, _SZ, _F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
 
@@ -49,7 +51,8 @@ class GlAdamArgs(ctypes.Structure):
 
 STRUCTS = (GlFwdArgs, GlBwdArgs, GlEdgeArgs, GlAdamArgs)  # gl_struct_layout ids 0..3
 # every symbol include/granulelayer_amd.h declares
-EXPORTS = ("gl_abi_version", "gl_struct_layout", "gl_error_string", "gl_fwd_workspace", "gl_fwd", "gl_edges_size",
+EXPORTS = ("gl_abi_version", "gl_struct_layout", "gl_error_string", "gl_fwd_workspace", "gl_fwd", "gl_fwd_static",
+           "gl_edges_size",
            "gl_edges_build", "gl_bwd_workspace", "gl_bwd", "gl_adam", "gl_sched_size", "gl_sched_build_host",
            "gl_window_build_host", "gl_trace_begin", "gl_trace_end")
 KERNEL_NAMES = {1: "tile_x_kernel", 2: "fwd_kernel", 3: "fwd_finalize_kernel", 4: "c1t_kernel", 5: "bwd_w_kernel",
@@ -80,8 +83,8 @@ class Library:
         L.gl_struct_layout.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_longlong), ctypes.c_int]
         L.gl_error_string.restype = ctypes.c_char_p
         L.gl_error_string.argtypes = [ctypes.c_int]
-        for name, st in (("gl_fwd", GlFwdArgs), ("gl_bwd", GlBwdArgs), ("gl_edges_build", GlEdgeArgs),
-                         ("gl_adam", GlAdamArgs)):
+        for name, st in (("gl_fwd", GlFwdArgs), ("gl_fwd_static", GlFwdArgs), ("gl_bwd", GlBwdArgs),
+                         ("gl_edges_build", GlEdgeArgs), ("gl_adam", GlAdamArgs)):
             f = getattr(L, name)
             f.restype, f.argtypes = ctypes.c_int, [ctypes.POINTER(st), _P]
         for name, st in (("gl_fwd_workspace", GlFwdArgs), ("gl_bwd_workspace", GlBwdArgs)):

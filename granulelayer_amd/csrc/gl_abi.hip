@@ -141,6 +141,9 @@ extern "C" const char* gl_error_string(int code) {
     case GL_ERR_LDS: return "input tile (D features x 4 tokens x 4 bytes) exceeds the device's LDS per workgroup";
     case GL_ERR_EDGES: return "edge structure does not match this layer shape";
     case GL_ERR_DEVICE: return "no current HIP device or device attribute query failed";
+    case GL_ERR_SCRATCH:
+      return "gl_fwd_static: the partial results of one 4-token tile of this layer exceed the 64 MiB static scratch "
+             "(use gl_fwd with a caller workspace)";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }
 }

@@ -9,6 +9,8 @@
 // tensor [B, H] never exists; only per-(chunk, token) partial sums are written and a finalize
 // kernel merges the chunks of a group in a fixed order (reference: fwd_pool_kernel +
 // merge_finalize, sparse_pooling/kernels/triton_fused.py:289-358, kernels/ops.py:182-199).
+#include <mutex>
+
 #include "gl_common.h"
 #include "gl_internal.h"
 
@@ -761,6 +763,44 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
   return 0;
 }
 
+// ---- the forward without a caller workspace ----------------------------------------------------
+// gl_fwd_static keeps its token tiles and partial results in this file-scope device array (one
+// copy per GPU, held until the process ends) instead of a caller workspace, for callers that cannot
+// allocate.  Host code never passes the array's name to a kernel: it passes the per-device address
+// that hipGetSymbolAddress returns.  The forward runs as many token passes as the array needs; the
+// results are those of gl_fwd (every token's arithmetic and order are the same).
+static __device__ __align__(256) unsigned char scratch[GL_FWD_STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];  // per device; null until resolved
+}  // namespace
+
+// the address of this device's scratch (resolved once per device, with the device current)
+static int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return GL_ERR_DEVICE;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return GL_ERR_DEVICE;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+// the largest token chunk whose tiles and partials fit the scratch (0: not even one tile)
+static long long static_chunk(const GlFwdArgs* a) {
+  const long long cpg = ceil_div(a->S, 64 * FWD_NPL);
+  const long long per_token = fwd_part_per_token(a, (long long)a->G * cpg) + (long long)a->D * 4;
+  const long long room = (long long)GL_FWD_STATIC_SCRATCH_BYTES - 3 * 256;  // three sections rounded to 256
+  return room / per_token / BT * BT;
+}
+
 }  // namespace gl
 
 using namespace gl;
@@ -782,4 +822,18 @@ extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
   if (!a->ws || a->ws_bytes < need) return GL_ERR_WORKSPACE;
   if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;
   return fwd_run(a, a->ws, fwd_plan(a), (hipStream_t)stream);
+}
+
+extern "C" int gl_fwd_static(const GlFwdArgs* a, void* stream) {
+  if (!a || !a->pre) return GL_ERR_ARG;
+  size_t need = 0;
+  GL_TRY(gl_fwd_workspace(a, &need));  // argument checks; ws / ws_bytes are ignored
+  if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;
+  const long long bf = static_chunk(a);
+  if (bf < BT) return GL_ERR_SCRATCH;
+  const FwdPlan q = fwd_plan(a, bf);
+  if (q.xt_bytes + q.part_bytes + q.slot_bytes > (size_t)GL_FWD_STATIC_SCRATCH_BYTES) return GL_ERR_SCRATCH;
+  void* ws = nullptr;
+  GL_TRY(scratch_address(&ws));
+  return fwd_run(a, ws, q, (hipStream_t)stream);
 }

@@ -37,7 +37,8 @@ enum {
   GL_ERR_WORKSPACE = -3,    /* workspace / output buffer smaller than required */
   GL_ERR_LDS = -4,          /* the input tile (D features x 4 tokens) exceeds the device's LDS */
   GL_ERR_EDGES = -5,        /* edge structure built for a different layer shape */
-  GL_ERR_DEVICE = -7        /* no current HIP device or attribute query failed */
+  GL_ERR_DEVICE = -7,       /* no current HIP device or attribute query failed */
+  GL_ERR_SCRATCH = -8       /* gl_fwd_static: one token tile of this layer exceeds the static scratch */
 };
 enum { GL_ACT_IDENTITY = 0, GL_ACT_RELU = 1 };
 /* max: pytorch_reference.py:61-67 (winner = first maximum of act(z) over the pool's valid
@@ -145,6 +146,18 @@ const char* gl_error_string(int code);
 /* Forward.  gl_fwd_workspace writes the workspace size for these arguments to *bytes. */
 int gl_fwd_workspace(const GlFwdArgs* a, size_t* bytes);
 int gl_fwd(const GlFwdArgs* a, void* stream);
+
+/* Forward that allocates nothing and takes no workspace.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The token tiles and partial results live in a
+ * library-owned static device array of GL_FWD_STATIC_SCRATCH_BYTES per GPU (held from the first
+ * call on that GPU until the process ends); a->ws, a->ws_bytes are ignored.  The forward runs as
+ * many token passes as the array needs, with the results of gl_fwd; layers whose partials for one
+ * 4-token tile exceed the array are refused with GL_ERR_SCRATCH.  Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (different streams, different threads) race and must
+ * be serialized by the caller.  Nothing in it needs zeroing between calls. */
+#define GL_FWD_STATIC_SCRATCH_BYTES (64u << 20)
+int gl_fwd_static(const GlFwdArgs* a, void* stream);
 
 /* Edge structure: sizes (output and scratch) for a layer shape, then the build. */
 int gl_edges_size(const GlEdgeArgs* a, size_t* edges_bytes, size_t* ws_bytes);
