@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgranulelayer_amd.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 GL_ACT = {"identity": 0, "relu": 1}
 GL_POOL = {"mean": 0, "sum": 1, "max": 2, "topk_mean": 3}
@@ -26,21 +26,22 @@ _P, _I32, _I64, _SZ, _F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctype
 
 class GlFwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
-                ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
+                ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("rec_shift", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("pre", _P), ("winner", _P), ("ws", _P),
                 ("ws_bytes", _SZ), ("part_budget", _SZ)]
 
 
 class GlBwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
-                ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
+                ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("rec_shift", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("g_pre", _P), ("winner", _P), ("dW", _P), ("db", _P),
                 ("dX", _P), ("edges", _P), ("edges_bytes", _SZ),
                 ("ws", _P), ("ws_bytes", _SZ)]
 
 
 class GlEdgeArgs(ctypes.Structure):
-    _fields_ = [("idx", _P), ("counts", _P), ("D", _I32), ("G", _I32), ("S", _I32), ("K", _I32), ("edges", _P),
+    _fields_ = [("idx", _P), ("counts", _P), ("D", _I32), ("G", _I32), ("S", _I32), ("K", _I32), ("rec_shift", _I32),
+                ("edges", _P),
                 ("edges_bytes", _SZ), ("ws", _P), ("ws_bytes", _SZ)]
 
 
@@ -49,15 +50,22 @@ class GlAdamArgs(ctypes.Structure):
                 ("beta1", _F), ("beta2", _F), ("eps", _F), ("weight_decay", _F), ("bc1", _F), ("bc2", _F)]
 
 
-STRUCTS = (GlFwdArgs, GlBwdArgs, GlEdgeArgs, GlAdamArgs)  # gl_struct_layout ids 0..3
+class GlCoverArgs(ctypes.Structure):
+    _fields_ = [("W", _P), ("a", _P), ("nvalid", _P), ("cand", _P), ("R", _I32), ("gpb", _I32), ("k", _I32),
+                ("repair", _I32), ("importance", _P), ("env", _P), ("rec_idx", _P), ("W_out", _P), ("missing0", _P),
+                ("swaps", _P), ("loss", _P), ("status", _P)]
+
+
+STRUCTS = (GlFwdArgs, GlBwdArgs, GlEdgeArgs, GlAdamArgs, GlCoverArgs)  # gl_struct_layout ids 0..4
 # every symbol include/granulelayer_amd.h declares
 EXPORTS = ("gl_abi_version", "gl_struct_layout", "gl_error_string", "gl_fwd_workspace", "gl_fwd", "gl_fwd_static",
            "gl_edges_size",
            "gl_edges_build", "gl_bwd_workspace", "gl_bwd", "gl_adam", "gl_sched_size", "gl_sched_build_host",
-           "gl_window_build_host", "gl_trace_begin", "gl_trace_end")
+           "gl_window_build_host", "gl_cover_select", "gl_trace_begin", "gl_trace_end")
 KERNEL_NAMES = {1: "tile_x_kernel", 2: "fwd_kernel", 3: "fwd_finalize_kernel", 4: "c1t_kernel", 5: "bwd_w_kernel",
                 6: "dx_kernel", 7: "dx_reduce_kernel", 8: "adam_kernel", 9: "edges_build", 10: "fwd_kernel_win",
-                11: "bwd_w_kernel_win", 12: "max_events_dw_kernel", 13: "max_events_dx_kernel"}
+                11: "bwd_w_kernel_win", 12: "max_events_dw_kernel", 13: "max_events_dx_kernel",
+                14: "cover_select_kernel"}
 
 
 class NativeError(RuntimeError):
@@ -84,7 +92,7 @@ class Library:
         L.gl_error_string.restype = ctypes.c_char_p
         L.gl_error_string.argtypes = [ctypes.c_int]
         for name, st in (("gl_fwd", GlFwdArgs), ("gl_fwd_static", GlFwdArgs), ("gl_bwd", GlBwdArgs),
-                         ("gl_edges_build", GlEdgeArgs), ("gl_adam", GlAdamArgs)):
+                         ("gl_edges_build", GlEdgeArgs), ("gl_adam", GlAdamArgs), ("gl_cover_select", GlCoverArgs)):
             f = getattr(L, name)
             f.restype, f.argtypes = ctypes.c_int, [ctypes.POINTER(st), _P]
         for name, st in (("gl_fwd_workspace", GlFwdArgs), ("gl_bwd_workspace", GlBwdArgs)):
@@ -101,7 +109,7 @@ class Library:
         L.gl_sched_build_host.restype = ctypes.c_int
         L.gl_sched_build_host.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _P, _I32]
         L.gl_window_build_host.restype = ctypes.c_int
-        L.gl_window_build_host.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(_I32)]
+        L.gl_window_build_host.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(_I32)]
         self.check_abi()
 
     def check_abi(self):
@@ -149,18 +157,18 @@ class Library:
         self.call("gl_sched_build_host", idx.ctypes.data, counts.ctypes.data, D, G, S, K, out.ctypes.data, threads)
         return out
 
-    def window_build(self, idx, counts, D: int, G: int, S: int, K: int):
-        """Per-pool input windows from host int32 arrays idx [G*S, K] and counts [G]: (lo uint32 [G],
-        widest window width)."""
+    def window_build(self, idx, counts, D: int, G: int, S: int, K: int, rec_shift: int = 0):
+        """Per-pool input windows from host int32 arrays idx [G*S >> rec_shift, K] and counts [G]:
+        (lo uint32 [G], widest window width)."""
         import numpy as np
 
         idx = np.ascontiguousarray(idx, dtype=np.int32)
         counts = np.ascontiguousarray(counts, dtype=np.int32)
-        if idx.size != G * S * K or counts.size != G:
-            raise ValueError("idx must hold G*S*K and counts G entries")
+        if idx.size != (G * S >> rec_shift) * K or counts.size != G:
+            raise ValueError("idx must hold (G*S >> rec_shift)*K and counts G entries")
         lo = np.empty(G, dtype=np.uint32)
         width = _I32(0)
-        self.call("gl_window_build_host", idx.ctypes.data, counts.ctypes.data, D, G, S, K, lo.ctypes.data,
+        self.call("gl_window_build_host", idx.ctypes.data, counts.ctypes.data, D, G, S, K, rec_shift, lo.ctypes.data,
                   ctypes.byref(width))
         return lo, int(width.value)
 

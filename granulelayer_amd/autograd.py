@@ -108,7 +108,7 @@ class Level1Runtime:
         reason = level.hip_reason()
         if reason:
             raise NotImplementedError(reason)
-        if layout.shared_indices:
+        if layout.shared_indices and not getattr(layout, "rec_shift", 0):
             raise NotImplementedError("Mode B (block-shared indices) is not on the MI355X path")
         if nps is not None:
             raise NotImplementedError("semantic two-level pooling is not on the MI355X path")

@@ -84,6 +84,12 @@ class HipBackend:
         return L, G, S, K
 
     @staticmethod
+    def rec_shift(rt) -> int:
+        """log2 slots per shared index record: 0 for Mode A, 4 for the K16 / C16 records of
+        Cover-TopK/16 (granulelayer_amd.cover_topk16.CompactLayout)."""
+        return int(getattr(rt.layout, "rec_shift", 0))
+
+    @staticmethod
     def _codes(rt):
         lv = rt.level
         reason = lv.hip_reason()
@@ -128,7 +134,7 @@ class HipBackend:
             return out
         win_lo, win_width = self.windows(rt)
         a = N.GlFwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=L.input_dim, G=G, S=S, K=K, act=act, pool=pool,
-                        topk=topk, idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
+                        topk=topk, rec_shift=self.rec_shift(rt), idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, pre=_ptr(pre),
                         winner=_ptr(winner), part_budget=self.part_budget(rt))
         with torch.cuda.device(x.device):
@@ -154,7 +160,7 @@ class HipBackend:
         """Gather schedule of rt's index tensor for the forward / dW kernels (fan-in 8; built on the
         host once per index tensor and cached on rt), or None for fan-in 16."""
         L, G, S, K = self._layer(rt)
-        if K != 8:
+        if K != 8 or self.rec_shift(rt):
             return None
         key = (rt.idx.data_ptr(), rt.idx._version)
         cached = getattr(rt, "_hip_sched", None)
@@ -179,7 +185,7 @@ class HipBackend:
         if cached is not None and cached[0] == key:
             return cached[1]
         lo, width = self.lib.window_build(rt.idx.reshape(-1, K).cpu().numpy(), rt.counts_i32.cpu().numpy(),
-                                          L.input_dim, G, S, K)
+                                          L.input_dim, G, S, K, self.rec_shift(rt))
         out = (torch.from_numpy(lo.view(np.int32)).to(rt.idx.device), width)
         rt._hip_win = (key, out)
         return out
@@ -192,7 +198,8 @@ class HipBackend:
         if cached is not None and cached[0] == key:
             return cached[1]
         L, G, S, K = self._layer(rt)
-        a = N.GlEdgeArgs(idx=_ptr(rt.idx), counts=_ptr(rt.counts_i32), D=L.input_dim, G=G, S=S, K=K)
+        a = N.GlEdgeArgs(idx=_ptr(rt.idx), counts=_ptr(rt.counts_i32), D=L.input_dim, G=G, S=S, K=K,
+                         rec_shift=self.rec_shift(rt))
         dev = rt.idx.device
         with torch.cuda.device(dev):
             eb, wb = self.lib.edges_size(a)
@@ -236,7 +243,7 @@ class HipBackend:
         win_lo, win_width = self.windows(rt)
         edges = self.edges(rt)
         a = N.GlBwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=D, G=G, S=S, K=K, act=act, pool=pool,
-                        topk=topk, idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
+                        topk=topk, rec_shift=self.rec_shift(rt), idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, g_pre=_ptr(g_pre),
                         winner=_ptr(winner),
                         dW=_ptr(dw_buf), db=_ptr(db_buf), dX=_ptr(dx), edges=_ptr(edges),

@@ -21,7 +21,7 @@ LIB = OUT_DIR / "libgranulelayer_amd.so"
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 SOURCES = ["gl_abi.hip", "gl_forward.hip", "gl_backward.hip", "gl_max_bwd.hip", "gl_edges.hip", "gl_adam.hip",
-           "gl_sched.hip"]
+           "gl_sched.hip", "gl_cover.hip"]
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # keep the compiler from emitting packed fp32 (v_pk_*_f32) instructions

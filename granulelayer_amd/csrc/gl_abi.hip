@@ -93,8 +93,9 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
     case 0: {
       typedef GlFwdArgs S;
       long long t[] = {(long long)sizeof(S), OFF(S, X), OFF(S, sxb), OFF(S, x_dtype), OFF(S, B), OFF(S, D), OFF(S, G),
-                       OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, idx), OFF(S, W), OFF(S, bias),
-                       OFF(S, counts), OFF(S, sched), OFF(S, win), OFF(S, win_width), OFF(S, pre), OFF(S, winner), OFF(S, ws),
+                       OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, rec_shift), OFF(S, idx), OFF(S, W),
+                       OFF(S, bias), OFF(S, counts), OFF(S, sched), OFF(S, win), OFF(S, win_width), OFF(S, pre), OFF(S, winner),
+                       OFF(S, ws),
                        OFF(S, ws_bytes), OFF(S, part_budget)};
       for (long long x : t) v[c++] = x;
       break;
@@ -102,8 +103,9 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
     case 1: {
       typedef GlBwdArgs S;
       long long t[] = {(long long)sizeof(S), OFF(S, X), OFF(S, sxb), OFF(S, x_dtype), OFF(S, B), OFF(S, D), OFF(S, G),
-                       OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, idx), OFF(S, W), OFF(S, bias),
-                       OFF(S, counts), OFF(S, sched), OFF(S, win), OFF(S, win_width), OFF(S, g_pre), OFF(S, winner), OFF(S, dW),
+                       OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, rec_shift), OFF(S, idx), OFF(S, W),
+                       OFF(S, bias), OFF(S, counts), OFF(S, sched), OFF(S, win), OFF(S, win_width), OFF(S, g_pre), OFF(S, winner),
+                       OFF(S, dW),
                        OFF(S, db), OFF(S, dX), OFF(S, edges),
                        OFF(S, edges_bytes), OFF(S, ws), OFF(S, ws_bytes)};
       for (long long x : t) v[c++] = x;
@@ -112,7 +114,7 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
     case 2: {
       typedef GlEdgeArgs S;
       long long t[] = {(long long)sizeof(S), OFF(S, idx), OFF(S, counts), OFF(S, D), OFF(S, G), OFF(S, S), OFF(S, K),
-                       OFF(S, edges), OFF(S, edges_bytes), OFF(S, ws), OFF(S, ws_bytes)};
+                       OFF(S, rec_shift), OFF(S, edges), OFF(S, edges_bytes), OFF(S, ws), OFF(S, ws_bytes)};
       for (long long x : t) v[c++] = x;
       break;
     }
@@ -121,6 +123,14 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
       long long t[] = {(long long)sizeof(S), OFF(S, p), OFF(S, g), OFF(S, m), OFF(S, v), OFF(S, n),
                        OFF(S, moments_dtype), OFF(S, lr), OFF(S, beta1), OFF(S, beta2), OFF(S, eps),
                        OFF(S, weight_decay), OFF(S, bc1), OFF(S, bc2)};
+      for (long long x : t) v[c++] = x;
+      break;
+    }
+    case 4: {
+      typedef GlCoverArgs S;
+      long long t[] = {(long long)sizeof(S), OFF(S, W), OFF(S, a), OFF(S, nvalid), OFF(S, cand), OFF(S, R), OFF(S, gpb),
+                       OFF(S, k), OFF(S, repair), OFF(S, importance), OFF(S, env), OFF(S, rec_idx), OFF(S, W_out),
+                       OFF(S, missing0), OFF(S, swaps), OFF(S, loss), OFF(S, status)};
       for (long long x : t) v[c++] = x;
       break;
     }

@@ -76,6 +76,7 @@ struct BwK {
   long long n_chunks, NS;
   int D, S, cpg, n_tiles, cap, mw2, nwin;
   int G, ww, npw;         // window staging: pools, padded window width, pools per workgroup
+  int rs;                 // log2 slots per shared index record
 };
 
 // One token tile of the dW pass (LDS at xsb): recompute z, form dz = c1 * act'(z), accumulate
@@ -165,7 +166,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
 #pragma unroll
     for (int ks = 0; ks < K; ++ks) {
       const int k = sched_k<K>(order, ks);
-      int d = p.idx[n * K + k];
+      int d = rec_index(p.idx, n, k, K, p.rs);
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
       addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * 16u;
       const float wl = p.W[n * K + k];
@@ -678,6 +679,7 @@ extern "C" int gl_bwd_workspace(const GlBwdArgs* a, size_t* bytes) {
                      a->x_dtype));
   BwdPlan q = bwd_plan(a->B, a->D, a->G, a->S, a->K);
   GL_TRY(check_topk(a->pool, a->topk, a->S));
+  GL_TRY(check_rec_shift(a->rec_shift, a->S, a->sched));
   // max / top-k pooling: the transposed selected slots, laid out like c1t (times k for top-k)
   const size_t kpe = a->pool == GL_POOL_TOPK_MEAN ? (size_t)a->topk : (a->pool == GL_POOL_MAX ? 1 : 0);
   *bytes = q.xt_bytes + q.c1_bytes + q.mask_bytes + q.part_bytes + kpe * q.c1_bytes;
@@ -725,13 +727,13 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
         GL_CHECK_LAUNCH();
       }
       const MaxEvKArgs ev{xt, a->idx, a->W, a->bias, a->counts, c1t, wint, a->g_pre, a->winner, a->dW, a->db, a->dX,
-                          a->D, a->G, a->S, cap, Bc, b0, kpe, a->pool == GL_POOL_TOPK_MEAN};
+                          a->D, a->G, a->S, cap, Bc, b0, kpe, a->rec_shift, a->pool == GL_POOL_TOPK_MEAN};
       GL_TRY(launch_max_events(a->K, a->act, ev, s));
       continue;
     }
     const long long NS = (long long)a->G * a->S;
     BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, a->sched, nullptr, q.n_chunks, NS,
-           a->D, a->S, q.cpg, n_tiles, cap, 2 * T, ceil_div(a->S, SCHED_WIN), a->G, 0, 0};
+           a->D, a->S, q.cpg, n_tiles, cap, 2 * T, ceil_div(a->S, SCHED_WIN), a->G, 0, 0, a->rec_shift};
     if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &bk.ww, &bk.npw)) bk.win = a->win;
     GL_TRY(launch_bwd_w_any(a->K, a->act, bk, s));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),

@@ -68,6 +68,11 @@ __device__ __forceinline__ int sched_k(uint32_t order, int ks) {
 }
 constexpr long long round_up(long long a, long long b) { return (a + b - 1) / b * b; }
 
+// input k of neuron n when 2^rs consecutive slots share one index record (rs = 0: own record)
+__device__ __forceinline__ int rec_index(const int32_t* __restrict__ idx, long long n, int k, int K, int rs) {
+  return idx[(n >> rs) * K + k];
+}
+
 // Tokens of one dX wave: 64 lanes x T slots, T in {1, 2, 4}, for a chunk of B tokens.
 inline int dx_slots(int B) { return B <= 64 ? 1 : (B <= 128 ? 2 : 4); }
 inline int dx_cap(int B) { return (int)round_up(B, 64 * dx_slots(B)); }

@@ -31,17 +31,18 @@ __device__ __forceinline__ void unit_slots(int u, int P, int S, const int32_t* c
 // non-empty flag in the high 32 bits, for the segment count).
 __global__ void __launch_bounds__(EB_THREADS) edges_count_kernel(const int32_t* __restrict__ idx,
                                                                  const int32_t* __restrict__ counts, int D, int S, int K,
-                                                                 int P, int U, int FR, unsigned long long* __restrict__ cnt) {
+                                                                 int rs, int P, int U, int FR,
+                                                                 unsigned long long* __restrict__ cnt) {
   extern __shared__ unsigned hist[];
   const int u = blockIdx.x;
   int g, s0, s1;
   unit_slots(u, P, S, counts, &g, &s0, &s1);
   for (int f = threadIdx.x; f < FR; f += blockDim.x) hist[f] = 0;
   __syncthreads();
-  const long long base = ((long long)g * S + s0) * K;
+  const long long n0 = (long long)g * S + s0;
   const int ne = (s1 - s0) * K;
   for (int i = threadIdx.x; i < ne; i += blockDim.x) {
-    int d = idx[base + i];
+    int d = rec_index(idx, n0 + i / K, i % K, K, rs);
     d = d < 0 ? 0 : (d >= D ? D - 1 : d);
     atomicAdd(&hist[d / FW], 1u);
   }
@@ -127,6 +128,7 @@ struct ScatterK {
   int32_t* seg_unit;
   uint32_t* seg_begin;
   int D, S, K, P, U, FR, npow2;
+  int rs;  // log2 slots per shared index record
 };
 
 __global__ void __launch_bounds__(EB_THREADS) edges_scatter_kernel(ScatterK p) {
@@ -135,12 +137,12 @@ __global__ void __launch_bounds__(EB_THREADS) edges_scatter_kernel(ScatterK p) {
   const int u = blockIdx.x;
   int g, s0, s1;
   unit_slots(u, p.P, p.S, p.counts, &g, &s0, &s1);
-  const long long base = ((long long)g * p.S + s0) * p.K;
+  const long long n0 = (long long)g * p.S + s0;
   const int ne = (s1 - s0) * p.K;
   for (int i = threadIdx.x; i < p.npow2; i += blockDim.x) {
     unsigned long long key = ~0ull;
     if (i < ne) {
-      int d = p.idx[base + i];
+      int d = rec_index(p.idx, n0 + i / p.K, i % p.K, p.K, p.rs);
       d = d < 0 ? 0 : (d >= p.D ? p.D - 1 : d);
       key = ((unsigned long long)(unsigned)d << 32) | (unsigned)i;
     }
@@ -219,6 +221,7 @@ extern "C" int gl_edges_size(const GlEdgeArgs* a, size_t* edges_bytes, size_t* w
   if (a->D < 1 || a->G < 1 || a->S < 1) return GL_ERR_ARG;
   if (a->K != 8 && a->K != 16) return GL_ERR_UNSUPPORTED;
   if ((long long)a->G * a->S * a->K >= (1LL << 32)) return GL_ERR_UNSUPPORTED;
+  GL_TRY(check_rec_shift(a->rec_shift, a->S, nullptr));
   EdgeHeader h;
   edge_layout(a->D, a->G, a->S, a->K, &h, edges_bytes);
   const long long n = (long long)h.FR * h.U;
@@ -247,7 +250,7 @@ extern "C" int gl_edges_build(const GlEdgeArgs* a, void* stream) {
   if (hist_lds > max_lds_bytes()) return GL_ERR_LDS;
   GL_TRY(set_lds_limit((const void*)edges_count_kernel, hist_lds));
   GL_LAUNCH(GL_KERNEL_EDGES, edges_count_kernel, dim3((unsigned)h.U), dim3(EB_THREADS), hist_lds, s, a->idx, a->counts, a->D,
-                     a->S, a->K, h.P, h.U, h.FR, cnt);
+                     a->S, a->K, a->rec_shift, h.P, h.U, h.FR, cnt);
   GL_CHECK_LAUNCH();
   GL_LAUNCH(GL_KERNEL_EDGES, scan_local_kernel, dim3((unsigned)nb), dim3(256), 0, s, cnt, n, bsum);
   GL_CHECK_LAUNCH();
@@ -263,7 +266,7 @@ extern "C" int gl_edges_build(const GlEdgeArgs* a, void* stream) {
   if (sort_lds > max_lds_bytes()) return GL_ERR_LDS;
   GL_TRY(set_lds_limit((const void*)edges_scatter_kernel, sort_lds));
   ScatterK sk{a->idx, a->counts, cnt, (uint32_t*)(e + h.off_rec), (int32_t*)(e + h.off_seg_unit),
-              (uint32_t*)(e + h.off_seg_begin), a->D, a->S, a->K, h.P, h.U, h.FR, npow2};
+              (uint32_t*)(e + h.off_seg_begin), a->D, a->S, a->K, h.P, h.U, h.FR, npow2, a->rec_shift};
   GL_LAUNCH(GL_KERNEL_EDGES, edges_scatter_kernel, dim3((unsigned)h.U), dim3(EB_THREADS), sort_lds, s, sk);
   GL_CHECK_LAUNCH();
   GL_LAUNCH(GL_KERNEL_EDGES, edges_finish_kernel, dim3((unsigned)ceil_div(h.FR, 256)), dim3(256), 0, s,

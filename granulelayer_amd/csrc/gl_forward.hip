@@ -60,6 +60,7 @@ struct FwdK {
   long long n_chunks;
   int D, S, cpg, n_tiles, b_pad, nwin;
   int G, ww, npw;         // window staging: pools, padded window width, pools per workgroup
+  int rs;                 // log2 slots per shared index record
 };
 
 // One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
@@ -185,10 +186,12 @@ __device__ __forceinline__ void fwd_tile_max(const char* xsb, const unsigned (&a
 // maps the fp32 value to an unsigned integer of the same order (negative values bit-inverted,
 // the others with the sign bit set; -0 is first made +0, so equal values compare equal); the low
 // word is ~slot, so that of two equal values the smaller slot ranks higher.  Slots are distinct
-// within a wave, so keys never tie.
+// within a wave, so keys never tie.  The finalize merges the chunk lists with the same keys, so the
+// selection does not depend on how a pool is split into chunks.
 using cand_t = unsigned long long;
 __device__ __forceinline__ cand_t cand_key(float v, unsigned nslot) {
-  const unsigned b = __float_as_uint(v + 0.f);
+  // NaN of either sign ranks above every number (torch.sort's order); -0 is made +0
+  const unsigned b = __builtin_isnan(v) ? 0x7fc00000u : __float_as_uint(v + 0.f);
   const unsigned o = b ^ ((unsigned)((int)b >> 31) | 0x80000000u);
   return ((cand_t)o << 32) | nslot;
 }
@@ -355,7 +358,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
 #pragma unroll
     for (int ks = 0; ks < K; ++ks) {
       const int k = sched_k<K>(order, ks);  // the pooled sum does not depend on the visiting order
-      int d = p.idx[n * K + k];
+      int d = rec_index(p.idx, n, k, K, p.rs);
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
       addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * 16u;
       const float wl = p.W[n * K + k];
@@ -517,7 +520,7 @@ __global__ void __launch_bounds__(256) fwd_finalize_topk_kernel(const float* __r
         const long long o = (((long long)g * cpg + c) * b_pad + b) * k + ptr[c];
         const float v = part[o];
         const int sl = pslot[o];
-        if (best < 0 || v > bv || (v == bv && sl < bs)) best = c, bv = v, bs = sl;
+        if (best < 0 || cand_key(v, ~(unsigned)sl) > cand_key(bv, ~(unsigned)bs)) best = c, bv = v, bs = sl;
       }
     }
 #pragma unroll
@@ -575,7 +578,7 @@ __global__ void __launch_bounds__(256) fwd_finalize_top8_kernel(const float* __r
     int bs = s[0][0];
 #pragma unroll
     for (int c = 1; c < CP; ++c) {
-      const bool tk = v[c][0] > bv || (v[c][0] == bv && s[c][0] < bs);
+      const bool tk = cand_key(v[c][0], ~(unsigned)s[c][0]) > cand_key(bv, ~(unsigned)bs);
       bc = tk ? c : bc, bv = tk ? v[c][0] : bv, bs = tk ? s[c][0] : bs;
     }
     out[j] = j < kk ? bs : -1;
@@ -707,6 +710,12 @@ int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void
   return 0;
 }
 
+int check_rec_shift(int rec_shift, int S, const void* sched) {
+  if (rec_shift < 0 || rec_shift > 4) return GL_ERR_ARG;
+  if (rec_shift > 0 && (S % (1 << rec_shift) != 0 || sched != nullptr)) return GL_ERR_ARG;
+  return 0;
+}
+
 // top-k mean: k a power of two in [1, 64] (the reference's LevelSpec check) and pools that the
 // finalize's merge covers (cpg <= FWD_TOPK_CPG chunks of 256 slots)
 int check_topk(int pool, int topk, int S) {
@@ -730,7 +739,7 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
     int32_t* winner = a->winner ? a->winner + (long long)b0 * a->G * kpe : nullptr;
     GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles, xt, s));
     FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, pslot, kpe, a->sched, nullptr, q.n_chunks, a->D, a->S, q.cpg,
-           n_tiles, b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0};
+           n_tiles, b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0, a->rec_shift};
     if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) k.win = a->win;
     dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(b_pad, 32));
     if (a->pool == GL_POOL_MAX) {
@@ -810,6 +819,7 @@ extern "C" int gl_fwd_workspace(const GlFwdArgs* a, size_t* bytes) {
   GL_TRY(check_layer(a->B, a->D, a->G, a->S, a->K, a->act, a->pool, a->X, a->idx, a->W, a->bias, a->counts,
                      a->x_dtype));
   GL_TRY(check_topk(a->pool, a->topk, a->S));
+  GL_TRY(check_rec_shift(a->rec_shift, a->S, a->sched));
   FwdPlan q = fwd_plan(a);
   *bytes = q.xt_bytes + q.part_bytes + q.slot_bytes;
   return 0;

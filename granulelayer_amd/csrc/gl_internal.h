@@ -16,6 +16,9 @@ int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void
 // GL_POOL_TOPK_MEAN arguments (k, pool size); 0 for other pools
 int check_topk(int pool, int topk, int S);
 
+// shared index records: 0 <= rec_shift <= 4, S a multiple of 2^rec_shift, no gather schedule
+int check_rec_shift(int rec_shift, int S, const void* sched);
+
 // Window staging for a kernel whose workgroups hold `waves` chunks of cpg per pool: true (with the
 // padded width *ww and pools per workgroup *npw) when the pools' windows fit a stage tile.
 bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, int G, int* ww, int* npw);
@@ -42,6 +45,7 @@ struct MaxEvKArgs {
   float* dX;
   int D, G, S, cap, Bc, b0;
   int kpe;    // selected slots per (token, pool): 1 (max) or k (top-k mean)
+  int rs;     // log2 slots per shared index record
   bool topk;  // coef = g_pre / min(n_g, kpe) (top-k mean) instead of g_pre
 };
 int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s);

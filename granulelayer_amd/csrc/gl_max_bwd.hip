@@ -13,9 +13,9 @@
 //     (one writer per neuron);
 //   * max_events_dx_kernel, one workgroup per token: the events' dz * W[n*, k] are summed into
 //     dX[b, idx[n*, k]] as 64-bit fixed-point integers (LDS atomics: integer sums do not depend on
-//     their order).  A first pass bounds every term by |g_pre| * max_k |W[n*, k]| and picks a
-//     power-of-two scale under which the sum of all G * K terms stays below 2^62; the result is
-//     converted back once per input.
+//     their order).  A first pass bounds the terms of every input d by the largest |g_pre| *
+//     |W[n*, k]| with idx[n*, k] = d and picks that input's power-of-two scale, under which the sum
+//     of all G * kpe * K terms stays below 2^62; the result is converted back once per input.
 #include "gl_common.h"
 #include "gl_internal.h"
 
@@ -35,6 +35,7 @@ struct MaxEvK {
   float* db;                          // [G*S] accumulated
   float* dX;                          // [B, D] overwritten
   int D, G, S, cap, Bc, b0, npow2, kpe, tsub;
+  int rs;     // log2 slots per shared index record
   bool topk;  // coef = g_pre / min(n_g, kpe)
 };
 
@@ -51,7 +52,7 @@ __device__ __forceinline__ float event_dz(const MaxEvK& p, long long n, float c1
   float z = p.bias[n];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    int d = p.idx[n * K + k];
+    int d = rec_index(p.idx, n, k, K, p.rs);
     d = d < 0 ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps reads in bounds
     dk[k] = d;
     wk[k] = p.W[n * K + k];
@@ -126,54 +127,57 @@ __global__ void __launch_bounds__(256) max_events_dw_kernel(MaxEvK p) {
   }
 }
 
-// dX of one token.  LDS: the token's X row (D floats), then D 64-bit fixed-point accumulators.
+// 2^e as a double for a power e kept in the normal range
+__device__ __forceinline__ double pow2(int e) {
+  e = e > 1000 ? 1000 : (e < -1000 ? -1000 : e);
+  return __longlong_as_double((long long)(1023 + e) << 52);
+}
+
+// dX of one token.  LDS: D 64-bit fixed-point accumulators, the token's X row (D floats), then per
+// input the bound of its terms (float bits), replaced by the input's scale exponent.
 template <int K, int ACT>
 __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
   extern __shared__ unsigned long long ldsq[];
-  unsigned long long* acc = ldsq;                               // [D]
-  float* xrow = reinterpret_cast<float*>(ldsq + p.D);            // [D]
-  __shared__ float wmax[16];
-  __shared__ double scale_s;
+  unsigned long long* acc = ldsq;                                       // [D]
+  float* xrow = reinterpret_cast<float*>(ldsq + p.D);                    // [D]
+  unsigned* tmax = reinterpret_cast<unsigned*>(xrow + p.D);              // [D]
   const int b = blockIdx.x;
   const long long row = (long long)(p.b0 + b) * p.G;  // [B, G] row of the token; winners: row * kpe
   for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
     xrow[d] = tile_x(p.xt, p.D, b, d);
     acc[d] = 0ull;
+    tmax[d] = 0u;
   }
-  // pass 1: every term |dz * W[n*, k]| is at most |g_pre| * max_k |W[n*, k]|
-  float m = 0.f;
+  __syncthreads();
+  // pass 1: every term dz * W[n*, k] into input d = idx[n*, k] is at most |g_pre| * |W[n*, k]|;
+  // tmax[d] = the largest such bound (the bits of non-negative floats order like the values, so
+  // the integer maximum is the float maximum, whatever the order of the updates)
   for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
     const int g = e / p.kpe;
-    int s = p.winner[row * p.kpe + e];
-    s = s < 0 ? 0 : (s >= p.S ? p.S - 1 : s);
+    const int s = p.winner[row * p.kpe + e];
+    if (s < 0 || s >= p.S) continue;
     const long long n = (long long)g * p.S + s;
-    float wm = 0.f;
+    const float gb = __builtin_fabsf(p.g_pre[row + g]);
 #pragma unroll
-    for (int k = 0; k < K; ++k) wm = __builtin_fmaxf(wm, __builtin_fabsf(p.W[n * K + k]));
-    m = __builtin_fmaxf(m, __builtin_fabsf(p.g_pre[row + g]) * wm);
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float t = 0.f;
-    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t = __builtin_fmaxf(t, wmax[w]);
-    const double total = (double)t * (double)p.G * (double)p.kpe * (double)K;  // bound of |sum| over all terms
-    // |sum| * scale < 2^62 (and no term's scaled value exceeds it): scale = 2^(61 - floor(log2 total)),
-    // floor(log2) read from the (normal) double's exponent field, the power kept in the normal range
-    double sc = 1.0;
-    if (total > 0.0) {
-      const int e2 = (int)((__double_as_longlong(total) >> 52) & 0x7ff) - 1023;
-      int e = 61 - e2;
-      e = e > 1000 ? 1000 : (e < -1000 ? -1000 : e);
-      sc = __longlong_as_double((long long)(1023 + e) << 52);
+    for (int k = 0; k < K; ++k) {
+      int d = rec_index(p.idx, n, k, K, p.rs);
+      d = d < 0 ? 0 : (d >= p.D ? p.D - 1 : d);
+      atomicMax(&tmax[d], __float_as_uint(gb * __builtin_fabsf(p.W[n * K + k])));
     }
-    scale_s = sc;
   }
   __syncthreads();
-  const double scale = scale_s;
-  // pass 2: the events' dz * W[n*, k] as fixed-point integers
+  // per input: at most G * kpe * K terms of magnitude <= tmax[d], so |sum| * 2^e_d < 2^62 with
+  // e_d = 61 - floor(log2(tmax[d] * G * kpe * K)); floor(log2) read from the (normal) double's
+  // exponent field.  The scale follows each input's own largest term: small inputs keep ~2^-38
+  // (at 2^23 terms) of their own magnitude, not of the token's largest term.
+  const double nterm = (double)p.G * (double)p.kpe * (double)K;
+  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
+    const double bound = (double)__uint_as_float(tmax[d]) * nterm;
+    const int e2 = bound > 0.0 ? (int)((__double_as_longlong(bound) >> 52) & 0x7ff) - 1023 : 0;
+    tmax[d] = (unsigned)(61 - e2);  // a signed exponent, stored in the same word
+  }
+  __syncthreads();
+  // pass 2: the events' dz * W[n*, k] as fixed-point integers at their input's scale
   for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
     const int g = e / p.kpe;
     int s = p.winner[row * p.kpe + e];
@@ -191,19 +195,19 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
     if (!ok || dz == 0.f) continue;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      const long long q = __double2ll_rn((double)(dz * wk[k]) * scale);
+      const long long q = __double2ll_rn((double)(dz * wk[k]) * pow2((int)tmax[dk[k]]));
       atomicAdd(&acc[dk[k]], (unsigned long long)q);
     }
   }
   __syncthreads();
   for (int d = threadIdx.x; d < p.D; d += blockDim.x)
-    p.dX[(long long)(p.b0 + b) * p.D + d] = (float)((double)(long long)acc[d] / scale);
+    p.dX[(long long)(p.b0 + b) * p.D + d] = (float)((double)(long long)acc[d] / pow2((int)tmax[d]));
 }
 
 template <int K, int ACT>
 static int launch_max_events_k(const MaxEvK& k, hipStream_t s) {
   const size_t dw_lds = (size_t)k.npow2 * 4 + (size_t)k.tsub * k.kpe * (K + 1) * 4;
-  const size_t dx_lds = (size_t)k.D * 12;
+  const size_t dx_lds = (size_t)k.D * 16;
   if (dw_lds > max_lds_bytes() || dx_lds > max_lds_bytes()) return GL_ERR_LDS;
   GL_TRY(set_lds_limit((const void*)max_events_dw_kernel<K, ACT>, dw_lds));
   GL_TRY(set_lds_limit((const void*)max_events_dx_kernel<K, ACT>, dx_lds));
@@ -220,7 +224,7 @@ int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s) {
   int npow2 = 1;
   while (npow2 < tsub * a.kpe) npow2 <<= 1;
   const MaxEvK k{a.xt, a.idx, a.W, a.bias, a.counts, a.c1t, a.wint, a.g_pre, a.winner, a.dW, a.db, a.dX,
-                 a.D, a.G, a.S, a.cap, a.Bc, a.b0, npow2, a.kpe, tsub, a.topk};
+                 a.D, a.G, a.S, a.cap, a.Bc, a.b0, npow2, a.kpe, tsub, a.rs, a.topk};
   if (K == 8) return act == GL_ACT_RELU ? launch_max_events_k<8, GL_ACT_RELU>(k, s) : launch_max_events_k<8, GL_ACT_IDENTITY>(k, s);
   return act == GL_ACT_RELU ? launch_max_events_k<16, GL_ACT_RELU>(k, s) : launch_max_events_k<16, GL_ACT_IDENTITY>(k, s);
 }

@@ -228,15 +228,18 @@ extern "C" int gl_sched_build_host(const int32_t* idx, const int32_t* counts, in
 // of pool g's valid neurons, *width = max over pools of (largest - smallest + 1).  With narrow
 // windows the forward and dW kernels stage only each pool's window of X in LDS.
 extern "C" int gl_window_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S,
-                                    int32_t K, uint32_t* lo, int32_t* width) {
+                                    int32_t K, int32_t rec_shift, uint32_t* lo, int32_t* width) {
   if (!idx || !counts || !lo || !width || D < 1 || G < 1 || S < 1 || K < 1) return GL_ERR_ARG;
+  if (rec_shift < 0 || rec_shift > 4 || S % (1 << rec_shift) != 0) return GL_ERR_ARG;
   int32_t wmax = 0;
   for (long long g = 0; g < G; ++g) {
     const int n_g = counts[g] < S ? counts[g] : S;
     int32_t mn = D, mx = -1;
-    const int32_t* r = idx + g * (long long)S * K;
-    for (long long e = 0; e < (long long)n_g * K; ++e) {
-      int32_t d = r[e];
+    // the records that hold the pool's valid slots [0, n_g): rows (g S) >> r .. (g S + n_g - 1) >> r
+    const long long r0 = (g * S) >> rec_shift;
+    const long long r1 = n_g > 0 ? ((g * S + n_g - 1) >> rec_shift) + 1 : r0;
+    for (long long e = r0 * K; e < r1 * K; ++e) {
+      int32_t d = idx[e];
       d = d < 0 ? 0 : (d >= D ? D - 1 : d);
       mn = d < mn ? d : mn;
       mx = d > mx ? d : mx;

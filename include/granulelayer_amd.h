@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 6
+#define GL_ABI_VERSION 7
 
 enum {
   GL_OK = 0,
@@ -58,7 +58,10 @@ typedef struct GlFwdArgs {
   int32_t B, D, G, S, K;  /* tokens, inputs, groups, padded slots per group, fan-in (8 | 16) */
   int32_t act, pool;      /* GL_ACT_*, GL_POOL_* */
   int32_t topk;           /* GL_POOL_TOPK_MEAN: k, a power of two in [1, 64] (pools of <= 4096 slots) */
-  const int32_t* idx;     /* [G*S, K] input indices in [0, D) */
+  int32_t rec_shift;      /* 0: every slot owns its index record; r in 1..4: 2^r consecutive slots share
+                             one record (idx is [G*S >> r, K]; S a multiple of 2^r), e.g. r = 4 for the
+                             K16 / C16 records of Cover-TopK/16 (sparse_pooling/cover_topk16.py:1-12) */
+  const int32_t* idx;     /* [G*S >> rec_shift, K] input indices in [0, D) */
   const float* W;         /* [G*S, K] */
   const float* bias;      /* [G*S] */
   const int32_t* counts;  /* [G] valid neurons per group, 1 <= counts[g] <= S */
@@ -87,6 +90,7 @@ typedef struct GlBwdArgs {
   int32_t B, D, G, S, K;
   int32_t act, pool;
   int32_t topk;           /* as GlFwdArgs.topk */
+  int32_t rec_shift;      /* as GlFwdArgs.rec_shift */
   const int32_t* idx;
   const float* W;
   const float* bias;
@@ -111,9 +115,10 @@ typedef struct GlBwdArgs {
  * (sparse_pooling/kernels/triton_fused.py:442-445); this structure turns it into a
  * deterministic segmented reduction (the fixed-owner pattern of kernels/cuda/sg_det.cu:1-46). */
 typedef struct GlEdgeArgs {
-  const int32_t* idx;
+  const int32_t* idx;     /* [G*S >> rec_shift, K] */
   const int32_t* counts;
   int32_t D, G, S, K;
+  int32_t rec_shift;      /* as GlFwdArgs.rec_shift */
   void* edges;            /* out, gl_edges_size() bytes */
   size_t edges_bytes;
   void* ws;               /* scratch, gl_edges_size() bytes */
@@ -134,10 +139,39 @@ typedef struct GlAdamArgs {
   float lr, beta1, beta2, eps, weight_decay, bc1, bc2;
 } GlAdamArgs;
 
+/* Cover-TopK support selection of an envelope (one-time preprocessing of CoverTopK16Layer).
+ * Replaces local_supports.feature_importance / topk_select / cover_repair
+ * (sparse_pooling/experimental/local_supports.py:209-222, 279-282, 294-375) as used by
+ * CoverTopK16Layer.from_envelope (sparse_pooling/cover_topk16.py:80-146).  R envelope records of
+ * C = 16 gpb neurons share 64 candidate inputs each; the valid neurons of a record are a prefix.
+ * Per 16-neuron row group u: importance a[u, j] = sum over its valid neurons of W^2 (float64, in
+ * neuron order); the k largest (ties to the lower position); with repair, every candidate of a
+ * record is then kept by at least one valid group through greedy minimum-energy-loss swaps. */
+typedef struct GlCoverArgs {
+  const float* W;         /* [R * C, 64] envelope weights, or NULL when a is given */
+  const double* a;        /* [R * gpb, 64] importances to select from, or NULL (computed from W) */
+  const int32_t* nvalid;  /* [R] valid neurons of each record (0..C) */
+  const int32_t* cand;    /* [R, 64] global input of each candidate, or NULL (rec_idx gets positions) */
+  int32_t R, gpb, k;      /* records, row groups per record (1..16), kept candidates per group (1..64) */
+  int32_t repair;         /* 1: Cover-TopK (coverage repair after TopK), 0: TopK only */
+  double* importance;     /* out [R * gpb, 64] or NULL */
+  int32_t* env;           /* out [R * gpb, k] kept positions, ascending (groups with no valid neuron: 0..k-1) */
+  int32_t* rec_idx;       /* out [R * gpb, k] cand[record, env] or NULL */
+  float* W_out;           /* out [R * C, k] every neuron's weights at its group's kept positions (0 for
+                             padded neurons), or NULL */
+  int32_t* missing0;      /* out [R] candidates kept by no valid group after TopK, or NULL */
+  int32_t* swaps;         /* out [R] repair swaps, or NULL */
+  double* loss;           /* out [R] energy loss of the swaps (float64, in swap order), or NULL */
+  int32_t* status;        /* out [R] 0 ok, 1 infeasible record (valid groups * k < 64: nothing repaired),
+                             or NULL */
+} GlCoverArgs;
+
+int gl_cover_select(const GlCoverArgs* a, void* stream);
+
 /* ABI identity: version and struct layouts (sizeof, then every field offset in declaration
  * order) so a binding can refuse a mismatched library.  Replaces sp_abi_version /
  * sp_struct_layout (sparse_pooling/kernels/cuda/abi.cu:17-62, checked in runtime.py:103-120).
- * which: 0 GlFwdArgs, 1 GlBwdArgs, 2 GlEdgeArgs, 3 GlAdamArgs.  Returns the number of values
+ * which: 0 GlFwdArgs, 1 GlBwdArgs, 2 GlEdgeArgs, 3 GlAdamArgs, 4 GlCoverArgs.  Returns the number of values
  * written (or needed, when n is too small), negative on an unknown struct. */
 int gl_abi_version(void);
 int gl_struct_layout(int which, long long* out, int n);
@@ -172,7 +206,7 @@ int gl_bwd(const GlBwdArgs* a, void* stream);
 int gl_adam(const GlAdamArgs* a, void* stream);
 
 /* Gather schedule of the forward and dW kernels (K = 8 only), built on the HOST once per index
- * tensor from host copies of idx [G*S, 8] and counts [G]; upload the result and pass it as
+ * tensor from host copies of idx [G*S, 8] and counts [G] (rec_shift 0); upload the result and pass it as
  * GlFwdArgs.sched / GlBwdArgs.sched.  It reorders, within windows of 128 slots, which neurons
  * share a 16-lane LDS gather and the order of each neuron's 8 edges, so the kernels' 16-byte LDS
  * reads hit distinct banks more often; results are unchanged up to fp32 summation order.  No
@@ -191,14 +225,15 @@ int gl_sched_build_host(const int32_t* idx, const int32_t* counts, int32_t D, in
  * (the reference stages per-supergroup feature sets in its Mode-B grouped kernels,
  * sparse_pooling/supergroups.py:1-40, kernels/cuda/sparse_pool_sg.cuh). */
 int gl_window_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
-                         uint32_t* lo, int32_t* width);
+                         int32_t rec_shift, uint32_t* lo, int32_t* width);
 
 /* Kernel ids reported by the trace below. */
 enum {
   GL_KERNEL_TILE_X = 1, GL_KERNEL_FWD = 2, GL_KERNEL_FWD_FINALIZE = 3, GL_KERNEL_C1T = 4, GL_KERNEL_BWD_W = 5,
   GL_KERNEL_DX = 6, GL_KERNEL_DX_REDUCE = 7, GL_KERNEL_ADAM = 8, GL_KERNEL_EDGES = 9,
   GL_KERNEL_FWD_WIN = 10, GL_KERNEL_BWD_W_WIN = 11, /* forward / dW with pool-window staging */
-  GL_KERNEL_MAX_EV_DW = 12, GL_KERNEL_MAX_EV_DX = 13  /* max-pooling backward: winner events */
+  GL_KERNEL_MAX_EV_DW = 12, GL_KERNEL_MAX_EV_DX = 13, /* max-pooling backward: winner events */
+  GL_KERNEL_COVER = 14                                 /* Cover-TopK support selection */
 };
 
 /* Launch trace for benchmarks and tests (process-wide, not for concurrent callers): after
