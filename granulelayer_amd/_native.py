@@ -61,11 +61,12 @@ STRUCTS = (GlFwdArgs, GlBwdArgs, GlEdgeArgs, GlAdamArgs, GlCoverArgs)  # gl_stru
 EXPORTS = ("gl_abi_version", "gl_struct_layout", "gl_error_string", "gl_fwd_workspace", "gl_fwd", "gl_fwd_static",
            "gl_edges_size",
            "gl_edges_build", "gl_bwd_workspace", "gl_bwd", "gl_adam", "gl_sched_size", "gl_sched_build_host",
-           "gl_window_build_host", "gl_cover_select", "gl_trace_begin", "gl_trace_end")
+           "gl_sched_build", "gl_window_build_host", "gl_window_build", "gl_cover_select", "gl_trace_begin",
+           "gl_trace_end")
 KERNEL_NAMES = {1: "tile_x_kernel", 2: "fwd_kernel", 3: "fwd_finalize_kernel", 4: "c1t_kernel", 5: "bwd_w_kernel",
                 6: "dx_kernel", 7: "dx_reduce_kernel", 8: "adam_kernel", 9: "edges_build", 10: "fwd_kernel_win",
                 11: "bwd_w_kernel_win", 12: "max_events_dw_kernel", 13: "max_events_dx_kernel",
-                14: "cover_select_kernel"}
+                14: "cover_select_kernel", 15: "sched_build_kernel"}
 
 
 class NativeError(RuntimeError):
@@ -108,6 +109,10 @@ class Library:
         L.gl_sched_size.argtypes = [_I32, _I32, _I32, ctypes.POINTER(_SZ)]
         L.gl_sched_build_host.restype = ctypes.c_int
         L.gl_sched_build_host.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _P, _I32]
+        L.gl_sched_build.restype = ctypes.c_int
+        L.gl_sched_build.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _P, _P]
+        L.gl_window_build.restype = ctypes.c_int
+        L.gl_window_build.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P]
         L.gl_window_build_host.restype = ctypes.c_int
         L.gl_window_build_host.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(_I32)]
         self.check_abi()

@@ -157,8 +157,9 @@ class HipBackend:
 
     # ------------------------------------------------------------------ gather schedule
     def schedule(self, rt) -> Optional[torch.Tensor]:
-        """Gather schedule of rt's index tensor for the forward / dW kernels (fan-in 8; built on the
-        host once per index tensor and cached on rt), or None for fan-in 16."""
+        """Gather schedule of rt's index tensor for the forward / dW kernels (fan-in 8, one index
+        record per slot), built on the GPU once per index tensor (gl_sched_build, the host
+        builder's algorithm) and cached on rt; None otherwise."""
         L, G, S, K = self._layer(rt)
         if K != 8 or self.rec_shift(rt):
             return None
@@ -166,17 +167,21 @@ class HipBackend:
         cached = getattr(rt, "_hip_sched", None)
         if cached is not None and cached[0] == key:
             return cached[1]
-        host = self.lib.sched_build(rt.idx.reshape(-1, K).cpu().numpy(), rt.counts_i32.cpu().numpy(), L.input_dim,
-                                    G, S, K)
-        sched = torch.from_numpy(host.view(np.int32)).to(rt.idx.device)
+        dev = rt.idx.device
+        n = ctypes.c_size_t(0)
+        self.lib.call("gl_sched_size", G, S, K, ctypes.byref(n))
+        sched = torch.empty(n.value // 4, dtype=torch.int32, device=dev)
+        with torch.cuda.device(dev):
+            self.lib.call("gl_sched_build", _ptr(rt.idx), _ptr(rt.counts_i32), L.input_dim, G, S, K, _ptr(sched),
+                          ctypes.c_void_p(_stream(dev)))
         rt._hip_sched = (key, sched)
         return sched
 
     # ------------------------------------------------------------------ pool windows
     def windows(self, rt):
         """Per-pool input windows of rt's index tensor (first input per pool on the device, widest
-        width), built on the host once per index tensor and cached on rt; (None, 0) when
-        ``window_staging`` is off.  The library stages only the windows when they are narrow."""
+        width), built on the GPU once per index tensor (gl_window_build) and cached on rt; (None, 0)
+        when ``window_staging`` is off.  The library stages only the windows when they are narrow."""
         if not self.window_staging:
             return None, 0
         L, G, S, K = self._layer(rt)
@@ -184,9 +189,13 @@ class HipBackend:
         cached = getattr(rt, "_hip_win", None)
         if cached is not None and cached[0] == key:
             return cached[1]
-        lo, width = self.lib.window_build(rt.idx.reshape(-1, K).cpu().numpy(), rt.counts_i32.cpu().numpy(),
-                                          L.input_dim, G, S, K, self.rec_shift(rt))
-        out = (torch.from_numpy(lo.view(np.int32)).to(rt.idx.device), width)
+        dev = rt.idx.device
+        lo = torch.empty(G, dtype=torch.int32, device=dev)
+        width = torch.empty(1, dtype=torch.int32, device=dev)
+        with torch.cuda.device(dev):
+            self.lib.call("gl_window_build", _ptr(rt.idx), _ptr(rt.counts_i32), L.input_dim, G, S, K,
+                          self.rec_shift(rt), _ptr(lo), _ptr(width), ctypes.c_void_p(_stream(dev)))
+        out = (lo, int(width.item()))  # the launch needs the width on the host: one 4-byte copy
         rt._hip_win = (key, out)
         return out
 

@@ -34,24 +34,47 @@ constexpr int WIN = 128;
 constexpr int SETS = WIN / 16;
 constexpr int KS = 8;
 
+// One window of 128 slots.  The same code runs on the host (gl_sched_build_host, one thread per
+// range of windows) and on the GPU (gl_sched_build, one lane per window), so both builders give
+// the same schedule bit for bit.
 struct Window {
-  int res[WIN][KS];  // residue of edge k of slot p (-1: invalid slot)
-  int hist[WIN][16];
+  int8_t res[WIN][KS];    // residue of edge k of slot p (-1: invalid slot)
+  uint8_t hist[WIN][16];  // multiplicity of each residue among slot p's edges
   bool valid[WIN];
 };
 
+// stable insertion sort of v[0..n) by key (larger first when desc): the order std::stable_sort
+// gives for the same comparator
+template <typename KeyF>
+__host__ __device__ inline void stable_sort_by(int* v, int n, KeyF key, bool desc) {
+  for (int i = 1; i < n; ++i) {
+    const int x = v[i];
+    const int kx = key(x);
+    int j = i - 1;
+    while (j >= 0 && (desc ? key(v[j]) < kx : key(v[j]) > kx)) {
+      v[j + 1] = v[j];
+      --j;
+    }
+    v[j + 1] = x;
+  }
+}
+
 // greedy balance: slots with the most repeated residue first; each goes to the set (with room)
 // whose sum over residues of (count - 8)^2 for counts above 8 grows least (ties: lower set)
-void balance(const Window& W, int members[SETS][16]) {
+__host__ __device__ inline void balance(const Window& W, uint8_t members[SETS][16]) {
   int order[WIN], mx[WIN];
   for (int p = 0; p < WIN; ++p) {
     order[p] = p;
     mx[p] = 0;
-    for (int r = 0; r < 16; ++r) mx[p] = std::max(mx[p], W.hist[p][r]);
+    for (int r = 0; r < 16; ++r) mx[p] = mx[p] > W.hist[p][r] ? mx[p] : W.hist[p][r];
   }
-  std::stable_sort(order, order + WIN, [&](int a, int b) { return mx[a] > mx[b]; });
-  int H[SETS][16] = {};
-  int cnt[SETS] = {};
+  stable_sort_by(order, WIN, [&](int a) { return mx[a]; }, true);
+  int H[SETS][16];
+  int cnt[SETS];
+  for (int set = 0; set < SETS; ++set) {
+    cnt[set] = 0;
+    for (int r = 0; r < 16; ++r) H[set][r] = 0;
+  }
   for (int oi = 0; oi < WIN; ++oi) {
     const int p = order[oi];
     int rs[KS], hs[KS], nr = 0;  // distinct residues of slot p and their multiplicities
@@ -68,47 +91,67 @@ void balance(const Window& W, int members[SETS][16]) {
       if (best < 0 || c < best_cost) best = set, best_cost = c;
     }
     for (int i = 0; i < nr; ++i) H[best][rs[i]] += hs[i];
-    members[best][cnt[best]++] = p;
+    members[best][cnt[best]++] = (uint8_t)p;
   }
 }
 
 // Kuhn's augmenting paths over 16 lanes and 16 residues; cand[l] = residues of lane l's unused
-// edges, tried in the round's residue order (most remaining edges first)
+// edges, tried in the round's residue order (most remaining edges first).  Depth-first search with
+// an explicit stack: frame f holds its lane, the next residue position to try and the residue it
+// is trying; a free residue found at depth d gives every frame on the path its residue.
 struct Matcher {
   uint32_t cand[16];
   int ord[16];
   int owner[16];
-  uint32_t seen;
 
-  bool try_lane(int l) {
-    for (int i = 0; i < 16; ++i) {
-      const int r = ord[i];
-      if (!((cand[l] >> r) & 1u) || ((seen >> r) & 1u)) continue;
-      seen |= 1u << r;
-      if (owner[r] < 0 || try_lane(owner[r])) {
-        owner[r] = l;
-        return true;
+  __host__ __device__ bool try_lane(int l0) {
+    int lane[17], pos[17], tried[17];
+    uint32_t seen = 0;
+    int d = 0;
+    lane[0] = l0;
+    pos[0] = 0;
+    for (;;) {
+      const int l = lane[d];
+      bool pushed = false;
+      while (pos[d] < 16) {
+        const int r = ord[pos[d]++];
+        if (!((cand[l] >> r) & 1u) || ((seen >> r) & 1u)) continue;
+        seen |= 1u << r;
+        if (owner[r] < 0) {
+          owner[r] = l;
+          for (int f = d - 1; f >= 0; --f) owner[tried[f]] = lane[f];
+          return true;
+        }
+        tried[d] = r;
+        lane[d + 1] = owner[r];
+        pos[d + 1] = 0;
+        ++d;
+        pushed = true;
+        break;
       }
+      if (pushed) continue;
+      if (d == 0) return false;
+      --d;  // the child found no augmenting path: continue this frame's residues
     }
-    return false;
   }
 };
 
 // visiting order kperm[lane][round] of the set's lanes; invalid lanes keep the identity
-void match_set(const Window& W, const int mem[16], int kperm[16][KS]) {
-  int rem[16][KS];  // residue of each lane's unused edge k (-1 = used)
+__host__ __device__ inline void match_set(const Window& W, const uint8_t mem[16], uint8_t kperm[16][KS]) {
+  int8_t rem[16][KS];  // residue of each lane's unused edge k (-1 = used)
   bool live[16];
   for (int l = 0; l < 16; ++l) {
     live[l] = W.valid[mem[l]];
     for (int k = 0; k < KS; ++k) {
-      rem[l][k] = live[l] ? W.res[mem[l]][k] : -1;
-      kperm[l][k] = k;
+      rem[l][k] = live[l] ? W.res[mem[l]][k] : (int8_t)-1;
+      kperm[l][k] = (uint8_t)k;
     }
   }
   Matcher M;
   for (int round = 0; round < KS; ++round) {
-    int deg[16] = {};
+    int deg[16];
     int ndist[16];
+    for (int r = 0; r < 16; ++r) deg[r] = 0;
     for (int l = 0; l < 16; ++l) {
       M.cand[l] = 0;
       for (int k = 0; k < KS; ++k)
@@ -116,18 +159,17 @@ void match_set(const Window& W, const int mem[16], int kperm[16][KS]) {
       ndist[l] = __builtin_popcount(M.cand[l]);
     }
     for (int r = 0; r < 16; ++r) M.ord[r] = r, M.owner[r] = -1;
-    std::stable_sort(M.ord, M.ord + 16, [&](int a, int b) { return deg[a] > deg[b]; });
+    stable_sort_by(M.ord, 16, [&](int a) { return deg[a]; }, true);
     int order[16];
     for (int l = 0; l < 16; ++l) order[l] = l;
-    std::stable_sort(order, order + 16, [&](int a, int b) { return ndist[a] < ndist[b]; });
+    stable_sort_by(order, 16, [&](int a) { return ndist[a]; }, false);
     for (int i = 0; i < 16; ++i) {
       const int l = order[i];
       if (!live[l]) continue;
-      M.seen = 0;
       M.try_lane(l);
     }
-    int lane_res[16], used[16] = {};
-    for (int l = 0; l < 16; ++l) lane_res[l] = -1;
+    int lane_res[16], used[16];
+    for (int l = 0; l < 16; ++l) lane_res[l] = -1, used[l] = 0;
     for (int r = 0; r < 16; ++r)
       if (M.owner[r] >= 0) lane_res[M.owner[r]] = r, used[r]++;
     for (int l = 0; l < 16; ++l) {  // unmatched lanes: the residue this round uses least
@@ -147,10 +189,43 @@ void match_set(const Window& W, const int mem[16], int kperm[16][KS]) {
       if (!live[l]) continue;
       for (int k = 0; k < KS; ++k)  // the lowest unused edge with that residue
         if (rem[l][k] == lane_res[l]) {
-          kperm[l][round] = k;
+          kperm[l][round] = (uint8_t)k;
           rem[l][k] = -1;
           break;
         }
+    }
+  }
+}
+
+// slot p's residues and histogram (window w of group g)
+__host__ __device__ inline void load_slot(Window& W, const int32_t* idx, int D, int S, long long g, int w, int n_g,
+                                          int p) {
+  const int s = w * WIN + p;
+  W.valid[p] = s < n_g;
+  for (int r = 0; r < 16; ++r) W.hist[p][r] = 0;
+  for (int k = 0; k < KS; ++k) {
+    int r = -1;
+    if (W.valid[p]) {
+      int d = idx[((long long)g * S + s) * KS + k];
+      d = d < 0 ? 0 : (d >= D ? D - 1 : d);
+      r = d & 15;
+      W.hist[p][r]++;
+    }
+    W.res[p][k] = (int8_t)r;
+  }
+}
+
+// the 128 records of one loaded window
+__host__ __device__ inline void schedule_window(const Window& W, uint32_t* out) {
+  uint8_t members[SETS][16];
+  balance(W, members);
+  for (int set = 0; set < SETS; ++set) {
+    uint8_t kperm[16][KS];
+    match_set(W, members[set], kperm);
+    for (int l = 0; l < 16; ++l) {
+      uint32_t rec = (uint32_t)members[set][l];
+      for (int ks = 0; ks < KS - 1; ++ks) rec |= (uint32_t)kperm[l][ks] << (7 + 3 * ks);
+      out[set * 16 + l] = rec;
     }
   }
 }
@@ -163,33 +238,59 @@ void build_range(const int32_t* idx, const int32_t* counts, int D, int G, int S,
     const long long g = gw / nwin;
     const int w = (int)(gw % nwin);
     const int n_g = std::min(counts[g], S);
-    for (int p = 0; p < WIN; ++p) {
-      const int s = w * WIN + p;
-      W.valid[p] = s < n_g;
-      for (int r = 0; r < 16; ++r) W.hist[p][r] = 0;
-      for (int k = 0; k < KS; ++k) {
-        int r = -1;
-        if (W.valid[p]) {
-          int d = idx[((long long)g * S + s) * KS + k];
-          d = d < 0 ? 0 : (d >= D ? D - 1 : d);
-          r = d & 15;
-          W.hist[p][r]++;
-        }
-        W.res[p][k] = r;
-      }
-    }
-    int members[SETS][16];
-    balance(W, members);
-    uint32_t* out = sched + gw * WIN;
-    for (int set = 0; set < SETS; ++set) {
-      int kperm[16][KS];
-      match_set(W, members[set], kperm);
-      for (int l = 0; l < 16; ++l) {
-        uint32_t rec = (uint32_t)members[set][l];
-        for (int ks = 0; ks < KS - 1; ++ks) rec |= (uint32_t)kperm[l][ks] << (7 + 3 * ks);
-        out[set * 16 + l] = rec;
-      }
-    }
+    for (int p = 0; p < WIN; ++p) load_slot(W, idx, D, S, g, w, n_g, p);
+    schedule_window(W, sched + gw * WIN);
+  }
+}
+
+// GPU builder: one window per lane (the windows of a wave run the same code on different data;
+// their private arrays are interleaved per lane, so the lanes' accesses to them coalesce)
+__global__ void __launch_bounds__(64) sched_build_kernel(const int32_t* __restrict__ idx,
+                                                         const int32_t* __restrict__ counts, int D, int S, int nwin,
+                                                         long long nw, uint32_t* __restrict__ sched) {
+  const long long gw = (long long)blockIdx.x * 64 + threadIdx.x;
+  if (gw >= nw) return;
+  const long long g = gw / nwin;
+  const int w = (int)(gw % nwin);
+  const int n_g = counts[g] < S ? counts[g] : S;
+  Window W;
+  for (int p = 0; p < WIN; ++p) load_slot(W, idx, D, S, g, w, n_g, p);
+  schedule_window(W, sched + gw * WIN);
+}
+
+__global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = v;
+}
+
+// GPU pool windows: one workgroup per pool, the smallest and largest index of its valid slots'
+// records; the widest window by an integer atomic maximum (order-independent)
+__global__ void __launch_bounds__(256) window_build_kernel(const int32_t* __restrict__ idx,
+                                                           const int32_t* __restrict__ counts, int D, int S, int K,
+                                                           int rs, uint32_t* __restrict__ lo, int32_t* __restrict__ width) {
+  __shared__ int smn[4], smx[4];
+  const long long g = blockIdx.x;
+  const int n_g = counts[g] < S ? counts[g] : S;
+  const long long r0 = (g * S) >> rs;
+  const long long r1 = n_g > 0 ? ((g * S + n_g - 1) >> rs) + 1 : r0;
+  int mn = D, mx = -1;
+  for (long long e = r0 * K + threadIdx.x; e < r1 * K; e += blockDim.x) {
+    int d = idx[e];
+    d = d < 0 ? 0 : (d >= D ? D - 1 : d);
+    mn = d < mn ? d : mn;
+    mx = d > mx ? d : mx;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const int a = __shfl_xor(mn, o), b = __shfl_xor(mx, o);
+    mn = a < mn ? a : mn;
+    mx = b > mx ? b : mx;
+  }
+  if ((threadIdx.x & 63) == 0) smn[threadIdx.x >> 6] = mn, smx[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 4; ++i) mn = smn[i] < mn ? smn[i] : mn, mx = smx[i] > mx ? smx[i] : mx;
+    if (mx < 0) mn = mx = 0;
+    lo[g] = (uint32_t)mn;
+    atomicMax(width, mx - mn + 1);
   }
 }
 
@@ -249,5 +350,30 @@ extern "C" int gl_window_build_host(const int32_t* idx, const int32_t* counts, i
     wmax = mx - mn + 1 > wmax ? mx - mn + 1 : wmax;
   }
   *width = wmax;
+  return 0;
+}
+
+extern "C" int gl_sched_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
+                              uint32_t* sched, void* stream) {
+  if (!idx || !counts || !sched || D < 1 || G < 1 || S < 1) return GL_ERR_ARG;
+  if (K != 8) return GL_ERR_UNSUPPORTED;
+  const long long nw = (long long)G * ceil_div(S, WIN);
+  if (nw >= (1LL << 31)) return GL_ERR_UNSUPPORTED;
+  GL_LAUNCH(GL_KERNEL_SCHED, sched_build_kernel, dim3((unsigned)ceil_div(nw, 64)), dim3(64), 0, (hipStream_t)stream, idx,
+            counts, D, S, ceil_div(S, WIN), nw, sched);
+  GL_CHECK_LAUNCH();
+  return 0;
+}
+
+extern "C" int gl_window_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
+                               int32_t rec_shift, uint32_t* lo, int32_t* width, void* stream) {
+  if (!idx || !counts || !lo || !width || D < 1 || G < 1 || S < 1 || K < 1) return GL_ERR_ARG;
+  if (rec_shift < 0 || rec_shift > 4 || S % (1 << rec_shift) != 0) return GL_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  GL_LAUNCH(GL_KERNEL_SCHED, fill_i32_kernel, dim3(1), dim3(64), 0, s, width, 1, 0);
+  GL_CHECK_LAUNCH();
+  GL_LAUNCH(GL_KERNEL_SCHED, window_build_kernel, dim3((unsigned)G), dim3(256), 0, s, idx, counts, D, S, K, rec_shift,
+            lo, width);
+  GL_CHECK_LAUNCH();
   return 0;
 }

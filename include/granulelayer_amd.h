@@ -216,6 +216,11 @@ int gl_sched_size(int32_t G, int32_t S, int32_t K, size_t* bytes);
 int gl_sched_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
                         uint32_t* sched, int32_t threads);
 
+/* The same schedule built on the GPU from device copies of idx and counts (one lane per 128-slot
+ * window, the host builder's code), bit-identical to gl_sched_build_host; enqueued on stream. */
+int gl_sched_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
+                   uint32_t* sched, void* stream);
+
 /* Per-pool input windows, built on the HOST once per index tensor: lo[g] = the smallest input
  * index of pool g's valid neurons, *width = the widest window (largest - smallest + 1) over all
  * pools.  Pass lo as GlFwdArgs.win / GlBwdArgs.win and *width as win_width: when every workgroup's
@@ -226,6 +231,9 @@ int gl_sched_build_host(const int32_t* idx, const int32_t* counts, int32_t D, in
  * sparse_pooling/supergroups.py:1-40, kernels/cuda/sparse_pool_sg.cuh). */
 int gl_window_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
                          int32_t rec_shift, uint32_t* lo, int32_t* width);
+/* The same windows built on the GPU from device copies (lo [G] and *width in device memory). */
+int gl_window_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
+                    int32_t rec_shift, uint32_t* lo, int32_t* width, void* stream);
 
 /* Kernel ids reported by the trace below. */
 enum {
@@ -233,7 +241,8 @@ enum {
   GL_KERNEL_DX = 6, GL_KERNEL_DX_REDUCE = 7, GL_KERNEL_ADAM = 8, GL_KERNEL_EDGES = 9,
   GL_KERNEL_FWD_WIN = 10, GL_KERNEL_BWD_W_WIN = 11, /* forward / dW with pool-window staging */
   GL_KERNEL_MAX_EV_DW = 12, GL_KERNEL_MAX_EV_DX = 13, /* max-pooling backward: winner events */
-  GL_KERNEL_COVER = 14                                 /* Cover-TopK support selection */
+  GL_KERNEL_COVER = 14,                                /* Cover-TopK support selection */
+  GL_KERNEL_SCHED = 15                                 /* gather schedule / pool windows on the GPU */
 };
 
 /* Launch trace for benchmarks and tests (process-wide, not for concurrent callers): after

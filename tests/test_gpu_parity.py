@@ -677,3 +677,25 @@ def test_topk_largest_pools(k):
     assert_parity(dx, wdX, mX, what="dX")
     assert_parity(dw.cpu().numpy().reshape(-1, K), wdW, mW, what="dW")
     assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, what="db")
+
+
+@pytest.mark.parametrize("D,H,G,window", [(4096, 200_000, 200, 0), (300, 9000, 7, 0), (2048, 8192, 8, 256),
+                                          (64, 3000, 8, 0)])
+def test_gpu_setup_builders_equal_the_host_builders(D, H, G, window):
+    """The gather schedule and the pool windows built on the GPU (gl_sched_build, gl_window_build)
+    are bit-identical to the host builders' (gl_sched_build_host, gl_window_build_host)."""
+    from granulelayer_amd import _native as N
+
+    if window:
+        L, idx, w, b, x, _ = make_window_case(D, H, G, 8, 1, window)
+    else:
+        L, idx, w, b, x, _ = make_case(D, H, G, 8, 1)
+    rt = runtime(L, idx, "sum", "relu")
+    be = HipBackend.get()
+    lib = N.library()
+    S = L.slots_per_group
+    host_sched = lib.sched_build(idx.reshape(-1, 8).numpy(), L.counts_tensor("cpu").numpy(), D, G, S, 8)
+    assert np.array_equal(be.schedule(rt).cpu().numpy().view(np.uint32), host_sched)
+    lo, width = lib.window_build(idx.reshape(-1, 8).numpy(), L.counts_tensor("cpu").numpy(), D, G, S, 8)
+    glo, gwidth = be.windows(rt)
+    assert gwidth == width and np.array_equal(glo.cpu().numpy().view(np.uint32), lo)
