@@ -13,10 +13,10 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgranulelayer_amd.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 GL_ACT = {"identity": 0, "relu": 1}
-GL_POOL = {"mean": 0, "sum": 1, "max": 2, "topk_mean": 3}
+GL_POOL = {"mean": 0, "sum": 1, "max": 2, "topk_mean": 3, "logmeanexp": 4, "power_mean": 5, "softmax_weighted": 6}
 GL_DTYPE_F32, GL_DTYPE_BF16 = 0, 1
 GL_ERR_SCRATCH = -8
 FWD_STATIC_SCRATCH_BYTES = 64 << 20  # GL_FWD_STATIC_SCRATCH_BYTES
@@ -27,14 +27,15 @@ _P, _I32, _I64, _SZ, _F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctype
 class GlFwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
                 ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("rec_shift", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
-                ("sched", _P), ("win", _P), ("win_width", _I32), ("pre", _P), ("winner", _P), ("ws", _P),
-                ("ws_bytes", _SZ), ("part_budget", _SZ)]
+                ("sched", _P), ("win", _P), ("win_width", _I32), ("pre", _P), ("winner", _P), ("pool_param", _F),
+                ("lse", _P), ("ws", _P), ("ws_bytes", _SZ), ("part_budget", _SZ)]
 
 
 class GlBwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
                 ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("rec_shift", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
-                ("sched", _P), ("win", _P), ("win_width", _I32), ("g_pre", _P), ("winner", _P), ("dW", _P), ("db", _P),
+                ("sched", _P), ("win", _P), ("win_width", _I32), ("g_pre", _P), ("winner", _P), ("pool_param", _F),
+                ("pre", _P), ("lse", _P), ("dW", _P), ("db", _P),
                 ("dX", _P), ("edges", _P), ("edges_bytes", _SZ),
                 ("ws", _P), ("ws_bytes", _SZ)]
 
@@ -66,7 +67,7 @@ EXPORTS = ("gl_abi_version", "gl_struct_layout", "gl_error_string", "gl_fwd_work
 KERNEL_NAMES = {1: "tile_x_kernel", 2: "fwd_kernel", 3: "fwd_finalize_kernel", 4: "c1t_kernel", 5: "bwd_w_kernel",
                 6: "dx_kernel", 7: "dx_reduce_kernel", 8: "adam_kernel", 9: "edges_build", 10: "fwd_kernel_win",
                 11: "bwd_w_kernel_win", 12: "max_events_dw_kernel", 13: "max_events_dx_kernel",
-                14: "cover_select_kernel", 15: "sched_build_kernel"}
+                14: "cover_select_kernel", 15: "sched_build_kernel", 16: "dx_dense_kernel"}
 
 
 class NativeError(RuntimeError):

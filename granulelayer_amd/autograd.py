@@ -204,14 +204,16 @@ def _grad_buffers(w, b):
 
 
 def _saved_stats(level: LevelSpec, out: Dict[str, torch.Tensor], policy: str) -> Dict[str, torch.Tensor]:
-    """What the forward keeps for backward (autograd.py:366-377): pre, and with save_winners the
-    max-pooling winner ids or the top-k slots."""
+    """What the forward keeps for backward (autograd.py:366-377): pre, with save_winners the
+    max-pooling winner ids or the top-k slots, and softmax-weighted pooling's L2."""
     if policy == "recompute_stats":
         return {}
     keep = {"pre": out["pre"]}
     for key in ("winner", "topk_slot"):
         if policy == "save_winners" and key in out:
             keep[key] = out[key]
+    if level.type == "softmax_weighted" and policy == "minimal_stats":
+        keep["L2"] = out["L2"]  # its backward needs the log-normaliser (autograd.py:375-376)
     return keep
 
 
@@ -260,7 +262,7 @@ class SparsePoolFunction(torch.autograd.Function):
         xc, wc, bc = _compute_operands(x, w, b, ctx.compute_dtype)
         # statistics the backward needs and the policy did not save (autograd.py:246-258): max
         # pooling needs the winners, so minimal_stats recomputes the forward with track_ids
-        need = {"max": "winner", "topk_mean": "topk_slot"}.get(lv.type)
+        need = {"max": "winner", "topk_mean": "topk_slot", "softmax_weighted": "L2"}.get(lv.type)
         recomputed = "pre" not in saved or (need is not None and need not in saved)
         dw_buf, db_buf, use_main = _grad_buffers(w, b)
         B = x.shape[0]

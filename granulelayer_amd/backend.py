@@ -130,13 +130,20 @@ class HipBackend:
         elif track_ids and topk:
             winner, key = torch.empty((B, G, topk), device=x.device, dtype=torch.int32), "topk_slot"
         out = {"pre": pre} if winner is None else {"pre": pre, key: winner}
+        # LogMeanExp / softmax-weighted: the base-2 log-normaliser, the reference's "L2" statistic
+        # (kernels/ops.py:201-209)
+        lse = None
+        if rt.level.type in ("logmeanexp", "softmax_weighted"):
+            lse = torch.empty((B, G), device=x.device, dtype=torch.float32)
+            out["L2"] = lse
         if B == 0:
             return out
         win_lo, win_width = self.windows(rt)
         a = N.GlFwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=L.input_dim, G=G, S=S, K=K, act=act, pool=pool,
                         topk=topk, rec_shift=self.rec_shift(rt), idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, pre=_ptr(pre),
-                        winner=_ptr(winner), part_budget=self.part_budget(rt))
+                        winner=_ptr(winner), pool_param=self.pool_param(rt), lse=_ptr(lse),
+                        part_budget=self.part_budget(rt))
         with torch.cuda.device(x.device):
             need = self.lib.size_query("gl_fwd_workspace", a)
             ws = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)
@@ -144,6 +151,13 @@ class HipBackend:
             self.lib.call("gl_fwd", ctypes.byref(a), ctypes.c_void_p(_stream(x.device)))
         rt.last_info["workspace_bytes"] = need
         return out
+
+    @staticmethod
+    def pool_param(rt) -> float:
+        """The smooth operators' parameter: temperature (LogMeanExp), p (power mean), beta
+        (softmax-weighted); 0 otherwise."""
+        lv = rt.level
+        return {"logmeanexp": lv.temperature, "power_mean": lv.p, "softmax_weighted": lv.beta}.get(lv.type, 0.0)
 
     @staticmethod
     def part_budget(rt) -> int:
@@ -246,6 +260,15 @@ class HipBackend:
             if winner.dtype != torch.int32 or tuple(winner.shape) != shape or winner.device != x.device:
                 raise ValueError(f"{key} must be an int32 {list(shape)} tensor on {x.device}")
             winner = winner.contiguous()
+        # smooth pools: the forward's pooled values and L2 give the backward's coefficients
+        pre, lse = None, None
+        if rt.level.type in ("logmeanexp", "power_mean", "softmax_weighted"):
+            pre = stats.get("pre")
+            lse = stats.get("L2")
+            if pre is None or (rt.level.type == "softmax_weighted" and lse is None):
+                raise ValueError(f"{rt.level.type} backward needs the forward's statistics (pre and L2)")
+            pre = _f32(pre, "pre")
+            lse = None if lse is None else _f32(lse, "L2")
         dx = torch.empty((B, D), device=x.device, dtype=torch.float32)
         if B == 0:
             return dx
@@ -254,7 +277,7 @@ class HipBackend:
         a = N.GlBwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=D, G=G, S=S, K=K, act=act, pool=pool,
                         topk=topk, rec_shift=self.rec_shift(rt), idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, g_pre=_ptr(g_pre),
-                        winner=_ptr(winner),
+                        winner=_ptr(winner), pool_param=self.pool_param(rt), pre=_ptr(pre), lse=_ptr(lse),
                         dW=_ptr(dw_buf), db=_ptr(db_buf), dX=_ptr(dx), edges=_ptr(edges),
                         edges_bytes=edges.numel())
         with torch.cuda.device(x.device):

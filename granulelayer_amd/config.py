@@ -2,9 +2,10 @@
 
 ``LevelSpec`` / ``PoolingConfig`` / ``PhysicalPlan`` keep the reference's names, fields, defaults
 and validation (sparse_pooling/config.py:22-224, 240-421) so existing call sites construct
-them unchanged.  The MI355X hot path executes single-level Mean pooling with a ReLU or identity
-neuron activation, plus ``"sum"`` (Mean x n_g, BASELINE's "sum pooling"); any other operator
-parses exactly as in the reference but is refused by the runtime with a clear error.
+them unchanged.  The MI355X path executes single-level Mean pooling with a ReLU or identity neuron activation,
+``"sum"`` (Mean x n_g, BASELINE's "sum pooling"), Max, Top-K mean, LogMeanExp, power mean and
+softmax-weighted pooling; two-level hierarchies and the GELU activation parse exactly as in the
+reference but are refused by the runtime with a clear error.
 """
 from __future__ import annotations
 
@@ -20,7 +21,7 @@ POOL_ID = {name: i for i, name in enumerate(POOL_TYPES)}
 ACT_ID = {name: i for i, name in enumerate(ACTIVATIONS)}
 
 # operators executed by the HIP path (everything else parses but is refused at run time)
-HIP_POOLS = ("mean", "sum", "max", "topk_mean")
+HIP_POOLS = ("mean", "sum", "max", "topk_mean", "logmeanexp", "power_mean", "softmax_weighted")
 HIP_ACTIVATIONS = ("identity", "relu")
 
 _DEFAULT_ACT = {"max": "identity", "topk_mean": "identity", "mean": "relu", "logmeanexp": "identity",

@@ -95,7 +95,7 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
       long long t[] = {(long long)sizeof(S), OFF(S, X), OFF(S, sxb), OFF(S, x_dtype), OFF(S, B), OFF(S, D), OFF(S, G),
                        OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, rec_shift), OFF(S, idx), OFF(S, W),
                        OFF(S, bias), OFF(S, counts), OFF(S, sched), OFF(S, win), OFF(S, win_width), OFF(S, pre), OFF(S, winner),
-                       OFF(S, ws),
+                       OFF(S, pool_param), OFF(S, lse), OFF(S, ws),
                        OFF(S, ws_bytes), OFF(S, part_budget)};
       for (long long x : t) v[c++] = x;
       break;
@@ -105,7 +105,7 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
       long long t[] = {(long long)sizeof(S), OFF(S, X), OFF(S, sxb), OFF(S, x_dtype), OFF(S, B), OFF(S, D), OFF(S, G),
                        OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, rec_shift), OFF(S, idx), OFF(S, W),
                        OFF(S, bias), OFF(S, counts), OFF(S, sched), OFF(S, win), OFF(S, win_width), OFF(S, g_pre), OFF(S, winner),
-                       OFF(S, dW),
+                       OFF(S, pool_param), OFF(S, pre), OFF(S, lse), OFF(S, dW),
                        OFF(S, db), OFF(S, dX), OFF(S, edges),
                        OFF(S, edges_bytes), OFF(S, ws), OFF(S, ws_bytes)};
       for (long long x : t) v[c++] = x;
@@ -146,7 +146,8 @@ extern "C" const char* gl_error_string(int code) {
   switch (code) {
     case GL_OK: return "ok";
     case GL_ERR_ARG: return "invalid argument, shape or null pointer";
-    case GL_ERR_UNSUPPORTED: return "unsupported variant (fan-in must be 8 or 16; activation identity|relu; pool mean|sum)";
+    case GL_ERR_UNSUPPORTED:
+      return "unsupported variant (fan-in 8 or 16; activation identity|relu; pool mean|sum|max|topk_mean|lme|power|softmax)";
     case GL_ERR_WORKSPACE: return "workspace or output buffer smaller than required";
     case GL_ERR_LDS: return "input tile (D features x 4 tokens x 4 bytes) exceeds the device's LDS per workgroup";
     case GL_ERR_EDGES: return "edge structure does not match this layer shape";

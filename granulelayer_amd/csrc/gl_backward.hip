@@ -562,6 +562,289 @@ __global__ void __launch_bounds__(256) dx_reduce_kernel(const float* __restrict_
   }
 }
 
+// ---- smooth pools (LogMeanExp, power mean, softmax-weighted) ------------------------------------
+// Per (pool, token) coefficients (kernels/ops.py:242-262), transposed to [G][cap] like c1t:
+//   LogMeanExp:       c1 = g_pre, c2 = L2 (from lse, or recovered as pre * scale + log2 n_g)
+//   power mean:       c1 = g_pre / n_g, c2 = 1 / pre (both 0 when pre <= 0)
+//   softmax-weighted: c1 = g_pre, c2 = L2, c3 = pre
+// zero past the chunk's Bc tokens.
+__global__ void __launch_bounds__(256) coef_smooth_kernel(const float* __restrict__ g_pre, const float* __restrict__ pre,
+                                                          const float* __restrict__ lse, const int32_t* __restrict__ counts,
+                                                          float* __restrict__ c1t, float* __restrict__ c2t,
+                                                          float* __restrict__ c3t, int G, int b0, int Bc, int cap, int pool,
+                                                          float scale) {
+  __shared__ float tg[32][33], tp[32][33], tl[32][33];
+  const int g0 = blockIdx.x * 32, bb = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int r = ty; r < 32; r += 8) {
+    const int b = bb + r, g = g0 + tx;
+    const bool in = b < Bc && g < G;
+    const long long i = (long long)(b0 + b) * G + g;
+    tg[r][tx] = in ? g_pre[i] : 0.f;
+    tp[r][tx] = in && pre ? pre[i] : 0.f;
+    tl[r][tx] = in && lse ? lse[i] : 0.f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const int g = g0 + r, b = bb + tx;
+    if (g >= G || b >= cap) continue;
+    const float gp = tg[tx][r], pv = tp[tx][r], L2 = tl[tx][r];
+    const float n = (float)counts[g];
+    float c1 = 0.f, c2 = 0.f, c3 = 0.f;
+    if (b < Bc) {
+      if (pool == GL_POOL_POWER) {
+        c1 = pv > 0.f ? gp / n : 0.f;
+        c2 = pv > 0.f ? 1.f / pv : 0.f;
+      } else {
+        c1 = gp;
+        c2 = lse ? L2 : pv * scale + __builtin_amdgcn_logf(n);
+        c3 = pv;
+      }
+    }
+    const long long o = (long long)g * cap + b;
+    c1t[o] = c1, c2t[o] = c2, c3t[o] = c3;
+  }
+}
+
+// dL/dz of one (token, neuron) of a smooth pool (triton_fused.py:364-399 _dz_from_z)
+template <int OP, int ACT>
+__device__ __forceinline__ float smooth_dz(float z, float c1, float c2, float c3, float scale, float p, int pint) {
+  if constexpr (OP == SM_POW) {
+    if (!(z > 0.f)) return 0.f;
+    const float q = z * c2;  // a / pre
+    float qp;  // q^(p - 1)
+    if (pint == 1) qp = 1.f;
+    else if (pint == 2) qp = q;
+    else if (pint == 4) qp = q * q * q;
+    else if (pint == 8) { const float q2 = q * q, q4 = q2 * q2; qp = q4 * q2 * q; }
+    else qp = q > 0.f ? __builtin_amdgcn_exp2f((p - 1.f) * __builtin_amdgcn_logf(q)) : 0.f;
+    return c1 * qp;
+  } else {
+    const float a = ACT == GL_ACT_RELU ? __builtin_fmaxf(z, 0.f) : z;
+    const float da = ACT == GL_ACT_RELU ? (z > 0.f ? 1.f : 0.f) : 1.f;
+    const float pw = __builtin_amdgcn_exp2f(a * scale - c2);
+    if constexpr (OP == SM_SW) return c1 * pw * (1.f + p * (a - c3)) * da;
+    return c1 * pw * da;
+  }
+}
+
+struct BsK {
+  const float4* __restrict__ xt;
+  const int32_t* __restrict__ idx;
+  const float* __restrict__ W;
+  const float* __restrict__ bias;
+  const int32_t* __restrict__ counts;
+  const float* __restrict__ c1t;
+  const float* __restrict__ c2t;
+  const float* __restrict__ c3t;
+  float* dW;
+  float* db;
+  float* dz;  // [G*S][cap] dL/dz of the chunk's tokens
+  const uint32_t* sched;
+  long long n_chunks;
+  int D, S, cpg, n_tiles, cap, nwin, rs;
+  float scale, pparam;
+  int pint;
+};
+
+// Neuron-stationary recompute pass of a smooth pool: per token tile z, dz = c1 f(z, c2, c3), db and dW
+// accumulated in registers over the chunk's tokens and added to the caller's buffers once; dz of
+// every valid neuron stored for the dX pass.  Token tiles stream through LDS as in bwd_w_kernel.
+template <int K, int NPL, int WAVES, int ACT, int OP, bool DBUF>
+__global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
+  __shared__ float4 xs[DBUF ? 2 * XTILE_DB : XTILE_SB];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  long long chunk = (long long)blockIdx.x * WAVES + wave;
+  const bool active = chunk < p.n_chunks;
+  if (!active) chunk = p.n_chunks - 1;
+  const long long g = chunk / p.cpg;
+  const int s_lo = (int)(chunk % p.cpg) * 64 * NPL;
+  const int n_g = p.counts[g];
+  unsigned addr[NPL][K];
+  float w[NPL][K], dw[NPL][K];
+  float bias[NPL], dbv[NPL];
+  int slot[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    uint32_t order;
+    const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, lane, order);
+    slot[j] = s < n_g ? s : -1;
+    const long long n = g * p.S + (s < p.S ? s : p.S - 1);
+#pragma unroll
+    for (int ks = 0; ks < K; ++ks) {
+      const int k = sched_k<K>(order, ks);
+      int d = rec_index(p.idx, n, k, K, p.rs);
+      d = (d < 0 || s >= n_g) ? 0 : (d >= p.D ? p.D - 1 : d);
+      addr[j][ks] = (unsigned)d * 16u;
+      w[j][ks] = s < n_g ? p.W[n * K + k] : 0.f;
+      dw[j][ks] = 0.f;
+    }
+    bias[j] = s < n_g ? p.bias[n] : 0.f;
+    dbv[j] = 0.f;
+  }
+  const float* c1row = p.c1t + g * p.cap;
+  const float* c2row = p.c2t + g * p.cap;
+  const float* c3row = p.c3t + g * p.cap;
+  constexpr int NT = WAVES * 64;
+  if constexpr (DBUF) {
+    dma_tile(p.xt, xs, p.D, NT);
+    stage_wait();
+    __syncthreads();
+  }
+  for (int t = 0; t < p.n_tiles; ++t) {
+    const char* xb;
+    if constexpr (DBUF) {
+      const int cur = t & 1;
+      if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xs + (cur ^ 1) * XTILE_DB, p.D, NT);
+      xb = reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16);
+    } else {
+      __syncthreads();
+      dma_tile(p.xt + (long long)t * p.D, xs, p.D, NT);
+      stage_wait();
+      __syncthreads();
+      xb = reinterpret_cast<const char*>(xs);
+    }
+    const float4 c1 = ld_uniform4(c1row, t * BT), c2 = ld_uniform4(c2row, t * BT), c3 = ld_uniform4(c3row, t * BT);
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      float4 xc[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) xc[k] = *reinterpret_cast<const float4*>(xb + addr[j][k]);
+      float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
+        z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
+        z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
+        z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
+      }
+      const bool v = slot[j] >= 0;
+      const float d0 = v ? smooth_dz<OP, ACT>(z0, c1.x, c2.x, c3.x, p.scale, p.pparam, p.pint) : 0.f;
+      const float d1 = v ? smooth_dz<OP, ACT>(z1, c1.y, c2.y, c3.y, p.scale, p.pparam, p.pint) : 0.f;
+      const float d2 = v ? smooth_dz<OP, ACT>(z2, c1.z, c2.z, c3.z, p.scale, p.pparam, p.pint) : 0.f;
+      const float d3 = v ? smooth_dz<OP, ACT>(z3, c1.w, c2.w, c3.w, p.scale, p.pparam, p.pint) : 0.f;
+      dbv[j] = dbv[j] + d0 + d1 + d2 + d3;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        float a = dw[j][k];
+        a = __builtin_fmaf(d0, xc[k].x, a);
+        a = __builtin_fmaf(d1, xc[k].y, a);
+        a = __builtin_fmaf(d2, xc[k].z, a);
+        a = __builtin_fmaf(d3, xc[k].w, a);
+        dw[j][k] = a;
+      }
+      if (active && v)
+        *reinterpret_cast<float4*>(p.dz + (g * p.S + slot[j]) * (long long)p.cap + t * BT) = make_float4(d0, d1, d2, d3);
+    }
+    if constexpr (DBUF) {
+      stage_wait();
+      __syncthreads();
+    }
+  }
+  if (!active) return;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    uint32_t order;
+    const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, opaque(lane), order);
+    if (s >= n_g) continue;
+    const long long n = g * p.S + s;
+#pragma unroll
+    for (int ks = 0; ks < K; ++ks) p.dW[n * K + sched_k<K>(order, ks)] += dw[j][ks];
+    p.db[n] += dbv[j];
+  }
+}
+
+// dX of a smooth pool: dX[b, d] = sum over edges (n, k) -> d of dz[b, n] W[n, k], walking the
+// input-major edges like dx_kernel (one wave per feature range, unit range and token slice); per
+// edge every lane reads its T tokens of the neuron's dz row.
+template <int K, int T>
+__global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __restrict__ dz) {
+  const int lane = threadIdx.x;
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7;
+  const int loc = bid >> 3;
+  const int F = loc % p.FR;
+  const int rest = loc / p.FR;
+  const int ql = rest % p.QL;
+  const int tc = rest / p.QL;
+  const int q = ql * 8 + xcd;
+  const int u_lo = q * p.UQ;
+  const int u_hi = min(u_lo + p.UQ, p.U);
+  int lo = (int)p.seg_ptr[F], hi = (int)p.seg_ptr[F + 1];
+  {
+    int a = lo, b = hi;
+    while (a < b) {
+      int mid = (a + b) >> 1;
+      if (p.seg_unit[mid] < u_lo) a = mid + 1; else b = mid;
+    }
+    lo = a;
+    b = hi;
+    while (a < b) {
+      int mid = (a + b) >> 1;
+      if (p.seg_unit[mid] < u_hi) a = mid + 1; else b = mid;
+    }
+    hi = a;
+  }
+  float acc[FW][T];
+#pragma unroll
+  for (int f = 0; f < FW; ++f)
+#pragma unroll
+    for (int j = 0; j < T; ++j) acc[f][j] = 0.f;
+  const int tok0 = tc * 64 * T + T * lane;
+  __shared__ uint2 st[64];  // (record, weight bits) of the chunk's edges
+  for (int si = lo; si < hi; ++si) {
+    const int u = p.seg_unit[si];
+    const long long nb = (long long)(u / p.P) * p.S + (long long)(u % p.P) * US;  // first neuron of the unit
+    const unsigned e_end = p.seg_begin[si + 1];
+    for (unsigned e0 = p.seg_begin[si]; e0 < e_end; e0 += 64) {
+      const int n = (int)min(e_end - e0, 64u);
+      if (lane < n) {
+        const unsigned rec = p.rec[e0 + lane];
+        const float wv = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.W + nb * K) +
+                                                          (rec & REC_OFF_MASK));
+        st[lane] = make_uint2(rec, __float_as_uint(wv));
+      }
+      __syncthreads();
+      for (int i = 0; i < n; ++i) {
+        uint2 e = st[i];
+        e.x = __builtin_amdgcn_readfirstlane(e.x);  // the same edge in every lane
+        e.y = __builtin_amdgcn_readfirstlane(e.y);
+        const int f = (int)((e.x >> REC_F_SHIFT) & REC_F_MASK);
+        const long long nn = nb + ((e.x & REC_OFF_MASK) >> (K == 8 ? 5 : 6));
+        const float wv = __uint_as_float(e.y);
+        const float* row = dz + nn * p.cap + tok0;
+        float v[T];
+        if constexpr (T == 4) {
+          const float4 x = *reinterpret_cast<const float4*>(row);
+          v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
+        } else if constexpr (T == 2) {
+          const float2 x = *reinterpret_cast<const float2*>(row);
+          v[0] = x.x, v[1] = x.y;
+        } else {
+          v[0] = row[0];
+        }
+#pragma unroll
+        for (int x = 0; x < FW; ++x)  // f is wave-uniform: one branch taken, accumulators stay in registers
+          if (x == f) {
+#pragma unroll
+            for (int j = 0; j < T; ++j) acc[x][j] = __builtin_fmaf(wv, v[j], acc[x][j]);
+          }
+      }
+      __syncthreads();
+    }
+  }
+  float* out = p.part + (long long)q * p.D * p.cap;
+#pragma unroll
+  for (int f = 0; f < FW; ++f) {
+    const int d = F * FW + f;
+    if (d < p.D) {
+#pragma unroll
+      for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j] = acc[f][j];
+    }
+  }
+}
+
 // ---- host side -------------------------------------------------------------------------------
 // dW pass: 4 neurons per lane in 12 waves at K = 8 (3 waves per SIMD), 3 in 8 waves at K = 16; a
 // workgroup covers 3072 neurons per staged token tile either way
@@ -571,12 +854,22 @@ constexpr int bwd_waves(int K) { return K == 8 ? 12 : 8; }
 struct BwdPlan {
   int bc_max, npl, waves, cpg, tiles_max, cap_max, rs_max, FR, P, U, Q, QL, UQ;
   long long n_chunks, e_max, nseg_max;
-  size_t xt_bytes, c1_bytes, mask_bytes, part_bytes, edges_bytes;
+  size_t xt_bytes, c1_bytes, mask_bytes, part_bytes, edges_bytes, dz_bytes;
 };
 
-static BwdPlan bwd_plan(int B, int D, int G, int S, int K) {
+// smooth pools keep dz [G*S][cap] of one token chunk: chunks of at most 1024 tokens whose dz fits
+// SMOOTH_DZ_BUDGET (at least 64 tokens)
+constexpr size_t SMOOTH_DZ_BUDGET = 8ull << 30;
+static bool is_smooth(int pool) { return pool == GL_POOL_LME || pool == GL_POOL_POWER || pool == GL_POOL_SOFTMAX; }
+
+static BwdPlan bwd_plan(int B, int D, int G, int S, int K, bool smooth = false) {
   BwdPlan q;
   q.bc_max = B < BWD_TOKEN_CHUNK ? B : BWD_TOKEN_CHUNK;
+  if (smooth) {
+    long long c = (long long)(SMOOTH_DZ_BUDGET / ((size_t)G * S * 4)) / 64 * 64;
+    if (c < 64) c = 64;
+    if (c < q.bc_max) q.bc_max = (int)c;
+  }
   q.npl = bwd_npl(K);
   q.waves = bwd_waves(K);
   q.cpg = ceil_div(S, 64 * q.npl);
@@ -606,6 +899,8 @@ static BwdPlan bwd_plan(int B, int D, int G, int S, int K) {
   q.xt_bytes = (size_t)round_up((long long)q.tiles_max * D * 16, 256);
   q.c1_bytes = (size_t)round_up((long long)G * q.cap_max * 4, 256);
   q.mask_bytes = (size_t)round_up((long long)G * S * q.rs_max * 4, 256);
+  q.dz_bytes = smooth ? (size_t)round_up((long long)G * S * q.cap_max * 4, 256) : 0;
+  if (smooth) q.mask_bytes = 0;
   q.part_bytes = (size_t)round_up((long long)q.Q * D * q.cap_max * 4, 256);
   q.e_max = (long long)G * S * K;
   q.nseg_max = (long long)q.FR * q.U < q.e_max ? (long long)q.FR * q.U : q.e_max;
@@ -669,6 +964,41 @@ static int launch_dx(int K, int T, const DxK& k, hipStream_t s) {
   return K == 8 ? launch_dx_k<8>(T, k, s) : launch_dx_k<16>(T, k, s);
 }
 
+template <int K, int ACT, int OP>
+static int launch_bwd_smooth_k(const BsK& k, hipStream_t s) {
+  constexpr int NPL = 4, WAVES = 8;
+  auto fn = k.D <= XTILE_DB ? bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, true> : bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, false>;
+  GL_LAUNCH(GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)), dim3(WAVES * 64), 0, s, k);
+  GL_CHECK_LAUNCH();
+  return 0;
+}
+
+template <int K>
+static int launch_bwd_smooth_kk(int pool, int act, const BsK& k, hipStream_t s) {
+  if (pool == GL_POOL_POWER) return launch_bwd_smooth_k<K, GL_ACT_RELU, SM_POW>(k, s);
+  if (pool == GL_POOL_LME)
+    return act == GL_ACT_RELU ? launch_bwd_smooth_k<K, GL_ACT_RELU, SM_LME>(k, s) : launch_bwd_smooth_k<K, GL_ACT_IDENTITY, SM_LME>(k, s);
+  return act == GL_ACT_RELU ? launch_bwd_smooth_k<K, GL_ACT_RELU, SM_SW>(k, s) : launch_bwd_smooth_k<K, GL_ACT_IDENTITY, SM_SW>(k, s);
+}
+
+template <int K, int T>
+static int launch_dx_dense_kt(const DxK& k, const float* dz, hipStream_t s) {
+  GL_LAUNCH(GL_KERNEL_DX_DENSE, (dx_dense_kernel<K, T>), dim3((unsigned)(8LL * k.FR * k.QL * k.n_tc)), dim3(64), 0, s, k,
+            dz);
+  GL_CHECK_LAUNCH();
+  return 0;
+}
+
+static int launch_dx_dense(int K, int T, const DxK& k, const float* dz, hipStream_t s) {
+  if (K == 8) return T == 1 ? launch_dx_dense_kt<8, 1>(k, dz, s) : (T == 2 ? launch_dx_dense_kt<8, 2>(k, dz, s) : launch_dx_dense_kt<8, 4>(k, dz, s));
+  return T == 1 ? launch_dx_dense_kt<16, 1>(k, dz, s) : (T == 2 ? launch_dx_dense_kt<16, 2>(k, dz, s) : launch_dx_dense_kt<16, 4>(k, dz, s));
+}
+
+static float smooth_scale_b(int pool, float param) {
+  const float log2e = 1.4426950408889634f;
+  return pool == GL_POOL_LME ? log2e / param : (pool == GL_POOL_SOFTMAX ? log2e * param : 1.f);
+}
+
 }  // namespace gl
 
 using namespace gl;
@@ -677,12 +1007,16 @@ extern "C" int gl_bwd_workspace(const GlBwdArgs* a, size_t* bytes) {
   if (!a || !bytes) return GL_ERR_ARG;
   GL_TRY(check_layer(a->B, a->D, a->G, a->S, a->K, a->act, a->pool, a->X, a->idx, a->W, a->bias, a->counts,
                      a->x_dtype));
-  BwdPlan q = bwd_plan(a->B, a->D, a->G, a->S, a->K);
+  const bool smooth = is_smooth(a->pool);
+  BwdPlan q = bwd_plan(a->B, a->D, a->G, a->S, a->K, smooth);
   GL_TRY(check_topk(a->pool, a->topk, a->S));
   GL_TRY(check_rec_shift(a->rec_shift, a->S, a->sched));
-  // max / top-k pooling: the transposed selected slots, laid out like c1t (times k for top-k)
+  GL_TRY(check_smooth(a->pool, a->pool_param, a->act));
+  // max / top-k pooling: the transposed selected slots, laid out like c1t (times k for top-k);
+  // smooth pools: c2t and c3t beside c1t
   const size_t kpe = a->pool == GL_POOL_TOPK_MEAN ? (size_t)a->topk : (a->pool == GL_POOL_MAX ? 1 : 0);
-  *bytes = q.xt_bytes + q.c1_bytes + q.mask_bytes + q.part_bytes + kpe * q.c1_bytes;
+  *bytes = q.xt_bytes + q.c1_bytes + q.mask_bytes + q.part_bytes + kpe * q.c1_bytes + q.dz_bytes +
+           (smooth ? 2 * q.c1_bytes : 0);
   return 0;
 }
 
@@ -700,7 +1034,10 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
   edge_layout(a->D, a->G, a->S, a->K, &h, &edge_bytes);
   if (a->edges_bytes < edge_bytes) return GL_ERR_EDGES;
   hipStream_t s = (hipStream_t)stream;
-  BwdPlan q = bwd_plan(a->B, a->D, a->G, a->S, a->K);
+  const bool smooth = is_smooth(a->pool);
+  if (smooth && (!a->pre && !(a->pool == GL_POOL_LME && a->lse))) return GL_ERR_ARG;  // coefficients need pre
+  if (a->pool == GL_POOL_SOFTMAX && !a->lse) return GL_ERR_ARG;
+  BwdPlan q = bwd_plan(a->B, a->D, a->G, a->S, a->K, smooth);
   char* ws = (char*)a->ws;
   float4* xt = (float4*)ws;
   float* c1t = (float*)(ws + q.xt_bytes);
@@ -715,6 +1052,31 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     const int T = dx_slots(Bc);
     const int cap = dx_cap(Bc);
     GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles, xt, s));
+    if (smooth) {  // coefficients, recompute pass (dW, db, dz), dX from dz
+      float* c2t = (float*)(ws + q.xt_bytes + q.c1_bytes + q.part_bytes);
+      float* c3t = (float*)((char*)c2t + q.c1_bytes);
+      float* dz = (float*)((char*)c3t + q.c1_bytes);
+      const float scale = smooth_scale_b(a->pool, a->pool_param);
+      GL_LAUNCH(GL_KERNEL_C1T, coef_smooth_kernel, dim3((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(cap, 32)),
+                dim3(256), 0, s, a->g_pre, a->pre, a->lse, a->counts, c1t, c2t, c3t, a->G, b0, Bc, cap, a->pool, scale);
+      GL_CHECK_LAUNCH();
+      const int pint = a->pool == GL_POOL_POWER &&
+                               (a->pool_param == 1.f || a->pool_param == 2.f || a->pool_param == 4.f || a->pool_param == 8.f)
+                           ? (int)a->pool_param
+                           : 0;
+      const BsK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, c2t, c3t, a->dW, a->db, dz, a->sched, q.n_chunks, a->D,
+                   a->S, q.cpg, n_tiles, cap, ceil_div(a->S, SCHED_WIN), a->rec_shift, scale, a->pool_param, pint};
+      GL_TRY(a->K == 8 ? launch_bwd_smooth_kk<8>(a->pool, a->act, bk, s) : launch_bwd_smooth_kk<16>(a->pool, a->act, bk, s));
+      const long long NS = (long long)a->G * a->S;
+      DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
+             (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, nullptr, a->W, part,
+             NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * T)};
+      GL_TRY(launch_dx_dense(a->K, T, dk, dz, s));
+      GL_LAUNCH(GL_KERNEL_DX_REDUCE, dx_reduce_kernel, dim3((unsigned)ceil_div(a->D, 32), (unsigned)ceil_div(Bc, 32)),
+                dim3(256), 0, s, part, a->dX, a->D, cap, q.Q, b0, Bc);
+      GL_CHECK_LAUNCH();
+      continue;
+    }
     const int kpe = a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1;
     GL_LAUNCH(GL_KERNEL_C1T, c1t_kernel, dim3((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(cap, 32)), dim3(256), 0, s,
                        a->g_pre, a->counts, c1t, a->G, b0, Bc, cap, a->pool, a->topk, kpe == 1 ? a->winner : nullptr,

@@ -283,4 +283,37 @@ __device__ __forceinline__ void wave_max4(float a0, float a1, float a2, float a3
   vmax_pair(m, s, __uint_as_float(c32[1]), (int)u32[1]);
 }
 
+// ---- smooth pooling states (LogMeanExp, power mean, softmax-weighted) ---------------------------
+// LogMeanExp / softmax-weighted keep (m, s, t) per token: m the largest u = a * scale, s = sum 2^(u - m),
+// t = sum 2^(u - m) a (softmax-weighted only); power mean keeps m the largest a and s = sum (a / m)^p.
+// Two states merge by rescaling to the larger m (kernels/triton_fused.py:180-222 restated as a
+// pairwise merge); an empty state has m = -inf (exp2 forms) or m = 0 (power).
+constexpr int SM_LME = 0, SM_POW = 1, SM_SW = 2;
+
+// q^p for q >= 0: exact products for p in {1, 2, 4, 8} (pint), else exp2(p log2 q)
+__device__ __forceinline__ float pow_p(float q, float p, int pint) {
+  if (pint == 1) return q;
+  if (pint == 2) return q * q;
+  if (pint == 4) { const float q2 = q * q; return q2 * q2; }
+  if (pint == 8) { const float q2 = q * q, q4 = q2 * q2; return q4 * q4; }
+  return q > 0.f ? __builtin_amdgcn_exp2f(p * __builtin_amdgcn_logf(q)) : 0.f;
+}
+
+template <int OP>
+__device__ __forceinline__ void sm_merge(float& m, float& s, float& t, float m2, float s2, float t2, float p, int pint) {
+  if constexpr (OP == SM_POW) {
+    const float M = __builtin_fmaxf(m, m2);
+    const float inv = M > 0.f ? 1.f / M : 0.f;
+    s = M > 0.f ? s * pow_p(m * inv, p, pint) + s2 * pow_p(m2 * inv, p, pint) : 0.f;
+    m = M;
+  } else {
+    const float M = __builtin_fmaxf(m, m2);
+    const float base = M == -__builtin_inff() ? 0.f : M;  // both empty: keep s = t = 0
+    const float r1 = __builtin_amdgcn_exp2f(m - base), r2 = __builtin_amdgcn_exp2f(m2 - base);
+    s = s * r1 + s2 * r2;
+    if constexpr (OP == SM_SW) t = t * r1 + t2 * r2;
+    m = M;
+  }
+}
+
 }  // namespace gl

@@ -61,6 +61,8 @@ struct FwdK {
   int D, S, cpg, n_tiles, b_pad, nwin;
   int G, ww, npw;         // window staging: pools, padded window width, pools per workgroup
   int rs;                 // log2 slots per shared index record
+  float scale, pparam;    // smooth pools: u = a * scale (LogMeanExp / softmax-weighted); p (power mean)
+  int pint;               // power mean: p when it is 1, 2, 4 or 8 (exact products), else 0
 };
 
 // One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
@@ -314,8 +316,127 @@ __device__ __forceinline__ void fwd_tile_topk(const char* xsb, const unsigned (&
   }
 }
 
+// wave_sum4's reduce-scatter for smooth pooling states: every lane ends with the wave's merged
+// (m, s, t) of token wave_sum4_token(lane).  Merges are commutative bit for bit, and the two swap
+// steps hand both lanes of a pair the same two operands, so the result does not depend on the lane.
+template <int OP>
+__device__ __forceinline__ void wave_merge4(const float (&m)[4], const float (&s)[4], const float (&t)[4], int lane,
+                                            float p, int pint, float& mo, float& so, float& to) {
+  const bool odd = lane & 1, hi = lane & 2;
+  float m0 = odd ? m[2] : m[0], s0 = odd ? s[2] : s[0], t0 = odd ? t[2] : t[0];
+  float m1 = odd ? m[3] : m[1], s1 = odd ? s[3] : s[1], t1 = odd ? t[3] : t[1];
+  sm_merge<OP>(m0, s0, t0, dpp<0xB1>(odd ? m[0] : m[2]), dpp<0xB1>(odd ? s[0] : s[2]), dpp<0xB1>(odd ? t[0] : t[2]), p,
+               pint);  // quad_perm(1,0,3,2)
+  sm_merge<OP>(m1, s1, t1, dpp<0xB1>(odd ? m[1] : m[3]), dpp<0xB1>(odd ? s[1] : s[3]), dpp<0xB1>(odd ? t[1] : t[3]), p,
+               pint);
+  float cm = hi ? m1 : m0, cs = hi ? s1 : s0, ct = hi ? t1 : t0;
+  sm_merge<OP>(cm, cs, ct, dpp<0x4E>(hi ? m0 : m1), dpp<0x4E>(hi ? s0 : s1), dpp<0x4E>(hi ? t0 : t1), p,
+               pint);  // quad_perm(2,3,0,1)
+  sm_merge<OP>(cm, cs, ct, dpp<0x124>(cm), dpp<0x124>(cs), dpp<0x124>(ct), p, pint);  // row_ror:4
+  sm_merge<OP>(cm, cs, ct, dpp<0x128>(cm), dpp<0x128>(cs), dpp<0x128>(ct), p, pint);  // row_ror:8
+  {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(cm), __float_as_uint(cm), false, false);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(cs), __float_as_uint(cs), false, false);
+    const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(ct), __float_as_uint(ct), false, false);
+    cm = __uint_as_float(a[0]), cs = __uint_as_float(b[0]), ct = __uint_as_float(c[0]);
+    sm_merge<OP>(cm, cs, ct, __uint_as_float(a[1]), __uint_as_float(b[1]), __uint_as_float(c[1]), p, pint);
+  }
+  {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(cm), __float_as_uint(cm), false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(cs), __float_as_uint(cs), false, false);
+    const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(ct), __float_as_uint(ct), false, false);
+    cm = __uint_as_float(a[0]), cs = __uint_as_float(b[0]), ct = __uint_as_float(c[0]);
+    sm_merge<OP>(cm, cs, ct, __uint_as_float(a[1]), __uint_as_float(b[1]), __uint_as_float(c[1]), p, pint);
+  }
+  mo = cm, so = cs, to = ct;
+}
+
+// Smooth pooling tile (LogMeanExp, power mean, softmax-weighted; pytorch_reference.py:80-100): z of
+// the lane's neurons for the tile's 4 tokens, then per token the lane's state over its valid neurons
+// (vmask bit j: neuron j valid) -- the largest u (or a), the sum of 2^(u - m) (or (a / m)^p) and, for
+// softmax-weighted, of 2^(u - m) a -- merged over the wave; lanes 0-3 store (m, s, t) per token.
+template <int K, int NPL, int ACT, bool FAR, int OP, int RA = (K == 8 ? 4 : 8)>
+__device__ __forceinline__ void fwd_tile_smooth(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+                                                const float (&bias)[NPL], unsigned vmask, float* out, bool store,
+                                                int lane, float scale, float p, int pint) {
+  float z[NPL][4];
+  float4 xc[K];
+#pragma unroll
+  for (int k = 0; k < RA; ++k) xc[k] = lds_x<FAR>(xsb, addr[0][k]);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+#pragma unroll
+    for (int k = RA; k < K; ++k) xc[k] = lds_x<FAR>(xsb, addr[j][k]);
+    float4 xn[RA];
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xn[k] = lds_x<FAR>(xsb, addr[j + 1][k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
+      z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
+      z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
+      z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
+    }
+    z[j][0] = z0, z[j][1] = z1, z[j][2] = z2, z[j][3] = z3;
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xc[k] = xn[k];
+    }
+  }
+  float m[4], s[4], t[4];
+  const float ninf = -__builtin_inff();
+#pragma unroll
+  for (int tk = 0; tk < 4; ++tk) {
+    if constexpr (OP == SM_POW) {
+      float a[NPL], mx = 0.f;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        a[j] = ((vmask >> j) & 1u) ? __builtin_fmaxf(z[j][tk], 0.f) : 0.f;
+        mx = __builtin_fmaxf(mx, a[j]);
+      }
+      const float inv = mx > 0.f ? 1.f / mx : 0.f;
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) acc += pow_p(a[j] * inv, p, pint);
+      m[tk] = mx, s[tk] = acc, t[tk] = 0.f;
+    } else {
+      float a[NPL], u[NPL], mx = ninf;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        const bool v = (vmask >> j) & 1u;
+        const float aj = ACT == GL_ACT_RELU ? __builtin_fmaxf(z[j][tk], 0.f) : z[j][tk];
+        a[j] = v ? aj : 0.f;
+        u[j] = v ? aj * scale : ninf;
+        mx = __builtin_fmaxf(mx, u[j]);
+      }
+      const float base = mx == ninf ? 0.f : mx;
+      float acc = 0.f, acct = 0.f;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        const float e = __builtin_amdgcn_exp2f(u[j] - base);
+        acc += e;
+        if constexpr (OP == SM_SW) acct = __builtin_fmaf(e, a[j], acct);
+      }
+      m[tk] = mx, s[tk] = acc, t[tk] = acct;
+    }
+  }
+  float mo, so, to;
+  wave_merge4<OP>(m, s, t, lane, p, pint, mo, so, to);
+  if (store && lane < 4) {
+    float* o = out + wave_sum4_token(lane) * 3;
+    o[0] = mo, o[1] = so, o[2] = to;
+  }
+}
+
 // pool kinds of the forward tile
-constexpr int PK_SUM = 0, PK_MAX = 1, PK_TOPK = 2;
+constexpr int PK_SUM = 0, PK_MAX = 1, PK_TOPK = 2, PK_LME = 3, PK_POW = 4, PK_SW = 5;
+constexpr bool pk_smooth(int pk) { return pk >= PK_LME; }
+constexpr int pk_sm_op(int pk) { return pk == PK_LME ? SM_LME : (pk == PK_POW ? SM_POW : SM_SW); }
 
 // sum / mean, max or top-k tile
 template <int K, int NPL, int ACT, bool FAR, int PK>
@@ -325,6 +446,18 @@ __device__ __forceinline__ void fwd_tile_any(const char* xsb, const unsigned (&a
   if constexpr (PK == PK_MAX) fwd_tile_max<K, NPL, ACT, FAR>(xsb, addr, w, bias, slot, out, oslot, store, lane);
   else if constexpr (PK == PK_TOPK) fwd_tile_topk<K, NPL, ACT, FAR>(xsb, addr, w, bias, slot, out, oslot, k, store, lane);
   else fwd_tile<K, NPL, ACT, FAR>(xsb, addr, w, bias, out, store, lane);
+}
+
+// smooth pools: the tile needs the validity bits and the operator's parameters
+template <int K, int NPL, int ACT, bool FAR, int PK>
+__device__ __forceinline__ void fwd_tile_dispatch(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+                                                  const float (&bias)[NPL], const int (&slot)[NPL], unsigned vmask,
+                                                  float* out, int* oslot, int k, bool store, int lane, const FwdK& p) {
+  if constexpr (pk_smooth(PK))
+    fwd_tile_smooth<K, NPL, ACT, FAR, pk_sm_op(PK)>(xsb, addr, w, bias, vmask, out, store, lane, p.scale, p.pparam,
+                                                    p.pint);
+  else
+    fwd_tile_any<K, NPL, ACT, FAR, PK>(xsb, addr, w, bias, slot, out, oslot, k, store, lane);
 }
 
 template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, int PK = PK_SUM>
@@ -345,6 +478,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   float w[NPL][K];
   float bias[NPL];
   int slot[NPL];  // max / top-k pooling: pool slot of each neuron
+  unsigned vmask = 0u;  // smooth pools: bit j set when neuron j is a valid slot
   // window staging: this wave's pool is slot pk of the workgroup's staged pools, window start lo
   const int g_first = (int)((long long)blockIdx.x * WAVES / p.cpg);
   const int pk = WS ? (int)(g - g_first) : 0;
@@ -365,8 +499,9 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       w[j][ks] = valid ? wl : 0.f;
     }
     const float bl = p.bias[n];
-    bias[j] = valid ? bl : (PK != PK_SUM ? -__builtin_inff() : 0.f);
+    bias[j] = valid ? bl : ((PK == PK_MAX || PK == PK_TOPK) ? -__builtin_inff() : 0.f);
     slot[j] = s;
+    vmask |= (unsigned)valid << j;
   }
 
   // Token tiles reach LDS by LDS-DMA (dma_tile).  DBUF: tile t + 1 is loaded into the other
@@ -375,9 +510,9 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   // from inline asm: a copy the compiler sees in flight during the gather makes it wait for all
   // LDS reads (lgkmcnt(0)) before each use instead of only the ones the use needs.
   constexpr int NT = WAVES * 64;
-  const int kp = PK == PK_TOPK ? p.topk : 1;  // candidates per token
+  const int kp = PK == PK_TOPK ? p.topk : (pk_smooth(PK) ? 3 : 1);  // floats per token: candidates or state
   float* out = p.part + chunk * p.b_pad * kp;
-  int* oslot = PK != PK_SUM ? p.pslot + chunk * p.b_pad * kp : nullptr;
+  int* oslot = (PK == PK_MAX || PK == PK_TOPK) ? p.pslot + chunk * p.b_pad * kp : nullptr;
   const bool store = active;
   if constexpr (WS) {
     // window staging: WS_TILES tiles per stage and barrier; tile t at slot (t mod 2 WS_TILES) * nsl
@@ -394,8 +529,8 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       const int tn = p.n_tiles - t0 < WS_TILES ? p.n_tiles - t0 : WS_TILES;
       for (int tt = 0; tt < tn; ++tt) {
         const int t = t0 + tt;
-        fwd_tile_any<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT * kp,
-                                             oslot + t * BT * kp, kp, store, lane);
+        fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
+                                                  out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
         // next tile's slot; after the last tile of region 1 back to region 0
         const unsigned step = (t & (2 * WS_TILES - 1)) == 2 * WS_TILES - 1 ? tstep - 2u * WS_TILES * tstep : tstep;
 #pragma unroll
@@ -412,14 +547,14 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       stage_wait();
       __syncthreads();  // tile t is in xa; every wave is done with xb (tile t - 1)
       if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xb, p.D, NT);
-      fwd_tile_any<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT * kp,
-                                           oslot + t * BT * kp, kp, store, lane);
+      fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
+                                                out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
       if (t + 1 < p.n_tiles) {
         stage_wait();
         __syncthreads();  // tile t + 1 is in xb; every wave is done with xa
         if (t + 2 < p.n_tiles) dma_tile(p.xt + (long long)(t + 2) * p.D, xa, p.D, NT);
-        fwd_tile_any<K, NPL, ACT, true, PK>(reinterpret_cast<const char*>(xb), addr, w, bias, slot,
-                                            out + (t + 1) * BT * kp, oslot + (t + 1) * BT * kp, kp, store, lane);
+        fwd_tile_dispatch<K, NPL, ACT, true, PK>(reinterpret_cast<const char*>(xb), addr, w, bias, slot, vmask,
+                                                 out + (t + 1) * BT * kp, oslot + (t + 1) * BT * kp, kp, store, lane, p);
       }
     }
   } else {
@@ -428,8 +563,8 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       dma_tile(p.xt + (long long)t * p.D, xa, p.D, NT);
       stage_wait();
       __syncthreads();
-      fwd_tile_any<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, out + t * BT * kp,
-                                           oslot + t * BT * kp, kp, store, lane);
+      fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
+                                                out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
     }
   }
 }
@@ -599,6 +734,37 @@ __global__ void __launch_bounds__(256) fwd_finalize_top8_kernel(const float* __r
   pre[i] = sum / (float)kk;
 }
 
+// Smooth pools: merge the pool's cpg chunk states in a fixed order, then pre and L2 = m + log2 s
+// (kernels/ops.py:201-219): LogMeanExp pre = (L2 - log2 n_g) / scale, softmax-weighted pre = t / s,
+// power mean pre = m (s / n_g)^(1/p) (0 when every activation is 0).  One thread per (token, pool).
+template <int OP>
+__global__ void __launch_bounds__(256) fwd_finalize_smooth_kernel(const float* __restrict__ part,
+                                                                  const int32_t* __restrict__ counts, float* __restrict__ pre,
+                                                                  float* __restrict__ lse, int B, int G, int cpg, int b_pad,
+                                                                  float scale, float p, int pint) {
+  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long long)B * G) return;
+  const int b = (int)(t % B), g = (int)(t / B);
+  const float* q = part + ((long long)g * cpg * b_pad + b) * 3;
+  float m = q[0], sv = q[1], tv = q[2];
+  for (int c = 1; c < cpg; ++c) {
+    const float* r = q + (long long)c * b_pad * 3;
+    sm_merge<OP>(m, sv, tv, r[0], r[1], r[2], p, pint);
+  }
+  const float n = (float)counts[g];
+  const long long i = (long long)b * G + g;
+  if constexpr (OP == SM_POW) {
+    float v = 0.f;
+    if (m > 0.f) v = pint == 1 ? m * (sv / n) : m * __builtin_amdgcn_exp2f(__builtin_amdgcn_logf(sv / n) / p);
+    pre[i] = v;
+    if (lse) lse[i] = 0.f;
+  } else {
+    const float L2 = m + __builtin_amdgcn_logf(sv);
+    pre[i] = OP == SM_LME ? (L2 - __builtin_amdgcn_logf(n)) / scale : tv / sv;
+    if (lse) lse[i] = L2;
+  }
+}
+
 // ---- host side -------------------------------------------------------------------------------
 // 4 neurons per lane; 16 waves per workgroup at K = 8 (4 waves per SIMD, 128 VGPRs), 8 at K = 16
 // (2 per SIMD: the parameters of 4 neurons of fan-in 16 take twice the registers).  Max pooling
@@ -608,7 +774,28 @@ constexpr int FWD_NPL = 4;
 constexpr int fwd_waves(int K, int pk = PK_SUM) {
   return K == 8 ? (pk == PK_SUM ? 16 : (pk == PK_MAX ? 12 : 8)) : (pk == PK_SUM ? 8 : 4);
 }
-static int pool_kind(int pool) { return pool == GL_POOL_MAX ? PK_MAX : (pool == GL_POOL_TOPK_MEAN ? PK_TOPK : PK_SUM); }
+static int pool_kind(int pool) {
+  switch (pool) {
+    case GL_POOL_MAX: return PK_MAX;
+    case GL_POOL_TOPK_MEAN: return PK_TOPK;
+    case GL_POOL_LME: return PK_LME;
+    case GL_POOL_POWER: return PK_POW;
+    case GL_POOL_SOFTMAX: return PK_SW;
+    default: return PK_SUM;
+  }
+}
+static bool pool_smooth(int pool) { return pool == GL_POOL_LME || pool == GL_POOL_POWER || pool == GL_POOL_SOFTMAX; }
+
+// smooth pools: u = a * scale with scale = log2(e) / tau (LogMeanExp) or log2(e) * beta (softmax-weighted),
+// the exact-product power for p in {1, 2, 4, 8}
+static float smooth_scale(int pool, float param) {
+  const float log2e = 1.4426950408889634f;
+  return pool == GL_POOL_LME ? log2e / param : (pool == GL_POOL_SOFTMAX ? log2e * param : 1.f);
+}
+static int smooth_pint(int pool, float param) {
+  if (pool != GL_POOL_POWER) return 0;
+  return (param == 1.f || param == 2.f || param == 4.f || param == 8.f) ? (int)param : 0;
+}
 
 // Forward plan: the forward runs over token chunks of bf tokens (a multiple of BT) whose per-chunk
 // partials (part_bytes + slot_bytes) fit the caller's part budget; every pass reloads the chunk
@@ -624,7 +811,8 @@ struct FwdPlan {
 
 // bytes of partial results (values, plus slots for max / top-k) one token of a pass holds
 static long long fwd_part_per_token(const GlFwdArgs* a, long long n_chunks) {
-  const long long kp = a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1;  // candidates per chunk and token
+  // candidates per chunk and token (top-k), a smooth pool's (m, s, t) state, else one partial sum
+  const long long kp = a->pool == GL_POOL_TOPK_MEAN ? a->topk : (pool_smooth(a->pool) ? 3 : 1);
   const bool sel = a->pool == GL_POOL_MAX || a->pool == GL_POOL_TOPK_MEAN;
   return n_chunks * kp * 4 * (sel ? 2 : 1);
 }
@@ -636,7 +824,7 @@ static FwdPlan fwd_plan(const GlFwdArgs* a, long long bf_cap = 0) {
   q.waves = fwd_waves(a->K, pool_kind(a->pool));
   q.cpg = ceil_div(a->S, 64 * q.npl);
   q.n_chunks = (long long)a->G * q.cpg;
-  const long long kp = a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1;
+  const long long kp = a->pool == GL_POOL_TOPK_MEAN ? a->topk : (pool_smooth(a->pool) ? 3 : 1);
   const bool sel = a->pool == GL_POOL_MAX || a->pool == GL_POOL_TOPK_MEAN;
   const long long per_token = fwd_part_per_token(a, q.n_chunks);
   const size_t budget = a->part_budget ? a->part_budget : FWD_PART_BUDGET_DEFAULT;
@@ -702,11 +890,18 @@ int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void
   if (B < 1 || D < 1 || G < 1 || S < 1) return GL_ERR_ARG;
   if (K != 8 && K != 16) return GL_ERR_UNSUPPORTED;
   if (act != GL_ACT_IDENTITY && act != GL_ACT_RELU) return GL_ERR_UNSUPPORTED;
-  if (pool != GL_POOL_MEAN && pool != GL_POOL_SUM && pool != GL_POOL_MAX && pool != GL_POOL_TOPK_MEAN)
-    return GL_ERR_UNSUPPORTED;
+  if (pool < GL_POOL_MEAN || pool > GL_POOL_SOFTMAX) return GL_ERR_UNSUPPORTED;
   if (x_dtype != GL_DTYPE_F32 && x_dtype != GL_DTYPE_BF16) return GL_ERR_UNSUPPORTED;
   if ((long long)G * S > (1LL << 31) / 16) return GL_ERR_UNSUPPORTED;
   if (D > XTILE_SB) return GL_ERR_LDS;  // one token tile (D x 16 bytes) must fit the LDS tile buffer
+  return 0;
+}
+
+// smooth pools: temperature / beta > 0, p >= 1 with relu activations (the reference's LevelSpec
+// checks, sparse_pooling/config.py:120-127)
+int check_smooth(int pool, float param, int act) {
+  if (pool == GL_POOL_LME || pool == GL_POOL_SOFTMAX) return param > 0.f && param < 3.0e38f ? 0 : GL_ERR_ARG;
+  if (pool == GL_POOL_POWER) return (param >= 1.f && param < 3.0e38f && act == GL_ACT_RELU) ? 0 : GL_ERR_ARG;
   return 0;
 }
 
@@ -739,7 +934,8 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
     int32_t* winner = a->winner ? a->winner + (long long)b0 * a->G * kpe : nullptr;
     GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles, xt, s));
     FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, pslot, kpe, a->sched, nullptr, q.n_chunks, a->D, a->S, q.cpg,
-           n_tiles, b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0, a->rec_shift};
+           n_tiles, b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0, a->rec_shift,
+           smooth_scale(a->pool, a->pool_param), a->pool_param, smooth_pint(a->pool, a->pool_param)};
     if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) k.win = a->win;
     dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(b_pad, 32));
     if (a->pool == GL_POOL_MAX) {
@@ -762,6 +958,22 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
       else
         GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_topk_kernel<GL_ACT_IDENTITY>, g1, dim3(256), 0, s, part, pslot,
                   a->counts, pre, winner, Bc, a->G, q.cpg, b_pad, a->topk);
+    } else if (pool_smooth(a->pool)) {
+      const dim3 g1((unsigned)ceil_div((long long)Bc * a->G, 256));
+      float* lse = a->lse ? a->lse + (long long)b0 * a->G : nullptr;
+      if (a->pool == GL_POOL_LME) {
+        GL_TRY(launch_fwd_any<PK_LME>(a->act, a->K, a->D, k, s));
+        GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_smooth_kernel<SM_LME>, g1, dim3(256), 0, s, part, a->counts, pre,
+                  lse, Bc, a->G, q.cpg, b_pad, k.scale, k.pparam, k.pint);
+      } else if (a->pool == GL_POOL_POWER) {
+        GL_TRY(launch_fwd_any<PK_POW>(a->act, a->K, a->D, k, s));
+        GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_smooth_kernel<SM_POW>, g1, dim3(256), 0, s, part, a->counts, pre,
+                  lse, Bc, a->G, q.cpg, b_pad, k.scale, k.pparam, k.pint);
+      } else {
+        GL_TRY(launch_fwd_any<PK_SW>(a->act, a->K, a->D, k, s));
+        GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_smooth_kernel<SM_SW>, g1, dim3(256), 0, s, part, a->counts, pre,
+                  lse, Bc, a->G, q.cpg, b_pad, k.scale, k.pparam, k.pint);
+      }
     } else {
       GL_TRY(launch_fwd_any<PK_SUM>(a->act, a->K, a->D, k, s));
       GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_kernel, grid, dim3(256), 0, s, part, a->counts, pre, Bc, a->G,
@@ -820,6 +1032,7 @@ extern "C" int gl_fwd_workspace(const GlFwdArgs* a, size_t* bytes) {
                      a->x_dtype));
   GL_TRY(check_topk(a->pool, a->topk, a->S));
   GL_TRY(check_rec_shift(a->rec_shift, a->S, a->sched));
+  GL_TRY(check_smooth(a->pool, a->pool_param, a->act));
   FwdPlan q = fwd_plan(a);
   *bytes = q.xt_bytes + q.part_bytes + q.slot_bytes;
   return 0;

@@ -16,6 +16,9 @@ int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void
 // GL_POOL_TOPK_MEAN arguments (k, pool size); 0 for other pools
 int check_topk(int pool, int topk, int S);
 
+// smooth pools' parameter (temperature, p with relu activations, beta)
+int check_smooth(int pool, float param, int act);
+
 // shared index records: 0 <= rec_shift <= 4, S a multiple of 2^rec_shift, no gather schedule
 int check_rec_shift(int rec_shift, int S, const void* sched);
 

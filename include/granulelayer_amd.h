@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 7
+#define GL_ABI_VERSION 8
 
 enum {
   GL_OK = 0,
@@ -44,7 +44,11 @@ enum { GL_ACT_IDENTITY = 0, GL_ACT_RELU = 1 };
 /* max: pytorch_reference.py:61-67 (winner = first maximum of act(z) over the pool's valid
  * slots), merged as kernels/ops.py:189-195; top-k mean: pytorch_reference.py:68-77 (the k largest
  * raw z, ties to the smaller slot, mean of act(z) over min(n_g, k) of them), ops.py:212-228 */
-enum { GL_POOL_MEAN = 0, GL_POOL_SUM = 1, GL_POOL_MAX = 2, GL_POOL_TOPK_MEAN = 3 };
+/* smooth operators (pytorch_reference.py:80-100), parameter in pool_param: LogMeanExp
+ * pre = tau (logsumexp(a / tau) - log n_g) (tau = temperature); power mean (relu activations only)
+ * pre = (mean a^p)^(1/p); softmax-weighted pre = sum softmax(beta a) a (beta) */
+enum { GL_POOL_MEAN = 0, GL_POOL_SUM = 1, GL_POOL_MAX = 2, GL_POOL_TOPK_MEAN = 3, GL_POOL_LME = 4,
+       GL_POOL_POWER = 5, GL_POOL_SOFTMAX = 6 };
 enum { GL_DTYPE_F32 = 0, GL_DTYPE_BF16 = 1 };
 
 /* Forward arguments.  Replaces the reference's FwdArgs + sp_fwd
@@ -72,6 +76,10 @@ typedef struct GlFwdArgs {
   int32_t* winner;        /* out [B, G, KPE] or NULL: the selected pool-local slots, KPE = 1 for
                              GL_POOL_MAX (the reference's "winner", ops.py:192-195), k for
                              GL_POOL_TOPK_MEAN ("topk_slot", best first, -1 past min(n_g, k)) */
+  float pool_param;       /* GL_POOL_LME: temperature > 0; GL_POOL_POWER: p >= 1; GL_POOL_SOFTMAX: beta > 0 */
+  float* lse;             /* out [B, G] or NULL: GL_POOL_LME / GL_POOL_SOFTMAX, the base-2 log-normaliser
+                             L2 = log2 sum 2^(a * scale), scale = log2(e) / tau or log2(e) * beta (the
+                             reference's "L2" statistic, kernels/ops.py:201-209) */
   void* ws;               /* workspace of gl_fwd_workspace() bytes */
   size_t ws_bytes;
   size_t part_budget;     /* bytes of per-chunk partial results one pass may hold (0: 4 GiB).  The
@@ -101,6 +109,11 @@ typedef struct GlBwdArgs {
   const float* g_pre;     /* [B, G] dL/dpre (fp32) */
   const int32_t* winner;  /* [B, G, KPE] the forward's selected slots: required for GL_POOL_MAX and
                              GL_POOL_TOPK_MEAN, NULL otherwise */
+  float pool_param;       /* as GlFwdArgs.pool_param */
+  const float* pre;       /* [B, G] the forward's pooled values: required for GL_POOL_POWER, GL_POOL_SOFTMAX
+                             and (without lse) GL_POOL_LME */
+  const float* lse;       /* [B, G] the forward's L2: required for GL_POOL_SOFTMAX; GL_POOL_LME recovers it
+                             from pre when NULL (kernels/ops.py:251-254) */
   float* dW;              /* [G*S, K] ACCUMULATED (+=), e.g. W.main_grad; padded slots untouched */
   float* db;              /* [G*S] ACCUMULATED (+=) */
   float* dX;              /* out [B, D] fp32, overwritten */
@@ -242,7 +255,8 @@ enum {
   GL_KERNEL_FWD_WIN = 10, GL_KERNEL_BWD_W_WIN = 11, /* forward / dW with pool-window staging */
   GL_KERNEL_MAX_EV_DW = 12, GL_KERNEL_MAX_EV_DX = 13, /* max-pooling backward: winner events */
   GL_KERNEL_COVER = 14,                                /* Cover-TopK support selection */
-  GL_KERNEL_SCHED = 15                                 /* gather schedule / pool windows on the GPU */
+  GL_KERNEL_SCHED = 15,                                /* gather schedule / pool windows on the GPU */
+  GL_KERNEL_DX_DENSE = 16                              /* dX of the smooth pools from per-neuron dz */
 };
 
 /* Launch trace for benchmarks and tests (process-wide, not for concurrent callers): after

@@ -31,6 +31,17 @@
  *     pre[b,g] = sum of act(z) over the first kk of them / kk
  *     backward (autograd.py:290-295): dz = dy[b,g] / kk * act'(z) for the kk selected neurons
  *
+ *   smooth pooling (pools 4 LogMeanExp, 5 power mean, 6 softmax-weighted; pytorch_reference.py:80-100):
+ *     LME (temperature tau):  pre = tau * (logsumexp(a / tau) - log n_g)
+ *     power (p >= 1, a = relu(z) >= 0): pre = M * (mean_n (a_n / M)^p)^(1/p), M = max a (0 if M == 0)
+ *     softmax-weighted (beta): pre = sum_n softmax(beta a)_n * a_n
+ *     the base-2 log-normaliser L2 = log2 sum_n 2^(u_n), u = a * scale, scale = log2(e) / tau (LME),
+ *     log2(e) * beta (softmax-weighted) (kernels/ops.py:74-79, 201-209)
+ *     backward (kernels/ops.py:242-262 dense_coefficients, triton_fused.py:364-399 _dz_from_z):
+ *       LME:     dz = dy * 2^(u - L2) * act'(z)
+ *       power:   dz = pre > 0 ? dy / n_g * (a / pre)^(p - 1) : 0, for z > 0
+ *       softmax: dz = dy * 2^(u - L2) * (1 + beta (a - pre)) * act'(z)
+ *
  *   Adam (sparse_pooling/optim.py:26-64, fp32 parameters: HAS_MASTER=False, STOCH=False):
  *     m = b1*m + (1-b1)*g ; v = b2*v + (1-b2)*g*g ; upd = (m/bc1) / (sqrt(v/bc2) + eps)
  *     p = p*(1 - lr*wd) - lr*upd ; g = 0        evaluated in fp32, in this order, unfused.
@@ -324,3 +335,113 @@ void glo_adam_f32(long n, float* p, float* g, float* m, float* v, float lr, floa
     p[i] = pi;
   }
 }
+
+/* ---- smooth pooling (pools 4, 5, 6) --------------------------------------------------------- */
+static inline double smooth_scale(int pool, double param) {
+  return pool == 4 ? 1.4426950408889634 / param : (pool == 6 ? 1.4426950408889634 * param : 1.0);
+}
+
+/* pooled value, L2 and the pool's largest |u| (LME / softmax) or a (power) of token row xb; z[] [n_g] */
+static void smooth_pool(const double* z, int n_g, int act, int pool, double param, double* pre, double* L2,
+                        double* amax) {
+  if (pool == 5) {
+    double M = 0.0;
+    for (int s = 0; s < n_g; ++s) M = fmax(M, act_f(z[s], 1));
+    double acc = 0.0;
+    if (M > 0.0)
+      for (int s = 0; s < n_g; ++s) acc += pow(act_f(z[s], 1) / M, param);
+    *pre = M > 0.0 ? M * pow(acc / (double)n_g, 1.0 / param) : 0.0;
+    *L2 = 0.0;
+    *amax = M;
+    return;
+  }
+  const double sc = smooth_scale(pool, param);
+  double M = -INFINITY, am = 0.0;
+  for (int s = 0; s < n_g; ++s) {
+    M = fmax(M, act_f(z[s], act) * sc);
+    am = fmax(am, fabs(act_f(z[s], act)));
+  }
+  double S = 0.0, T = 0.0;
+  for (int s = 0; s < n_g; ++s) {
+    const double a = act_f(z[s], act), e = exp2(a * sc - M);
+    S += e;
+    T += e * a;
+  }
+  *L2 = M + log2(S);
+  *pre = pool == 4 ? (*L2 - log2((double)n_g)) / sc : T / S;
+  *amax = am;
+}
+
+/*
+ * Smooth pooling forward.  pre [B, G]; lse [B, G] (optional) the log2-normaliser L2 (0 for
+ * power); mag [B, G] (optional): the scale of an fp32 evaluation's error: |pre| + the pool's
+ * largest |a| + the largest sum_k |x w| + |bias| of its neurons, times (1 + beta * spread) for
+ * softmax-weighted and (M / pre)^(p - 1) for power.
+ */
+void glo_forward_smooth_f64(int B, int D, int G, int S, int K, const float* x, const int32_t* idx, const float* w,
+                            const float* bias, const int32_t* counts, int act, int pool, double param, double* pre,
+                            double* lse, double* mag) {
+  double* z = (double*)malloc(sizeof(double) * (size_t)S);
+  for (int b = 0; b < B; ++b) {
+    const float* xb = x + (size_t)b * D;
+    for (int g = 0; g < G; ++g) {
+      const int n_g = counts[g];
+      double zmax = 0.0, zm;
+      for (int s = 0; s < n_g; ++s) {
+        z[s] = neuron_z(xb, idx, w, bias, (long)g * S + s, K, &zm);
+        zmax = fmax(zmax, zm);
+      }
+      double P, L2, am;
+      smooth_pool(z, n_g, act, pool, param, &P, &L2, &am);
+      pre[(size_t)b * G + g] = P;
+      if (lse) lse[(size_t)b * G + g] = L2;
+      if (mag) {
+        double amp = 1.0;
+        if (pool == 6) amp = 1.0 + param * 2.0 * am;
+        if (pool == 5) amp = P > 0.0 ? pow(am / P, param - 1.0) : 1.0;
+        mag[(size_t)b * G + g] = fabs(P) + am + zmax * amp;
+      }
+    }
+  }
+  free(z);
+}
+
+/* Smooth pooling backward (dW, db, dX accumulated in float64, with the sum of |terms| scales). */
+void glo_backward_smooth_f64(int B, int D, int G, int S, int K, const float* x, const int32_t* idx, const float* w,
+                             const float* bias, const int32_t* counts, int act, int pool, double param, const float* dy,
+                             double* dW, double* db, double* dX, double* magW, double* magb, double* magX) {
+  double* z = (double*)malloc(sizeof(double) * (size_t)S);
+  const double sc = smooth_scale(pool, param);
+  for (int b = 0; b < B; ++b) {
+    const float* xb = x + (size_t)b * D;
+    for (int g = 0; g < G; ++g) {
+      const int n_g = counts[g];
+      for (int s = 0; s < n_g; ++s) z[s] = neuron_z(xb, idx, w, bias, (long)g * S + s, K, NULL);
+      double P, L2, am;
+      smooth_pool(z, n_g, act, pool, param, &P, &L2, &am);
+      const double g_pre = (double)dy[(size_t)b * G + g];
+      for (int s = 0; s < n_g; ++s) {
+        double dz;
+        if (pool == 5) {
+          const double a = act_f(z[s], 1);
+          dz = (P > 0.0 && z[s] > 0.0) ? g_pre / (double)n_g * pow(a / P, param - 1.0) : 0.0;
+        } else {
+          const double a = act_f(z[s], act), pw = exp2(a * sc - L2);
+          dz = g_pre * pw * (pool == 6 ? 1.0 + param * (a - P) : 1.0) * dact_f(z[s], act);
+        }
+        const long n = (long)g * S + s;
+        db[n] += dz;
+        if (magb) magb[n] += fabs(dz);
+        for (int k = 0; k < K; ++k) {
+          const int d = idx[n * K + k];
+          dW[n * K + k] += dz * (double)xb[d];
+          dX[(size_t)b * D + d] += dz * (double)w[n * K + k];
+          if (magW) magW[n * K + k] += fabs(dz * (double)xb[d]);
+          if (magX) magX[(size_t)b * D + d] += fabs(dz * (double)w[n * K + k]);
+        }
+      }
+    }
+  }
+  free(z);
+}
+

@@ -9,6 +9,9 @@ Contents (each restates the reference; file:line citations are relative to the r
   restatement (``gl_oracle.c``) of
   ``sparse_pooling/reference/pytorch_reference.py:29-79`` (Mode A) and of the recompute backward
   ``sparse_pooling/kernels/triton_fused.py:364-445`` + ``kernels/ops.py:242-249``.
+* ``forward_smooth`` / ``backward_smooth`` -- LogMeanExp, power mean and softmax-weighted pooling
+  (``pytorch_reference.py:80-100``; coefficients ``kernels/ops.py:242-262``, dz
+  ``kernels/triton_fused.py:364-399``), float64.
 * ``adam`` -- fp32 restatement of ``sparse_pooling/optim.py:26-64`` (fp32 parameters).
 * ``partition`` -- group partition of ``sparse_pooling/layout.py:68-120``.
 * ``xedges`` -- the input-major (transposed) edge list consumed by the HIP dX kernel, in its exact
@@ -25,6 +28,8 @@ Parity status (what pins each function; see tests/test_oracle.py):
   backward  pinned: torch autograd of the dense-GEMM forward, float64 central differences; max
             pooling: autograd of the winner gather (pytorch_reference.py:61-67); top-k mean:
             autograd of the selected-value mean.
+  forward_smooth / backward_smooth pinned: torch float64 logsumexp / softmax / pow of the dense z
+            and its autograd (tests/test_oracle.py), float64 central differences.
   adam      pinned: torch.optim.Adam / AdamW (library), step-1 closed form.
   partition pinned: invariants of test_sparse_projection.py:14-27 (enumerates range(H)).
   xedges    pinned: brute force per feature on tiny inputs; invariants (permutation of the valid
@@ -67,8 +72,12 @@ def _load():
         lib.glo_backward_topk_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, i, P, P, P, P, ctypes.c_double,
                                               P, P, P, P, P, P]
         lib.glo_backward_events_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, i, i, P, P, P, P, P, P, P, P]
+        d = ctypes.c_double
+        lib.glo_forward_smooth_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, i, d, P, P, P]
+        lib.glo_backward_smooth_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, i, d, P, P, P, P, P, P, P]
         for fn in (lib.glo_forward_f64, lib.glo_backward_f64, lib.glo_adam_f32, lib.glo_forward_max_f64,
-                   lib.glo_forward_topk_f64, lib.glo_backward_topk_f64, lib.glo_backward_events_f64):
+                   lib.glo_forward_topk_f64, lib.glo_backward_topk_f64, lib.glo_backward_events_f64,
+                   lib.glo_forward_smooth_f64, lib.glo_backward_smooth_f64):
             fn.restype = None
         _lib = lib
     return _lib
@@ -208,6 +217,44 @@ def backward(x, idx, w, bias, counts, S, dy, act="relu", pool="mean", with_bound
     if with_bounds:
         return dW, db, dX, {"mag": mag, "unc": unc}
     return dW, db, dX
+
+
+# pool codes of the smooth operators (gl_oracle.c); param: temperature, p or beta
+SMOOTH = {"logmeanexp": 4, "power_mean": 5, "softmax_weighted": 6}
+
+
+def _operands(x, idx, w, bias, counts, S):
+    B, D, G, K = _shapes(x, idx, counts, S)
+    x, px = _c(x, np.float32)
+    idx, pi = _c(idx, np.int32)
+    w, pw = _c(np.asarray(w).reshape(G * S, K), np.float32)
+    bias, pb = _c(np.asarray(bias).reshape(G * S), np.float32)
+    counts, pc = _c(counts, np.int32)
+    return (B, D, G, K), (x, idx, w, bias, counts), (px, pi, pw, pb, pc)
+
+
+def forward_smooth(x, idx, w, bias, counts, S, pool, param, act="identity"):
+    """LogMeanExp (param = temperature), power mean (param = p, relu activations) or softmax-weighted
+    (param = beta) pooling: (pre [B, G], lse [B, G] the log2-normaliser (0 for power), mag [B, G] the
+    scale of an fp32 evaluation's error), float64 (pytorch_reference.py:80-100)."""
+    (B, D, G, K), keep, ptrs = _operands(x, idx, w, bias, counts, S)
+    pre, lse, mag = (np.zeros((B, G), np.float64) for _ in range(3))
+    _load().glo_forward_smooth_f64(B, D, G, S, K, *ptrs, _ACT[act], SMOOTH[pool], float(param), _p(pre), _p(lse),
+                                   _p(mag))
+    return pre, lse, mag
+
+
+def backward_smooth(x, idx, w, bias, counts, S, dy, pool, param, act="identity"):
+    """(dW, db, dX, (magW, magb, magX)) float64 of the smooth pooling operators for upstream dy [B, G]
+    (kernels/ops.py:242-262 coefficients, triton_fused.py:364-399 dz)."""
+    (B, D, G, K), keep, ptrs = _operands(x, idx, w, bias, counts, S)
+    dy, pdy = _c(dy, np.float32)
+    shapes = ((G * S, K), (G * S,), (B, D))
+    dW, db, dX = (np.zeros(s, np.float64) for s in shapes)
+    mag = tuple(np.zeros(s, np.float64) for s in shapes)
+    _load().glo_backward_smooth_f64(B, D, G, S, K, *ptrs, _ACT[act], SMOOTH[pool], float(param), pdy, _p(dW), _p(db),
+                                    _p(dX), *map(_p, mag))
+    return dW, db, dX, mag
 
 
 def adam(p, g, m, v, lr, b1, b2, eps, wd, step, moments_bf16=False):

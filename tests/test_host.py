@@ -83,7 +83,9 @@ def test_config_parsing_matches_reference_semantics():
     assert PoolingConfig.parse({"type": "mean", "activation": "identity"}).levels[0].hip_reason() == ""
     assert LevelSpec("max").out_activation == "relu"
     assert LevelSpec("max").hip_reason() == ""  # max pooling with winner ids is on the HIP path
-    assert LevelSpec("logmeanexp").hip_reason()
+    for t in ("logmeanexp", "power_mean", "softmax_weighted"):  # smooth operators are on the HIP path
+        assert LevelSpec(t).hip_reason() == ""
+    assert LevelSpec("mean", neurons_per_shard=64).hip_reason()  # semantic two-level pooling is not
     assert LevelSpec("mean", out_activation="gelu").hip_reason()
     assert LevelSpec("mean", activation="gelu").hip_reason()
     with pytest.raises(ValueError):
@@ -95,7 +97,7 @@ def test_config_parsing_matches_reference_semantics():
 
 @pytest.mark.parametrize("kwargs,exc", [
     (dict(shared_neurons=8, pooling="mean"), NotImplementedError),
-    (dict(shared_neurons=None, pooling="logmeanexp"), NotImplementedError),
+    (dict(shared_neurons=None, pooling={"type": "mean", "activation": "gelu"}), NotImplementedError),
     (dict(shared_neurons=None, pooling={"type": "mean", "activation": "gelu"}), NotImplementedError),
     (dict(shared_neurons=None, pooling="mean", backend="triton"), ValueError),
     (dict(shared_neurons=None, pooling="mean", weight_layout="packed"), ValueError),

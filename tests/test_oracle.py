@@ -407,3 +407,84 @@ def test_xedges_matches_bruteforce(oracle, D, G, S, K, Fw, US):
                 n = g * S + piece * US + nl
                 got.append((F, u, f, n * K + k, n, k))
     assert got == want
+
+
+def _dense_pool_torch(x, idx, w, b, counts, S, pool, param, act):
+    """The reference's pooling formulas (pytorch_reference.py:80-100) on the dense z of a small
+    layer, float64 torch, differentiable in x, w, b."""
+    import torch
+
+    G = len(counts)
+    xg = x[:, torch.as_tensor(idx, dtype=torch.long)]
+    z = (xg * w).sum(-1) + b  # [B, G*S]
+    z = z.view(x.shape[0], G, S)
+    a = torch.relu(z) if (act == "relu" or pool == "power_mean") else z
+    mask = torch.arange(S)[None, :] < torch.as_tensor(counts)[:, None]
+    n = torch.as_tensor(counts, dtype=torch.float64)
+    if pool == "logmeanexp":
+        u = torch.where(mask, a / param, torch.tensor(float("-inf"), dtype=torch.float64))
+        return param * (torch.logsumexp(u, -1) - torch.log(n))
+    if pool == "power_mean":
+        am = torch.where(mask, a, torch.zeros_like(a))
+        m = am.amax(-1, keepdim=True)
+        safe = torch.where(m > 0, m, torch.ones_like(m))
+        s = ((am / safe) ** param).sum(-1) / n
+        return torch.where(m.squeeze(-1) > 0, safe.squeeze(-1) * s ** (1.0 / param), torch.zeros_like(s))
+    u = torch.where(mask, param * a, torch.tensor(float("-inf"), dtype=torch.float64))
+    return (torch.softmax(u, -1) * torch.where(mask, a, torch.zeros_like(a))).sum(-1)
+
+
+@pytest.mark.parametrize("pool,param,act", [("logmeanexp", 1.0, "identity"), ("logmeanexp", 0.3, "relu"),
+                                            ("power_mean", 2.0, "relu"), ("power_mean", 3.5, "relu"),
+                                            ("softmax_weighted", 1.0, "identity"), ("softmax_weighted", 2.5, "relu")])
+def test_smooth_pools_match_torch_formulas_and_autograd(oracle, pool, param, act):
+    """Forward against the reference's pooling formulas in float64 torch, backward against torch
+    autograd of them (dW, db, dX), on ragged pools (padded slots)."""
+    import torch
+
+    B, D, G, S, K = 5, 40, 4, 16, 8
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((B, D)).astype(np.float32)
+    idx = np.stack([np.sort(rng.choice(D, K, replace=False)) for _ in range(G * S)]).astype(np.int32)
+    w = (rng.standard_normal((G * S, K)) / 3).astype(np.float32)
+    b = (rng.standard_normal(G * S) * 0.3).astype(np.float32)
+    counts = np.array([16, 11, 5, 16], np.int32)
+    dy = rng.standard_normal((B, G)).astype(np.float32)
+    pre, lse, mag = oracle.forward_smooth(x, idx, w, b, counts, S, pool, param, act)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
+    bt = torch.tensor(b, dtype=torch.float64, requires_grad=True)
+    want = _dense_pool_torch(xt, idx, wt, bt, counts, S, pool, param, act)
+    np.testing.assert_allclose(pre, want.detach().numpy(), rtol=1e-12, atol=1e-12)
+    (want * torch.tensor(dy, dtype=torch.float64)).sum().backward()
+    dW, db, dX, _ = oracle.backward_smooth(x, idx, w, b, counts, S, dy, pool, param, act)
+    valid = (np.arange(S)[None, :] < counts[:, None]).reshape(-1)
+    np.testing.assert_allclose(dX, xt.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dW[valid], wt.grad.numpy()[valid], rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(db[valid], bt.grad.numpy()[valid], rtol=1e-10, atol=1e-12)
+    assert not dW[~valid].any() and not db[~valid].any()
+    if pool != "power_mean":  # L2 = log2 sum 2^(u), u = a * scale
+        sc = np.log2(np.e) / param if pool == "logmeanexp" else np.log2(np.e) * param
+        np.testing.assert_allclose(lse, (pre * sc + np.log2(counts)) if pool == "logmeanexp" else lse, rtol=1e-12)
+
+
+def test_smooth_backward_finite_differences(oracle):
+    """Central differences of the float64 oracle forward give its backward (softmax-weighted)."""
+    B, D, G, S, K = 2, 12, 2, 8, 8
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((B, D)).astype(np.float32)
+    idx = np.stack([np.sort(rng.choice(D, K, replace=False)) for _ in range(G * S)]).astype(np.int32)
+    w = (rng.standard_normal((G * S, K)) / 3).astype(np.float32)
+    b = (rng.standard_normal(G * S) * 0.3).astype(np.float32)
+    counts = np.array([8, 6], np.int32)
+    dy = np.ones((B, G), np.float32)
+    _, db, _, _ = oracle.backward_smooth(x, idx, w, b, counts, S, dy, "softmax_weighted", 1.7, "identity")
+    h = 1e-3
+    for n in (0, 3, 9, 13):
+        bp, bm = b.copy(), b.copy()
+        bp[n] += h
+        bm[n] -= h
+        fp = oracle.forward_smooth(x, idx, w, bp, counts, S, "softmax_weighted", 1.7)[0].sum()
+        fm = oracle.forward_smooth(x, idx, w, bm, counts, S, "softmax_weighted", 1.7)[0].sum()
+        # bias steps of 1e-3 are exact in fp32 only approximately: compare at the 1e-5 level
+        assert abs((fp - fm) / (2 * h) - db[n]) < 1e-4 * max(1.0, abs(db[n]))
