@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgranulelayer_amd.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 GL_ACT = {"identity": 0, "relu": 1}
 GL_POOL = {"mean": 0, "sum": 1, "max": 2, "topk_mean": 3, "logmeanexp": 4, "power_mean": 5, "softmax_weighted": 6}
@@ -26,14 +26,14 @@ _P, _I32, _I64, _SZ, _F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctype
 
 class GlFwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
-                ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("rec_shift", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
+                ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("rec_shift", _I32), ("sps", _I32), ("gs", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("pre", _P), ("winner", _P), ("pool_param", _F),
                 ("lse", _P), ("ws", _P), ("ws_bytes", _SZ), ("part_budget", _SZ)]
 
 
 class GlBwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
-                ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("rec_shift", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
+                ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("rec_shift", _I32), ("sps", _I32), ("gs", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("g_pre", _P), ("winner", _P), ("pool_param", _F),
                 ("pre", _P), ("lse", _P), ("dW", _P), ("db", _P),
                 ("dX", _P), ("edges", _P), ("edges_bytes", _SZ),
@@ -42,7 +42,7 @@ class GlBwdArgs(ctypes.Structure):
 
 class GlEdgeArgs(ctypes.Structure):
     _fields_ = [("idx", _P), ("counts", _P), ("D", _I32), ("G", _I32), ("S", _I32), ("K", _I32), ("rec_shift", _I32),
-                ("edges", _P),
+                ("sps", _I32), ("gs", _I32), ("edges", _P),
                 ("edges_bytes", _SZ), ("ws", _P), ("ws_bytes", _SZ)]
 
 
@@ -109,13 +109,13 @@ class Library:
         L.gl_sched_size.restype = ctypes.c_int
         L.gl_sched_size.argtypes = [_I32, _I32, _I32, ctypes.POINTER(_SZ)]
         L.gl_sched_build_host.restype = ctypes.c_int
-        L.gl_sched_build_host.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _P, _I32]
+        L.gl_sched_build_host.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I32]
         L.gl_sched_build.restype = ctypes.c_int
-        L.gl_sched_build.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _P, _P]
+        L.gl_sched_build.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P]
         L.gl_window_build.restype = ctypes.c_int
-        L.gl_window_build.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P]
+        L.gl_window_build.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _P]
         L.gl_window_build_host.restype = ctypes.c_int
-        L.gl_window_build_host.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(_I32)]
+        L.gl_window_build_host.argtypes = [_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(_I32)]
         self.check_abi()
 
     def check_abi(self):
@@ -149,33 +149,37 @@ class Library:
         self.call("gl_edges_size", ctypes.byref(args), ctypes.byref(e), ctypes.byref(w))
         return int(e.value), int(w.value)
 
-    def sched_build(self, idx, counts, D: int, G: int, S: int, K: int, threads: int = 0):
-        """Gather schedule (numpy uint32 array) from host int32 arrays idx [G*S, K] and counts [G]."""
+    def sched_build(self, idx, counts, D: int, G: int, S: int, K: int, threads: int = 0, sps: int = 1, gs: int = 0):
+        """Gather schedule (numpy uint32 array) from host int32 arrays idx [neurons, K] and counts [G]
+        (G pools of S slots; sps > 1: the level-1 shards of G / sps groups of gs slots)."""
         import numpy as np
 
         idx = np.ascontiguousarray(idx, dtype=np.int32)
         counts = np.ascontiguousarray(counts, dtype=np.int32)
-        if idx.size != G * S * K or counts.size != G:
-            raise ValueError("idx must hold G*S*K and counts G entries")
+        rows = G * S if sps <= 1 else G // sps * gs
+        if idx.size != rows * K or counts.size != G:
+            raise ValueError("idx must hold one record per neuron and counts G entries")
         n = _SZ(0)
         self.call("gl_sched_size", G, S, K, ctypes.byref(n))
         out = np.empty(int(n.value) // 4, dtype=np.uint32)
-        self.call("gl_sched_build_host", idx.ctypes.data, counts.ctypes.data, D, G, S, K, out.ctypes.data, threads)
+        self.call("gl_sched_build_host", idx.ctypes.data, counts.ctypes.data, D, G, S, sps, gs, K, out.ctypes.data,
+                  threads)
         return out
 
-    def window_build(self, idx, counts, D: int, G: int, S: int, K: int, rec_shift: int = 0):
-        """Per-pool input windows from host int32 arrays idx [G*S >> rec_shift, K] and counts [G]:
+    def window_build(self, idx, counts, D: int, G: int, S: int, K: int, rec_shift: int = 0, sps: int = 1, gs: int = 0):
+        """Per-pool input windows from host int32 arrays idx [neurons >> rec_shift, K] and counts [G]:
         (lo uint32 [G], widest window width)."""
         import numpy as np
 
         idx = np.ascontiguousarray(idx, dtype=np.int32)
         counts = np.ascontiguousarray(counts, dtype=np.int32)
-        if idx.size != (G * S >> rec_shift) * K or counts.size != G:
-            raise ValueError("idx must hold (G*S >> rec_shift)*K and counts G entries")
+        rows = G * S if sps <= 1 else G // sps * gs
+        if idx.size != (rows >> rec_shift) * K or counts.size != G:
+            raise ValueError("idx must hold one record per neuron (>> rec_shift) and counts G entries")
         lo = np.empty(G, dtype=np.uint32)
         width = _I32(0)
-        self.call("gl_window_build_host", idx.ctypes.data, counts.ctypes.data, D, G, S, K, rec_shift, lo.ctypes.data,
-                  ctypes.byref(width))
+        self.call("gl_window_build_host", idx.ctypes.data, counts.ctypes.data, D, G, S, sps, gs, K, rec_shift,
+                  lo.ctypes.data, ctypes.byref(width))
         return lo, int(width.value)
 
 

@@ -1,6 +1,6 @@
 """Custom autograd: forward saves no hidden activations; backward recomputes them.
 
-Mirrors sparse_pooling/autograd.py for the single-level Mean / Sum path:
+Mirrors sparse_pooling/autograd.py for the level-1 path (the two-level function is in semantic.py):
 
 * ``Level1Runtime`` (autograd.py:68-300): executes the fused kernels of one layer, holds no
   tensor of size [B, H], records ``last_info``;
@@ -70,18 +70,25 @@ def recompute_chunk(rt: "Level1Runtime") -> int:
 
 
 def act_torch(x: torch.Tensor, name: str) -> torch.Tensor:
+    """Out-activation of the pooled value (kernels/ops.py:165-170): identity, relu or exact (erf) gelu."""
     if name == "identity":
         return x
     if name == "relu":
         return torch.relu(x)
+    if name == "gelu":
+        return torch.nn.functional.gelu(x)
     raise NotImplementedError(f"out-activation {name!r}")
 
 
 def dact_torch(x: torch.Tensor, name: str) -> torch.Tensor:
+    """Derivative of act_torch (kernels/ops.py:173-179): gelu'(x) = Phi(x) + x phi(x)."""
     if name == "identity":
         return torch.ones_like(x)
     if name == "relu":
         return (x > 0).to(x.dtype)
+    if name == "gelu":
+        cdf = 0.5 * (1.0 + torch.erf(x * 0.7071067811865476))
+        return cdf + x * 0.3989422804014327 * torch.exp(-0.5 * x * x)
     raise NotImplementedError(f"out-activation {name!r}")
 
 
@@ -99,6 +106,23 @@ class Units:
         return self.counts.numel()
 
 
+def make_units(layout: SparseLayout, nps: Optional[int], device) -> Units:
+    """Pooling units (sparse_pooling/kernels/ops.py:45-56): the groups, or with neurons_per_shard
+    nps the S = ceil(max_group / nps) shards of every group, unit u = g * S + s pooling slots
+    [s * nps, s * nps + counts[u]) of group g.  Every shard must hold a neuron."""
+    n_g = layout.counts_tensor(device).to(torch.float32)
+    if nps is None:
+        return Units(1, layout.blocks_per_group, None, n_g)
+    if nps % (4 * layout.block) != 0:
+        raise ValueError(f"neurons_per_shard must be a multiple of 4*C = {4 * layout.block}")
+    S = -(-layout.max_group // nps)
+    s = torch.arange(S, device=device, dtype=torch.float32)
+    cnt = torch.clamp(n_g[:, None] - s[None, :] * nps, min=0, max=nps)
+    if bool((cnt == 0).any()):
+        raise ValueError("a semantic shard would be empty; choose a different neurons_per_shard")
+    return Units(S, nps // layout.block, nps, cnt.reshape(-1))
+
+
 class Level1Runtime:
     """Executes the fused level-1 kernels for one layer (sparse_pooling/autograd.py:68-300)."""
 
@@ -110,8 +134,8 @@ class Level1Runtime:
             raise NotImplementedError(reason)
         if layout.shared_indices and not getattr(layout, "rec_shift", 0):
             raise NotImplementedError("Mode B (block-shared indices) is not on the MI355X path")
-        if nps is not None:
-            raise NotImplementedError("semantic two-level pooling is not on the MI355X path")
+        if nps is not None and getattr(layout, "rec_shift", 0):
+            raise NotImplementedError("semantic two-level pooling over shared index records is not on the MI355X path")
         if plan.backend == "triton":
             raise NotImplementedError("backend='triton': the MI355X build has no Triton path (use 'hip')")
         self.layout = layout
@@ -119,7 +143,10 @@ class Level1Runtime:
         self.level = level
         self.plan = plan
         self.counts_i32 = layout.counts_tensor(idx.device).contiguous()
-        self.units = Units(1, layout.blocks_per_group, None, self.counts_i32.to(torch.float32))
+        self.units = make_units(layout, nps, idx.device)
+        # valid neurons per pooling unit (the groups, or the level-1 shards), as the kernels read them
+        self.unit_counts_i32 = (self.counts_i32 if nps is None
+                                else self.units.counts.to(torch.int32).contiguous())
         self.workspace_budget = workspace_budget
         if backend is None and idx.is_cuda:
             from .backend import backend_for
@@ -217,6 +244,25 @@ def _saved_stats(level: LevelSpec, out: Dict[str, torch.Tensor], policy: str) ->
     return keep
 
 
+def _level1_backward(rt: Level1Runtime, xc, wc, bc, dy, saved: Dict[str, torch.Tensor], policy: str, dw_buf,
+                     db_buf, recomputed: bool = False) -> torch.Tensor:
+    """dX of the level-1 kernels for dy [B, U], the gradient of out_act(pre); dW / db accumulate
+    into the buffers.  Statistics the backward needs and the policy did not keep are recomputed
+    (autograd.py:246-258): max / top-k pooling need the selected slots, softmax-weighted the L2;
+    when the whole batch's slots would exceed CHECKPOINT_BUDGET they are recomputed and consumed
+    one token chunk at a time (autograd.py:255-259, 329-343)."""
+    lv = rt.level
+    need = {"max": "winner", "topk_mean": "topk_slot", "softmax_weighted": "L2"}.get(lv.type)
+    B = xc.shape[0]
+    if need is not None and need not in saved and B * _ids_per_token(rt) * 4 > CHECKPOINT_BUDGET:
+        return _chunked_selection_backward(rt, xc, wc, bc, dy, saved.get("pre"), policy, dw_buf, db_buf)
+    if "pre" not in saved or (need is not None and need not in saved):
+        saved.update(rt.forward(xc, wc, bc, track_ids=True))
+        recomputed = True
+    g_pre = dy.float() * dact_torch(saved["pre"], lv.out_activation)
+    return rt.backward(xc, wc, bc, g_pre.contiguous(), saved, policy, dw_buf, db_buf, recomputed)
+
+
 def _chunked_selection_backward(rt: Level1Runtime, xc, wc, bc, dy, pre, policy, dw_buf, db_buf):
     """Max / top-k backward with the selection ids recomputed per token chunk, so the [b, U, k] id
     tensor of one chunk stays within RECOMPUTE_CHUNK_BYTES; dW / db accumulate over the chunks.
@@ -258,23 +304,13 @@ class SparsePoolFunction(torch.autograd.Function):
         x, w, b, *svals = ctx.saved_tensors
         saved = dict(zip(ctx.saved_keys, svals))
         rt: Level1Runtime = ctx.rt
-        lv = rt.level
         xc, wc, bc = _compute_operands(x, w, b, ctx.compute_dtype)
-        # statistics the backward needs and the policy did not save (autograd.py:246-258): max
-        # pooling needs the winners, so minimal_stats recomputes the forward with track_ids
-        need = {"max": "winner", "topk_mean": "topk_slot", "softmax_weighted": "L2"}.get(lv.type)
-        recomputed = "pre" not in saved or (need is not None and need not in saved)
         dw_buf, db_buf, use_main = _grad_buffers(w, b)
-        B = x.shape[0]
-        if need is not None and need not in saved and B * _ids_per_token(rt) * 4 > CHECKPOINT_BUDGET:
-            # the ids of the whole batch would exceed the budget: recompute and consume them one
-            # token chunk at a time (sparse_pooling/autograd.py:255-259, 329-343)
-            dx = _chunked_selection_backward(rt, xc, wc, bc, dy, saved.get("pre"), ctx.policy, dw_buf, db_buf)
-        else:
-            if recomputed:
-                saved.update(rt.forward(xc, wc, bc, track_ids=True))
-            g_pre = dy.float() * dact_torch(saved["pre"], lv.out_activation)
-            dx = rt.backward(xc, wc, bc, g_pre.contiguous(), saved, ctx.policy, dw_buf, db_buf, recomputed)
+        dx = _level1_backward(rt, xc, wc, bc, dy, saved, ctx.policy, dw_buf, db_buf)
         gw = None if use_main else dw_buf.to(w.dtype)
         gb = None if use_main else db_buf.to(b.dtype)
         return dx.to(x.dtype, memory_format=torch.contiguous_format), gw, gb, None, None, None
+
+
+# the two-level function lives beside its level-2 code; exported here as the reference's module does
+from .semantic import SemanticPoolFunction  # noqa: E402,F401

@@ -84,6 +84,27 @@ class HipBackend:
         return L, G, S, K
 
     @staticmethod
+    def _pools(rt):
+        """Pool geometry of the launches: (pools U, slots per pool, shards per group sps, group
+        stride gs, valid neurons per pool [U] int32).  A single level pools the groups; a two-level
+        layer's level 1 pools the S shards of nps slots of every group (unit u = g * S + s,
+        sparse_pooling/kernels/ops.py:30-56)."""
+        L = rt.layout
+        u = getattr(rt, "units", None)
+        counts = getattr(rt, "unit_counts_i32", rt.counts_i32)
+        if u is None or u.nps is None or u.S == 1:
+            # one unit per group (a single shard spans its whole group): the groups' own geometry
+            geo = (L.groups, L.slots_per_group, 1, L.slots_per_group, counts)
+        else:
+            geo = (L.groups * u.S, u.nps, u.S, L.slots_per_group, counts)
+        U, S, sps, gs, _ = geo
+        rows = U * S if sps == 1 else U // sps * gs
+        if rows != L.groups * L.slots_per_group or counts.numel() != U:
+            raise RuntimeError(f"pool geometry (U={U}, S={S}, sps={sps}, gs={gs}) does not address the layout's "
+                               f"{L.groups * L.slots_per_group} slots")
+        return geo
+
+    @staticmethod
     def rec_shift(rt) -> int:
         """log2 slots per shared index record: 0 for Mode A, 4 for the K16 / C16 records of
         Cover-TopK/16 (granulelayer_amd.cover_topk16.CompactLayout)."""
@@ -114,7 +135,8 @@ class HipBackend:
     # ------------------------------------------------------------------ forward
     def forward(self, rt, x, w, b, track_ids: bool = False) -> Dict[str, torch.Tensor]:
         self._check(rt, x, w, b)
-        L, G, S, K = self._layer(rt)
+        L, _, _, K = self._layer(rt)
+        G, S, sps, gs, counts = self._pools(rt)
         act, pool = self._codes(rt)
         x, xcode, sxb = _x_operand(x)
         w, b = _f32(w, "weight"), _f32(b, "bias")
@@ -140,7 +162,8 @@ class HipBackend:
             return out
         win_lo, win_width = self.windows(rt)
         a = N.GlFwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=L.input_dim, G=G, S=S, K=K, act=act, pool=pool,
-                        topk=topk, rec_shift=self.rec_shift(rt), idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
+                        topk=topk, rec_shift=self.rec_shift(rt), sps=sps, gs=gs, idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b),
+                        counts=_ptr(counts),
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, pre=_ptr(pre),
                         winner=_ptr(winner), pool_param=self.pool_param(rt), lse=_ptr(lse),
                         part_budget=self.part_budget(rt))
@@ -174,7 +197,8 @@ class HipBackend:
         """Gather schedule of rt's index tensor for the forward / dW kernels (fan-in 8, one index
         record per slot), built on the GPU once per index tensor (gl_sched_build, the host
         builder's algorithm) and cached on rt; None otherwise."""
-        L, G, S, K = self._layer(rt)
+        L, _, _, K = self._layer(rt)
+        G, S, sps, gs, counts = self._pools(rt)
         if K != 8 or self.rec_shift(rt):
             return None
         key = (rt.idx.data_ptr(), rt.idx._version)
@@ -186,7 +210,7 @@ class HipBackend:
         self.lib.call("gl_sched_size", G, S, K, ctypes.byref(n))
         sched = torch.empty(n.value // 4, dtype=torch.int32, device=dev)
         with torch.cuda.device(dev):
-            self.lib.call("gl_sched_build", _ptr(rt.idx), _ptr(rt.counts_i32), L.input_dim, G, S, K, _ptr(sched),
+            self.lib.call("gl_sched_build", _ptr(rt.idx), _ptr(counts), L.input_dim, G, S, sps, gs, K, _ptr(sched),
                           ctypes.c_void_p(_stream(dev)))
         rt._hip_sched = (key, sched)
         return sched
@@ -198,7 +222,8 @@ class HipBackend:
         when ``window_staging`` is off.  The library stages only the windows when they are narrow."""
         if not self.window_staging:
             return None, 0
-        L, G, S, K = self._layer(rt)
+        L, _, _, K = self._layer(rt)
+        G, S, sps, gs, counts = self._pools(rt)
         key = (rt.idx.data_ptr(), rt.idx._version)
         cached = getattr(rt, "_hip_win", None)
         if cached is not None and cached[0] == key:
@@ -207,7 +232,7 @@ class HipBackend:
         lo = torch.empty(G, dtype=torch.int32, device=dev)
         width = torch.empty(1, dtype=torch.int32, device=dev)
         with torch.cuda.device(dev):
-            self.lib.call("gl_window_build", _ptr(rt.idx), _ptr(rt.counts_i32), L.input_dim, G, S, K,
+            self.lib.call("gl_window_build", _ptr(rt.idx), _ptr(counts), L.input_dim, G, S, sps, gs, K,
                           self.rec_shift(rt), _ptr(lo), _ptr(width), ctypes.c_void_p(_stream(dev)))
         out = (lo, int(width.item()))  # the launch needs the width on the host: one 4-byte copy
         rt._hip_win = (key, out)
@@ -220,9 +245,10 @@ class HipBackend:
         cached = getattr(rt, "_hip_edges", None)
         if cached is not None and cached[0] == key:
             return cached[1]
-        L, G, S, K = self._layer(rt)
-        a = N.GlEdgeArgs(idx=_ptr(rt.idx), counts=_ptr(rt.counts_i32), D=L.input_dim, G=G, S=S, K=K,
-                         rec_shift=self.rec_shift(rt))
+        L, _, _, K = self._layer(rt)
+        G, S, sps, gs, counts = self._pools(rt)
+        a = N.GlEdgeArgs(idx=_ptr(rt.idx), counts=_ptr(counts), D=L.input_dim, G=G, S=S, K=K,
+                         rec_shift=self.rec_shift(rt), sps=sps, gs=gs)
         dev = rt.idx.device
         with torch.cuda.device(dev):
             eb, wb = self.lib.edges_size(a)
@@ -238,7 +264,8 @@ class HipBackend:
     # ------------------------------------------------------------------ backward
     def backward(self, rt, x, w, b, g_pre, stats, dw_buf, db_buf) -> torch.Tensor:
         self._check(rt, x, w, b)
-        L, G, S, K = self._layer(rt)
+        L, _, _, K = self._layer(rt)
+        G, S, sps, gs, counts = self._pools(rt)
         act, pool = self._codes(rt)
         x, xcode, sxb = _x_operand(x)
         w, b = _f32(w, "weight"), _f32(b, "bias")
@@ -275,7 +302,8 @@ class HipBackend:
         win_lo, win_width = self.windows(rt)
         edges = self.edges(rt)
         a = N.GlBwdArgs(X=_ptr(x), sxb=sxb, x_dtype=xcode, B=B, D=D, G=G, S=S, K=K, act=act, pool=pool,
-                        topk=topk, rec_shift=self.rec_shift(rt), idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b), counts=_ptr(rt.counts_i32),
+                        topk=topk, rec_shift=self.rec_shift(rt), sps=sps, gs=gs, idx=_ptr(rt.idx), W=_ptr(w), bias=_ptr(b),
+                        counts=_ptr(counts),
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, g_pre=_ptr(g_pre),
                         winner=_ptr(winner), pool_param=self.pool_param(rt), pre=_ptr(pre), lse=_ptr(lse),
                         dW=_ptr(dw_buf), db=_ptr(db_buf), dX=_ptr(dx), edges=_ptr(edges),

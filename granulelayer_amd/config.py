@@ -94,10 +94,9 @@ class LevelSpec:
             return f"pooling {self.type!r} is not on the MI355X path (supported: {', '.join(HIP_POOLS)})"
         if self.activation not in HIP_ACTIVATIONS:
             return f"activation {self.activation!r} is not on the MI355X path (supported: relu, identity)"
-        if self.out_activation not in HIP_ACTIVATIONS:  # applied to pre by the autograd layer (torch)
-            return f"out_activation {self.out_activation!r} is not on the MI355X path (supported: relu, identity)"
-        if self.neurons_per_shard is not None:
-            return "semantic two-level pooling is not on the MI355X path"
+        # out_activation is applied to pre by the autograd layer (torch): identity, relu and gelu
+        if self.neurons_per_shard is not None and self.neurons_per_shard % 32 != 0:
+            return "neurons_per_shard must be a multiple of 4*C = 32"
         return ""
 
     def describe(self) -> str:

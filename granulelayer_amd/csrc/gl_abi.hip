@@ -93,7 +93,7 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
     case 0: {
       typedef GlFwdArgs S;
       long long t[] = {(long long)sizeof(S), OFF(S, X), OFF(S, sxb), OFF(S, x_dtype), OFF(S, B), OFF(S, D), OFF(S, G),
-                       OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, rec_shift), OFF(S, idx), OFF(S, W),
+                       OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, rec_shift), OFF(S, sps), OFF(S, gs), OFF(S, idx), OFF(S, W),
                        OFF(S, bias), OFF(S, counts), OFF(S, sched), OFF(S, win), OFF(S, win_width), OFF(S, pre), OFF(S, winner),
                        OFF(S, pool_param), OFF(S, lse), OFF(S, ws),
                        OFF(S, ws_bytes), OFF(S, part_budget)};
@@ -103,7 +103,7 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
     case 1: {
       typedef GlBwdArgs S;
       long long t[] = {(long long)sizeof(S), OFF(S, X), OFF(S, sxb), OFF(S, x_dtype), OFF(S, B), OFF(S, D), OFF(S, G),
-                       OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, rec_shift), OFF(S, idx), OFF(S, W),
+                       OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, rec_shift), OFF(S, sps), OFF(S, gs), OFF(S, idx), OFF(S, W),
                        OFF(S, bias), OFF(S, counts), OFF(S, sched), OFF(S, win), OFF(S, win_width), OFF(S, g_pre), OFF(S, winner),
                        OFF(S, pool_param), OFF(S, pre), OFF(S, lse), OFF(S, dW),
                        OFF(S, db), OFF(S, dX), OFF(S, edges),
@@ -114,7 +114,8 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
     case 2: {
       typedef GlEdgeArgs S;
       long long t[] = {(long long)sizeof(S), OFF(S, idx), OFF(S, counts), OFF(S, D), OFF(S, G), OFF(S, S), OFF(S, K),
-                       OFF(S, rec_shift), OFF(S, edges), OFF(S, edges_bytes), OFF(S, ws), OFF(S, ws_bytes)};
+                       OFF(S, rec_shift), OFF(S, sps), OFF(S, gs), OFF(S, edges), OFF(S, edges_bytes), OFF(S, ws),
+                       OFF(S, ws_bytes)};
       for (long long x : t) v[c++] = x;
       break;
     }

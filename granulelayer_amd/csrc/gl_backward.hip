@@ -77,6 +77,7 @@ struct BwK {
   int D, S, cpg, n_tiles, cap, mw2, nwin;
   int G, ww, npw;         // window staging: pools, padded window width, pools per workgroup
   int rs;                 // log2 slots per shared index record
+  int sps, gs;            // pool geometry (pool_base)
 };
 
 // One token tile of the dW pass (LDS at xsb): recompute z, form dz = c1 * act'(z), accumulate
@@ -145,7 +146,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   if (!active) chunk = p.n_chunks - 1;  // idle waves of the last block recompute a real chunk, store nothing
   const long long g = chunk / p.cpg;
   const int s_lo = (int)(chunk % p.cpg) * 64 * NPL;
-  const int n_g = p.counts[g];
+  const int ext = pool_ext((int)g, p.S, p.sps, p.gs);  // slots of the pool inside its group
+  const int n_g = min(p.counts[g], ext);
 
   unsigned addr[NPL][K];
   float w[NPL][K], dw[NPL][K];
@@ -162,7 +164,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
     const unsigned s16 = (unsigned)(s < 0xffff ? s : 0xffff);
     if (j % 2 == 0) slot2[j / 2] = s16; else slot2[j / 2] |= s16 << 16;
     const bool valid = s < n_g;
-    const long long n = g * p.S + (s < p.S ? s : p.S - 1);  // in-bounds address; invalid slots masked
+    const long long n = pool_base((int)g, p.S, p.sps, p.gs) + (s < ext ? s : ext - 1);  // in bounds; invalid slots masked
 #pragma unroll
     for (int ks = 0; ks < K; ++ks) {
       const int k = sched_k<K>(order, ks);
@@ -251,7 +253,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
     }
     // odd word: (word - 1, word) in one row of one slab (mw2 is even); a last even word alone
     const int w0 = word & ~1;
-    uint32_t* mslab = p.mask + ((long long)(w0 / p.mw2) * p.NS + g * p.S) * p.mw2 + w0 % p.mw2;
+    uint32_t* mslab = p.mask + ((long long)(w0 / p.mw2) * p.NS + pool_base((int)g, p.S, p.sps, p.gs)) * p.mw2 + w0 % p.mw2;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
       const int s = (int)((opaque((int)slot2[j / 2]) >> (16 * (j % 2))) & 0xffff);  // address math kept local
@@ -269,7 +271,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
     uint32_t order;
     const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, opaque(lane), order);
     if (s >= n_g) continue;
-    const long long n = g * p.S + s;
+    const long long n = pool_base((int)g, p.S, p.sps, p.gs) + s;
 #pragma unroll
     for (int ks = 0; ks < K; ++ks) p.dW[n * K + sched_k<K>(order, ks)] += dw[j][ks];
     p.db[n] += dbv[j];
@@ -287,6 +289,7 @@ struct DxK {
   float* part;  // [Q][D][cap]
   long long NS;
   int D, S, P, U, QL, UQ, FR, cap, n_tc;
+  int sps, gs;  // pool geometry (pool_base)
 };
 
 // ---- dX ----------------------------------------------------------------------------------------
@@ -342,7 +345,7 @@ __device__ __forceinline__ unsigned dx_load_rec(const DxK& p, const DxChunk& c, 
 template <int K, int T>
 __device__ __forceinline__ void dx_gather(const DxK& p, const uint32_t* mask_tc, const DxChunk& c, unsigned rec,
                                           DxGather<T>& g) {
-  const long long nb = (long long)(c.u / p.P) * p.S + (long long)(c.u % p.P) * US;  // first neuron of the unit
+  const long long nb = pool_base(c.u / p.P, p.S, p.sps, p.gs) + (long long)(c.u % p.P) * US;  // first neuron of the unit
   const unsigned woff = rec & REC_OFF_MASK;  // byte offset of W[n, k] in the unit
   const unsigned nl = woff >> (K == 8 ? 5 : 6);
   g.rec = rec;
@@ -645,6 +648,7 @@ struct BsK {
   int D, S, cpg, n_tiles, cap, nwin, rs;
   float scale, pparam;
   int pint;
+  int sps, gs;  // pool geometry (pool_base)
 };
 
 // Neuron-stationary recompute pass of a smooth pool: per token tile z, dz = c1 f(z, c2, c3), db and dW
@@ -660,7 +664,9 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
   if (!active) chunk = p.n_chunks - 1;
   const long long g = chunk / p.cpg;
   const int s_lo = (int)(chunk % p.cpg) * 64 * NPL;
-  const int n_g = p.counts[g];
+  const int ext = pool_ext((int)g, p.S, p.sps, p.gs);  // slots of the pool inside its group
+  const int n_g = min(p.counts[g], ext);
+  const long long nb = pool_base((int)g, p.S, p.sps, p.gs);  // the pool's first neuron
   unsigned addr[NPL][K];
   float w[NPL][K], dw[NPL][K];
   float bias[NPL], dbv[NPL];
@@ -670,7 +676,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
     uint32_t order;
     const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, lane, order);
     slot[j] = s < n_g ? s : -1;
-    const long long n = g * p.S + (s < p.S ? s : p.S - 1);
+    const long long n = nb + (s < ext ? s : ext - 1);
 #pragma unroll
     for (int ks = 0; ks < K; ++ks) {
       const int k = sched_k<K>(order, ks);
@@ -735,7 +741,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
         dw[j][k] = a;
       }
       if (active && v)
-        *reinterpret_cast<float4*>(p.dz + (g * p.S + slot[j]) * (long long)p.cap + t * BT) = make_float4(d0, d1, d2, d3);
+        *reinterpret_cast<float4*>(p.dz + (nb + slot[j]) * (long long)p.cap + t * BT) = make_float4(d0, d1, d2, d3);
     }
     if constexpr (DBUF) {
       stage_wait();
@@ -748,7 +754,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
     uint32_t order;
     const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, opaque(lane), order);
     if (s >= n_g) continue;
-    const long long n = g * p.S + s;
+    const long long n = pool_base((int)g, p.S, p.sps, p.gs) + s;
 #pragma unroll
     for (int ks = 0; ks < K; ++ks) p.dW[n * K + sched_k<K>(order, ks)] += dw[j][ks];
     p.db[n] += dbv[j];
@@ -795,7 +801,7 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
   __shared__ uint2 st[64];  // (record, weight bits) of the chunk's edges
   for (int si = lo; si < hi; ++si) {
     const int u = p.seg_unit[si];
-    const long long nb = (long long)(u / p.P) * p.S + (long long)(u % p.P) * US;  // first neuron of the unit
+    const long long nb = pool_base(u / p.P, p.S, p.sps, p.gs) + (long long)(u % p.P) * US;  // first neuron of the unit
     const unsigned e_end = p.seg_begin[si + 1];
     for (unsigned e0 = p.seg_begin[si]; e0 < e_end; e0 += 64) {
       const int n = (int)min(e_end - e0, 64u);
@@ -1012,6 +1018,9 @@ extern "C" int gl_bwd_workspace(const GlBwdArgs* a, size_t* bytes) {
   GL_TRY(check_topk(a->pool, a->topk, a->S));
   GL_TRY(check_rec_shift(a->rec_shift, a->S, a->sched));
   GL_TRY(check_smooth(a->pool, a->pool_param, a->act));
+  int32_t sps = a->sps, gs = a->gs;
+  GL_TRY(check_geometry(a->G, a->S, &sps, &gs));
+  if (sps > 1 && a->rec_shift > 0) return GL_ERR_UNSUPPORTED;
   // max / top-k pooling: the transposed selected slots, laid out like c1t (times k for top-k);
   // smooth pools: c2t and c3t beside c1t
   const size_t kpe = a->pool == GL_POOL_TOPK_MEAN ? (size_t)a->topk : (a->pool == GL_POOL_MAX ? 1 : 0);
@@ -1038,6 +1047,7 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
   if (smooth && (!a->pre && !(a->pool == GL_POOL_LME && a->lse))) return GL_ERR_ARG;  // coefficients need pre
   if (a->pool == GL_POOL_SOFTMAX && !a->lse) return GL_ERR_ARG;
   BwdPlan q = bwd_plan(a->B, a->D, a->G, a->S, a->K, smooth);
+  const int sps = a->sps > 1 ? a->sps : 1, gs = a->sps > 1 ? a->gs : a->S;  // checked by gl_bwd_workspace
   char* ws = (char*)a->ws;
   float4* xt = (float4*)ws;
   float* c1t = (float*)(ws + q.xt_bytes);
@@ -1065,12 +1075,13 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
                            ? (int)a->pool_param
                            : 0;
       const BsK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, c2t, c3t, a->dW, a->db, dz, a->sched, q.n_chunks, a->D,
-                   a->S, q.cpg, n_tiles, cap, ceil_div(a->S, SCHED_WIN), a->rec_shift, scale, a->pool_param, pint};
+                   a->S, q.cpg, n_tiles, cap, ceil_div(a->S, SCHED_WIN), a->rec_shift, scale, a->pool_param, pint,
+                   sps, gs};
       GL_TRY(a->K == 8 ? launch_bwd_smooth_kk<8>(a->pool, a->act, bk, s) : launch_bwd_smooth_kk<16>(a->pool, a->act, bk, s));
       const long long NS = (long long)a->G * a->S;
       DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
              (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, nullptr, a->W, part,
-             NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * T)};
+             NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * T), sps, gs};
       GL_TRY(launch_dx_dense(a->K, T, dk, dz, s));
       GL_LAUNCH(GL_KERNEL_DX_REDUCE, dx_reduce_kernel, dim3((unsigned)ceil_div(a->D, 32), (unsigned)ceil_div(Bc, 32)),
                 dim3(256), 0, s, part, a->dX, a->D, cap, q.Q, b0, Bc);
@@ -1089,18 +1100,18 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
         GL_CHECK_LAUNCH();
       }
       const MaxEvKArgs ev{xt, a->idx, a->W, a->bias, a->counts, c1t, wint, a->g_pre, a->winner, a->dW, a->db, a->dX,
-                          a->D, a->G, a->S, cap, Bc, b0, kpe, a->rec_shift, a->pool == GL_POOL_TOPK_MEAN};
+                          a->D, a->G, a->S, cap, Bc, b0, kpe, a->rec_shift, a->pool == GL_POOL_TOPK_MEAN, sps, gs};
       GL_TRY(launch_max_events(a->K, a->act, ev, s));
       continue;
     }
     const long long NS = (long long)a->G * a->S;
     BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, a->sched, nullptr, q.n_chunks, NS,
-           a->D, a->S, q.cpg, n_tiles, cap, 2 * T, ceil_div(a->S, SCHED_WIN), a->G, 0, 0, a->rec_shift};
+           a->D, a->S, q.cpg, n_tiles, cap, 2 * T, ceil_div(a->S, SCHED_WIN), a->G, 0, 0, a->rec_shift, sps, gs};
     if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &bk.ww, &bk.npw)) bk.win = a->win;
     GL_TRY(launch_bwd_w_any(a->K, a->act, bk, s));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
            (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, a->W, part,
-           NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * T)};
+           NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * T), sps, gs};
     GL_TRY(launch_dx(a->K, T, dk, s));
     GL_LAUNCH(GL_KERNEL_DX_REDUCE, dx_reduce_kernel, dim3((unsigned)ceil_div(a->D, 32), (unsigned)ceil_div(Bc, 32)), dim3(256), 0,
                        s, part, a->dX, a->D, cap, q.Q, b0, Bc);

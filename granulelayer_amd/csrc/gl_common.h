@@ -68,6 +68,23 @@ __device__ __forceinline__ int sched_k(uint32_t order, int ks) {
 }
 constexpr long long round_up(long long a, long long b) { return (a + b - 1) / b * b; }
 
+// ---- where a pool's slots live --------------------------------------------------------------
+// Pools are the groups (sps <= 1: pool g's S slots start at neuron g * S), or, for two-level
+// pooling, the sps level-1 shards of each group: pool u is shard u % sps of group u / sps, its
+// slots start at (u % sps) * S inside a group of gs slots, and the group's last shard may end
+// inside the group (gs < sps * S), which pool_ext reports.  Pool-indexed data (counts, partials,
+// schedules, windows) is per pool; neuron-indexed data (idx, W, bias, dW, db, masks) is per
+// physical neuron.
+__host__ __device__ __forceinline__ long long pool_base(int g, int S, int sps, int gs) {
+  return sps <= 1 ? (long long)g * S : (long long)(g / sps) * gs + (long long)(g % sps) * S;
+}
+// slots of pool g inside its group (>= 1): the clamp target of padded slots' addresses
+__host__ __device__ __forceinline__ int pool_ext(int g, int S, int sps, int gs) {
+  if (sps <= 1) return S;
+  const int r = gs - (g % sps) * S;
+  return r < S ? r : S;
+}
+
 // input k of neuron n when 2^rs consecutive slots share one index record (rs = 0: own record)
 __device__ __forceinline__ int rec_index(const int32_t* __restrict__ idx, long long n, int k, int K, int rs) {
   return idx[(n >> rs) * K + k];

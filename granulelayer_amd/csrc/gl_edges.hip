@@ -15,13 +15,16 @@ void edge_layout(int D, int G, int S, int K, EdgeHeader* h, size_t* total);
 
 constexpr int EB_THREADS = 512;
 
-// slots of unit u that are valid: [s0, s1)
-__device__ __forceinline__ void unit_slots(int u, int P, int S, const int32_t* counts, int* g, int* s0, int* s1) {
+// slots of unit u that are valid: [s0, s1) of pool *g, whose first neuron is *nb
+__device__ __forceinline__ void unit_slots(int u, int P, int S, int sps, int gs, const int32_t* counts, int* g,
+                                           int* s0, int* s1, long long* nb) {
   *g = u / P;
   const int piece = u % P;
   *s0 = piece * US;
+  *nb = pool_base(*g, S, sps, gs);
+  const int ext = pool_ext(*g, S, sps, gs);
   int e = *s0 + US;
-  if (e > S) e = S;
+  if (e > ext) e = ext;
   const int n_g = counts[*g];
   if (e > n_g) e = n_g;
   *s1 = e < *s0 ? *s0 : e;
@@ -31,15 +34,16 @@ __device__ __forceinline__ void unit_slots(int u, int P, int S, const int32_t* c
 // non-empty flag in the high 32 bits, for the segment count).
 __global__ void __launch_bounds__(EB_THREADS) edges_count_kernel(const int32_t* __restrict__ idx,
                                                                  const int32_t* __restrict__ counts, int D, int S, int K,
-                                                                 int rs, int P, int U, int FR,
+                                                                 int rs, int sps, int gs, int P, int U, int FR,
                                                                  unsigned long long* __restrict__ cnt) {
   extern __shared__ unsigned hist[];
   const int u = blockIdx.x;
   int g, s0, s1;
-  unit_slots(u, P, S, counts, &g, &s0, &s1);
+  long long nb;
+  unit_slots(u, P, S, sps, gs, counts, &g, &s0, &s1, &nb);
   for (int f = threadIdx.x; f < FR; f += blockDim.x) hist[f] = 0;
   __syncthreads();
-  const long long n0 = (long long)g * S + s0;
+  const long long n0 = nb + s0;
   const int ne = (s1 - s0) * K;
   for (int i = threadIdx.x; i < ne; i += blockDim.x) {
     int d = rec_index(idx, n0 + i / K, i % K, K, rs);
@@ -129,6 +133,7 @@ struct ScatterK {
   uint32_t* seg_begin;
   int D, S, K, P, U, FR, npow2;
   int rs;  // log2 slots per shared index record
+  int sps, gs;  // pool geometry (pool_base)
 };
 
 __global__ void __launch_bounds__(EB_THREADS) edges_scatter_kernel(ScatterK p) {
@@ -136,8 +141,9 @@ __global__ void __launch_bounds__(EB_THREADS) edges_scatter_kernel(ScatterK p) {
   unsigned* loc = reinterpret_cast<unsigned*>(keys + p.npow2);
   const int u = blockIdx.x;
   int g, s0, s1;
-  unit_slots(u, p.P, p.S, p.counts, &g, &s0, &s1);
-  const long long n0 = (long long)g * p.S + s0;
+  long long nb;
+  unit_slots(u, p.P, p.S, p.sps, p.gs, p.counts, &g, &s0, &s1, &nb);
+  const long long n0 = nb + s0;
   const int ne = (s1 - s0) * p.K;
   for (int i = threadIdx.x; i < p.npow2; i += blockDim.x) {
     unsigned long long key = ~0ull;
@@ -222,6 +228,9 @@ extern "C" int gl_edges_size(const GlEdgeArgs* a, size_t* edges_bytes, size_t* w
   if (a->K != 8 && a->K != 16) return GL_ERR_UNSUPPORTED;
   if ((long long)a->G * a->S * a->K >= (1LL << 32)) return GL_ERR_UNSUPPORTED;
   GL_TRY(check_rec_shift(a->rec_shift, a->S, nullptr));
+  int32_t sps = a->sps, gs = a->gs;
+  GL_TRY(check_geometry(a->G, a->S, &sps, &gs));
+  if (sps > 1 && a->rec_shift > 0) return GL_ERR_UNSUPPORTED;
   EdgeHeader h;
   edge_layout(a->D, a->G, a->S, a->K, &h, edges_bytes);
   const long long n = (long long)h.FR * h.U;
@@ -236,6 +245,7 @@ extern "C" int gl_edges_build(const GlEdgeArgs* a, void* stream) {
   GL_TRY(gl_edges_size(a, &eb, &wb));
   if (a->edges_bytes < eb || a->ws_bytes < wb) return GL_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
+  const int sps = a->sps > 1 ? a->sps : 1, gs = a->sps > 1 ? a->gs : a->S;  // checked by gl_edges_size
   EdgeHeader h;
   edge_layout(a->D, a->G, a->S, a->K, &h, &eb);
   h.nseg = 0;
@@ -250,7 +260,7 @@ extern "C" int gl_edges_build(const GlEdgeArgs* a, void* stream) {
   if (hist_lds > max_lds_bytes()) return GL_ERR_LDS;
   GL_TRY(set_lds_limit((const void*)edges_count_kernel, hist_lds));
   GL_LAUNCH(GL_KERNEL_EDGES, edges_count_kernel, dim3((unsigned)h.U), dim3(EB_THREADS), hist_lds, s, a->idx, a->counts, a->D,
-                     a->S, a->K, a->rec_shift, h.P, h.U, h.FR, cnt);
+                     a->S, a->K, a->rec_shift, sps, gs, h.P, h.U, h.FR, cnt);
   GL_CHECK_LAUNCH();
   GL_LAUNCH(GL_KERNEL_EDGES, scan_local_kernel, dim3((unsigned)nb), dim3(256), 0, s, cnt, n, bsum);
   GL_CHECK_LAUNCH();
@@ -266,7 +276,7 @@ extern "C" int gl_edges_build(const GlEdgeArgs* a, void* stream) {
   if (sort_lds > max_lds_bytes()) return GL_ERR_LDS;
   GL_TRY(set_lds_limit((const void*)edges_scatter_kernel, sort_lds));
   ScatterK sk{a->idx, a->counts, cnt, (uint32_t*)(e + h.off_rec), (int32_t*)(e + h.off_seg_unit),
-              (uint32_t*)(e + h.off_seg_begin), a->D, a->S, a->K, h.P, h.U, h.FR, npow2, a->rec_shift};
+              (uint32_t*)(e + h.off_seg_begin), a->D, a->S, a->K, h.P, h.U, h.FR, npow2, a->rec_shift, sps, gs};
   GL_LAUNCH(GL_KERNEL_EDGES, edges_scatter_kernel, dim3((unsigned)h.U), dim3(EB_THREADS), sort_lds, s, sk);
   GL_CHECK_LAUNCH();
   GL_LAUNCH(GL_KERNEL_EDGES, edges_finish_kernel, dim3((unsigned)ceil_div(h.FR, 256)), dim3(256), 0, s,

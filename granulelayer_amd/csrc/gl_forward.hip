@@ -63,6 +63,7 @@ struct FwdK {
   int rs;                 // log2 slots per shared index record
   float scale, pparam;    // smooth pools: u = a * scale (LogMeanExp / softmax-weighted); p (power mean)
   int pint;               // power mean: p when it is 1, 2, 4 or 8 (exact products), else 0
+  int sps, gs;            // pool geometry (pool_base): shards per group and group stride in slots
 };
 
 // One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
@@ -472,7 +473,9 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   if (!active) chunk = p.n_chunks - 1;  // idle waves of the last block recompute a real chunk, store nothing
   const long long g = chunk / p.cpg;
   const int s_lo = (int)(chunk % p.cpg) * 64 * NPL;
-  const int n_g = p.counts[g];
+  const int ext = pool_ext((int)g, p.S, p.sps, p.gs);  // slots of the pool inside its group
+  const int n_g = min(p.counts[g], ext);
+  const long long nb = pool_base((int)g, p.S, p.sps, p.gs);  // the pool's first neuron
 
   unsigned addr[NPL][K];
   float w[NPL][K];
@@ -488,7 +491,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
     uint32_t order;
     const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, lane, order);
     const bool valid = s < n_g;
-    const long long n = g * p.S + (s < p.S ? s : p.S - 1);  // in-bounds address; invalid slots masked
+    const long long n = nb + (s < ext ? s : ext - 1);  // in-bounds address; invalid slots masked
 #pragma unroll
     for (int ks = 0; ks < K; ++ks) {
       const int k = sched_k<K>(order, ks);  // the pooled sum does not depend on the visiting order
@@ -911,6 +914,18 @@ int check_rec_shift(int rec_shift, int S, const void* sched) {
   return 0;
 }
 
+int check_geometry(int G, int S, int32_t* sps, int32_t* gs) {
+  if (*sps < 0) return GL_ERR_ARG;
+  if (*sps <= 1) {  // pools are groups: a group stride, if given, must be the pool size
+    if (*gs != 0 && *gs != S) return GL_ERR_ARG;
+    *sps = 1;
+    *gs = S;
+    return 0;
+  }
+  if (G % *sps != 0 || (long long)(*sps - 1) * S >= *gs || *gs > (long long)*sps * S) return GL_ERR_ARG;
+  return 0;
+}
+
 // top-k mean: k a power of two in [1, 64] (the reference's LevelSpec check) and pools that the
 // finalize's merge covers (cpg <= FWD_TOPK_CPG chunks of 256 slots)
 int check_topk(int pool, int topk, int S) {
@@ -936,6 +951,8 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
     FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, pslot, kpe, a->sched, nullptr, q.n_chunks, a->D, a->S, q.cpg,
            n_tiles, b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0, a->rec_shift,
            smooth_scale(a->pool, a->pool_param), a->pool_param, smooth_pint(a->pool, a->pool_param)};
+    k.sps = a->sps > 1 ? a->sps : 1;
+    k.gs = a->sps > 1 ? a->gs : a->S;
     if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) k.win = a->win;
     dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(b_pad, 32));
     if (a->pool == GL_POOL_MAX) {
@@ -1033,6 +1050,9 @@ extern "C" int gl_fwd_workspace(const GlFwdArgs* a, size_t* bytes) {
   GL_TRY(check_topk(a->pool, a->topk, a->S));
   GL_TRY(check_rec_shift(a->rec_shift, a->S, a->sched));
   GL_TRY(check_smooth(a->pool, a->pool_param, a->act));
+  int32_t sps = a->sps, gs = a->gs;
+  GL_TRY(check_geometry(a->G, a->S, &sps, &gs));
+  if (sps > 1 && a->rec_shift > 0) return GL_ERR_UNSUPPORTED;
   FwdPlan q = fwd_plan(a);
   *bytes = q.xt_bytes + q.part_bytes + q.slot_bytes;
   return 0;

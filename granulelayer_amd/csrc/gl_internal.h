@@ -22,6 +22,11 @@ int check_smooth(int pool, float param, int act);
 // shared index records: 0 <= rec_shift <= 4, S a multiple of 2^rec_shift, no gather schedule
 int check_rec_shift(int rec_shift, int S, const void* sched);
 
+// Pool geometry (pool_base): *sps <= 1 becomes 1 with *gs = S (pools are groups; a given *gs must
+// equal S); otherwise G a multiple of *sps and (*sps - 1) * S < *gs <= *sps * S, so every shard
+// starts inside its group.
+int check_geometry(int G, int S, int32_t* sps, int32_t* gs);
+
 // Window staging for a kernel whose workgroups hold `waves` chunks of cpg per pool: true (with the
 // padded width *ww and pools per workgroup *npw) when the pools' windows fit a stage tile.
 bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, int G, int* ww, int* npw);
@@ -50,6 +55,7 @@ struct MaxEvKArgs {
   int kpe;    // selected slots per (token, pool): 1 (max) or k (top-k mean)
   int rs;     // log2 slots per shared index record
   bool topk;  // coef = g_pre / min(n_g, kpe) (top-k mean) instead of g_pre
+  int sps, gs;  // pool geometry (pool_base)
 };
 int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s);
 

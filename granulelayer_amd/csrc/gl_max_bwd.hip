@@ -37,6 +37,7 @@ struct MaxEvK {
   int D, G, S, cap, Bc, b0, npow2, kpe, tsub;
   int rs;     // log2 slots per shared index record
   bool topk;  // coef = g_pre / min(n_g, kpe)
+  int sps, gs;  // pool geometry (pool_base)
 };
 
 // x[b, d] of the chunk's token b from the token tiles
@@ -77,8 +78,8 @@ __global__ void __launch_bounds__(256) max_events_dw_kernel(MaxEvK p) {
       if (i < nev) {
         const int bl = t0 + i / p.kpe;  // token of the chunk
         const int s = p.wint[((long long)g * p.cap + bl) * p.kpe + i % p.kpe];
-        if (s >= 0 && s < p.S) {
-          const long long n = (long long)g * p.S + s;
+        if (s >= 0 && s < pool_ext(g, p.S, p.sps, p.gs)) {
+          const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
           float xk[K], wk[K];
           int dk[K];
           const float dz = event_dz<K, ACT>(p, n, p.c1t[(long long)g * p.cap + bl],
@@ -118,7 +119,7 @@ __global__ void __launch_bounds__(256) max_events_dw_kernel(MaxEvK p) {
 #pragma unroll
         for (int k = 0; k <= K; ++k) acc[k] += e[k];
       }
-      const long long n = (long long)g * p.S + s;
+      const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
       p.db[n] += acc[0];
 #pragma unroll
       for (int k = 0; k < K; ++k) p.dW[n * K + k] += acc[1 + k];
@@ -155,8 +156,8 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
   for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
     const int g = e / p.kpe;
     const int s = p.winner[row * p.kpe + e];
-    if (s < 0 || s >= p.S) continue;
-    const long long n = (long long)g * p.S + s;
+    if (s < 0 || s >= pool_ext(g, p.S, p.sps, p.gs)) continue;
+    const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
     const float gb = __builtin_fabsf(p.g_pre[row + g]);
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -181,9 +182,9 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
   for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
     const int g = e / p.kpe;
     int s = p.winner[row * p.kpe + e];
-    const bool ok = s >= 0 && s < p.S;
+    const bool ok = s >= 0 && s < pool_ext(g, p.S, p.sps, p.gs);
     s = ok ? s : 0;
-    const long long n = (long long)g * p.S + s;
+    const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
     float xk[K], wk[K];
     int dk[K];
     float coef = p.g_pre[row + g];
@@ -224,7 +225,7 @@ int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s) {
   int npow2 = 1;
   while (npow2 < tsub * a.kpe) npow2 <<= 1;
   const MaxEvK k{a.xt, a.idx, a.W, a.bias, a.counts, a.c1t, a.wint, a.g_pre, a.winner, a.dW, a.db, a.dX,
-                 a.D, a.G, a.S, a.cap, a.Bc, a.b0, npow2, a.kpe, tsub, a.rs, a.topk};
+                 a.D, a.G, a.S, a.cap, a.Bc, a.b0, npow2, a.kpe, tsub, a.rs, a.topk, a.sps, a.gs};
   if (K == 8) return act == GL_ACT_RELU ? launch_max_events_k<8, GL_ACT_RELU>(k, s) : launch_max_events_k<8, GL_ACT_IDENTITY>(k, s);
   return act == GL_ACT_RELU ? launch_max_events_k<16, GL_ACT_RELU>(k, s) : launch_max_events_k<16, GL_ACT_IDENTITY>(k, s);
 }

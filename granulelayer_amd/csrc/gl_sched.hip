@@ -198,15 +198,14 @@ __host__ __device__ inline void match_set(const Window& W, const uint8_t mem[16]
 }
 
 // slot p's residues and histogram (window w of group g)
-__host__ __device__ inline void load_slot(Window& W, const int32_t* idx, int D, int S, long long g, int w, int n_g,
-                                          int p) {
+__host__ __device__ inline void load_slot(Window& W, const int32_t* idx, int D, long long nb, int w, int n_g, int p) {
   const int s = w * WIN + p;
   W.valid[p] = s < n_g;
   for (int r = 0; r < 16; ++r) W.hist[p][r] = 0;
   for (int k = 0; k < KS; ++k) {
     int r = -1;
     if (W.valid[p]) {
-      int d = idx[((long long)g * S + s) * KS + k];
+      int d = idx[(nb + s) * KS + k];
       d = d < 0 ? 0 : (d >= D ? D - 1 : d);
       r = d & 15;
       W.hist[p][r]++;
@@ -230,15 +229,16 @@ __host__ __device__ inline void schedule_window(const Window& W, uint32_t* out) 
   }
 }
 
-void build_range(const int32_t* idx, const int32_t* counts, int D, int G, int S, long long w_begin,
+void build_range(const int32_t* idx, const int32_t* counts, int D, int S, int sps, int gs, long long w_begin,
                  long long w_end, uint32_t* sched) {
   const int nwin = ceil_div(S, WIN);
   Window W;
   for (long long gw = w_begin; gw < w_end; ++gw) {
     const long long g = gw / nwin;
     const int w = (int)(gw % nwin);
-    const int n_g = std::min(counts[g], S);
-    for (int p = 0; p < WIN; ++p) load_slot(W, idx, D, S, g, w, n_g, p);
+    const int n_g = std::min(counts[g], pool_ext((int)g, S, sps, gs));
+    const long long nb = pool_base((int)g, S, sps, gs);
+    for (int p = 0; p < WIN; ++p) load_slot(W, idx, D, nb, w, n_g, p);
     schedule_window(W, sched + gw * WIN);
   }
 }
@@ -246,15 +246,17 @@ void build_range(const int32_t* idx, const int32_t* counts, int D, int G, int S,
 // GPU builder: one window per lane (the windows of a wave run the same code on different data;
 // their private arrays are interleaved per lane, so the lanes' accesses to them coalesce)
 __global__ void __launch_bounds__(64) sched_build_kernel(const int32_t* __restrict__ idx,
-                                                         const int32_t* __restrict__ counts, int D, int S, int nwin,
-                                                         long long nw, uint32_t* __restrict__ sched) {
+                                                         const int32_t* __restrict__ counts, int D, int S, int sps,
+                                                         int gs, int nwin, long long nw, uint32_t* __restrict__ sched) {
   const long long gw = (long long)blockIdx.x * 64 + threadIdx.x;
   if (gw >= nw) return;
   const long long g = gw / nwin;
   const int w = (int)(gw % nwin);
-  const int n_g = counts[g] < S ? counts[g] : S;
+  const int ext = pool_ext((int)g, S, sps, gs);
+  const int n_g = counts[g] < ext ? counts[g] : ext;
+  const long long nb = pool_base((int)g, S, sps, gs);
   Window W;
-  for (int p = 0; p < WIN; ++p) load_slot(W, idx, D, S, g, w, n_g, p);
+  for (int p = 0; p < WIN; ++p) load_slot(W, idx, D, nb, w, n_g, p);
   schedule_window(W, sched + gw * WIN);
 }
 
@@ -265,13 +267,16 @@ __global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
 // GPU pool windows: one workgroup per pool, the smallest and largest index of its valid slots'
 // records; the widest window by an integer atomic maximum (order-independent)
 __global__ void __launch_bounds__(256) window_build_kernel(const int32_t* __restrict__ idx,
-                                                           const int32_t* __restrict__ counts, int D, int S, int K,
-                                                           int rs, uint32_t* __restrict__ lo, int32_t* __restrict__ width) {
+                                                           const int32_t* __restrict__ counts, int D, int S, int sps,
+                                                           int gs, int K, int rs, uint32_t* __restrict__ lo,
+                                                           int32_t* __restrict__ width) {
   __shared__ int smn[4], smx[4];
-  const long long g = blockIdx.x;
-  const int n_g = counts[g] < S ? counts[g] : S;
-  const long long r0 = (g * S) >> rs;
-  const long long r1 = n_g > 0 ? ((g * S + n_g - 1) >> rs) + 1 : r0;
+  const int g = blockIdx.x;
+  const int ext = pool_ext(g, S, sps, gs);
+  const int n_g = counts[g] < ext ? counts[g] : ext;
+  const long long nb = pool_base(g, S, sps, gs);
+  const long long r0 = nb >> rs;
+  const long long r1 = n_g > 0 ? ((nb + n_g - 1) >> rs) + 1 : r0;
   int mn = D, mx = -1;
   for (long long e = r0 * K + threadIdx.x; e < r1 * K; e += blockDim.x) {
     int d = idx[e];
@@ -307,8 +312,9 @@ extern "C" int gl_sched_size(int32_t G, int32_t S, int32_t K, size_t* bytes) {
 }
 
 extern "C" int gl_sched_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S,
-                                   int32_t K, uint32_t* sched, int32_t threads) {
+                                   int32_t sps, int32_t gs, int32_t K, uint32_t* sched, int32_t threads) {
   if (!idx || !counts || !sched || D < 1 || G < 1 || S < 1) return GL_ERR_ARG;
+  GL_TRY(check_geometry(G, S, &sps, &gs));
   if (K != 8) return GL_ERR_UNSUPPORTED;
   const long long nw = (long long)G * ceil_div(S, WIN);
   int nt = threads > 0 ? threads : (int)std::thread::hardware_concurrency();
@@ -318,7 +324,7 @@ extern "C" int gl_sched_build_host(const int32_t* idx, const int32_t* counts, in
   std::vector<std::thread> pool;
   for (int t = 0; t < nt; ++t) {
     const long long b = nw * t / nt, e = nw * (t + 1) / nt;
-    pool.emplace_back(build_range, idx, counts, D, G, S, b, e, sched);
+    pool.emplace_back(build_range, idx, counts, D, S, sps, gs, b, e, sched);
   }
   for (auto& th : pool) th.join();
   return 0;
@@ -329,16 +335,20 @@ extern "C" int gl_sched_build_host(const int32_t* idx, const int32_t* counts, in
 // of pool g's valid neurons, *width = max over pools of (largest - smallest + 1).  With narrow
 // windows the forward and dW kernels stage only each pool's window of X in LDS.
 extern "C" int gl_window_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S,
-                                    int32_t K, int32_t rec_shift, uint32_t* lo, int32_t* width) {
+                                    int32_t sps, int32_t gs, int32_t K, int32_t rec_shift, uint32_t* lo, int32_t* width) {
   if (!idx || !counts || !lo || !width || D < 1 || G < 1 || S < 1 || K < 1) return GL_ERR_ARG;
   if (rec_shift < 0 || rec_shift > 4 || S % (1 << rec_shift) != 0) return GL_ERR_ARG;
+  GL_TRY(check_geometry(G, S, &sps, &gs));
+  if (rec_shift > 0 && sps > 1) return GL_ERR_UNSUPPORTED;
   int32_t wmax = 0;
-  for (long long g = 0; g < G; ++g) {
-    const int n_g = counts[g] < S ? counts[g] : S;
+  for (int g = 0; g < G; ++g) {
+    const int ext = pool_ext(g, S, sps, gs);
+    const int n_g = counts[g] < ext ? counts[g] : ext;
     int32_t mn = D, mx = -1;
-    // the records that hold the pool's valid slots [0, n_g): rows (g S) >> r .. (g S + n_g - 1) >> r
-    const long long r0 = (g * S) >> rec_shift;
-    const long long r1 = n_g > 0 ? ((g * S + n_g - 1) >> rec_shift) + 1 : r0;
+    // the records that hold the pool's valid slots [0, n_g): rows nb >> r .. (nb + n_g - 1) >> r
+    const long long nb = pool_base(g, S, sps, gs);
+    const long long r0 = nb >> rec_shift;
+    const long long r1 = n_g > 0 ? ((nb + n_g - 1) >> rec_shift) + 1 : r0;
     for (long long e = r0 * K; e < r1 * K; ++e) {
       int32_t d = idx[e];
       d = d < 0 ? 0 : (d >= D ? D - 1 : d);
@@ -353,27 +363,30 @@ extern "C" int gl_window_build_host(const int32_t* idx, const int32_t* counts, i
   return 0;
 }
 
-extern "C" int gl_sched_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
-                              uint32_t* sched, void* stream) {
+extern "C" int gl_sched_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t sps,
+                              int32_t gs, int32_t K, uint32_t* sched, void* stream) {
   if (!idx || !counts || !sched || D < 1 || G < 1 || S < 1) return GL_ERR_ARG;
+  GL_TRY(check_geometry(G, S, &sps, &gs));
   if (K != 8) return GL_ERR_UNSUPPORTED;
   const long long nw = (long long)G * ceil_div(S, WIN);
   if (nw >= (1LL << 31)) return GL_ERR_UNSUPPORTED;
   GL_LAUNCH(GL_KERNEL_SCHED, sched_build_kernel, dim3((unsigned)ceil_div(nw, 64)), dim3(64), 0, (hipStream_t)stream, idx,
-            counts, D, S, ceil_div(S, WIN), nw, sched);
+            counts, D, S, sps, gs, ceil_div(S, WIN), nw, sched);
   GL_CHECK_LAUNCH();
   return 0;
 }
 
-extern "C" int gl_window_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
-                               int32_t rec_shift, uint32_t* lo, int32_t* width, void* stream) {
+extern "C" int gl_window_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t sps,
+                               int32_t gs, int32_t K, int32_t rec_shift, uint32_t* lo, int32_t* width, void* stream) {
   if (!idx || !counts || !lo || !width || D < 1 || G < 1 || S < 1 || K < 1) return GL_ERR_ARG;
   if (rec_shift < 0 || rec_shift > 4 || S % (1 << rec_shift) != 0) return GL_ERR_ARG;
+  GL_TRY(check_geometry(G, S, &sps, &gs));
+  if (rec_shift > 0 && sps > 1) return GL_ERR_UNSUPPORTED;
   hipStream_t s = (hipStream_t)stream;
   GL_LAUNCH(GL_KERNEL_SCHED, fill_i32_kernel, dim3(1), dim3(64), 0, s, width, 1, 0);
   GL_CHECK_LAUNCH();
-  GL_LAUNCH(GL_KERNEL_SCHED, window_build_kernel, dim3((unsigned)G), dim3(256), 0, s, idx, counts, D, S, K, rec_shift,
-            lo, width);
+  GL_LAUNCH(GL_KERNEL_SCHED, window_build_kernel, dim3((unsigned)G), dim3(256), 0, s, idx, counts, D, S, sps, gs, K,
+            rec_shift, lo, width);
   GL_CHECK_LAUNCH();
   return 0;
 }

@@ -3,7 +3,10 @@
 Same constructor signature, buffers/parameters (``indices``, ``weight``, ``bias``), ``forward``,
 ``enable_main_grad`` / ``zero_main_grad``, ``last_info``, ``explain`` and ``effective_policy``.
 On the MI355X path the layer runs the reference's Mode A (``shared_neurons=None``: every
-neuron owns its own fan-in record) with Mean (ReLU | identity) or Sum pooling; other
+neuron owns its own fan-in record) with every level-1 operator (mean, sum, max, top-k mean,
+LogMeanExp, power mean, softmax-weighted; relu or identity neuron activations) and the semantic
+two-level hierarchies (level-1 shards on the HIP kernels, level 2 in PyTorch, with the learned
+transform / weighted-sum parameters ``t_alpha``, ``t_beta``, ``t_v`` of layer.py:89-100); other
 configurations raise NotImplementedError naming what is unsupported.
 """
 from __future__ import annotations
@@ -14,6 +17,7 @@ import torch
 from torch import nn
 
 from .autograd import Level1Runtime, SparsePoolFunction, resolve_policy
+from .semantic import SemanticPoolFunction
 from .config import DEFAULT_WORKSPACE_BUDGET, PhysicalPlan, PoolingConfig
 from .layout import SparseLayout, check_indices, init_parameters
 
@@ -54,8 +58,6 @@ class SparsePoolingLayer(nn.Module):
         self.cfg = PoolingConfig.parse(pooling, checkpoint_policy)
         if isinstance(pooling, (str, PoolingConfig)) or "checkpoint_policy" not in (pooling or {}):
             self.cfg.checkpoint_policy = checkpoint_policy
-        if self.cfg.is_semantic_hierarchy:
-            raise NotImplementedError("semantic two-level pooling is not on the MI355X path")
         reason = self.cfg.levels[0].hip_reason()
         if reason:
             raise NotImplementedError(reason)
@@ -70,6 +72,19 @@ class SparsePoolingLayer(nn.Module):
         self.weight = nn.Parameter(w)
         self.bias = nn.Parameter(b)
         self._tnames = []
+        if self.cfg.is_semantic_hierarchy:
+            # level-2 parameters per (group, shard), initialised as the reference does (layer.py:89-100)
+            l1, l2 = self.cfg.levels
+            S = -(-self.layout.max_group // l1.neurons_per_shard)
+            self.num_shards = S
+            G = output_dim
+            if l1.transform in ("affine", "gate"):
+                self.t_alpha = nn.Parameter(torch.ones(G, S, device=device))
+                self.t_beta = nn.Parameter(torch.zeros(G, S, device=device))
+                self._tnames += ["alpha", "beta"]
+            if l2.type == "weighted_sum":
+                self.t_v = nn.Parameter(torch.full((G, S), 1.0 / S, device=device))
+                self._tnames += ["v"]
         self._rt = None
         self._rt_key = None
 
@@ -78,7 +93,9 @@ class SparsePoolingLayer(nn.Module):
         key = (self.indices.device, self.indices.data_ptr(), self.indices._version, id(self.plan))
         if self._rt is None or self._rt_key != key:
             check_indices(self.layout, self.indices)
-            self._rt = Level1Runtime(self.layout, self.indices, self.cfg.levels[0], self.plan, None,
+            l1 = self.cfg.levels[0]
+            self._rt = Level1Runtime(self.layout, self.indices, l1, self.plan,
+                                     l1.neurons_per_shard if self.cfg.is_semantic_hierarchy else None,
                                      self.workspace_budget, None)
             self._rt_key = key
         return self._rt
@@ -130,7 +147,12 @@ class SparsePoolingLayer(nn.Module):
         lead = x.shape[:-1]
         x2 = x.reshape(-1, x.shape[-1])
         rt = self._runtime()
-        y = SparsePoolFunction.apply(x2, self.weight, self.bias, rt, self.effective_policy, self.compute_dtype)
+        if self.cfg.is_semantic_hierarchy:
+            tparams = [getattr(self, "t_" + n) for n in self._tnames]
+            y = SemanticPoolFunction.apply(x2, self.weight, self.bias, rt, self.cfg, self.effective_policy,
+                                           self.compute_dtype, self._tnames, *tparams)
+        else:
+            y = SparsePoolFunction.apply(x2, self.weight, self.bias, rt, self.effective_policy, self.compute_dtype)
         return y.reshape(*lead, y.shape[-1])
 
     def extra_repr(self) -> str:

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 8
+#define GL_ABI_VERSION 9
 
 enum {
   GL_OK = 0,
@@ -65,10 +65,17 @@ typedef struct GlFwdArgs {
   int32_t rec_shift;      /* 0: every slot owns its index record; r in 1..4: 2^r consecutive slots share
                              one record (idx is [G*S >> r, K]; S a multiple of 2^r), e.g. r = 4 for the
                              K16 / C16 records of Cover-TopK/16 (sparse_pooling/cover_topk16.py:1-12) */
+  int32_t sps, gs;        /* pool geometry.  sps <= 1: the G pools are the groups (S slots each; gs
+                             0 or S).  sps > 1: two-level pooling's level-1 shards
+                             (sparse_pooling/kernels/ops.py:45-56): the G pools are the sps shards of
+                             G / sps groups of gs slots, pool u pooling slots
+                             [(u % sps) * S, (u % sps) * S + counts[u]) of group u / sps, with
+                             (sps - 1) * S < gs <= sps * S; tensors below indexed by neuron then have
+                             G / sps * gs rows instead of G*S, and rec_shift must be 0 */
   const int32_t* idx;     /* [G*S >> rec_shift, K] input indices in [0, D) */
   const float* W;         /* [G*S, K] */
   const float* bias;      /* [G*S] */
-  const int32_t* counts;  /* [G] valid neurons per group, 1 <= counts[g] <= S */
+  const int32_t* counts;  /* [G] valid neurons per pool, 1 <= counts[g] <= S (and inside its group) */
   const uint32_t* sched;  /* gather schedule from gl_sched_build_host (K = 8), or NULL */
   const uint32_t* win;    /* [G] first input of each pool's window (gl_window_build_host), or NULL */
   int32_t win_width;      /* widest pool window; the kernels stage only the windows when narrow */
@@ -99,6 +106,7 @@ typedef struct GlBwdArgs {
   int32_t act, pool;
   int32_t topk;           /* as GlFwdArgs.topk */
   int32_t rec_shift;      /* as GlFwdArgs.rec_shift */
+  int32_t sps, gs;        /* as GlFwdArgs.sps / gs */
   const int32_t* idx;
   const float* W;
   const float* bias;
@@ -132,6 +140,7 @@ typedef struct GlEdgeArgs {
   const int32_t* counts;
   int32_t D, G, S, K;
   int32_t rec_shift;      /* as GlFwdArgs.rec_shift */
+  int32_t sps, gs;        /* as GlFwdArgs.sps / gs */
   void* edges;            /* out, gl_edges_size() bytes */
   size_t edges_bytes;
   void* ws;               /* scratch, gl_edges_size() bytes */
@@ -226,13 +235,13 @@ int gl_adam(const GlAdamArgs* a, void* stream);
  * reference counterpart (the reference's Triton Mode-A kernels gather from global memory,
  * sparse_pooling/kernels/triton_fused.py:253-264).  threads <= 0: one per hardware thread. */
 int gl_sched_size(int32_t G, int32_t S, int32_t K, size_t* bytes);
-int gl_sched_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
-                        uint32_t* sched, int32_t threads);
+int gl_sched_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t sps,
+                        int32_t gs, int32_t K, uint32_t* sched, int32_t threads);
 
 /* The same schedule built on the GPU from device copies of idx and counts (one lane per 128-slot
  * window, the host builder's code), bit-identical to gl_sched_build_host; enqueued on stream. */
-int gl_sched_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
-                   uint32_t* sched, void* stream);
+int gl_sched_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t sps,
+                   int32_t gs, int32_t K, uint32_t* sched, void* stream);
 
 /* Per-pool input windows, built on the HOST once per index tensor: lo[g] = the smallest input
  * index of pool g's valid neurons, *width = the widest window (largest - smallest + 1) over all
@@ -242,11 +251,11 @@ int gl_sched_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t
  * Results are unchanged (same arithmetic, same order).  No reference counterpart in Mode A
  * (the reference stages per-supergroup feature sets in its Mode-B grouped kernels,
  * sparse_pooling/supergroups.py:1-40, kernels/cuda/sparse_pool_sg.cuh). */
-int gl_window_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
-                         int32_t rec_shift, uint32_t* lo, int32_t* width);
+int gl_window_build_host(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t sps,
+                         int32_t gs, int32_t K, int32_t rec_shift, uint32_t* lo, int32_t* width);
 /* The same windows built on the GPU from device copies (lo [G] and *width in device memory). */
-int gl_window_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t K,
-                    int32_t rec_shift, uint32_t* lo, int32_t* width, void* stream);
+int gl_window_build(const int32_t* idx, const int32_t* counts, int32_t D, int32_t G, int32_t S, int32_t sps,
+                    int32_t gs, int32_t K, int32_t rec_shift, uint32_t* lo, int32_t* width, void* stream);
 
 /* Kernel ids reported by the trace below. */
 enum {

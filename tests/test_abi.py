@@ -120,3 +120,30 @@ def test_forward_workspace_is_bounded_as_the_batch_grows():
     assert small <= (64 << 20) + (1 << 16) * 4096 * 4
     # a budget below one token tile's partials still runs (one tile per pass)
     assert ws(64, "topk_mean", 64, budget=1) == 4 * 4096 * 4 + 2 * 98_304 * 4 * 4 * 64 * 4
+
+
+def test_pool_geometry_is_validated_by_the_size_queries():
+    """sps / gs (two-level pooling's level-1 shards): sps <= 1 means the pools are the groups and a
+    given gs must equal S; sps > 1 needs G a multiple of sps and (sps - 1) S < gs <= sps S, so every
+    shard starts inside its group.  Host-side checks of gl_fwd_workspace, gl_bwd_workspace and
+    gl_edges_size (placeholder pointers, never dereferenced)."""
+    lib = N.library()
+    out, e, w = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+
+    def q(sps, gs, G=16, S=256, rec_shift=0):
+        kw = dict(X=16, idx=16, W=16, bias=16, counts=16, B=8, D=64, G=G, S=S, K=8, act=N.GL_ACT["relu"],
+                  pool=N.GL_POOL["mean"], sps=sps, gs=gs, rec_shift=rec_shift)
+        f = lib.lib.gl_fwd_workspace(ctypes.byref(N.GlFwdArgs(**kw)), ctypes.byref(out))
+        b = lib.lib.gl_bwd_workspace(ctypes.byref(N.GlBwdArgs(**kw)), ctypes.byref(out))
+        ea = N.GlEdgeArgs(idx=16, counts=16, D=64, G=G, S=S, K=8, sps=sps, gs=gs, rec_shift=rec_shift)
+        x = lib.lib.gl_edges_size(ctypes.byref(ea), ctypes.byref(e), ctypes.byref(w))
+        assert f == b == x, (f, b, x)
+        return f
+
+    assert q(0, 0) == 0 and q(1, 0) == 0 and q(1, 256) == 0
+    assert q(1, 384) == -1 and q(0, 512) == -1  # groups are not pools of S slots
+    assert q(2, 384) == 0 and q(2, 512) == 0 and q(4, 1000) == 0
+    assert q(2, 256) == -1 and q(2, 513) == -1  # the second shard would start outside / end past the group
+    assert q(3, 600, G=16) == -1  # G not a multiple of sps
+    assert q(-1, 0) == -1
+    assert q(2, 384, S=256, rec_shift=4) == -2  # shared index records are not sharded

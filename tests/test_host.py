@@ -85,9 +85,10 @@ def test_config_parsing_matches_reference_semantics():
     assert LevelSpec("max").hip_reason() == ""  # max pooling with winner ids is on the HIP path
     for t in ("logmeanexp", "power_mean", "softmax_weighted"):  # smooth operators are on the HIP path
         assert LevelSpec(t).hip_reason() == ""
-    assert LevelSpec("mean", neurons_per_shard=64).hip_reason()  # semantic two-level pooling is not
-    assert LevelSpec("mean", out_activation="gelu").hip_reason()
-    assert LevelSpec("mean", activation="gelu").hip_reason()
+    assert LevelSpec("mean", neurons_per_shard=64).hip_reason() == ""  # level-1 shards of two-level pooling
+    assert LevelSpec("mean", neurons_per_shard=48).hip_reason()  # not a multiple of 4*C = 32
+    assert LevelSpec("mean", out_activation="gelu").hip_reason() == ""  # applied to pre in torch
+    assert LevelSpec("mean", activation="gelu").hip_reason()  # the neuron activation runs in the kernels
     with pytest.raises(ValueError):
         LevelSpec("topk_mean", k=3)
     with pytest.raises(ValueError):
