@@ -67,8 +67,27 @@ def algorithmic(kernel: str, B: int, N: int, K: int, D: int, G: int, x_bytes: in
         return E * (4 + 4 + B // 8) + 4 * B * D, 2 * B * E
     if kernel == "adam_kernel":
         return 32 * (E + N), 12 * (E + N)
+    if kernel == "bwd_smooth_kernel":
+        # as bwd_w_kernel, with every neuron's dz row (fp32 per token) written instead of mask bits
+        return 4 * E + 4 * E + 4 * N + B * D * x_bytes + 8 * E + 8 * N + 4 * N * B, 4 * B * E
+    if kernel == "dx_dense_kernel":
+        # per edge: record, weight and the neuron's dz row; dX written once
+        return E * (4 + 4 + 4 * B) + 4 * B * D, 2 * B * E
     return None, None
 
+
+# --pooling choices: (pooling spec of the layer, description in the bench line)
+POOLINGS = {
+    "sum": ("sum", "sum(relu)"),
+    "mean": ("mean", "mean(relu)"),
+    "max": ("max", "relu(max z)"),
+    "topk": ({"type": "topk_mean", "k": 8}, "top-8 mean(z)"),
+    "lme": ({"type": "logmeanexp", "temperature": 1.0, "activation": "relu"}, "logmeanexp(relu, tau 1)"),
+    "power": ({"type": "power_mean", "p": 2.0, "activation": "relu"}, "power mean(relu, p 2)"),
+    "softmax": ({"type": "softmax_weighted", "beta": 1.0, "activation": "relu"}, "softmax-weighted(relu, beta 1)"),
+    "two_level": ({"levels": [{"type": "mean", "neurons_per_shard": 256}, {"type": "logmeanexp"}]},
+                  "mean(relu) over shards of 256, then logmeanexp over 4 shards"),
+}
 
 CONFIG_WORK = {"C1": "fwd+bwd+adam", "C2": "fwd", "C3": "fwd+bwd", "C4": "fwd+bwd+adam", "C5": "fwd+bwd"}
 
@@ -326,10 +345,11 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the C1 and C4 extra measurements")
     ap.add_argument("--config", choices=sorted(CONFIG_WORK), default=None,
                     help="time one BASELINE config's own work at full size instead of the headline step")
-    ap.add_argument("--pooling", choices=("sum", "mean", "max", "topk"), default="sum",
+    ap.add_argument("--pooling", choices=sorted(POOLINGS), default="sum",
                     help="pooling of the train-step layer (default: the headline's sum of relu; max: the "
                          "reference's defaults, relu(max z), winners saved for backward; topk: top-8 mean, "
-                         "slots saved)")
+                         "slots saved; lme / power / softmax: the smooth operators; two_level: mean over "
+                         "shards of 256, then LogMeanExp over the 4 shard features)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -365,7 +385,7 @@ def main():
     dev = torch.device("cuda", 0)
     t0 = time.time()
     log(f"building layer N={N:,} K={K} D={D} G={G:,} on {torch.cuda.get_device_name(0)}")
-    pooling = {"type": "topk_mean", "k": 8} if args.pooling == "topk" else args.pooling
+    pooling = POOLINGS[args.pooling][0]
     lay = SparsePoolingLayer(D, N, G, fan_in=K, shared_neurons=None, pooling=pooling, dtype=torch.float32,
                              device=dev, seed=0)
     lay.enable_main_grad()
@@ -472,8 +492,7 @@ def main():
         "data": "synthetic (seeded: uniform distinct indices, W~N(0,1/8), bias 0, X and dY ~N(0,1))",
         "config": {"workload": "C2-shaped train step: fwd + recompute bwd (dX, dW, db) + fused AdamW",
                    "neurons": N, "fan_in": K, "d_in": D, "batch": B, "pool": pool, "groups": G,
-                   "pooling": {"sum": "sum(relu)", "mean": "mean(relu)", "max": "relu(max z)",
-                               "topk": "top-8 mean(z)"}[args.pooling], "x_dtype": "f32", "moments": "f32",
+                   "pooling": POOLINGS[args.pooling][1], "x_dtype": "f32", "moments": "f32",
                    "parallelism": "single GPU"},
         "fwd_ms": round(fwd_ms, 3),
         "fwd_G_edge_macs_per_s": round(B * E / (fwd_ms * 1e-3) / 1e9, 2),
