@@ -150,7 +150,7 @@ extern "C" const char* gl_error_string(int code) {
     case GL_ERR_UNSUPPORTED:
       return "unsupported variant (fan-in 8 or 16; activation identity|relu; pool mean|sum|max|topk_mean|lme|power|softmax)";
     case GL_ERR_WORKSPACE: return "workspace or output buffer smaller than required";
-    case GL_ERR_LDS: return "input tile (D features x 4 tokens x 4 bytes) exceeds the device's LDS per workgroup";
+    case GL_ERR_LDS: return "a kernel's LDS working set exceeds the device's LDS per workgroup";
     case GL_ERR_EDGES: return "edge structure does not match this layer shape";
     case GL_ERR_DEVICE: return "no current HIP device or device attribute query failed";
     case GL_ERR_SCRATCH:

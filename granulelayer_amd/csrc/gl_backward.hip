@@ -83,21 +83,21 @@ struct BwK {
 // One token tile of the dW pass (LDS at xsb): recompute z, form dz = c1 * act'(z), accumulate
 // db, dW and the tile's 4 mask bits (bit 4 (t % 8) + i of word mw for token i of tile t).  The
 // first RA LDS reads of neuron j + 1 are issued before the arithmetic of neuron j.
-template <int K, int NPL, int ACT, int RA, bool FAR>
-__device__ __forceinline__ void bwd_w_tile(const char* xsb, int t, const float4 c1, const unsigned (&addr)[NPL][K],
+template <int K, int NPL, int ACT, int RA, bool FAR, typename SRC = const char*>
+__device__ __forceinline__ void bwd_w_tile(SRC xsb, int t, const float4 c1, const unsigned (&addr)[NPL][K],
                                            const float (&w)[NPL][K], const float (&bias)[NPL], float (&dw)[NPL][K],
                                            float (&dbv)[NPL], unsigned (&mw)[NPL]) {
   float4 xc[K];
 #pragma unroll
-  for (int k = 0; k < RA; ++k) xc[k] = lds_x<FAR>(xsb, addr[0][k]);
+  for (int k = 0; k < RA; ++k) xc[k] = gather_x<FAR>(xsb, addr[0][k]);
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
 #pragma unroll
-    for (int k = RA; k < K; ++k) xc[k] = lds_x<FAR>(xsb, addr[j][k]);
+    for (int k = RA; k < K; ++k) xc[k] = gather_x<FAR>(xsb, addr[j][k]);
     float4 xn[RA];
     if (j + 1 < NPL) {
 #pragma unroll
-      for (int k = 0; k < RA; ++k) xn[k] = lds_x<FAR>(xsb, addr[j + 1][k]);
+      for (int k = 0; k < RA; ++k) xn[k] = gather_x<FAR>(xsb, addr[j + 1][k]);
     }
     __builtin_amdgcn_sched_barrier(0);
     float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
@@ -136,9 +136,10 @@ __device__ __forceinline__ void bwd_w_tile(const char* xsb, int t, const float4 
 // VGPRs a wave has at 2 waves per SIMD with the dW accumulators live).  Otherwise one buffer:
 // load, wait, read.  The wave index goes through readfirstlane so the chunk's parameters and the
 // c1 row are addressed with scalar registers.
-template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF, bool WS = false>
+template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF, bool WS = false, bool XG = false>
 __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
-  __shared__ float4 xs[DBUF || WS ? 2 * XTILE_DB : XTILE_SB];
+  // XG (D > XTILE_SB): no LDS tile, the lanes gather from the token tiles in global memory
+  __shared__ float4 xs[DBUF || WS ? 2 * XTILE_DB : (XG ? 1 : XTILE_SB)];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   long long chunk = (long long)blockIdx.x * WAVES + wave;
@@ -227,7 +228,10 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
       }
     }
     for (int t = t0; t < t1 && !WS; ++t) {
-      if constexpr (DBUF) {
+      if constexpr (XG) {
+        const float4 c1 = ld_uniform4(c1row, t * BT);
+        bwd_w_tile<K, NPL, ACT, RA, false>(xbuf(p.xt + (long long)t * p.D, p.D), t, c1, addr, w, bias, dw, dbv, mw);
+      } else if constexpr (DBUF) {
         // buffer cur ^ 1 was last read in tile t - 1, which every wave finished before the barrier
         const int cur = t & 1;
         if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xs + (cur ^ 1) * XTILE_DB, p.D, NT);
@@ -654,9 +658,10 @@ struct BsK {
 // Neuron-stationary recompute pass of a smooth pool: per token tile z, dz = c1 f(z, c2, c3), db and dW
 // accumulated in registers over the chunk's tokens and added to the caller's buffers once; dz of
 // every valid neuron stored for the dX pass.  Token tiles stream through LDS as in bwd_w_kernel.
-template <int K, int NPL, int WAVES, int ACT, int OP, bool DBUF>
+template <int K, int NPL, int WAVES, int ACT, int OP, bool DBUF, bool XG = false>
 __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
-  __shared__ float4 xs[DBUF ? 2 * XTILE_DB : XTILE_SB];
+  // XG (D > XTILE_SB): no LDS tile, the lanes gather from the token tiles in global memory
+  __shared__ float4 xs[DBUF ? 2 * XTILE_DB : (XG ? 1 : XTILE_SB)];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   long long chunk = (long long)blockIdx.x * WAVES + wave;
@@ -699,8 +704,10 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
     __syncthreads();
   }
   for (int t = 0; t < p.n_tiles; ++t) {
-    const char* xb;
-    if constexpr (DBUF) {
+    const char* xb = nullptr;
+    const XBuf xg = xbuf(p.xt + (long long)t * p.D, p.D);  // XG: the tile in global memory
+    if constexpr (XG) {
+    } else if constexpr (DBUF) {
       const int cur = t & 1;
       if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xs + (cur ^ 1) * XTILE_DB, p.D, NT);
       xb = reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16);
@@ -716,7 +723,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
     for (int j = 0; j < NPL; ++j) {
       float4 xc[K];
 #pragma unroll
-      for (int k = 0; k < K; ++k) xc[k] = *reinterpret_cast<const float4*>(xb + addr[j][k]);
+      for (int k = 0; k < K; ++k) xc[k] = XG ? gather_x<false>(xg, addr[j][k]) : gather_x<false>(xb, addr[j][k]);
       float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
 #pragma unroll
       for (int k = 0; k < K; ++k) {
@@ -855,6 +862,9 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
 // dW pass: 4 neurons per lane in 12 waves at K = 8 (3 waves per SIMD), 3 in 8 waves at K = 16; a
 // workgroup covers 3072 neurons per staged token tile either way
 constexpr int bwd_npl(int K) { return K == 8 ? 4 : 3; }
+// the smooth pools' recompute pass keeps every gathered x of a neuron live across dz: fewer neurons
+// per lane at K = 16 keep it in registers
+constexpr int smooth_npl(int K) { return K == 8 ? 4 : 2; }
 constexpr int bwd_waves(int K) { return K == 8 ? 12 : 8; }
 
 struct BwdPlan {
@@ -876,7 +886,7 @@ static BwdPlan bwd_plan(int B, int D, int G, int S, int K, bool smooth = false) 
     if (c < 64) c = 64;
     if (c < q.bc_max) q.bc_max = (int)c;
   }
-  q.npl = bwd_npl(K);
+  q.npl = smooth ? smooth_npl(K) : bwd_npl(K);
   q.waves = bwd_waves(K);
   q.cpg = ceil_div(S, 64 * q.npl);
   q.n_chunks = (long long)G * q.cpg;
@@ -935,7 +945,9 @@ void edge_layout(int D, int G, int S, int K, EdgeHeader* h, size_t* total) {
 template <int K, int NPL, int WAVES, int ACT, int RA>
 static int launch_bwd_w(const BwK& k, hipStream_t s) {
   auto fn = k.win ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, true>
-                  : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true> : bwd_w_kernel<K, NPL, WAVES, ACT, RA, false>);
+                  : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true>
+                                     : (k.D <= XTILE_SB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false>
+                                                        : bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, false, true>));
   GL_LAUNCH(k.win ? GL_KERNEL_BWD_W_WIN : GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)),
             dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
@@ -972,8 +984,11 @@ static int launch_dx(int K, int T, const DxK& k, hipStream_t s) {
 
 template <int K, int ACT, int OP>
 static int launch_bwd_smooth_k(const BsK& k, hipStream_t s) {
-  constexpr int NPL = 4, WAVES = 8;
-  auto fn = k.D <= XTILE_DB ? bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, true> : bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, false>;
+  // neurons per lane: the plan's (its cpg chunks of 64 NPL slots cover every pool exactly)
+  constexpr int NPL = smooth_npl(K), WAVES = 8;
+  auto fn = k.D <= XTILE_DB ? bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, true>
+                            : (k.D <= XTILE_SB ? bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, false>
+                                               : bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, false, true>);
   GL_LAUNCH(GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)), dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;

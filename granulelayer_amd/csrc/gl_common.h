@@ -128,7 +128,8 @@ __device__ __forceinline__ int opaque(int v) {
 // A tile is D float4 slots (4 tokens per input feature).  Every lane copies 16-byte slots with
 // global_load_lds_dwordx4, which writes lane i's data to LDS at (wave-uniform base) + 16 i, so the
 // data never passes through VGPRs.  D <= XTILE_DB features: two static buffers, the next tile
-// lands while the current one is read; larger D (up to XTILE_SB): one buffer.
+// lands while the current one is read; larger D (up to XTILE_SB): one buffer; wider layers
+// gather from the token tiles in global memory (the XG kernel variants).
 constexpr int XTILE_DB = 4096;
 constexpr int XTILE_SB = 10112;
 
@@ -222,9 +223,24 @@ __device__ __forceinline__ float4 ld_uniform4(const float* row, int i) {
 // asm so the compiler keeps doing that add at the read instead of hoisting a second copy of every
 // address out of the tile loop (which would not fit the register file).
 template <bool FAR>
-__device__ __forceinline__ float4 lds_x(const char* buf, unsigned a) {
+__device__ __forceinline__ float4 gather_x(const char* buf, unsigned a) {
   if constexpr (FAR) asm volatile("" : "+v"(a));
   return *reinterpret_cast<const float4*>(buf + a);
+}
+// The same gather from a token tile in global memory (the XG kernels, D > XTILE_SB): a buffer
+// resource over the tile (wave-uniform, in SGPRs) and the slot's 32-bit byte offset, one
+// buffer_load_dwordx4 per read with no 64-bit address arithmetic; reads past the tile return 0.
+struct XBuf {
+  __amdgpu_buffer_rsrc_t r;
+};
+__device__ __forceinline__ XBuf xbuf(const float4* tile, int D) {
+  // dword 3 0x00020000: raw 32-bit data, the gfx9 buffer format of untyped loads
+  return XBuf{__builtin_amdgcn_make_buffer_rsrc(const_cast<float4*>(tile), (short)0, D * 16, 0x00020000)};
+}
+template <bool FAR>
+__device__ __forceinline__ float4 gather_x(XBuf b, unsigned a) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)a, 0, 0);
+  return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
 }
 // this wave's tile loads have reached LDS (vmcnt(0)); a barrier then publishes every wave's
 __device__ __forceinline__ void stage_wait() { __builtin_amdgcn_s_waitcnt(0x3f70); }

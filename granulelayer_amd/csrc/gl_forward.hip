@@ -70,21 +70,21 @@ struct FwdK {
 // pooled over the wave's neurons and lanes (wave_sum4; lanes 0-3 store the 4 token sums).  The
 // first RA LDS reads of neuron j + 1 are issued before the arithmetic of neuron j, so up to K + RA
 // reads are in flight per wave (the compiler's own schedule keeps two).
-template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8)>
-__device__ __forceinline__ void fwd_tile(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
+__device__ __forceinline__ void fwd_tile(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                          const float (&bias)[NPL], float* out, bool store, int lane) {
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
   float4 xc[K];
 #pragma unroll
-  for (int k = 0; k < RA; ++k) xc[k] = lds_x<FAR>(xsb, addr[0][k]);
+  for (int k = 0; k < RA; ++k) xc[k] = gather_x<FAR>(xsb, addr[0][k]);
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
 #pragma unroll
-    for (int k = RA; k < K; ++k) xc[k] = lds_x<FAR>(xsb, addr[j][k]);
+    for (int k = RA; k < K; ++k) xc[k] = gather_x<FAR>(xsb, addr[j][k]);
     float4 xn[RA];
     if (j + 1 < NPL) {
 #pragma unroll
-      for (int k = 0; k < RA; ++k) xn[k] = lds_x<FAR>(xsb, addr[j + 1][k]);
+      for (int k = 0; k < RA; ++k) xn[k] = gather_x<FAR>(xsb, addr[j + 1][k]);
     }
     __builtin_amdgcn_sched_barrier(0);
     float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
@@ -119,23 +119,23 @@ __device__ __forceinline__ void fwd_tile(const char* xsb, const unsigned (&addr)
 // smaller slot on ties), reduced over the lanes by wave_max4; lanes 0-3 store value and slot.
 // Padded slots carry z = -inf (bias -inf, weights 0) and slots >= n_g, so they never win: with
 // relu they tie at 0 with a valid slot and lose on the slot.
-template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8)>
-__device__ __forceinline__ void fwd_tile_max(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
+__device__ __forceinline__ void fwd_tile_max(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                              const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
                                              bool store, int lane) {
   float m0 = -__builtin_inff(), m1 = m0, m2 = m0, m3 = m0;
   int s0 = 0x7fffffff, s1 = s0, s2 = s0, s3 = s0;
   float4 xc[K];
 #pragma unroll
-  for (int k = 0; k < RA; ++k) xc[k] = lds_x<FAR>(xsb, addr[0][k]);
+  for (int k = 0; k < RA; ++k) xc[k] = gather_x<FAR>(xsb, addr[0][k]);
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
 #pragma unroll
-    for (int k = RA; k < K; ++k) xc[k] = lds_x<FAR>(xsb, addr[j][k]);
+    for (int k = RA; k < K; ++k) xc[k] = gather_x<FAR>(xsb, addr[j][k]);
     float4 xn[RA];
     if (j + 1 < NPL) {
 #pragma unroll
-      for (int k = 0; k < RA; ++k) xn[k] = lds_x<FAR>(xsb, addr[j + 1][k]);
+      for (int k = 0; k < RA; ++k) xn[k] = gather_x<FAR>(xsb, addr[j + 1][k]);
     }
     __builtin_amdgcn_sched_barrier(0);
     float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
@@ -255,23 +255,23 @@ __device__ __forceinline__ cand_t wave_max4_key(cand_t a0, cand_t a1, cand_t a2,
 // wave's neurons with their slots (ties to the smaller slot), best first.  Every lane sorts its 4
 // candidates per token; then k rounds take the wave's best head (wave_max4_key) and drop it from
 // the lane that holds it.  Lanes 0-3 store each round's pair; the finalize merges the pool's chunks.
-template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8)>
-__device__ __forceinline__ void fwd_tile_topk(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
+__device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                               const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
                                               int k, bool store, int lane) {
   static_assert(NPL == 4, "per-lane candidate lists of 4");
   cand_t c[4][4];  // [token][position]
   float4 xc[K];
 #pragma unroll
-  for (int k0 = 0; k0 < RA; ++k0) xc[k0] = lds_x<FAR>(xsb, addr[0][k0]);
+  for (int k0 = 0; k0 < RA; ++k0) xc[k0] = gather_x<FAR>(xsb, addr[0][k0]);
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
 #pragma unroll
-    for (int kk = RA; kk < K; ++kk) xc[kk] = lds_x<FAR>(xsb, addr[j][kk]);
+    for (int kk = RA; kk < K; ++kk) xc[kk] = gather_x<FAR>(xsb, addr[j][kk]);
     float4 xn[RA];
     if (j + 1 < NPL) {
 #pragma unroll
-      for (int kk = 0; kk < RA; ++kk) xn[kk] = lds_x<FAR>(xsb, addr[j + 1][kk]);
+      for (int kk = 0; kk < RA; ++kk) xn[kk] = gather_x<FAR>(xsb, addr[j + 1][kk]);
     }
     __builtin_amdgcn_sched_barrier(0);
     float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
@@ -356,22 +356,22 @@ __device__ __forceinline__ void wave_merge4(const float (&m)[4], const float (&s
 // the lane's neurons for the tile's 4 tokens, then per token the lane's state over its valid neurons
 // (vmask bit j: neuron j valid) -- the largest u (or a), the sum of 2^(u - m) (or (a / m)^p) and, for
 // softmax-weighted, of 2^(u - m) a -- merged over the wave; lanes 0-3 store (m, s, t) per token.
-template <int K, int NPL, int ACT, bool FAR, int OP, int RA = (K == 8 ? 4 : 8)>
-__device__ __forceinline__ void fwd_tile_smooth(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+template <int K, int NPL, int ACT, bool FAR, int OP, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
+__device__ __forceinline__ void fwd_tile_smooth(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                                 const float (&bias)[NPL], unsigned vmask, float* out, bool store,
                                                 int lane, float scale, float p, int pint) {
   float z[NPL][4];
   float4 xc[K];
 #pragma unroll
-  for (int k = 0; k < RA; ++k) xc[k] = lds_x<FAR>(xsb, addr[0][k]);
+  for (int k = 0; k < RA; ++k) xc[k] = gather_x<FAR>(xsb, addr[0][k]);
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
 #pragma unroll
-    for (int k = RA; k < K; ++k) xc[k] = lds_x<FAR>(xsb, addr[j][k]);
+    for (int k = RA; k < K; ++k) xc[k] = gather_x<FAR>(xsb, addr[j][k]);
     float4 xn[RA];
     if (j + 1 < NPL) {
 #pragma unroll
-      for (int k = 0; k < RA; ++k) xn[k] = lds_x<FAR>(xsb, addr[j + 1][k]);
+      for (int k = 0; k < RA; ++k) xn[k] = gather_x<FAR>(xsb, addr[j + 1][k]);
     }
     __builtin_amdgcn_sched_barrier(0);
     float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
@@ -440,8 +440,8 @@ constexpr bool pk_smooth(int pk) { return pk >= PK_LME; }
 constexpr int pk_sm_op(int pk) { return pk == PK_LME ? SM_LME : (pk == PK_POW ? SM_POW : SM_SW); }
 
 // sum / mean, max or top-k tile
-template <int K, int NPL, int ACT, bool FAR, int PK>
-__device__ __forceinline__ void fwd_tile_any(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+template <int K, int NPL, int ACT, bool FAR, int PK, typename SRC = const char*>
+__device__ __forceinline__ void fwd_tile_any(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                              const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
                                              int k, bool store, int lane) {
   if constexpr (PK == PK_MAX) fwd_tile_max<K, NPL, ACT, FAR>(xsb, addr, w, bias, slot, out, oslot, store, lane);
@@ -450,8 +450,8 @@ __device__ __forceinline__ void fwd_tile_any(const char* xsb, const unsigned (&a
 }
 
 // smooth pools: the tile needs the validity bits and the operator's parameters
-template <int K, int NPL, int ACT, bool FAR, int PK>
-__device__ __forceinline__ void fwd_tile_dispatch(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+template <int K, int NPL, int ACT, bool FAR, int PK, typename SRC = const char*>
+__device__ __forceinline__ void fwd_tile_dispatch(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                                   const float (&bias)[NPL], const int (&slot)[NPL], unsigned vmask,
                                                   float* out, int* oslot, int k, bool store, int lane, const FwdK& p) {
   if constexpr (pk_smooth(PK))
@@ -461,10 +461,10 @@ __device__ __forceinline__ void fwd_tile_dispatch(const char* xsb, const unsigne
     fwd_tile_any<K, NPL, ACT, FAR, PK>(xsb, addr, w, bias, slot, out, oslot, k, store, lane);
 }
 
-template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, int PK = PK_SUM>
+template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, int PK = PK_SUM, bool XG = false>
 __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
-  // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots)
-  __shared__ float4 xa[WS ? 2 * XTILE_DB : (DBUF ? XTILE_DB : XTILE_SB)];
+  // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots); XG: no LDS tile
+  __shared__ float4 xa[WS ? 2 * XTILE_DB : (XG ? 1 : (DBUF ? XTILE_DB : XTILE_SB))];
   __shared__ float4 xb[DBUF ? XTILE_DB : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar chunk addressing
@@ -544,6 +544,13 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       stage_wait();
       __syncthreads();
     }
+  } else if constexpr (XG) {
+    // D too wide for an LDS tile: the lanes gather their 16-byte slots straight from the token tile
+    // in global memory with buffer loads (D x 16 bytes, L2-resident while the workgroups of the
+    // launch read it), with no staging and no barriers
+    for (int t = 0; t < p.n_tiles; ++t)
+      fwd_tile_dispatch<K, NPL, ACT, false, PK>(xbuf(p.xt + (long long)t * p.D, p.D), addr, w, bias, slot, vmask,
+                                                out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
   } else if constexpr (DBUF) {
     dma_tile(p.xt, xa, p.D, NT);
     for (int t = 0; t < p.n_tiles; t += 2) {
@@ -844,9 +851,9 @@ static FwdPlan fwd_plan(const GlFwdArgs* a, long long bf_cap = 0) {
   return q;
 }
 
-template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS, int PK>
+template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS, int PK, bool XG = false>
 static int launch_fwd(const FwdK& k, hipStream_t s) {
-  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, PK>;
+  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, PK, XG>;
   dim3 grid((unsigned)ceil_div(k.n_chunks, WAVES));
   GL_LAUNCH(WS ? GL_KERNEL_FWD_WIN : GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
@@ -854,11 +861,12 @@ static int launch_fwd(const FwdK& k, hipStream_t s) {
 }
 
 // one workgroup per CU (the tile buffers take the LDS); pool windows when they fit, else two tile
-// buffers when D fits them, else one
+// buffers when D fits them, else one, else (D > XTILE_SB) gathers from the tiles in global memory
 template <int ACT, int K, int PK>
 static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
   constexpr int W = fwd_waves(K, PK);
   if (k.win) return launch_fwd<K, FWD_NPL, W, ACT, false, true, PK>(k, s);
+  if (D > XTILE_SB) return launch_fwd<K, FWD_NPL, W, ACT, false, false, PK, true>(k, s);
   return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true, false, PK>(k, s)
                        : launch_fwd<K, FWD_NPL, W, ACT, false, false, PK>(k, s);
 }
@@ -896,7 +904,7 @@ int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void
   if (pool < GL_POOL_MEAN || pool > GL_POOL_SOFTMAX) return GL_ERR_UNSUPPORTED;
   if (x_dtype != GL_DTYPE_F32 && x_dtype != GL_DTYPE_BF16) return GL_ERR_UNSUPPORTED;
   if ((long long)G * S > (1LL << 31) / 16) return GL_ERR_UNSUPPORTED;
-  if (D > XTILE_SB) return GL_ERR_LDS;  // one token tile (D x 16 bytes) must fit the LDS tile buffer
+  if (D > GL_MAX_INPUTS) return GL_ERR_UNSUPPORTED;  // wider tiles gather from global memory (XG kernels)
   return 0;
 }
 

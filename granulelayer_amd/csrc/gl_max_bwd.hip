@@ -38,6 +38,7 @@ struct MaxEvK {
   int rs;     // log2 slots per shared index record
   bool topk;  // coef = g_pre / min(n_g, kpe)
   int sps, gs;  // pool geometry (pool_base)
+  int dblk;     // dX: inputs per block (D when the token's row, bounds and accumulators fit the LDS)
 };
 
 // x[b, d] of the chunk's token b from the token tiles
@@ -134,82 +135,101 @@ __device__ __forceinline__ double pow2(int e) {
   return __longlong_as_double((long long)(1023 + e) << 52);
 }
 
-// dX of one token.  LDS: D 64-bit fixed-point accumulators, the token's X row (D floats), then per
-// input the bound of its terms (float bits), replaced by the input's scale exponent.
+// dX of one token, its inputs in blocks of dblk (the whole row when it fits the LDS).  LDS: dblk
+// 64-bit fixed-point accumulators, the inputs' term bounds (float bits, replaced by each input's
+// scale exponent), then, with a single block, the token's X row (with several, x is read from the
+// token tile in global memory).  Every input's sum and scale depend only on its own terms, so the
+// blocking does not change the result.
 template <int K, int ACT>
 __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
   extern __shared__ unsigned long long ldsq[];
-  unsigned long long* acc = ldsq;                                       // [D]
-  float* xrow = reinterpret_cast<float*>(ldsq + p.D);                    // [D]
-  unsigned* tmax = reinterpret_cast<unsigned*>(xrow + p.D);              // [D]
+  const int DB = p.dblk;
+  const bool one = DB >= p.D;
+  unsigned long long* acc = ldsq;                          // [DB]
+  unsigned* tmax = reinterpret_cast<unsigned*>(ldsq + DB);  // [DB]
+  float* xrow = reinterpret_cast<float*>(tmax + DB);        // [D], single block only
   const int b = blockIdx.x;
   const long long row = (long long)(p.b0 + b) * p.G;  // [B, G] row of the token; winners: row * kpe
-  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
-    xrow[d] = tile_x(p.xt, p.D, b, d);
-    acc[d] = 0ull;
-    tmax[d] = 0u;
-  }
-  __syncthreads();
-  // pass 1: every term dz * W[n*, k] into input d = idx[n*, k] is at most |g_pre| * |W[n*, k]|;
-  // tmax[d] = the largest such bound (the bits of non-negative floats order like the values, so
-  // the integer maximum is the float maximum, whatever the order of the updates)
-  for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
-    const int g = e / p.kpe;
-    const int s = p.winner[row * p.kpe + e];
-    if (s < 0 || s >= pool_ext(g, p.S, p.sps, p.gs)) continue;
-    const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
-    const float gb = __builtin_fabsf(p.g_pre[row + g]);
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      int d = rec_index(p.idx, n, k, K, p.rs);
-      d = d < 0 ? 0 : (d >= p.D ? p.D - 1 : d);
-      atomicMax(&tmax[d], __float_as_uint(gb * __builtin_fabsf(p.W[n * K + k])));
-    }
-  }
-  __syncthreads();
-  // per input: at most G * kpe * K terms of magnitude <= tmax[d], so |sum| * 2^e_d < 2^62 with
-  // e_d = 61 - floor(log2(tmax[d] * G * kpe * K)); floor(log2) read from the (normal) double's
-  // exponent field.  The scale follows each input's own largest term: small inputs keep ~2^-38
-  // (at 2^23 terms) of their own magnitude, not of the token's largest term.
+  if (one)
+    for (int d = threadIdx.x; d < p.D; d += blockDim.x) xrow[d] = tile_x(p.xt, p.D, b, d);
   const double nterm = (double)p.G * (double)p.kpe * (double)K;
-  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
-    const double bound = (double)__uint_as_float(tmax[d]) * nterm;
-    const int e2 = bound > 0.0 ? (int)((__double_as_longlong(bound) >> 52) & 0x7ff) - 1023 : 0;
-    tmax[d] = (unsigned)(61 - e2);  // a signed exponent, stored in the same word
-  }
-  __syncthreads();
-  // pass 2: the events' dz * W[n*, k] as fixed-point integers at their input's scale
-  for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
-    const int g = e / p.kpe;
-    int s = p.winner[row * p.kpe + e];
-    const bool ok = s >= 0 && s < pool_ext(g, p.S, p.sps, p.gs);
-    s = ok ? s : 0;
-    const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
-    float xk[K], wk[K];
-    int dk[K];
-    float coef = p.g_pre[row + g];
-    if (p.topk) {  // the same expression as c1t_kernel's
-      const int n_g = p.counts[g];
-      coef = coef / (float)(n_g < p.kpe ? n_g : p.kpe);
+  for (int lo = 0; lo < p.D; lo += DB) {
+    const int nb = p.D - lo < DB ? p.D - lo : DB;
+    for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+      acc[i] = 0ull;
+      tmax[i] = 0u;
     }
-    const float dz = event_dz<K, ACT>(p, n, coef, [&](int d) { return xrow[d]; }, xk, wk, dk);
-    if (!ok || dz == 0.f) continue;
+    __syncthreads();
+    // pass 1: every term dz * W[n*, k] into input d = idx[n*, k] is at most |g_pre| * |W[n*, k]|;
+    // tmax[d] = the largest such bound (the bits of non-negative floats order like the values, so
+    // the integer maximum is the float maximum, whatever the order of the updates)
+    for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
+      const int g = e / p.kpe;
+      const int s = p.winner[row * p.kpe + e];
+      if (s < 0 || s >= pool_ext(g, p.S, p.sps, p.gs)) continue;
+      const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
+      const float gb = __builtin_fabsf(p.g_pre[row + g]);
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const long long q = __double2ll_rn((double)(dz * wk[k]) * pow2((int)tmax[dk[k]]));
-      atomicAdd(&acc[dk[k]], (unsigned long long)q);
+      for (int k = 0; k < K; ++k) {
+        int d = rec_index(p.idx, n, k, K, p.rs);
+        d = d < 0 ? 0 : (d >= p.D ? p.D - 1 : d);
+        if ((unsigned)(d - lo) < (unsigned)nb) atomicMax(&tmax[d - lo], __float_as_uint(gb * __builtin_fabsf(p.W[n * K + k])));
+      }
     }
+    __syncthreads();
+    // per input: at most G * kpe * K terms of magnitude <= tmax[d], so |sum| * 2^e_d < 2^62 with
+    // e_d = 61 - floor(log2(tmax[d] * G * kpe * K)); floor(log2) read from the (normal) double's
+    // exponent field.  The scale follows each input's own largest term: small inputs keep ~2^-38
+    // (at 2^23 terms) of their own magnitude, not of the token's largest term.
+    for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+      const double bound = (double)__uint_as_float(tmax[i]) * nterm;
+      const int e2 = bound > 0.0 ? (int)((__double_as_longlong(bound) >> 52) & 0x7ff) - 1023 : 0;
+      tmax[i] = (unsigned)(61 - e2);  // a signed exponent, stored in the same word
+    }
+    __syncthreads();
+    // pass 2: the events' dz * W[n*, k] as fixed-point integers at their input's scale
+    for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
+      const int g = e / p.kpe;
+      int s = p.winner[row * p.kpe + e];
+      const bool ok = s >= 0 && s < pool_ext(g, p.S, p.sps, p.gs);
+      s = ok ? s : 0;
+      const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
+      float xk[K], wk[K];
+      int dk[K];
+      float coef = p.g_pre[row + g];
+      if (p.topk) {  // the same expression as c1t_kernel's
+        const int n_g = p.counts[g];
+        coef = coef / (float)(n_g < p.kpe ? n_g : p.kpe);
+      }
+      const float dz = event_dz<K, ACT>(
+          p, n, coef, [&](int d) { return one ? xrow[d] : tile_x(p.xt, p.D, b, d); }, xk, wk, dk);
+      if (!ok || dz == 0.f) continue;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int i = dk[k] - lo;
+        if ((unsigned)i >= (unsigned)nb) continue;
+        const long long q = __double2ll_rn((double)(dz * wk[k]) * pow2((int)tmax[i]));
+        atomicAdd(&acc[i], (unsigned long long)q);
+      }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nb; i += blockDim.x)
+      p.dX[(long long)(p.b0 + b) * p.D + lo + i] = (float)((double)(long long)acc[i] / pow2((int)tmax[i]));
+    __syncthreads();  // the next block reinitialises acc and tmax
   }
-  __syncthreads();
-  for (int d = threadIdx.x; d < p.D; d += blockDim.x)
-    p.dX[(long long)(p.b0 + b) * p.D + d] = (float)((double)(long long)acc[d] / pow2((int)tmax[d]));
 }
 
 template <int K, int ACT>
-static int launch_max_events_k(const MaxEvK& k, hipStream_t s) {
+static int launch_max_events_k(MaxEvK k, hipStream_t s) {
   const size_t dw_lds = (size_t)k.npow2 * 4 + (size_t)k.tsub * k.kpe * (K + 1) * 4;
-  const size_t dx_lds = (size_t)k.D * 16;
-  if (dw_lds > max_lds_bytes() || dx_lds > max_lds_bytes()) return GL_ERR_LDS;
+  // dX: the whole row (16 bytes per input) when it fits, else blocks of 12-byte inputs
+  size_t dx_lds = (size_t)k.D * 16;
+  k.dblk = k.D;
+  if (dx_lds > max_lds_bytes()) {
+    k.dblk = (int)(max_lds_bytes() / 12 / 64 * 64);
+    dx_lds = (size_t)k.dblk * 12;
+  }
+  if (dw_lds > max_lds_bytes() || k.dblk < 64) return GL_ERR_LDS;
   GL_TRY(set_lds_limit((const void*)max_events_dw_kernel<K, ACT>, dw_lds));
   GL_TRY(set_lds_limit((const void*)max_events_dx_kernel<K, ACT>, dx_lds));
   GL_LAUNCH(GL_KERNEL_MAX_EV_DW, (max_events_dw_kernel<K, ACT>), dim3((unsigned)k.G), dim3(256), dw_lds, s, k);
@@ -225,7 +245,7 @@ int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s) {
   int npow2 = 1;
   while (npow2 < tsub * a.kpe) npow2 <<= 1;
   const MaxEvK k{a.xt, a.idx, a.W, a.bias, a.counts, a.c1t, a.wint, a.g_pre, a.winner, a.dW, a.db, a.dX,
-                 a.D, a.G, a.S, a.cap, a.Bc, a.b0, npow2, a.kpe, tsub, a.rs, a.topk, a.sps, a.gs};
+                 a.D, a.G, a.S, a.cap, a.Bc, a.b0, npow2, a.kpe, tsub, a.rs, a.topk, a.sps, a.gs, a.D};
   if (K == 8) return act == GL_ACT_RELU ? launch_max_events_k<8, GL_ACT_RELU>(k, s) : launch_max_events_k<8, GL_ACT_IDENTITY>(k, s);
   return act == GL_ACT_RELU ? launch_max_events_k<16, GL_ACT_RELU>(k, s) : launch_max_events_k<16, GL_ACT_IDENTITY>(k, s);
 }

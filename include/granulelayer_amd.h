@@ -35,11 +35,15 @@ enum {
   GL_ERR_ARG = -1,          /* invalid argument, shape or null pointer */
   GL_ERR_UNSUPPORTED = -2,  /* valid request this build does not implement (e.g. K not in {8,16}) */
   GL_ERR_WORKSPACE = -3,    /* workspace / output buffer smaller than required */
-  GL_ERR_LDS = -4,          /* the input tile (D features x 4 tokens) exceeds the device's LDS */
+  GL_ERR_LDS = -4,          /* a kernel's LDS working set exceeds the device's LDS */
   GL_ERR_EDGES = -5,        /* edge structure built for a different layer shape */
   GL_ERR_DEVICE = -7,       /* no current HIP device or attribute query failed */
   GL_ERR_SCRATCH = -8       /* gl_fwd_static: one token tile of this layer exceeds the static scratch */
 };
+/* Largest input width D: the reference's int16 indices allow 32767 (sparse_pooling/layout.py:57-58).
+ * D <= 4096 stages two token tiles in LDS, D <= 10112 one; wider layers gather X from the token
+ * tiles in global memory (same results). */
+#define GL_MAX_INPUTS 65536
 enum { GL_ACT_IDENTITY = 0, GL_ACT_RELU = 1 };
 /* max: pytorch_reference.py:61-67 (winner = first maximum of act(z) over the pool's valid
  * slots), merged as kernels/ops.py:189-195; top-k mean: pytorch_reference.py:68-77 (the k largest
