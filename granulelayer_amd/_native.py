@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgranulelayer_amd.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 GL_ACT = {"identity": 0, "relu": 1}
 GL_POOL = {"mean": 0, "sum": 1, "max": 2, "topk_mean": 3, "logmeanexp": 4, "power_mean": 5, "softmax_weighted": 6}
@@ -48,7 +48,8 @@ class GlEdgeArgs(ctypes.Structure):
 
 class GlAdamArgs(ctypes.Structure):
     _fields_ = [("p", _P), ("g", _P), ("m", _P), ("v", _P), ("n", _I64), ("moments_dtype", _I32), ("lr", _F),
-                ("beta1", _F), ("beta2", _F), ("eps", _F), ("weight_decay", _F), ("bc1", _F), ("bc2", _F)]
+                ("beta1", _F), ("beta2", _F), ("eps", _F), ("weight_decay", _F), ("bc1", _F), ("bc2", _F),
+                ("p_dtype", _I32), ("stochastic", _I32), ("master", _P), ("seed", ctypes.c_uint64)]
 
 
 class GlCoverArgs(ctypes.Structure):

@@ -317,18 +317,29 @@ class HipBackend:
         return dx
 
     # ------------------------------------------------------------------ optimizer
-    def adam(self, p, g, m, v, lr, beta1, beta2, eps, weight_decay, bc1, bc2):
-        """In-place fused AdamW over fp32 p (and fp32 g); m/v fp32 or bf16."""
-        for name, t in (("param", p), ("grad", g)):
-            if t.dtype != torch.float32 or not t.is_contiguous():
-                raise TypeError(f"{name} must be a contiguous float32 tensor")
+    def adam(self, p, g, m, v, lr, beta1, beta2, eps, weight_decay, bc1, bc2, master=None, stochastic=False, seed=0):
+        """In-place fused AdamW: p fp32 or bf16, g fp32 (zeroed), m/v fp32 or bf16.  bf16 p: with an
+        fp32 ``master`` copy the update runs on it and p gets its nearest-even rounding; otherwise
+        p is rounded stochastically (``stochastic``, Philox noise of ``seed``) or to nearest even
+        (sparse_pooling/optim.py:26-64)."""
+        if p.dtype not in (torch.float32, torch.bfloat16) or not p.is_contiguous():
+            raise TypeError("param must be a contiguous float32 or bfloat16 tensor")
+        if g.dtype != torch.float32 or not g.is_contiguous():
+            raise TypeError("grad must be a contiguous float32 tensor")
         if m.dtype != v.dtype or m.dtype not in (torch.float32, torch.bfloat16):
             raise TypeError("moments must both be float32 or bfloat16")
         if not (p.numel() == g.numel() == m.numel() == v.numel()):
             raise ValueError("param, grad and moments must have the same number of elements")
+        if master is not None and (p.dtype != torch.bfloat16 or master.dtype != torch.float32
+                                   or not master.is_contiguous() or master.numel() != p.numel()):
+            raise ValueError("master must be a contiguous float32 copy of a bfloat16 parameter")
+        bf = p.dtype == torch.bfloat16
         a = N.GlAdamArgs(p=_ptr(p), g=_ptr(g), m=_ptr(m), v=_ptr(v), n=p.numel(),
                          moments_dtype=N.GL_DTYPE_F32 if m.dtype == torch.float32 else N.GL_DTYPE_BF16,
-                         lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, bc1=bc1, bc2=bc2)
+                         lr=lr, beta1=beta1, beta2=beta2, eps=eps, weight_decay=weight_decay, bc1=bc1, bc2=bc2,
+                         p_dtype=N.GL_DTYPE_BF16 if bf else N.GL_DTYPE_F32,
+                         stochastic=int(bf and master is None and stochastic), master=_ptr(master),
+                         seed=int(seed) & (2**64 - 1))
         with torch.cuda.device(p.device):
             self.lib.call("gl_adam", ctypes.byref(a), ctypes.c_void_p(_stream(p.device)))
 

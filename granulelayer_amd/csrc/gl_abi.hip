@@ -123,7 +123,8 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
       typedef GlAdamArgs S;
       long long t[] = {(long long)sizeof(S), OFF(S, p), OFF(S, g), OFF(S, m), OFF(S, v), OFF(S, n),
                        OFF(S, moments_dtype), OFF(S, lr), OFF(S, beta1), OFF(S, beta2), OFF(S, eps),
-                       OFF(S, weight_decay), OFF(S, bc1), OFF(S, bc2)};
+                       OFF(S, weight_decay), OFF(S, bc1), OFF(S, bc2), OFF(S, p_dtype), OFF(S, stochastic),
+                       OFF(S, master), OFF(S, seed)};
       for (long long x : t) v[c++] = x;
       break;
     }

@@ -1,6 +1,7 @@
-// Fused AdamW over fp32 parameters: one streaming pass reads p, g, m, v and writes p, m, v and
-// g = 0 (32 bytes per element with fp32 moments, 24 with bf16 moments).
-// Reference: _adamw_kernel, sparse_pooling/optim.py:26-64 (HAS_MASTER = STOCH = False).  The
+// Fused AdamW: one streaming pass reads p, g, m, v (and an fp32 master copy) and writes p, m, v and
+// g = 0 (32 bytes per element with fp32 parameters and moments, 24 with bf16 moments).
+// Reference: _adamw_kernel, sparse_pooling/optim.py:26-64 (fp32 parameters; bf16 parameters with
+// HAS_MASTER, with STOCH, or rounded to nearest even).  The
 // update is evaluated unfused in the reference's operation order; every element is read and
 // written by the same thread, so the in-place race fixed at optim.py:43-50 cannot occur.
 #include "gl_common.h"
@@ -41,15 +42,63 @@ __device__ __forceinline__ void st_nt(void* p, long long i, T v) {
   __builtin_nontemporal_store(v, reinterpret_cast<T*>(p) + i);
 }
 
-template <bool BF16M>
-__global__ void __launch_bounds__(256) adam_kernel(float* __restrict__ P, float* __restrict__ Gr, void* __restrict__ M,
-                                                   void* __restrict__ V, long long n, AdamK c) {
+// Parameter storage of the update: fp32, or bf16 rounded to nearest even, bf16 with an fp32
+// master copy (the update runs on the master, the parameter gets its rounding), or bf16 with
+// stochastic rounding (optim.py:59-62).
+enum { PM_F32 = 0, PM_BF16_RNE = 1, PM_BF16_MASTER = 2, PM_BF16_SR = 3 };
+
+// Triton's tl.randint(seed, offset) (triton/language/random.py, 3.6): Philox-4x32-10 (Salmon et
+// al., SC'11) of the counter (offset low, offset high, 0, 0) under the key (seed low, seed high),
+// first output word.
+__device__ __forceinline__ unsigned philox_randint(unsigned long long seed, unsigned long long off) {
+  unsigned c0 = (unsigned)off, c1 = (unsigned)(off >> 32), c2 = 0u, c3 = 0u;
+  unsigned k0 = (unsigned)seed, k1 = (unsigned)(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const unsigned h0 = __umulhi(0xD2511F53u, c0), l0 = 0xD2511F53u * c0;
+    const unsigned h1 = __umulhi(0xCD9E8D57u, c2), l1 = 0xCD9E8D57u * c2;
+    c0 = h1 ^ c1 ^ k0;
+    c2 = h0 ^ c3 ^ k1;
+    c1 = l1;
+    c3 = l0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c0;
+}
+
+// the bf16 parameter of element i from its fp32 update p
+template <int PM>
+__device__ __forceinline__ unsigned short round_param(float p, unsigned long long seed, long long i) {
+  if constexpr (PM == PM_BF16_SR) {
+    const unsigned u = (__float_as_uint(p) + (philox_randint(seed, (unsigned long long)i) & 0xffffu)) & 0xffff0000u;
+    return (unsigned short)(u >> 16);
+  } else {
+    return f32_to_bf16_rne(p);
+  }
+}
+
+template <bool BF16M, int PM>
+__global__ void __launch_bounds__(256) adam_kernel(void* __restrict__ P, float* __restrict__ Gr, void* __restrict__ M,
+                                                   void* __restrict__ V, float* __restrict__ MS, long long n, AdamK c,
+                                                   unsigned long long seed) {
+  constexpr bool BP = PM != PM_F32;  // bf16 parameter storage
   const long long n4 = n >> 2;
   const long long stride = (long long)gridDim.x * blockDim.x;
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-    const f4v pv = ld_nt<f4v>(P, i);
     const f4v g = ld_nt<f4v>(Gr, i);
-    float4 p = make_float4(pv.x, pv.y, pv.z, pv.w);
+    float4 p;
+    if constexpr (PM == PM_F32) {
+      const f4v pv = ld_nt<f4v>(P, i);
+      p = make_float4(pv.x, pv.y, pv.z, pv.w);
+    } else if constexpr (PM == PM_BF16_MASTER) {
+      const f4v pv = ld_nt<f4v>(MS, i);
+      p = make_float4(pv.x, pv.y, pv.z, pv.w);
+    } else {
+      const unsigned long long pb = ld_nt<unsigned long long>(P, i);
+      p = make_float4(bf16_bits_to_f32((unsigned short)pb), bf16_bits_to_f32((unsigned short)(pb >> 16)),
+                      bf16_bits_to_f32((unsigned short)(pb >> 32)), bf16_bits_to_f32((unsigned short)(pb >> 48)));
+    }
     float4 m, v;
     if constexpr (BF16M) {
       const unsigned long long mb = ld_nt<unsigned long long>(M, i), vb = ld_nt<unsigned long long>(V, i);
@@ -78,12 +127,25 @@ __global__ void __launch_bounds__(256) adam_kernel(float* __restrict__ P, float*
       st_nt<f4v>(V, i, (f4v){v.x, v.y, v.z, v.w});
     }
     st_nt<f4v>(Gr, i, (f4v){0.f, 0.f, 0.f, 0.f});
-    st_nt<f4v>(P, i, (f4v){p.x, p.y, p.z, p.w});
+    if constexpr (BP) {
+      if constexpr (PM == PM_BF16_MASTER) st_nt<f4v>(MS, i, (f4v){p.x, p.y, p.z, p.w});
+      const long long e = i << 2;
+      const unsigned long long po = (unsigned long long)round_param<PM>(p.x, seed, e) |
+                                    (unsigned long long)round_param<PM>(p.y, seed, e + 1) << 16 |
+                                    (unsigned long long)round_param<PM>(p.z, seed, e + 2) << 32 |
+                                    (unsigned long long)round_param<PM>(p.w, seed, e + 3) << 48;
+      st_nt<unsigned long long>(P, i, po);
+    } else {
+      st_nt<f4v>(P, i, (f4v){p.x, p.y, p.z, p.w});
+    }
   }
   // tail (n % 4 elements), handled by the first threads of block 0
   const long long t = (n4 << 2) + threadIdx.x;
   if (blockIdx.x == 0 && t < n) {
-    float p = P[t], g = Gr[t], m, v;
+    float g = Gr[t], m, v, p;
+    if constexpr (PM == PM_F32) p = reinterpret_cast<float*>(P)[t];
+    else if constexpr (PM == PM_BF16_MASTER) p = MS[t];
+    else p = bf16_bits_to_f32(reinterpret_cast<unsigned short*>(P)[t]);
     if constexpr (BF16M) {
       m = bf16_bits_to_f32(reinterpret_cast<unsigned short*>(M)[t]);
       v = bf16_bits_to_f32(reinterpret_cast<unsigned short*>(V)[t]);
@@ -100,8 +162,32 @@ __global__ void __launch_bounds__(256) adam_kernel(float* __restrict__ P, float*
       reinterpret_cast<float*>(V)[t] = v;
     }
     Gr[t] = 0.f;
-    P[t] = p;
+    if constexpr (BP) {
+      if constexpr (PM == PM_BF16_MASTER) MS[t] = p;
+      reinterpret_cast<unsigned short*>(P)[t] = round_param<PM>(p, seed, t);
+    } else {
+      reinterpret_cast<float*>(P)[t] = p;
+    }
   }
+}
+
+template <bool BF16M>
+static int launch_adam(int pm, dim3 grid, hipStream_t s, const GlAdamArgs* a, const AdamK& c) {
+  void* P = a->p;
+  if (pm == PM_F32)
+    GL_LAUNCH(GL_KERNEL_ADAM, (adam_kernel<BF16M, PM_F32>), grid, dim3(256), 0, s, P, a->g, a->m, a->v, a->master, a->n, c,
+              a->seed);
+  else if (pm == PM_BF16_RNE)
+    GL_LAUNCH(GL_KERNEL_ADAM, (adam_kernel<BF16M, PM_BF16_RNE>), grid, dim3(256), 0, s, P, a->g, a->m, a->v, a->master,
+              a->n, c, a->seed);
+  else if (pm == PM_BF16_MASTER)
+    GL_LAUNCH(GL_KERNEL_ADAM, (adam_kernel<BF16M, PM_BF16_MASTER>), grid, dim3(256), 0, s, P, a->g, a->m, a->v, a->master,
+              a->n, c, a->seed);
+  else
+    GL_LAUNCH(GL_KERNEL_ADAM, (adam_kernel<BF16M, PM_BF16_SR>), grid, dim3(256), 0, s, P, a->g, a->m, a->v, a->master,
+              a->n, c, a->seed);
+  GL_CHECK_LAUNCH();
+  return 0;
 }
 
 }  // namespace gl
@@ -113,10 +199,14 @@ extern "C" int gl_adam(const GlAdamArgs* a, void* stream) {
   if (a->n == 0) return 0;
   if (!a->p || !a->g || !a->m || !a->v) return GL_ERR_ARG;
   if (a->moments_dtype != GL_DTYPE_F32 && a->moments_dtype != GL_DTYPE_BF16) return GL_ERR_UNSUPPORTED;
-  // vector path needs 16-byte (8-byte for bf16 moments) alignment
-  const uintptr_t al = (uintptr_t)a->p | (uintptr_t)a->g;
+  if (a->p_dtype != GL_DTYPE_F32 && a->p_dtype != GL_DTYPE_BF16) return GL_ERR_UNSUPPORTED;
+  if (a->p_dtype == GL_DTYPE_F32 && (a->master || a->stochastic)) return GL_ERR_ARG;  // fp32 parameters round nothing
+  const int pm = a->p_dtype == GL_DTYPE_F32 ? PM_F32 : (a->master ? PM_BF16_MASTER : (a->stochastic ? PM_BF16_SR : PM_BF16_RNE));
+  // vector path: 16-byte fp32 streams (g, fp32 p, master), 8-byte bf16 streams (bf16 p, bf16 moments)
+  const uintptr_t a16 = (uintptr_t)a->g | (pm == PM_F32 ? (uintptr_t)a->p : 0) | (uintptr_t)a->master;
+  const uintptr_t a8 = (pm == PM_F32 ? 0 : (uintptr_t)a->p);
   const uintptr_t alm = (uintptr_t)a->m | (uintptr_t)a->v;
-  if ((al & 15) || (alm & (a->moments_dtype == GL_DTYPE_F32 ? 15 : 7))) return GL_ERR_ARG;
+  if ((a16 & 15) || (a8 & 7) || (alm & (a->moments_dtype == GL_DTYPE_F32 ? 15 : 7))) return GL_ERR_ARG;
   AdamK c{a->lr, a->beta1, a->beta2, a->eps, a->weight_decay, a->bc1, a->bc2};
   hipStream_t s = (hipStream_t)stream;
   // one vector per thread (a grid-stride loop covers grids past the launch limit)
@@ -124,10 +214,6 @@ extern "C" int gl_adam(const GlAdamArgs* a, void* stream) {
   long long blocks = (n4 + 255) / 256;
   if (blocks > (1LL << 30)) blocks = 1LL << 30;
   if (blocks < 1) blocks = 1;
-  if (a->moments_dtype == GL_DTYPE_F32)
-    GL_LAUNCH(GL_KERNEL_ADAM, adam_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, a->p, a->g, a->m, a->v, a->n, c);
-  else
-    GL_LAUNCH(GL_KERNEL_ADAM, adam_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, a->p, a->g, a->m, a->v, a->n, c);
-  GL_CHECK_LAUNCH();
-  return 0;
+  const dim3 grid((unsigned)blocks);
+  return a->moments_dtype == GL_DTYPE_F32 ? launch_adam<false>(pm, grid, s, a, c) : launch_adam<true>(pm, grid, s, a, c);
 }

@@ -1,13 +1,16 @@
-"""Fused AdamW for the fp32 layer parameters, mirroring sparse_pooling/optim.py (FusedAdamW).
+"""Fused AdamW for the layer parameters, mirroring sparse_pooling/optim.py (FusedAdamW).
 
 Reads the fp32 ``main_grad`` buffers written by the fused backward (or ``.grad``), updates the
 parameters and zeroes the gradient in the same streaming pass (the HIP kernel gl_adam).
 Semantics are dense AdamW for every element (optim.py:1-15): m = b1 m + (1-b1) g,
 v = b2 v + (1-b2) g^2, p = p (1 - lr wd) - lr (m / bc1) / (sqrt(v / bc2) + eps), bc_i = 1 - b_i^t.
 
-Moments are fp32 (``moments="fp32"``) or bf16 (``"bf16"``, the reference default).  The
-parameters must be fp32: the reference's bf16-parameter variants (master weights, stochastic
-rounding) are not on the MI355X path and raise NotImplementedError.
+Moments are fp32 (``moments="fp32"``) or bf16 (``"bf16"``, the reference default).  Parameters
+are fp32, or bf16 with the reference's three variants (optim.py:5-9, 52-62): an fp32 master copy
+in the optimizer state (``master_weights=True``; the update runs on it and the parameter gets its
+nearest-even rounding), stochastic rounding (the default without masters: noise from Triton's
+``tl.randint(seed, element)`` below the bf16 cut, the seed counting launches as the reference's
+``_seed`` does), or nearest-even rounding (``stochastic_rounding=False``).
 """
 from __future__ import annotations
 
@@ -54,10 +57,8 @@ class FusedAdamW(torch.optim.Optimizer):
                     if p.grad is None:
                         continue
                     g = p.grad.float().contiguous()
-                if p.dtype != torch.float32:
-                    raise NotImplementedError("FusedAdamW on the MI355X path updates fp32 parameters only "
-                                              f"(got {p.dtype}); bf16 master-weight / stochastic-rounding "
-                                              "variants are not implemented")
+                if p.dtype not in (torch.float32, torch.bfloat16):
+                    raise NotImplementedError(f"FusedAdamW updates fp32 or bf16 parameters (got {p.dtype})")
                 if not p.is_contiguous() or not g.is_contiguous():
                     raise ValueError("FusedAdamW needs contiguous parameters and gradients")
                 st = self.state[p]
@@ -65,11 +66,14 @@ class FusedAdamW(torch.optim.Optimizer):
                     st["step"] = 0
                     st["m"] = torch.zeros(p.shape, device=p.device, dtype=mdt)
                     st["v"] = torch.zeros(p.shape, device=p.device, dtype=mdt)
+                    if self.master_weights and p.dtype != torch.float32:
+                        st["master"] = p.detach().float().clone()
                 st["step"] += 1
                 t = st["step"]
                 self._seed += 1
                 backend_for(p.device).adam(p, g, st["m"], st["v"], group["lr"], b1, b2, group["eps"],
-                                           group["weight_decay"], 1 - b1 ** t, 1 - b2 ** t)
+                                           group["weight_decay"], 1 - b1 ** t, 1 - b2 ** t, master=st.get("master"),
+                                           stochastic=self.stochastic_rounding, seed=self._seed)
                 if getattr(p, "main_grad", None) is None:
                     p.grad = None
         return loss

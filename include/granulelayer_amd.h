@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 9
+#define GL_ABI_VERSION 10
 
 enum {
   GL_OK = 0,
@@ -156,13 +156,19 @@ typedef struct GlEdgeArgs {
  *   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2;  upd = (m/bc1) / (sqrt(v/bc2) + eps)
  *   p = p (1 - lr wd) - lr upd;  g = 0 (fused zero_grad) */
 typedef struct GlAdamArgs {
-  float* p;
-  float* g;
+  void* p;                /* parameters, fp32 or bf16 (p_dtype) */
+  float* g;               /* fp32 gradient (main_grad), zeroed */
   void* m;                /* fp32 or bf16 (moments_dtype) */
   void* v;
   int64_t n;
   int32_t moments_dtype;  /* GL_DTYPE_F32 | GL_DTYPE_BF16 */
   float lr, beta1, beta2, eps, weight_decay, bc1, bc2;
+  int32_t p_dtype;        /* GL_DTYPE_F32 | GL_DTYPE_BF16 */
+  int32_t stochastic;     /* bf16 p without master: 1 = stochastic rounding (optim.py:59-62), 0 = nearest even */
+  float* master;          /* bf16 p: fp32 master copy the update runs on (then p = nearest-even bf16 of it,
+                             optim.py:54-56), or NULL */
+  uint64_t seed;          /* stochastic rounding: element i adds the low 16 bits of Triton's
+                             tl.randint(seed, i) (Philox-4x32-10) below the bf16 cut, then truncates */
 } GlAdamArgs;
 
 /* Cover-TopK support selection of an envelope (one-time preprocessing of CoverTopK16Layer).

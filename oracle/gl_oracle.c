@@ -336,6 +336,74 @@ void glo_adam_f32(long n, float* p, float* g, float* m, float* v, float lr, floa
   }
 }
 
+/* Philox-4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3",
+ * SC'11; the Random123 generator): 10 rounds of (hi, lo) = M * c with the round multipliers
+ * 0xD2511F53 / 0xCD9E8D57 and the Weyl key increments 0x9E3779B9 / 0xBB67AE85.  out[4] for
+ * counter ctr[4] and key key[2]. */
+void glo_philox4x32(const uint32_t* ctr, const uint32_t* key, uint32_t* out) {
+  uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+    c1 = (uint32_t)p1;
+    c3 = (uint32_t)p0;
+    c0 = n0;
+    c2 = n2;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  out[0] = c0, out[1] = c1, out[2] = c2, out[3] = c3;
+}
+
+/* Triton's tl.randint(seed, offset) (triton/language/random.py, Triton 3.6: randint4x puts the
+ * 64-bit offset's halves in the counter's first two words, philox keys with the seed's halves) */
+uint32_t glo_randint(uint64_t seed, uint64_t offset) {
+  const uint32_t ctr[4] = {(uint32_t)offset, (uint32_t)(offset >> 32), 0u, 0u};
+  const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+  uint32_t out[4];
+  glo_philox4x32(ctr, key, out);
+  return out[0];
+}
+
+static inline uint16_t f32_bits_hi(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return (uint16_t)(u >> 16);
+}
+
+/* AdamW of bf16 parameters (sparse_pooling/optim.py:26-64): p holds bf16 bits.  With master (fp32,
+ * updated in place) the update runs on the master and p = RNE(master) (HAS_MASTER); otherwise on
+ * float(p), then p = RNE(p) or, with stochastic, the stochastic rounding of optim.py:59-62:
+ * bits(p) + (randint(seed, i) & 0xFFFF), truncated to bf16.  Moments as in glo_adam_f32. */
+void glo_adam_bf16(long n, uint16_t* p, float* master, float* g, float* m, float* v, float lr, float b1, float b2,
+                   float eps, float wd, float bc1, float bc2, int moments_bf16, int stochastic, uint64_t seed) {
+  for (long i = 0; i < n; ++i) {
+    float gi = g[i];
+    float mi = b1 * m[i] + (1.0f - b1) * gi;
+    float vi = b2 * v[i] + (1.0f - b2) * gi * gi;
+    float upd = (mi / bc1) / (sqrtf(vi / bc2) + eps);
+    uint32_t pb = (uint32_t)p[i] << 16;
+    float p0;
+    memcpy(&p0, &pb, 4);
+    if (master) p0 = master[i];
+    float pi = p0 * (1.0f - lr * wd) - lr * upd;
+    m[i] = moments_bf16 ? bf16_round(mi) : mi;
+    v[i] = moments_bf16 ? bf16_round(vi) : vi;
+    g[i] = 0.0f;
+    if (master) {
+      master[i] = pi;
+      p[i] = f32_bits_hi(bf16_round(pi));
+    } else if (stochastic) {
+      uint32_t u;
+      memcpy(&u, &pi, 4);
+      u = (u + (glo_randint(seed, (uint64_t)i) & 0xFFFFu)) & 0xFFFF0000u;
+      p[i] = (uint16_t)(u >> 16);
+    } else {
+      p[i] = f32_bits_hi(bf16_round(pi));
+    }
+  }
+}
+
 /* ---- smooth pooling (pools 4, 5, 6) --------------------------------------------------------- */
 static inline double smooth_scale(int pool, double param) {
   return pool == 4 ? 1.4426950408889634 / param : (pool == 6 ? 1.4426950408889634 * param : 1.0);

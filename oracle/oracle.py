@@ -75,9 +75,15 @@ def _load():
         d = ctypes.c_double
         lib.glo_forward_smooth_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, i, d, P, P, P]
         lib.glo_backward_smooth_f64.argtypes = [i, i, i, i, i, P, P, P, P, P, i, i, d, P, P, P, P, P, P, P]
+        u64 = ctypes.c_uint64
+        lib.glo_philox4x32.argtypes = [P, P, P]
+        lib.glo_randint.argtypes = [u64, u64]
+        lib.glo_randint.restype = ctypes.c_uint32
+        lib.glo_adam_bf16.argtypes = [ctypes.c_long, P, P, P, P, P, f, f, f, f, f, f, f, i, i, u64]
         for fn in (lib.glo_forward_f64, lib.glo_backward_f64, lib.glo_adam_f32, lib.glo_forward_max_f64,
                    lib.glo_forward_topk_f64, lib.glo_backward_topk_f64, lib.glo_backward_events_f64,
-                   lib.glo_forward_smooth_f64, lib.glo_backward_smooth_f64):
+                   lib.glo_forward_smooth_f64, lib.glo_backward_smooth_f64, lib.glo_philox4x32,
+                   lib.glo_adam_bf16):
             fn.restype = None
         _lib = lib
     return _lib
@@ -267,6 +273,36 @@ def adam(p, g, m, v, lr, b1, b2, eps, wd, step, moments_bf16=False):
     P = ctypes.c_void_p
     _load().glo_adam_f32(p.size, p.ctypes.data_as(P), g.ctypes.data_as(P), m.ctypes.data_as(P),
                          v.ctypes.data_as(P), lr, b1, b2, eps, wd, bc1, bc2, int(moments_bf16))
+
+
+def philox4x32(ctr, key):
+    """Philox-4x32-10 output (4 uint32) of counter ctr (4 uint32) and key key (2 uint32)."""
+    c = np.ascontiguousarray(ctr, np.uint32)
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.zeros(4, np.uint32)
+    P = ctypes.c_void_p
+    _load().glo_philox4x32(c.ctypes.data_as(P), k.ctypes.data_as(P), out.ctypes.data_as(P))
+    return out
+
+
+def randint(seed: int, offset: int) -> int:
+    """Triton's tl.randint(seed, offset) for a 64-bit offset (Triton 3.6 randint4x)."""
+    return int(_load().glo_randint(seed, offset))
+
+
+def adam_bf16(p_bits, g, m, v, lr, b1, b2, eps, wd, step, moments_bf16=False, master=None, stochastic=True, seed=0):
+    """In-place AdamW step of bf16 parameters (p_bits: numpy uint16 bf16 patterns; g, m, v and the
+    optional fp32 master copy: float32), the HAS_MASTER / STOCH branches of optim.py:26-64."""
+    if p_bits.dtype != np.uint16 or not p_bits.flags["C_CONTIGUOUS"]:
+        raise TypeError("adam_bf16 expects contiguous uint16 parameter bits")
+    for a in (g, m, v) + (() if master is None else (master,)):
+        if a.dtype != np.float32 or not a.flags["C_CONTIGUOUS"]:
+            raise TypeError("adam_bf16 expects contiguous float32 g / m / v / master")
+    bc1, bc2 = 1.0 - b1 ** step, 1.0 - b2 ** step
+    P = ctypes.c_void_p
+    _load().glo_adam_bf16(p_bits.size, p_bits.ctypes.data_as(P), None if master is None else master.ctypes.data_as(P),
+                          g.ctypes.data_as(P), m.ctypes.data_as(P), v.ctypes.data_as(P), lr, b1, b2, eps, wd, bc1,
+                          bc2, int(moments_bf16), int(stochastic), seed)
 
 
 _ACT = {"identity": 0, "relu": 1}

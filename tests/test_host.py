@@ -122,11 +122,15 @@ def test_runtime_refuses_triton_plan():
         Level1Runtime(L, idx, LevelSpec("mean"), PhysicalPlan(backend="triton"))
 
 
-def test_fused_adamw_refuses_bf16_params_on_cpu():
-    p = torch.nn.Parameter(torch.zeros(8, dtype=torch.bfloat16))
-    p.grad = torch.zeros(8, dtype=torch.bfloat16)
+def test_fused_adamw_refuses_what_it_cannot_update():
+    p = torch.nn.Parameter(torch.zeros(8, dtype=torch.float16))  # fp32 and bf16 only
+    p.grad = torch.zeros(8, dtype=torch.float16)
     with pytest.raises(NotImplementedError):
         FusedAdamW([p]).step()
+    q = torch.nn.Parameter(torch.zeros(8, dtype=torch.bfloat16))  # bf16 is supported, on a ROCm GPU only
+    q.grad = torch.zeros(8, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        FusedAdamW([q]).step()
 
 
 @pytest.mark.parametrize("name", list(CONFIGS))
