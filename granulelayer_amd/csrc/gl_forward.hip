@@ -461,10 +461,12 @@ __device__ __forceinline__ void fwd_tile_dispatch(SRC xsb, const unsigned (&addr
     fwd_tile_any<K, NPL, ACT, FAR, PK>(xsb, addr, w, bias, slot, out, oslot, k, store, lane);
 }
 
-template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, int PK = PK_SUM, bool XG = false>
+template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, int PK = PK_SUM, bool XG = false,
+          bool SMALL = false>
 __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
-  // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots); XG: no LDS tile
-  __shared__ float4 xa[WS ? 2 * XTILE_DB : (XG ? 1 : (DBUF ? XTILE_DB : XTILE_SB))];
+  // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots); XG: no LDS tile;
+  // SMALL: one single-buffered tile of at most XTILE_DB slots, so two workgroups share a CU
+  __shared__ float4 xa[WS ? 2 * XTILE_DB : (XG ? 1 : (DBUF || SMALL ? XTILE_DB : XTILE_SB))];
   __shared__ float4 xb[DBUF ? XTILE_DB : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar chunk addressing
@@ -851,22 +853,29 @@ static FwdPlan fwd_plan(const GlFwdArgs* a, long long bf_cap = 0) {
   return q;
 }
 
-template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS, int PK, bool XG = false>
+template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS, int PK, bool XG = false, bool SMALL = false>
 static int launch_fwd(const FwdK& k, hipStream_t s) {
-  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, PK, XG>;
+  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, PK, XG, SMALL>;
   dim3 grid((unsigned)ceil_div(k.n_chunks, WAVES));
   GL_LAUNCH(WS ? GL_KERNEL_FWD_WIN : GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;
 }
 
-// one workgroup per CU (the tile buffers take the LDS); pool windows when they fit, else two tile
-// buffers when D fits them, else one, else (D > XTILE_SB) gathers from the tiles in global memory
+// pool windows when they fit, else (D > XTILE_SB) gathers from the tiles in global memory, else
+// tiles in LDS: one per workgroup with two workgroups per CU, or two buffers or one in a single
+// workgroup per CU
 template <int ACT, int K, int PK>
 static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
   constexpr int W = fwd_waves(K, PK);
   if (k.win) return launch_fwd<K, FWD_NPL, W, ACT, false, true, PK>(k, s);
   if (D > XTILE_SB) return launch_fwd<K, FWD_NPL, W, ACT, false, false, PK, true>(k, s);
+  // D <= XTILE_DB: two workgroups of W / 2 waves per CU, each with one 64-KiB tile, when W / 2 waves
+  // spread evenly over the 4 SIMDs: while one workgroup waits at its tile barrier for its slowest
+  // wave, the other computes (12% faster than one workgroup of W waves with two buffers for sum /
+  // mean and top-k at C2; the smooth pools measured even)
+  if constexpr (W % 8 == 0 && !pk_smooth(PK))
+    if (D <= XTILE_DB) return launch_fwd<K, FWD_NPL, W / 2, ACT, false, false, PK, false, true>(k, s);
   return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true, false, PK>(k, s)
                        : launch_fwd<K, FWD_NPL, W, ACT, false, false, PK>(k, s);
 }
