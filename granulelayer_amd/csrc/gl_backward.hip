@@ -547,25 +547,37 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
   }
 }
 
-// dX[b0 + b, d] = sum_q part[q, d, b]  (fixed order), tiled transpose to [B, D].
+// dX[b0 + b, d] = sum_q part[q, d, b]  (fixed order, q ascending), transposed to [B, D] through
+// LDS.  A thread sums 4 adjacent tokens of one input with 16-byte loads, 8 partials in flight
+// (the add order per element is unchanged); 32 inputs x 32 tokens per workgroup.
 __global__ void __launch_bounds__(256) dx_reduce_kernel(const float* __restrict__ part, float* __restrict__ dX, int D,
                                                         int cap, int Q, int b0, int Bc) {
-  __shared__ float tile[32][33];
+  __shared__ float tile[32][33];  // [token][input]
   const int d0 = blockIdx.x * 32, bb = blockIdx.y * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-  for (int r = ty; r < 32; r += 8) {
-    const int d = d0 + r, b = bb + tx;
-    float v = 0.f;
-    if (d < D && b < Bc) {
-      const float* src = part + (long long)d * cap + b;
-      for (int q = 0; q < Q; ++q) v += src[(long long)q * D * cap];
+  const int dl = threadIdx.x >> 3, q4 = (threadIdx.x & 7) * 4;  // input d0 + dl, tokens bb + q4 .. + 3
+  const int d = d0 + dl;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (d < D && bb + q4 < cap) {  // cap is a multiple of 64: the 4 tokens lie inside the partial rows
+    const float4* src = reinterpret_cast<const float4*>(part + (long long)d * cap + bb + q4);
+    const long long qs = (long long)D * cap / 4;  // float4 stride between partials
+    int q = 0;
+    for (; q + 8 <= Q; q += 8) {
+      float4 t[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) t[i] = src[(q + i) * qs];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v.x += t[i].x, v.y += t[i].y, v.z += t[i].z, v.w += t[i].w;
     }
-    tile[r][tx] = v;
+    for (; q < Q; ++q) {
+      const float4 t = src[q * qs];
+      v.x += t.x, v.y += t.y, v.z += t.z, v.w += t.w;
+    }
   }
+  tile[q4][dl] = v.x, tile[q4 + 1][dl] = v.y, tile[q4 + 2][dl] = v.z, tile[q4 + 3][dl] = v.w;
   __syncthreads();
-  for (int r = ty; r < 32; r += 8) {
-    const int b = bb + r, d = d0 + tx;
-    if (d < D && b < Bc) dX[(long long)(b0 + b) * D + d] = tile[tx][r];
+  for (int r = threadIdx.x >> 5; r < 32; r += 8) {
+    const int b = bb + r, dd = d0 + (threadIdx.x & 31);
+    if (dd < D && b < Bc) dX[(long long)(b0 + b) * D + dd] = tile[r][threadIdx.x & 31];
   }
 }
 

@@ -30,9 +30,10 @@ constexpr int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b)
 
 // ---- gather schedule of the neuron-stationary kernels (gl_sched.hip) --------------------------
 // Slots are scheduled in windows of 128: neuron slot j of lane `lane` in a chunk starting at slot
-// s_lo (a multiple of 128) reads record ((g * nwin + s_lo / 128 + j / 2) * 128 + ((j % 2) * 4 +
-// lane / 16) * 16 + lane % 16) = s_local | k_0 << 7 | ... | k_6 << 25 (k_7 = 28 - sum).  Without a
-// schedule the slot is s_lo + 64 j + lane and edges are visited in k order.
+// s_lo (a multiple of 64) lies in half-window h = s_lo / 64 + j and reads record
+// ((g * nwin + h / 2) * 128 + ((h % 2) * 4 + lane / 16) * 16 + lane % 16) = s_local | k_0 << 7 |
+// ... | k_6 << 25 (k_7 = 28 - sum).  Without a schedule the slot is s_lo + 64 j + lane and edges
+// are visited in k order.
 constexpr int SCHED_WIN = 128;
 constexpr uint32_t SCHED_IDENTITY = 0u | 1u << 3 | 2u << 6 | 3u << 9 | 4u << 12 | 5u << 15 | 6u << 18;
 
@@ -43,12 +44,15 @@ __device__ __forceinline__ int sched_slot(const uint32_t* __restrict__ sched, in
     order = SCHED_IDENTITY;
     return s_lo + j * 64 + lane;
   }
-  const int w = s_lo / SCHED_WIN + (j >> 1);
+  // neuron j of the chunk is half-window h = s_lo / 64 + j (chunks start at multiples of 64 slots);
+  // half h % 2 of window h / 2 holds its 64 lanes' records
+  const int h = (s_lo >> 6) + j;
+  const int w = h >> 1;
   if (w >= nwin) {
     order = SCHED_IDENTITY;
     return S;
   }
-  const uint32_t rec = sched[((long long)g * nwin + w) * SCHED_WIN + ((j & 1) * 4 + (lane >> 4)) * 16 + (lane & 15)];
+  const uint32_t rec = sched[((long long)g * nwin + w) * SCHED_WIN + ((h & 1) * 4 + (lane >> 4)) * 16 + (lane & 15)];
   order = rec >> 7;
   return w * SCHED_WIN + (int)(rec & 127u);
 }

@@ -581,27 +581,42 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   }
 }
 
-// pre[b, g] = scale_g * sum_{c < cpg} part[g*cpg + c, b]  (fixed order), tiled transpose.
+// pre[b, g] = scale_g * sum_{c < cpg} part[g*cpg + c, b]  (fixed order, c ascending), transposed to
+// [B, G] through LDS.  A thread sums 4 adjacent tokens of one pool with 16-byte loads, 8 chunk
+// rows in flight (the add order per element is unchanged); 32 pools x 32 tokens per workgroup.
 __global__ void __launch_bounds__(256) fwd_finalize_kernel(const float* __restrict__ part, const int32_t* __restrict__ counts,
                                                            float* __restrict__ pre, int B, int G, int cpg, int b_pad,
                                                            int b0, int pool) {
-  __shared__ float tile[32][33];
+  __shared__ float tile[32][33];  // [token][pool]
   const int g0 = blockIdx.x * 32, bb0 = blockIdx.y * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
-  for (int r = ty; r < 32; r += 8) {
-    const int g = g0 + r, b = bb0 + tx;
-    float v = 0.f;
-    if (g < G && b < b_pad) {
-      const float* src = part + (long long)g * cpg * b_pad + b;
-      for (int c = 0; c < cpg; ++c) v += src[(long long)c * b_pad];
-      if (pool == GL_POOL_MEAN) v = v / (float)counts[g];
+  const int gl = threadIdx.x >> 3, q4 = (threadIdx.x & 7) * 4;  // pool g0 + gl, tokens bb0 + q4 .. + 3
+  const int g = g0 + gl;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (g < G && bb0 + q4 < b_pad) {  // b_pad is a multiple of 4: the 4 tokens lie inside the rows
+    const float4* src = reinterpret_cast<const float4*>(part + (long long)g * cpg * b_pad + bb0 + q4);
+    const long long cs = b_pad / 4;  // float4 stride between a pool's chunk rows
+    int c = 0;
+    for (; c + 8 <= cpg; c += 8) {
+      float4 t[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) t[i] = src[(c + i) * cs];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v.x += t[i].x, v.y += t[i].y, v.z += t[i].z, v.w += t[i].w;
     }
-    tile[r][tx] = v;
+    for (; c < cpg; ++c) {
+      const float4 t = src[c * cs];
+      v.x += t.x, v.y += t.y, v.z += t.z, v.w += t.w;
+    }
+    if (pool == GL_POOL_MEAN) {
+      const float n = (float)counts[g];
+      v.x = v.x / n, v.y = v.y / n, v.z = v.z / n, v.w = v.w / n;
+    }
   }
+  tile[q4][gl] = v.x, tile[q4 + 1][gl] = v.y, tile[q4 + 2][gl] = v.z, tile[q4 + 3][gl] = v.w;
   __syncthreads();
-  for (int r = ty; r < 32; r += 8) {
-    const int b = bb0 + r, g = g0 + tx;
-    if (g < G && b0 + b < B && b < b_pad) pre[(long long)(b0 + b) * G + g] = tile[tx][r];
+  for (int r = threadIdx.x >> 5; r < 32; r += 8) {
+    const int b = bb0 + r, gg = g0 + (threadIdx.x & 31);
+    if (gg < G && b0 + b < B && b < b_pad) pre[(long long)(b0 + b) * G + gg] = tile[r][threadIdx.x & 31];
   }
 }
 
