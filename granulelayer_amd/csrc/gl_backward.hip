@@ -340,10 +340,11 @@ __device__ __forceinline__ void dx_next(const DxK& p, DxChunk& c, int hi) {
   }
 }
 
-// record of the lane's edge (lanes past the chunk take the chunk's first edge: in bounds, unused)
+// record of the lane's edge (lanes past the chunk take the chunk's first edge: in bounds, unused);
+// the chunk's base address is wave-uniform (scalar registers), the lane adds a 32-bit offset
 __device__ __forceinline__ unsigned dx_load_rec(const DxK& p, const DxChunk& c, int lane) {
   const unsigned n = min(c.end - c.e, 64u);
-  return p.rec[c.e + ((unsigned)lane < n ? (unsigned)lane : 0u)];
+  return ld_uniform_u32(p.rec + c.e, (unsigned)lane < n ? (unsigned)lane * 4u : 0u);
 }
 
 template <int K, int T>
@@ -353,15 +354,18 @@ __device__ __forceinline__ void dx_gather(const DxK& p, const uint32_t* mask_tc,
   const unsigned woff = rec & REC_OFF_MASK;  // byte offset of W[n, k] in the unit
   const unsigned nl = woff >> (K == 8 ? 5 : 6);
   g.rec = rec;
-  g.w = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.W + nb * K) + woff);
-  const uint32_t* mr = mask_tc + (nb + nl) * (2 * T);
+  // the unit's weight and mask rows start at wave-uniform addresses (scalar registers); each lane
+  // adds a 32-bit offset (< 64 KiB), so the gathers need no 64-bit vector address arithmetic
+  g.w = __uint_as_float(ld_uniform_u32(p.W + nb * K, woff));
+  const uint32_t* mb = mask_tc + nb * (2 * T);
+  const unsigned mo = nl * (unsigned)(2 * T * 4);
   if constexpr (T == 1) {
-    const uint2 v = *reinterpret_cast<const uint2*>(mr);
+    const uint2 v = ld_uniform_u64(mb, mo);
     g.m[0] = v.x, g.m[1] = v.y;
   } else {
 #pragma unroll
     for (int h = 0; h < T / 2; ++h) {
-      const uint4 v = *reinterpret_cast<const uint4*>(mr + 4 * h);
+      const uint4 v = ld_uniform_u128(mb, mo + 16u * h);
       g.m[4 * h] = v.x, g.m[4 * h + 1] = v.y, g.m[4 * h + 2] = v.z, g.m[4 * h + 3] = v.w;
     }
   }
@@ -411,14 +415,18 @@ __device__ __forceinline__ void dx_bits(const DxStage<T>& st, unsigned mw, unsig
 template <int X, int T>
 __device__ __forceinline__ void dx_run(const DxStage<T>& st, int i0, int i1, int word, unsigned bit,
                                        const float (&c1)[T], float (&acc)[FW][T]) {
-  if (i0 >= i1) return;
+  // the run length as an opaque 32-bit scalar: compared on the scalar unit (bounds folded into the
+  // 64-bit LDS address arithmetic were compared with 64-bit vector compares)
+  int len = i1 - i0;
+  asm volatile("" : "+s"(len));
+  if (len <= 0) return;
   const uint2* e = &st.e[i0][word];
   float s[T], mf[T];
   uint2 mw = *e;
   dx_bits<T>(st, mw.x, bit, mf);
 #pragma unroll
   for (int j = 0; j < T; ++j) s[j] = mf[j] * __uint_as_float(mw.y);
-  for (int n = i1 - i0 - 1; n > 0; --n) {
+  for (int n = len - 1; n > 0; --n) {
     e += 2 * T + 1;
     mw = *e;
     dx_bits<T>(st, mw.x, bit, mf);

@@ -241,6 +241,24 @@ __device__ __forceinline__ XBuf xbuf(const float4* tile, int D) {
   // dword 3 0x00020000: raw 32-bit data, the gfx9 buffer format of untyped loads
   return XBuf{__builtin_amdgcn_make_buffer_rsrc(const_cast<float4*>(tile), (short)0, D * 16, 0x00020000)};
 }
+// A load from a wave-uniform base address plus the lane's 32-bit byte offset, as one buffer load:
+// the base goes into scalar registers (readfirstlane, then a buffer resource without a range
+// limit) and the lane supplies only the offset, so no 64-bit vector address arithmetic is needed.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(uniform_ptr(base)), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ unsigned ld_uniform_u32(const void* base, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(uniform_rsrc(base), (int)off, 0, 0);
+}
+__device__ __forceinline__ uint2 ld_uniform_u64(const void* base, unsigned off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(uniform_rsrc(base), (int)off, 0, 0);
+  return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint4 ld_uniform_u128(const void* base, unsigned off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(uniform_rsrc(base), (int)off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 template <bool FAR>
 __device__ __forceinline__ float4 gather_x(XBuf b, unsigned a) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)a, 0, 0);
