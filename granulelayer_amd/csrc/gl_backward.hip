@@ -78,6 +78,7 @@ struct BwK {
   int G, ww, npw;         // window staging: pools, padded window width, pools per workgroup
   int rs;                 // log2 slots per shared index record
   int sps, gs;            // pool geometry (pool_base)
+  int tb;                 // tokens per tile: 4, or 2 (two-token tiles; n_tiles counts those)
 };
 
 // One token tile of the dW pass (LDS at xsb): recompute z, form dz = c1 * act'(z), accumulate
@@ -130,15 +131,60 @@ __device__ __forceinline__ void bwd_w_tile(SRC xsb, int t, const float4 c1, cons
   }
 }
 
+// The same over a two-token tile (8-byte slots): bits 2 (t % 16) + i of the mask word.
+template <int K, int NPL, int ACT, int RA, bool FAR>
+__device__ __forceinline__ void bwd_w_tile2(const char* xsb, int t, const float2 c1, const unsigned (&addr)[NPL][K],
+                                            const float (&w)[NPL][K], const float (&bias)[NPL], float (&dw)[NPL][K],
+                                            float (&dbv)[NPL], unsigned (&mw)[NPL]) {
+  float2 xc[K];
+#pragma unroll
+  for (int k = 0; k < RA; ++k) xc[k] = gather_x2<FAR>(xsb, addr[0][k]);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+#pragma unroll
+    for (int k = RA; k < K; ++k) xc[k] = gather_x2<FAR>(xsb, addr[j][k]);
+    float2 xn[RA];
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xn[k] = gather_x2<FAR>(xsb, addr[j + 1][k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float z0 = bias[j], z1 = bias[j];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
+      z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
+    }
+    const bool m0 = ACT != GL_ACT_RELU || z0 > 0.f, m1 = ACT != GL_ACT_RELU || z1 > 0.f;
+    const float d0 = m0 ? c1.x : 0.f, d1 = m1 ? c1.y : 0.f;
+    dbv[j] = dbv[j] + d0 + d1;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      float a = dw[j][k];
+      a = __builtin_fmaf(d0, xc[k].x, a);
+      a = __builtin_fmaf(d1, xc[k].y, a);
+      dw[j][k] = a;
+    }
+    mw[j] |= ((unsigned)m0 | ((unsigned)m1 << 1)) << ((t & 15) * 2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xc[k] = xn[k];
+    }
+  }
+}
+
 // Token tiles reach LDS by LDS-DMA (dma_tile).  DBUF (D <= XTILE_DB): two buffers, tile t + 1
 // lands while tile t is read; one tile body reads buffer (t & 1) through a run-time base, so the
 // loop holds one copy of the gather code (two inlined copies, one per buffer, do not fit the 256
 // VGPRs a wave has at 2 waves per SIMD with the dW accumulators live).  Otherwise one buffer:
 // load, wait, read.  The wave index goes through readfirstlane so the chunk's parameters and the
 // c1 row are addressed with scalar registers.
-template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF, bool WS = false, bool XG = false>
+template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF, bool WS = false, bool XG = false, int TB = BT>
 __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
-  // XG (D > XTILE_SB): no LDS tile, the lanes gather from the token tiles in global memory
+  // XG (D > XTILE_SB): no LDS tile, the lanes gather from the token tiles in global memory.
+  // TB: tokens per tile, 4 or 2 (two-token tiles in the two buffers of DBUF: D <= 2 XTILE_DB)
+  static_assert(TB == BT || (TB == 2 && DBUF && !WS && !XG), "two-token tiles: double-buffered only");
   __shared__ float4 xs[DBUF || WS ? 2 * XTILE_DB : (XG ? 1 : XTILE_SB)];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -171,7 +217,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
       const int k = sched_k<K>(order, ks);
       int d = rec_index(p.idx, n, k, K, p.rs);
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-      addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * 16u;
+      addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * (4u * TB);
       const float wl = p.W[n * K + k];
       w[j][ks] = valid ? wl : 0.f;
       dw[j][ks] = 0.f;
@@ -182,6 +228,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   }
   const float* c1row = p.c1t + g * p.cap;
   constexpr int NT = WAVES * 64;
+  constexpr int TPW = 32 / TB;       // tiles per mask word
+  const int ns = p.D * TB / 4;       // 16-byte slots per tile (D even for two-token tiles)
 
   // window staging: WS_TILES tiles per stage and barrier; tile t at slot (t mod 2 WS_TILES) * nsl
   const WinLayout L{p.win, p.ww, p.npw, g_first, p.G};
@@ -192,19 +240,19 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
     stage_wait();
     __syncthreads();
   } else if constexpr (DBUF) {
-    dma_tile(p.xt, xs, p.D, NT);
+    dma_tile(p.xt, xs, ns, NT);
     stage_wait();
     __syncthreads();
   }
-  // 8 token tiles (32 tokens) per mask word.  An even word is held in mwe until the odd word after
-  // it is done, and the pair is stored as one 8-byte write: each store writes a separate 32-byte
-  // memory sector, so pairs halve the mask's write traffic.
+  // TPW token tiles (32 tokens) per mask word.  An even word is held in mwe until the odd word
+  // after it is done, and the pair is stored as one 8-byte write: each store writes a separate
+  // 32-byte memory sector, so pairs halve the mask's write traffic.
   unsigned mwe[NPL];
-  for (int t0 = 0; t0 < p.n_tiles; t0 += 8) {
+  for (int t0 = 0; t0 < p.n_tiles; t0 += TPW) {
     unsigned mw[NPL];
 #pragma unroll
     for (int j = 0; j < NPL; ++j) mw[j] = 0u;
-    const int t1 = t0 + 8 < p.n_tiles ? t0 + 8 : p.n_tiles;
+    const int t1 = t0 + TPW < p.n_tiles ? t0 + TPW : p.n_tiles;
     if constexpr (WS) {
       for (int ts0 = t0; ts0 < t1; ts0 += WS_TILES) {
         const int r = (ts0 / WS_TILES) & 1;
@@ -234,10 +282,16 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
       } else if constexpr (DBUF) {
         // buffer cur ^ 1 was last read in tile t - 1, which every wave finished before the barrier
         const int cur = t & 1;
-        if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xs + (cur ^ 1) * XTILE_DB, p.D, NT);
-        const float4 c1 = ld_uniform4(c1row, t * BT);
-        bwd_w_tile<K, NPL, ACT, RA, true>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t, c1,
-                                          addr, w, bias, dw, dbv, mw);
+        if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * ns, xs + (cur ^ 1) * XTILE_DB, ns, NT);
+        if constexpr (TB == 2) {
+          const float2 c1 = ld_uniform2(c1row, t * 2);
+          bwd_w_tile2<K, NPL, ACT, RA, true>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t, c1,
+                                             addr, w, bias, dw, dbv, mw);
+        } else {
+          const float4 c1 = ld_uniform4(c1row, t * BT);
+          bwd_w_tile<K, NPL, ACT, RA, true>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t, c1,
+                                            addr, w, bias, dw, dbv, mw);
+        }
         stage_wait();  // tile t + 1 is in LDS for this wave's copies; the barrier publishes every wave's
         __syncthreads();
       } else {
@@ -249,8 +303,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
         bwd_w_tile<K, NPL, ACT, RA, false>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw, dbv, mw);
       }
     }
-    const int word = t0 >> 3;
-    if ((word & 1) == 0 && t0 + 8 < p.n_tiles) {
+    const int word = t0 / TPW;
+    if ((word & 1) == 0 && t0 + TPW < p.n_tiles) {
 #pragma unroll
       for (int j = 0; j < NPL; ++j) mwe[j] = mw[j];
       continue;
@@ -965,6 +1019,7 @@ void edge_layout(int D, int G, int S, int K, EdgeHeader* h, size_t* total) {
 template <int K, int NPL, int WAVES, int ACT, int RA>
 static int launch_bwd_w(const BwK& k, hipStream_t s) {
   auto fn = k.win ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, true>
+                  : k.tb == 2 ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true, false, false, 2>
                   : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true>
                                      : (k.D <= XTILE_SB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false>
                                                         : bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, false, true>));
@@ -1096,7 +1151,12 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     const int n_tiles = ceil_div(Bc, BT);
     const int T = dx_slots(Bc);
     const int cap = dx_cap(Bc);
-    GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles, xt, s));
+    // the dense dW pass over full tiles of 4097..8192 inputs reads two-token tiles (two 64-KiB buffers)
+    int ww = 0, npw = 0;
+    const bool dense = !smooth && !a->winner;
+    const bool win = dense && window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &ww, &npw);
+    const int tb = dense && !win && tiles_of_two(a->D) ? 2 : BT;
+    GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles * BT / tb, xt, s, tb));
     if (smooth) {  // coefficients, recompute pass (dW, db, dz), dX from dz
       float* c2t = (float*)(ws + q.xt_bytes + q.c1_bytes + q.part_bytes);
       float* c3t = (float*)((char*)c2t + q.c1_bytes);
@@ -1141,8 +1201,9 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     }
     const long long NS = (long long)a->G * a->S;
     BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, a->sched, nullptr, q.n_chunks, NS,
-           a->D, a->S, q.cpg, n_tiles, cap, 2 * T, ceil_div(a->S, SCHED_WIN), a->G, 0, 0, a->rec_shift, sps, gs};
-    if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &bk.ww, &bk.npw)) bk.win = a->win;
+           a->D, a->S, q.cpg, n_tiles * BT / tb, cap, 2 * T, ceil_div(a->S, SCHED_WIN), a->G, ww, npw, a->rec_shift,
+           sps, gs, tb};
+    if (win) bk.win = a->win;
     GL_TRY(launch_bwd_w_any(a->K, a->act, bk, s));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
            (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, a->W, part,

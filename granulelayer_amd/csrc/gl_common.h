@@ -259,6 +259,20 @@ __device__ __forceinline__ uint4 ld_uniform_u128(const void* base, unsigned off)
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// Two-token tiles (8-byte slots, D x 8 bytes per tile): tokens 2t, 2t + 1 of input d at byte 8 d.
+// Inputs up to 2 XTILE_DB fit one 64-KiB buffer, so the wider layers keep two buffers (or two
+// workgroups) per CU; the price is twice the tiles, reductions and barriers per token.
+template <bool FAR>
+__device__ __forceinline__ float2 gather_x2(const char* buf, unsigned a) {
+  if constexpr (FAR) asm volatile("" : "+v"(a));
+  return *reinterpret_cast<const float2*>(buf + a);
+}
+__device__ __forceinline__ float2 ld_uniform2(const float* row, int i) {
+  typedef const __attribute__((address_space(4))) float CF;
+  const CF* q = (const CF*)(row + i);
+  return make_float2(q[0], q[1]);
+}
+
 template <bool FAR>
 __device__ __forceinline__ float4 gather_x(XBuf b, unsigned a) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)a, 0, 0);
@@ -292,6 +306,21 @@ __device__ __forceinline__ float wave_sum4(float a0, float a1, float a2, float a
   c += dpp<0x128>(c);  // row_ror:8
   // each swap returns (first operand with its odd rows / rows 2,3 replaced, second operand with
   // its even rows / rows 0,1 replaced); with both operands c their sum holds the row-pair sum
+  const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+  c = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+  return __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+}
+
+// The same reduction for two per-lane values (two-token tiles): after the first quad step even
+// lanes hold token 0 and odd lanes token 1; the remaining steps pair lanes of equal parity.
+// Every lane ends with the total of token lane & 1.
+__device__ __forceinline__ float wave_sum2(float a0, float a1, int lane) {
+  const bool odd = lane & 1;
+  float c = (odd ? a1 : a0) + dpp<0xB1>(odd ? a0 : a1);  // quad_perm(1,0,3,2)
+  c += dpp<0x4E>(c);   // quad_perm(2,3,0,1)
+  c += dpp<0x124>(c);  // row_ror:4
+  c += dpp<0x128>(c);  // row_ror:8
   const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(c), false, false);
   c = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
   const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);

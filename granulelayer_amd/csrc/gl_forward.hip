@@ -16,34 +16,44 @@
 
 namespace gl {
 
-// X [B, D] (fp32 | bf16, row stride sxb) -> XT [n_tiles][D][BT] fp32; tokens >= B are zero.
-template <typename XT>
+// X [B, D] (fp32 | bf16, row stride sxb) -> XT [n_tiles][D][TB] fp32 (TB = 4 tokens per 16-byte
+// slot, or 2 per 8-byte slot); tokens >= B are zero.
+template <typename XT, int TB>
 __global__ void __launch_bounds__(256) tile_x_kernel(const XT* __restrict__ X, long long sxb, int B, int D, int b0,
-                                                     int n_tiles, float4* __restrict__ out) {
+                                                     int n_tiles, float* __restrict__ out) {
   long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   long long total = (long long)n_tiles * D;
   if (i >= total) return;
   int t = (int)(i / D), d = (int)(i % D);
-  float v[BT];
+  float v[TB];
 #pragma unroll
-  for (int j = 0; j < BT; ++j) {
-    int b = b0 + t * BT + j;
+  for (int j = 0; j < TB; ++j) {
+    int b = b0 + t * TB + j;
     v[j] = b < B ? load_x(X, (long long)b * sxb + d) : 0.f;
   }
-  out[i] = make_float4(v[0], v[1], v[2], v[3]);
+  if constexpr (TB == 4) reinterpret_cast<float4*>(out)[i] = make_float4(v[0], v[1], v[2], v[3]);
+  else reinterpret_cast<float2*>(out)[i] = make_float2(v[0], v[1]);
 }
 
-int launch_tile_x(const void* X, long long sxb, int x_dtype, int B, int D, int b0, int n_tiles, float4* xt,
-                  hipStream_t s) {
+template <int TB>
+static int launch_tile_x_tb(const void* X, long long sxb, int x_dtype, int B, int D, int b0, int n_tiles, float* xt,
+                            hipStream_t s) {
   long long total = (long long)n_tiles * D;
   dim3 grid((unsigned)ceil_div(total, 256));
   if (x_dtype == GL_DTYPE_F32)
-    GL_LAUNCH(GL_KERNEL_TILE_X, tile_x_kernel<float>, grid, dim3(256), 0, s, (const float*)X, sxb, B, D, b0, n_tiles, xt);
+    GL_LAUNCH(GL_KERNEL_TILE_X, (tile_x_kernel<float, TB>), grid, dim3(256), 0, s, (const float*)X, sxb, B, D, b0,
+              n_tiles, xt);
   else
-    GL_LAUNCH(GL_KERNEL_TILE_X, tile_x_kernel<__hip_bfloat16>, grid, dim3(256), 0, s, (const __hip_bfloat16*)X, sxb, B, D,
-                       b0, n_tiles, xt);
+    GL_LAUNCH(GL_KERNEL_TILE_X, (tile_x_kernel<__hip_bfloat16, TB>), grid, dim3(256), 0, s, (const __hip_bfloat16*)X,
+              sxb, B, D, b0, n_tiles, xt);
   GL_CHECK_LAUNCH();
   return 0;
+}
+
+int launch_tile_x(const void* X, long long sxb, int x_dtype, int B, int D, int b0, int n_tiles, float4* xt,
+                  hipStream_t s, int tb) {
+  return tb == 2 ? launch_tile_x_tb<2>(X, sxb, x_dtype, B, D, b0, n_tiles, (float*)xt, s)
+                 : launch_tile_x_tb<4>(X, sxb, x_dtype, B, D, b0, n_tiles, (float*)xt, s);
 }
 
 struct FwdK {
@@ -64,6 +74,7 @@ struct FwdK {
   float scale, pparam;    // smooth pools: u = a * scale (LogMeanExp / softmax-weighted); p (power mean)
   int pint;               // power mean: p when it is 1, 2, 4 or 8 (exact products), else 0
   int sps, gs;            // pool geometry (pool_base): shards per group and group stride in slots
+  int tb;                 // tokens per tile: 4, or 2 (two-token tiles; n_tiles counts those)
 };
 
 // One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
@@ -113,6 +124,46 @@ __device__ __forceinline__ void fwd_tile(SRC xsb, const unsigned (&addr)[NPL][K]
   }
   const float tot = wave_sum4(a0, a1, a2, a3, lane);
   if (store && lane < 4) out[wave_sum4_token(lane)] = tot;  // 4 lanes, 16 contiguous bytes
+}
+
+// The sum / mean tile over a two-token tile (8-byte slots, ds_read_b64); lanes 0-1 store.
+template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8)>
+__device__ __forceinline__ void fwd_tile2(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+                                          const float (&bias)[NPL], float* out, bool store, int lane) {
+  float a0 = 0.f, a1 = 0.f;
+  float2 xc[K];
+#pragma unroll
+  for (int k = 0; k < RA; ++k) xc[k] = gather_x2<FAR>(xsb, addr[0][k]);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+#pragma unroll
+    for (int k = RA; k < K; ++k) xc[k] = gather_x2<FAR>(xsb, addr[j][k]);
+    float2 xn[RA];
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xn[k] = gather_x2<FAR>(xsb, addr[j + 1][k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float z0 = bias[j], z1 = bias[j];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
+      z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
+    }
+    if (ACT == GL_ACT_RELU) {
+      z0 = __builtin_fmaxf(z0, 0.f);
+      z1 = __builtin_fmaxf(z1, 0.f);
+    }
+    a0 += z0;
+    a1 += z1;
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xc[k] = xn[k];
+    }
+  }
+  const float tot = wave_sum2(a0, a1, lane);
+  if (store && lane < 2) out[lane] = tot;  // 2 lanes, 8 contiguous bytes
 }
 
 // Max pooling tile: per token the largest act(z) of the wave's neurons and its pool slot (the
@@ -462,10 +513,12 @@ __device__ __forceinline__ void fwd_tile_dispatch(SRC xsb, const unsigned (&addr
 }
 
 template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, int PK = PK_SUM, bool XG = false,
-          bool SMALL = false>
+          bool SMALL = false, int TB = BT>
 __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots); XG: no LDS tile;
-  // SMALL: one single-buffered tile of at most XTILE_DB slots, so two workgroups share a CU
+  // SMALL: one single-buffered tile of at most XTILE_DB 16-byte slots, so two workgroups share a
+  // CU.  TB: tokens per tile (4, or 2 for the two-token tiles of SMALL sum / mean: D x 8 bytes)
+  static_assert(TB == BT || (TB == 2 && DBUF && !WS && !XG && PK == PK_SUM), "two-token tiles: sum / mean, two buffers");
   __shared__ float4 xa[WS ? 2 * XTILE_DB : (XG ? 1 : (DBUF || SMALL ? XTILE_DB : XTILE_SB))];
   __shared__ float4 xb[DBUF ? XTILE_DB : 1];
   const int lane = threadIdx.x & 63;
@@ -499,7 +552,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       const int k = sched_k<K>(order, ks);  // the pooled sum does not depend on the visiting order
       int d = rec_index(p.idx, n, k, K, p.rs);
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-      addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * 16u;
+      addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * (4u * TB);
       const float wl = p.W[n * K + k];
       w[j][ks] = valid ? wl : 0.f;
     }
@@ -554,19 +607,26 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       fwd_tile_dispatch<K, NPL, ACT, false, PK>(xbuf(p.xt + (long long)t * p.D, p.D), addr, w, bias, slot, vmask,
                                                 out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
   } else if constexpr (DBUF) {
-    dma_tile(p.xt, xa, p.D, NT);
+    const int ns = p.D * TB / 4;  // 16-byte slots per tile
+    dma_tile(p.xt, xa, ns, NT);
     for (int t = 0; t < p.n_tiles; t += 2) {
       stage_wait();
       __syncthreads();  // tile t is in xa; every wave is done with xb (tile t - 1)
-      if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * p.D, xb, p.D, NT);
-      fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
-                                                out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
+      if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * ns, xb, ns, NT);
+      if constexpr (TB == 2)
+        fwd_tile2<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * 2, store, lane);
+      else
+        fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
+                                                  out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
       if (t + 1 < p.n_tiles) {
         stage_wait();
         __syncthreads();  // tile t + 1 is in xb; every wave is done with xa
-        if (t + 2 < p.n_tiles) dma_tile(p.xt + (long long)(t + 2) * p.D, xa, p.D, NT);
-        fwd_tile_dispatch<K, NPL, ACT, true, PK>(reinterpret_cast<const char*>(xb), addr, w, bias, slot, vmask,
-                                                 out + (t + 1) * BT * kp, oslot + (t + 1) * BT * kp, kp, store, lane, p);
+        if (t + 2 < p.n_tiles) dma_tile(p.xt + (long long)(t + 2) * ns, xa, ns, NT);
+        if constexpr (TB == 2)
+          fwd_tile2<K, NPL, ACT, true>(reinterpret_cast<const char*>(xb), addr, w, bias, out + (t + 1) * 2, store, lane);
+        else
+          fwd_tile_dispatch<K, NPL, ACT, true, PK>(reinterpret_cast<const char*>(xb), addr, w, bias, slot, vmask,
+                                                   out + (t + 1) * BT * kp, oslot + (t + 1) * BT * kp, kp, store, lane, p);
       }
     }
   } else {
@@ -868,9 +928,10 @@ static FwdPlan fwd_plan(const GlFwdArgs* a, long long bf_cap = 0) {
   return q;
 }
 
-template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS, int PK, bool XG = false, bool SMALL = false>
+template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS, int PK, bool XG = false, bool SMALL = false,
+          int TB = BT>
 static int launch_fwd(const FwdK& k, hipStream_t s) {
-  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, PK, XG, SMALL>;
+  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, PK, XG, SMALL, TB>;
   dim3 grid((unsigned)ceil_div(k.n_chunks, WAVES));
   GL_LAUNCH(WS ? GL_KERNEL_FWD_WIN : GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
@@ -891,6 +952,11 @@ static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
   // mean and top-k at C2; the smooth pools measured even)
   if constexpr (W % 8 == 0 && !pk_smooth(PK))
     if (D <= XTILE_DB) return launch_fwd<K, FWD_NPL, W / 2, ACT, false, false, PK, false, true>(k, s);
+  // two-token tiles (sum / mean, XTILE_DB < D <= 2 XTILE_DB): two 64-KiB buffers in one workgroup
+  // of W waves (at C4, 81.7 ms against 83.7 ms for two workgroups of W / 2 waves with one tile each:
+  // the copy of the next tile overlaps the gathers, and the tile is shared by twice the neurons)
+  if constexpr (PK == PK_SUM)
+    if (k.tb == 2) return launch_fwd<K, FWD_NPL, W, ACT, true, false, PK, false, false, 2>(k, s);
   return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true, false, PK>(k, s)
                        : launch_fwd<K, FWD_NPL, W, ACT, false, false, PK>(k, s);
 }
@@ -976,16 +1042,19 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
   for (int b0 = 0; b0 < a->B; b0 += q.bf) {
     // one pass: tokens [b0, b0 + Bc), written to rows b0.. of pre / winner
     const int Bc = a->B - b0 < q.bf ? a->B - b0 : q.bf;
-    const int n_tiles = ceil_div(Bc, BT), b_pad = n_tiles * BT;
+    const int b_pad = (int)round_up(Bc, BT);
     float* pre = a->pre + (long long)b0 * a->G;
     int32_t* winner = a->winner ? a->winner + (long long)b0 * a->G * kpe : nullptr;
-    GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles, xt, s));
     FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, pslot, kpe, a->sched, nullptr, q.n_chunks, a->D, a->S, q.cpg,
-           n_tiles, b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0, a->rec_shift,
+           b_pad / BT, b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0, a->rec_shift,
            smooth_scale(a->pool, a->pool_param), a->pool_param, smooth_pint(a->pool, a->pool_param)};
     k.sps = a->sps > 1 ? a->sps : 1;
     k.gs = a->sps > 1 ? a->gs : a->S;
     if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) k.win = a->win;
+    // sum / mean over full tiles of 4097..8192 inputs: two-token tiles (two 64-KiB buffers)
+    k.tb = (pool_kind(a->pool) == PK_SUM && !k.win && tiles_of_two(a->D)) ? 2 : BT;
+    k.n_tiles = b_pad / k.tb;
+    GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, k.n_tiles, xt, s, k.tb));
     dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(b_pad, 32));
     if (a->pool == GL_POOL_MAX) {
       GL_TRY(launch_fwd_any<PK_MAX>(a->act, a->K, a->D, k, s));

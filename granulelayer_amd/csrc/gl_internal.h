@@ -31,9 +31,13 @@ int check_geometry(int G, int S, int32_t* sps, int32_t* gs);
 // padded width *ww and pools per workgroup *npw) when the pools' windows fit a stage tile.
 bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, int G, int* ww, int* npw);
 
-// X rows [b0, b0 + n_tiles*BT) -> token tiles [n_tiles][D] float4 (zero past B).
+// X rows [b0, b0 + n_tiles*tb) -> token tiles [n_tiles][D] of tb floats (zero past B): float4
+// slots (tb = 4) or the two-token float2 slots (tb = 2).  The same bytes either way.
 int launch_tile_x(const void* X, long long sxb, int x_dtype, int B, int D, int b0, int n_tiles, float4* xt,
-                  hipStream_t s);
+                  hipStream_t s, int tb = 4);
+
+// Two-token tiles (tb = 2) for the inputs past one 16-byte-slot buffer: XTILE_DB < D <= 2 XTILE_DB, D even.
+inline bool tiles_of_two(int D) { return D > XTILE_DB && D <= 2 * XTILE_DB && D % 2 == 0; }
 
 // Max / top-k pooling backward as selection events (gl_max_bwd.hip): dW / db / dX of one token
 // chunk [b0, b0 + Bc) from the chunk's token tiles, transposed coef / slots (c1t_kernel,

@@ -3,7 +3,11 @@ sparse_pooling/layout.py:57-58): the forward, dW and smooth recompute kernels ga
 token tiles in global memory and the selection events' dX walks the inputs in blocks.  Forward and
 backward of every pooling kind against the float64 oracle on identical seeded inputs (fp32 bar of
 conftest.assert_parity), K = 8 and 16, bf16 X, window staging; the same layer at a narrow D gives
-the same bits through the LDS path (the gather source does not change any arithmetic)."""
+the same bits through the LDS path (the gather source does not change any arithmetic).
+
+Widths 4097..8192 (even) run sum / mean forward and dW over two-token tiles (8-byte slots, one
+64-KiB buffer per tile): the same oracle checks, ragged token counts, and the bits of the
+four-token path for the same layer."""
 import numpy as np
 import pytest
 import torch
@@ -25,6 +29,14 @@ WIDE = [
     (32767, 9000, 9, 8, 70, torch.bfloat16),
     (20000, 6000, 6, 16, 33, torch.float32),
 ]
+TWO_TOKEN = [
+    # D, H, G, K, B, x dtype: two-token tiles (even D in 4097..8192); 5001 is odd (one 16-byte-slot tile)
+    (8192, 12000, 12, 8, 37, torch.bfloat16),
+    (6000, 20011, 16, 8, 130, torch.float32),
+    (4098, 7000, 7, 16, 66, torch.float32),
+    (8190, 9000, 9, 8, 2, torch.float32),
+    (5001, 8000, 8, 8, 33, torch.float32),
+]
 _ids = lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}"  # noqa: E731
 
 
@@ -32,7 +44,7 @@ def _rt(L, idx, spec):
     return Level1Runtime(L, idx.to(DEV), spec, PhysicalPlan())
 
 
-@pytest.mark.parametrize("case", WIDE, ids=_ids)
+@pytest.mark.parametrize("case", WIDE + TWO_TOKEN, ids=_ids)
 @pytest.mark.parametrize("pool,act", [("mean", "relu"), ("sum", "identity")])
 def test_wide_sum_and_mean(case, pool, act):
     D, H, G, K, B, xdt = case
@@ -139,6 +151,32 @@ def test_global_gather_gives_the_bits_of_the_lds_path():
     for D in (4096, 12288):
         L = L4 if D == 4096 else SparseLayout(D, 8000, 8, 8, 8, False)
         x = torch.zeros(40, D)
+        x[:, :4096] = x4
+        rt = _rt(L, idx, LevelSpec("mean", activation="relu"))
+        xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+        pre = rt.forward(xd, wd, bd)["pre"]
+        dw = torch.zeros(L.weight_shape, device=DEV)
+        db = torch.zeros(L.bias_shape, device=DEV)
+        dx = rt.backward(xd, wd, bd, dy.to(DEV), {}, "minimal_stats", dw, db)
+        outs.append((pre.cpu(), dw.cpu(), db.cpu(), dx[:, :4096].cpu()))
+        if D > 4096:
+            assert not dx[:, 4096:].any()
+    for a, c in zip(*outs):
+        assert torch.equal(a, c)
+
+
+def test_two_token_tiles_give_the_bits_of_four_token_tiles():
+    """One layer's parameters (indices below 4096) at D = 4096 (four-token tiles) and D = 8192
+    (two-token tiles; X's extra columns unused): pre, dW, db and dX of the shared inputs are
+    bit-identical.  Per token the sums run over the same neurons, edges and lanes in the same
+    order; the two-token wave reduction pairs the lanes as the four-token one does."""
+    from granulelayer_amd.layout import SparseLayout
+
+    L4, idx, w, b, x4, dy = make_case(4096, 8000, 8, 8, 41, seed=10)
+    outs = []
+    for D in (4096, 8192):
+        L = L4 if D == 4096 else SparseLayout(D, 8000, 8, 8, 8, False)
+        x = torch.zeros(41, D)
         x[:, :4096] = x4
         rt = _rt(L, idx, LevelSpec("mean", activation="relu"))
         xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
