@@ -75,6 +75,7 @@ struct FwdK {
   int pint;               // power mean: p when it is 1, 2, 4 or 8 (exact products), else 0
   int sps, gs;            // pool geometry (pool_base): shards per group and group stride in slots
   int tb;                 // tokens per tile: 4, or 2 (two-token tiles; n_tiles counts those)
+  int ws_small;           // window staging in workgroups of half the waves (two per CU, 64 KiB of stages)
 };
 
 // One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
@@ -515,11 +516,12 @@ __device__ __forceinline__ void fwd_tile_dispatch(SRC xsb, const unsigned (&addr
 template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, int PK = PK_SUM, bool XG = false,
           bool SMALL = false, int TB = BT>
 __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
-  // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots); XG: no LDS tile;
-  // SMALL: one single-buffered tile of at most XTILE_DB 16-byte slots, so two workgroups share a
-  // CU.  TB: tokens per tile (4, or 2 for the two-token tiles of SMALL sum / mean: D x 8 bytes)
+  // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots, XTILE_DB with
+  // SMALL); XG: no LDS tile; SMALL: one single-buffered tile of at most XTILE_DB 16-byte slots, so
+  // two workgroups share a CU.  TB: tokens per tile (4, or 2 for the two-token tiles of DBUF sum /
+  // mean: D x 8 bytes per buffer)
   static_assert(TB == BT || (TB == 2 && DBUF && !WS && !XG && PK == PK_SUM), "two-token tiles: sum / mean, two buffers");
-  __shared__ float4 xa[WS ? 2 * XTILE_DB : (XG ? 1 : (DBUF || SMALL ? XTILE_DB : XTILE_SB))];
+  __shared__ float4 xa[WS ? (SMALL ? XTILE_DB : 2 * XTILE_DB) : (XG ? 1 : (DBUF || SMALL ? XTILE_DB : XTILE_SB))];
   __shared__ float4 xb[DBUF ? XTILE_DB : 1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar chunk addressing
@@ -944,7 +946,11 @@ static int launch_fwd(const FwdK& k, hipStream_t s) {
 template <int ACT, int K, int PK>
 static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
   constexpr int W = fwd_waves(K, PK);
-  if (k.win) return launch_fwd<K, FWD_NPL, W, ACT, false, true, PK>(k, s);
+  if (k.win) {
+    if constexpr (W % 8 == 0 && !pk_smooth(PK))
+      if (k.ws_small) return launch_fwd<K, FWD_NPL, W / 2, ACT, false, true, PK, false, true>(k, s);
+    return launch_fwd<K, FWD_NPL, W, ACT, false, true, PK>(k, s);
+  }
   if (D > XTILE_SB) return launch_fwd<K, FWD_NPL, W, ACT, false, false, PK, true>(k, s);
   // D <= XTILE_DB: two workgroups of W / 2 waves per CU, each with one 64-KiB tile, when W / 2 waves
   // spread evenly over the 4 SIMDs: while one workgroup waits at its tile barrier for its slowest
@@ -973,13 +979,14 @@ static int launch_fwd_any(int act, int K, int D, const FwdK& k, hipStream_t s) {
 
 // Window staging applies when the staged windows of a workgroup's pools (npw of them, each ww
 // inputs) fit a stage tile (<= WS_SLOTS) and are narrower than the full input width.
-bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, int G, int* ww, int* npw) {
+bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, int G, int* ww, int* npw,
+                    int max_slots) {
   if (!win || width < 1) return false;
   const int w = (int)round_up(width, 64);
   // pools spanned by `waves` consecutive chunks (cpg chunks per pool)
   int n = waves % cpg == 0 ? waves / cpg : (waves - 1) / cpg + 2;
   if (n > G) n = G;
-  if ((long long)n * w > WS_SLOTS || (long long)n * w >= D) return false;
+  if ((long long)n * w > max_slots || (long long)n * w >= D) return false;
   *ww = w;
   *npw = n;
   return true;
@@ -1050,7 +1057,15 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
            smooth_scale(a->pool, a->pool_param), a->pool_param, smooth_pint(a->pool, a->pool_param)};
     k.sps = a->sps > 1 ? a->sps : 1;
     k.gs = a->sps > 1 ? a->gs : a->S;
-    if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) k.win = a->win;
+    // window staging: two workgroups of half the waves per CU when their windows fit half the slots
+    // (the rule of the full-tile kernels: wave counts that spread evenly, not the smooth pools)
+    if (q.waves % 8 == 0 && !pool_smooth(a->pool) &&
+        window_staging(a->win, a->win_width, a->D, q.waves / 2, q.cpg, a->G, &k.ww, &k.npw, WS_SLOTS / 2)) {
+      k.win = a->win;
+      k.ws_small = 1;
+    } else if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) {
+      k.win = a->win;
+    }
     // sum / mean over full tiles of 4097..8192 inputs: two-token tiles (two 64-KiB buffers)
     k.tb = (pool_kind(a->pool) == PK_SUM && !k.win && tiles_of_two(a->D)) ? 2 : BT;
     k.n_tiles = b_pad / k.tb;
