@@ -135,59 +135,62 @@ __device__ __forceinline__ double pow2(int e) {
   return __longlong_as_double((long long)(1023 + e) << 52);
 }
 
-// dX of one token, its inputs in blocks of dblk (the whole row when it fits the LDS).  LDS: dblk
-// 64-bit fixed-point accumulators, the inputs' term bounds (float bits, replaced by each input's
-// scale exponent), then, with a single block, the token's X row (with several, x is read from the
-// token tile in global memory).  Every input's sum and scale depend only on its own terms, so the
-// blocking does not change the result.
-template <int K, int ACT>
+// dX of one token, its inputs in blocks of dblk (the whole row when it fits the LDS).  The events'
+// terms dz * W[n*, k] are summed into dX[b, idx] as fixed-point integers, so the sum does not
+// depend on the order of the LDS atomics.  One scale per token, 2^sh with
+// sh = 61 - floor(log2(bound)) + 32 for bound = (largest |g_pre| * |W| of the token's events) *
+// G * kpe * K: a term t = dz * w * 2^sh (|t| < 2^94, 24 significant bits) splits exactly into
+// t = hi * 2^32 + lo (hi = floor(t / 2^32), 0 <= lo < 2^32), and per input the hi parts and the lo
+// parts are summed in two 64-bit words (|sum hi| < 2^63; sum lo < 2^32 * 2^31 terms).  The
+// quantum is ~2^-70 of the token's largest term (~2^-38 with one 64-bit word), so inputs fed only
+// by terms many orders below it keep fp32 accuracy.  LDS: dblk pairs of words, then, with a single
+// block, the token's X row (with several, x is read from the token tile in global memory).
+template <int K, int ACT, bool ONE>
 __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
+  // ONE is a compile-time choice, so each instantiation reads X from one address space (a run-time
+  // choice between the LDS row and the global tile makes the compiler use flat loads for both)
   extern __shared__ unsigned long long ldsq[];
-  const int DB = p.dblk;
-  const bool one = DB >= p.D;
-  unsigned long long* acc = ldsq;                          // [DB]
-  unsigned* tmax = reinterpret_cast<unsigned*>(ldsq + DB);  // [DB]
-  float* xrow = reinterpret_cast<float*>(tmax + DB);        // [D], single block only
+  __shared__ unsigned tokmax;
+  const int DB = ONE ? p.D : p.dblk;
+  unsigned long long* acc_hi = ldsq;                          // [DB]
+  unsigned long long* acc_lo = ldsq + DB;                     // [DB]
+  float* xrow = reinterpret_cast<float*>(ldsq + 2 * DB);      // [D], single block only
   const int b = blockIdx.x;
   const long long row = (long long)(p.b0 + b) * p.G;  // [B, G] row of the token; winners: row * kpe
-  if (one)
+  if constexpr (ONE)
     for (int d = threadIdx.x; d < p.D; d += blockDim.x) xrow[d] = tile_x(p.xt, p.D, b, d);
-  const double nterm = (double)p.G * (double)p.kpe * (double)K;
+  if (threadIdx.x == 0) tokmax = 0u;
+  __syncthreads();
+  // pass 1: every term |dz * W[n*, k]| is at most |g_pre| * |W[n*, k]| (act' <= 1); the bits of
+  // non-negative floats order like the values, so an integer maximum is the float maximum
+  float m = 0.f;
+  for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
+    const int g = e / p.kpe;
+    const int s = p.winner[row * p.kpe + e];
+    if (s < 0 || s >= pool_ext(g, p.S, p.sps, p.gs)) continue;
+    const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
+    float wm = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) wm = __builtin_fmaxf(wm, __builtin_fabsf(p.W[n * K + k]));
+    m = __builtin_fmaxf(m, __builtin_fabsf(p.g_pre[row + g]) * wm);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
+  if ((threadIdx.x & 63) == 0) atomicMax(&tokmax, __float_as_uint(m));
+  __syncthreads();
+  const double bound = (double)__uint_as_float(tokmax) * ((double)p.G * (double)p.kpe * (double)K);
+  const int e2 = bound > 0.0 ? (int)((__double_as_longlong(bound) >> 52) & 0x7ff) - 1023 : 0;
+  const int sh = 61 - e2 + 32;
+  const double scale = pow2(sh), unscale = pow2(-sh);
+  const double two32 = 4294967296.0, inv32 = 1.0 / 4294967296.0;
   for (int lo = 0; lo < p.D; lo += DB) {
     const int nb = p.D - lo < DB ? p.D - lo : DB;
     for (int i = threadIdx.x; i < nb; i += blockDim.x) {
-      acc[i] = 0ull;
-      tmax[i] = 0u;
+      acc_hi[i] = 0ull;
+      acc_lo[i] = 0ull;
     }
     __syncthreads();
-    // pass 1: every term dz * W[n*, k] into input d = idx[n*, k] is at most |g_pre| * |W[n*, k]|;
-    // tmax[d] = the largest such bound (the bits of non-negative floats order like the values, so
-    // the integer maximum is the float maximum, whatever the order of the updates)
-    for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
-      const int g = e / p.kpe;
-      const int s = p.winner[row * p.kpe + e];
-      if (s < 0 || s >= pool_ext(g, p.S, p.sps, p.gs)) continue;
-      const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
-      const float gb = __builtin_fabsf(p.g_pre[row + g]);
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        int d = rec_index(p.idx, n, k, K, p.rs);
-        d = d < 0 ? 0 : (d >= p.D ? p.D - 1 : d);
-        if ((unsigned)(d - lo) < (unsigned)nb) atomicMax(&tmax[d - lo], __float_as_uint(gb * __builtin_fabsf(p.W[n * K + k])));
-      }
-    }
-    __syncthreads();
-    // per input: at most G * kpe * K terms of magnitude <= tmax[d], so |sum| * 2^e_d < 2^62 with
-    // e_d = 61 - floor(log2(tmax[d] * G * kpe * K)); floor(log2) read from the (normal) double's
-    // exponent field.  The scale follows each input's own largest term: small inputs keep ~2^-38
-    // (at 2^23 terms) of their own magnitude, not of the token's largest term.
-    for (int i = threadIdx.x; i < nb; i += blockDim.x) {
-      const double bound = (double)__uint_as_float(tmax[i]) * nterm;
-      const int e2 = bound > 0.0 ? (int)((__double_as_longlong(bound) >> 52) & 0x7ff) - 1023 : 0;
-      tmax[i] = (unsigned)(61 - e2);  // a signed exponent, stored in the same word
-    }
-    __syncthreads();
-    // pass 2: the events' dz * W[n*, k] as fixed-point integers at their input's scale
+    // pass 2: the events' terms, split into (hi, lo) words
     for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
       const int g = e / p.kpe;
       int s = p.winner[row * p.kpe + e];
@@ -202,39 +205,59 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
         coef = coef / (float)(n_g < p.kpe ? n_g : p.kpe);
       }
       const float dz = event_dz<K, ACT>(
-          p, n, coef, [&](int d) { return one ? xrow[d] : tile_x(p.xt, p.D, b, d); }, xk, wk, dk);
+          p, n, coef,
+          [&](int d) {
+            if constexpr (ONE) return xrow[d];
+            else return tile_x(p.xt, p.D, b, d);
+          },
+          xk, wk, dk);
       if (!ok || dz == 0.f) continue;
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         const int i = dk[k] - lo;
         if ((unsigned)i >= (unsigned)nb) continue;
-        const long long q = __double2ll_rn((double)(dz * wk[k]) * pow2((int)tmax[i]));
-        atomicAdd(&acc[i], (unsigned long long)q);
+        const double t = __builtin_rint((double)(dz * wk[k]) * scale);  // an integer (exact above 2^24)
+        const double h = __builtin_floor(t * inv32);                     // <= 24 significant bits
+        const double l = t - h * two32;                                  // exact, in [0, 2^32)
+        atomicAdd(&acc_hi[i], (unsigned long long)(long long)h);
+        atomicAdd(&acc_lo[i], (unsigned long long)(unsigned)l);
       }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < nb; i += blockDim.x)
-      p.dX[(long long)(p.b0 + b) * p.D + lo + i] = (float)((double)(long long)acc[i] / pow2((int)tmax[i]));
-    __syncthreads();  // the next block reinitialises acc and tmax
+    for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+      // value = hi * 2^32 + lo, carried in integers first so the one rounding is to double
+      const unsigned long long lw = acc_lo[i];
+      const long long hw = (long long)acc_hi[i] + (long long)(lw >> 32);
+      const double v = ((double)hw * two32 + (double)(unsigned)(lw & 0xffffffffull)) * unscale;
+      p.dX[(long long)(p.b0 + b) * p.D + lo + i] = (float)v;
+    }
+    __syncthreads();  // the next block reinitialises the accumulators
   }
 }
 
 template <int K, int ACT>
 static int launch_max_events_k(MaxEvK k, hipStream_t s) {
   const size_t dw_lds = (size_t)k.npow2 * 4 + (size_t)k.tsub * k.kpe * (K + 1) * 4;
-  // dX: the whole row (16 bytes per input) when it fits, else blocks of 12-byte inputs
-  size_t dx_lds = (size_t)k.D * 16;
+  // dX: the whole row (20 bytes per input: two accumulator words and x) when it fits, else blocks
+  // of 16-byte inputs (the kernel's static LDS word aside)
+  const size_t room = max_lds_bytes() - 64;
+  size_t dx_lds = (size_t)k.D * 20;
   k.dblk = k.D;
-  if (dx_lds > max_lds_bytes()) {
-    k.dblk = (int)(max_lds_bytes() / 12 / 64 * 64);
-    dx_lds = (size_t)k.dblk * 12;
+  if (dx_lds > room) {
+    k.dblk = (int)(room / 16 / 64 * 64);
+    dx_lds = (size_t)k.dblk * 16;
   }
   if (dw_lds > max_lds_bytes() || k.dblk < 64) return GL_ERR_LDS;
   GL_TRY(set_lds_limit((const void*)max_events_dw_kernel<K, ACT>, dw_lds));
-  GL_TRY(set_lds_limit((const void*)max_events_dx_kernel<K, ACT>, dx_lds));
+  const bool one = k.dblk >= k.D;
+  const void* dxk = one ? (const void*)max_events_dx_kernel<K, ACT, true> : (const void*)max_events_dx_kernel<K, ACT, false>;
+  GL_TRY(set_lds_limit(dxk, dx_lds));
   GL_LAUNCH(GL_KERNEL_MAX_EV_DW, (max_events_dw_kernel<K, ACT>), dim3((unsigned)k.G), dim3(256), dw_lds, s, k);
   GL_CHECK_LAUNCH();
-  GL_LAUNCH(GL_KERNEL_MAX_EV_DX, (max_events_dx_kernel<K, ACT>), dim3((unsigned)k.Bc), dim3(1024), dx_lds, s, k);
+  if (one)
+    GL_LAUNCH(GL_KERNEL_MAX_EV_DX, (max_events_dx_kernel<K, ACT, true>), dim3((unsigned)k.Bc), dim3(1024), dx_lds, s, k);
+  else
+    GL_LAUNCH(GL_KERNEL_MAX_EV_DX, (max_events_dx_kernel<K, ACT, false>), dim3((unsigned)k.Bc), dim3(1024), dx_lds, s, k);
   GL_CHECK_LAUNCH();
   return 0;
 }
