@@ -35,6 +35,24 @@ __global__ void __launch_bounds__(256) tile_x_kernel(const XT* __restrict__ X, l
   else reinterpret_cast<float2*>(out)[i] = make_float2(v[0], v[1]);
 }
 
+// bf16 X [B, D] -> XT [n_tiles][D] of 4 tokens as raw bf16 bits in 8 bytes: word 0 = token 1 << 16 |
+// token 0, word 1 = token 3 << 16 | token 2 (tokens >= B are +0).  The kernels widen each value
+// with one shift or mask, which is exact.
+__global__ void __launch_bounds__(256) tile_x_bf16x4_kernel(const unsigned short* __restrict__ X, long long sxb, int B,
+                                                            int D, int b0, int n_tiles, uint2* __restrict__ out) {
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  long long total = (long long)n_tiles * D;
+  if (i >= total) return;
+  int t = (int)(i / D), d = (int)(i % D);
+  unsigned v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    int b = b0 + t * 4 + j;
+    v[j] = b < B ? (unsigned)X[(long long)b * sxb + d] : 0u;
+  }
+  out[i] = make_uint2(v[1] << 16 | v[0], v[3] << 16 | v[2]);
+}
+
 template <int TB>
 static int launch_tile_x_tb(const void* X, long long sxb, int x_dtype, int B, int D, int b0, int n_tiles, float* xt,
                             hipStream_t s) {
@@ -46,6 +64,17 @@ static int launch_tile_x_tb(const void* X, long long sxb, int x_dtype, int B, in
   else
     GL_LAUNCH(GL_KERNEL_TILE_X, (tile_x_kernel<__hip_bfloat16, TB>), grid, dim3(256), 0, s, (const __hip_bfloat16*)X,
               sxb, B, D, b0, n_tiles, xt);
+  GL_CHECK_LAUNCH();
+  return 0;
+}
+
+// bf16 X only: 4-token tiles of raw bf16 (8-byte slots)
+static int launch_tile_x_bf16x4(const void* X, long long sxb, int B, int D, int b0, int n_tiles, void* xt,
+                                hipStream_t s) {
+  long long total = (long long)n_tiles * D;
+  dim3 grid((unsigned)ceil_div(total, 256));
+  GL_LAUNCH(GL_KERNEL_TILE_X, tile_x_bf16x4_kernel, grid, dim3(256), 0, s, (const unsigned short*)X, sxb, B, D, b0,
+            n_tiles, (uint2*)xt);
   GL_CHECK_LAUNCH();
   return 0;
 }
@@ -76,6 +105,7 @@ struct FwdK {
   int sps, gs;            // pool geometry (pool_base): shards per group and group stride in slots
   int tb;                 // tokens per tile: 4, or 2 (two-token tiles; n_tiles counts those)
   int ws_small;           // window staging in workgroups of half the waves (two per CU, 64 KiB of stages)
+  int xb;                 // 4-token tiles of raw bf16 (8-byte slots; bf16 X, sum / mean)
 };
 
 // One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
@@ -125,6 +155,58 @@ __device__ __forceinline__ void fwd_tile(SRC xsb, const unsigned (&addr)[NPL][K]
   }
   const float tot = wave_sum4(a0, a1, a2, a3, lane);
   if (store && lane < 4) out[wave_sum4_token(lane)] = tot;  // 4 lanes, 16 contiguous bytes
+}
+
+// The sum / mean tile over a 4-token tile of raw bf16 values (8-byte slots, ds_read_b64): the gathers
+// keep the packed words (the read-ahead holds 2 registers per slot, not 4) and each value is
+// widened (shift or mask: exact) right before its FMA.  The arithmetic is fwd_tile's.
+template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8)>
+__device__ __forceinline__ void fwd_tile_bf4(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+                                             const float (&bias)[NPL], float* out, bool store, int lane) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  uint2 xc[K];
+  auto ld = [&](unsigned a) {
+    if constexpr (FAR) asm volatile("" : "+v"(a));
+    return *reinterpret_cast<const uint2*>(xsb + a);
+  };
+#pragma unroll
+  for (int k = 0; k < RA; ++k) xc[k] = ld(addr[0][k]);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+#pragma unroll
+    for (int k = RA; k < K; ++k) xc[k] = ld(addr[j][k]);
+    uint2 xn[RA];
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xn[k] = ld(addr[j + 1][k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      z0 = __builtin_fmaf(__uint_as_float(xc[k].x << 16), w[j][k], z0);
+      z1 = __builtin_fmaf(__uint_as_float(xc[k].x & 0xffff0000u), w[j][k], z1);
+      z2 = __builtin_fmaf(__uint_as_float(xc[k].y << 16), w[j][k], z2);
+      z3 = __builtin_fmaf(__uint_as_float(xc[k].y & 0xffff0000u), w[j][k], z3);
+    }
+    if (ACT == GL_ACT_RELU) {
+      z0 = __builtin_fmaxf(z0, 0.f);
+      z1 = __builtin_fmaxf(z1, 0.f);
+      z2 = __builtin_fmaxf(z2, 0.f);
+      z3 = __builtin_fmaxf(z3, 0.f);
+    }
+    a0 += z0;
+    a1 += z1;
+    a2 += z2;
+    a3 += z3;
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xc[k] = xn[k];
+    }
+  }
+  const float tot = wave_sum4(a0, a1, a2, a3, lane);
+  if (store && lane < 4) out[wave_sum4_token(lane)] = tot;
 }
 
 // The sum / mean tile over a two-token tile (8-byte slots, ds_read_b64); lanes 0-1 store.
@@ -514,13 +596,16 @@ __device__ __forceinline__ void fwd_tile_dispatch(SRC xsb, const unsigned (&addr
 }
 
 template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, int PK = PK_SUM, bool XG = false,
-          bool SMALL = false, int TB = BT>
+          bool SMALL = false, int TB = BT, bool XB = false>
 __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots, XTILE_DB with
   // SMALL); XG: no LDS tile; SMALL: one single-buffered tile of at most XTILE_DB 16-byte slots, so
   // two workgroups share a CU.  TB: tokens per tile (4, or 2 for the two-token tiles of DBUF sum /
   // mean: D x 8 bytes per buffer)
+  // XB: 4-token tiles of raw bf16 (8-byte slots, bf16 X), one buffer (SMALL) or two
   static_assert(TB == BT || (TB == 2 && DBUF && !WS && !XG && PK == PK_SUM), "two-token tiles: sum / mean, two buffers");
+  static_assert(!XB || (TB == BT && (DBUF || SMALL) && !WS && !XG && PK == PK_SUM), "bf16 tiles: sum / mean");
+  constexpr unsigned SLOT = XB ? 8u : 4u * TB;  // bytes per input of a tile
   __shared__ float4 xa[WS ? (SMALL ? XTILE_DB : 2 * XTILE_DB) : (XG ? 1 : (DBUF || SMALL ? XTILE_DB : XTILE_SB))];
   __shared__ float4 xb[DBUF ? XTILE_DB : 1];
   const int lane = threadIdx.x & 63;
@@ -554,7 +639,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       const int k = sched_k<K>(order, ks);  // the pooled sum does not depend on the visiting order
       int d = rec_index(p.idx, n, k, K, p.rs);
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-      addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * (4u * TB);
+      addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * SLOT;
       const float wl = p.W[n * K + k];
       w[j][ks] = valid ? wl : 0.f;
     }
@@ -609,13 +694,15 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       fwd_tile_dispatch<K, NPL, ACT, false, PK>(xbuf(p.xt + (long long)t * p.D, p.D), addr, w, bias, slot, vmask,
                                                 out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
   } else if constexpr (DBUF) {
-    const int ns = p.D * TB / 4;  // 16-byte slots per tile
+    const int ns = (int)((long long)p.D * SLOT / 16);  // 16-byte slots per tile
     dma_tile(p.xt, xa, ns, NT);
     for (int t = 0; t < p.n_tiles; t += 2) {
       stage_wait();
       __syncthreads();  // tile t is in xa; every wave is done with xb (tile t - 1)
       if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * ns, xb, ns, NT);
-      if constexpr (TB == 2)
+      if constexpr (XB)
+        fwd_tile_bf4<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
+      else if constexpr (TB == 2)
         fwd_tile2<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * 2, store, lane);
       else
         fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
@@ -624,7 +711,10 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
         stage_wait();
         __syncthreads();  // tile t + 1 is in xb; every wave is done with xa
         if (t + 2 < p.n_tiles) dma_tile(p.xt + (long long)(t + 2) * ns, xa, ns, NT);
-        if constexpr (TB == 2)
+        if constexpr (XB)
+          fwd_tile_bf4<K, NPL, ACT, true>(reinterpret_cast<const char*>(xb), addr, w, bias, out + (t + 1) * BT, store,
+                                          lane);
+        else if constexpr (TB == 2)
           fwd_tile2<K, NPL, ACT, true>(reinterpret_cast<const char*>(xb), addr, w, bias, out + (t + 1) * 2, store, lane);
         else
           fwd_tile_dispatch<K, NPL, ACT, true, PK>(reinterpret_cast<const char*>(xb), addr, w, bias, slot, vmask,
@@ -632,13 +722,17 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       }
     }
   } else {
+    const int ns = (int)((long long)p.D * SLOT / 16);  // 16-byte slots per tile
     for (int t = 0; t < p.n_tiles; ++t) {
       __syncthreads();  // every wave is done with tile t - 1
-      dma_tile(p.xt + (long long)t * p.D, xa, p.D, NT);
+      dma_tile(p.xt + (long long)t * ns, xa, ns, NT);
       stage_wait();
       __syncthreads();
-      fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
-                                                out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
+      if constexpr (XB)
+        fwd_tile_bf4<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
+      else
+        fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
+                                                  out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
     }
   }
 }
@@ -931,9 +1025,9 @@ static FwdPlan fwd_plan(const GlFwdArgs* a, long long bf_cap = 0) {
 }
 
 template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS, int PK, bool XG = false, bool SMALL = false,
-          int TB = BT>
+          int TB = BT, bool XB = false>
 static int launch_fwd(const FwdK& k, hipStream_t s) {
-  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, PK, XG, SMALL, TB>;
+  auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, PK, XG, SMALL, TB, XB>;
   dim3 grid((unsigned)ceil_div(k.n_chunks, WAVES));
   GL_LAUNCH(WS ? GL_KERNEL_FWD_WIN : GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
@@ -963,6 +1057,10 @@ static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
   // the copy of the next tile overlaps the gathers, and the tile is shared by twice the neurons)
   if constexpr (PK == PK_SUM)
     if (k.tb == 2) return launch_fwd<K, FWD_NPL, W, ACT, true, false, PK, false, false, 2>(k, s);
+  // bf16 X at those widths: 4-token tiles of raw bf16 (64 KiB at D = 8192), one per workgroup and
+  // two workgroups per CU (C4 forward 81.8 -> 51.5 ms; two buffers in one workgroup: 56.3 ms)
+  if constexpr (PK == PK_SUM && W % 8 == 0)
+    if (k.xb) return launch_fwd<K, FWD_NPL, W / 2, ACT, false, false, PK, false, true, BT, true>(k, s);
   return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true, false, PK>(k, s)
                        : launch_fwd<K, FWD_NPL, W, ACT, false, false, PK>(k, s);
 }
@@ -1066,10 +1164,16 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
     } else if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) {
       k.win = a->win;
     }
-    // sum / mean over full tiles of 4097..8192 inputs: two-token tiles (two 64-KiB buffers)
-    k.tb = (pool_kind(a->pool) == PK_SUM && !k.win && tiles_of_two(a->D)) ? 2 : BT;
+    // sum / mean over full tiles of 4097..8192 inputs: bf16 X keeps its bf16 values, 4 tokens per
+    // 8-byte slot; fp32 X goes to two-token tiles (8-byte slots of 2 fp32 tokens)
+    const bool wide = pool_kind(a->pool) == PK_SUM && !k.win && tiles_of_two(a->D);
+    k.xb = wide && a->x_dtype == GL_DTYPE_BF16;
+    k.tb = wide && !k.xb ? 2 : BT;
     k.n_tiles = b_pad / k.tb;
-    GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, k.n_tiles, xt, s, k.tb));
+    if (k.xb)
+      GL_TRY(launch_tile_x_bf16x4(a->X, a->sxb, a->B, a->D, b0, k.n_tiles, xt, s));
+    else
+      GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, k.n_tiles, xt, s, k.tb));
     dim3 grid((unsigned)ceil_div(a->G, 32), (unsigned)ceil_div(b_pad, 32));
     if (a->pool == GL_POOL_MAX) {
       GL_TRY(launch_fwd_any<PK_MAX>(a->act, a->K, a->D, k, s));

@@ -189,3 +189,19 @@ def test_two_token_tiles_give_the_bits_of_four_token_tiles():
             assert not dx[:, 4096:].any()
     for a, c in zip(*outs):
         assert torch.equal(a, c)
+
+
+def test_bf16_tiles_give_the_bits_of_fp32_tiles():
+    """bf16 X at 4096 < D <= 8192 runs the forward over 4-token tiles of raw bf16 values (each
+    widened exactly before its FMA); the same values given as fp32 X run two-token fp32 tiles.
+    pre is bit-identical, and matches the oracle; ragged B."""
+    L, idx, w, b, x, dy = make_case(8192, 12000, 12, 8, 45, x_dtype=torch.bfloat16, seed=13)
+    rt = _rt(L, idx, LevelSpec("mean", activation="relu"))
+    wd, bd = w.to(DEV), b.to(DEV)
+    pre_b = rt.forward(x.to(DEV), wd, bd)["pre"]
+    pre_f = rt.forward(x.float().to(DEV), wd, bd)["pre"]
+    assert torch.equal(pre_b, pre_f)
+    fi, fw, fb = flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    want, mag = O.forward(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, "relu", "mean", with_mag=True)
+    assert_parity(pre_b.cpu().numpy(), want, mag, what="pre")
