@@ -79,6 +79,7 @@ struct BwK {
   int rs;                 // log2 slots per shared index record
   int sps, gs;            // pool geometry (pool_base)
   int tb;                 // tokens per tile: 4, or 2 (two-token tiles; n_tiles counts those)
+  int xb;                 // 4-token tiles of raw bf16 (8-byte slots; bf16 X)
 };
 
 // One token tile of the dW pass (LDS at xsb): recompute z, form dz = c1 * act'(z), accumulate
@@ -127,6 +128,64 @@ __device__ __forceinline__ void bwd_w_tile(SRC xsb, int t, const float4 c1, cons
     if (j + 1 < NPL) {
 #pragma unroll
       for (int k = 0; k < RA; ++k) xc[k] = xn[k];
+    }
+  }
+}
+
+// The same over a 4-token tile of raw bf16 values (8-byte slots): the gathers keep the packed
+// words, which are widened (exactly) once after the read-ahead and used for both z and dW.
+template <int K, int NPL, int ACT, int RA, bool FAR>
+__device__ __forceinline__ void bwd_w_tile_bf4(const char* xsb, int t, const float4 c1, const unsigned (&addr)[NPL][K],
+                                               const float (&w)[NPL][K], const float (&bias)[NPL], float (&dw)[NPL][K],
+                                               float (&dbv)[NPL], unsigned (&mw)[NPL]) {
+  uint2 xr[K];
+  auto ld = [&](unsigned a) {
+    if constexpr (FAR) asm volatile("" : "+v"(a));
+    return *reinterpret_cast<const uint2*>(xsb + a);
+  };
+#pragma unroll
+  for (int k = 0; k < RA; ++k) xr[k] = ld(addr[0][k]);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+#pragma unroll
+    for (int k = RA; k < K; ++k) xr[k] = ld(addr[j][k]);
+    uint2 xn[RA];
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xn[k] = ld(addr[j + 1][k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float4 xc[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      xc[k] = make_float4(__uint_as_float(xr[k].x << 16), __uint_as_float(xr[k].x & 0xffff0000u),
+                          __uint_as_float(xr[k].y << 16), __uint_as_float(xr[k].y & 0xffff0000u));
+    float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
+      z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
+      z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
+      z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
+    }
+    const bool m0 = ACT != GL_ACT_RELU || z0 > 0.f, m1 = ACT != GL_ACT_RELU || z1 > 0.f;
+    const bool m2 = ACT != GL_ACT_RELU || z2 > 0.f, m3 = ACT != GL_ACT_RELU || z3 > 0.f;
+    const float d0 = m0 ? c1.x : 0.f, d1 = m1 ? c1.y : 0.f, d2 = m2 ? c1.z : 0.f, d3 = m3 ? c1.w : 0.f;
+    dbv[j] = dbv[j] + d0 + d1 + d2 + d3;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      float a = dw[j][k];
+      a = __builtin_fmaf(d0, xc[k].x, a);
+      a = __builtin_fmaf(d1, xc[k].y, a);
+      a = __builtin_fmaf(d2, xc[k].z, a);
+      a = __builtin_fmaf(d3, xc[k].w, a);
+      dw[j][k] = a;
+    }
+    mw[j] |= ((unsigned)m0 | ((unsigned)m1 << 1) | ((unsigned)m2 << 2) | ((unsigned)m3 << 3)) << ((t & 7) * 4);
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xr[k] = xn[k];
     }
   }
 }
@@ -180,11 +239,15 @@ __device__ __forceinline__ void bwd_w_tile2(const char* xsb, int t, const float2
 // VGPRs a wave has at 2 waves per SIMD with the dW accumulators live).  Otherwise one buffer:
 // load, wait, read.  The wave index goes through readfirstlane so the chunk's parameters and the
 // c1 row are addressed with scalar registers.
-template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF, bool WS = false, bool XG = false, int TB = BT>
+template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF, bool WS = false, bool XG = false, int TB = BT,
+          bool XB = false>
 __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   // XG (D > XTILE_SB): no LDS tile, the lanes gather from the token tiles in global memory.
   // TB: tokens per tile, 4 or 2 (two-token tiles in the two buffers of DBUF: D <= 2 XTILE_DB)
   static_assert(TB == BT || (TB == 2 && DBUF && !WS && !XG), "two-token tiles: double-buffered only");
+  // XB: 4-token tiles of raw bf16 (8-byte slots, bf16 X), double-buffered
+  static_assert(!XB || (TB == BT && DBUF && !WS && !XG), "bf16 tiles: double-buffered only");
+  constexpr unsigned SLOT = XB ? 8u : 4u * TB;  // bytes per input of a tile
   __shared__ float4 xs[DBUF || WS ? 2 * XTILE_DB : (XG ? 1 : XTILE_SB)];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -217,7 +280,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
       const int k = sched_k<K>(order, ks);
       int d = rec_index(p.idx, n, k, K, p.rs);
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-      addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * (4u * TB);
+      addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * SLOT;
       const float wl = p.W[n * K + k];
       w[j][ks] = valid ? wl : 0.f;
       dw[j][ks] = 0.f;
@@ -229,7 +292,7 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   const float* c1row = p.c1t + g * p.cap;
   constexpr int NT = WAVES * 64;
   constexpr int TPW = 32 / TB;       // tiles per mask word
-  const int ns = p.D * TB / 4;       // 16-byte slots per tile (D even for two-token tiles)
+  const int ns = (int)((long long)p.D * SLOT / 16);  // 16-byte slots per tile (D even for 8-byte slots)
 
   // window staging: WS_TILES tiles per stage and barrier; tile t at slot (t mod 2 WS_TILES) * nsl
   const WinLayout L{p.win, p.ww, p.npw, g_first, p.G};
@@ -283,7 +346,11 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
         // buffer cur ^ 1 was last read in tile t - 1, which every wave finished before the barrier
         const int cur = t & 1;
         if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * ns, xs + (cur ^ 1) * XTILE_DB, ns, NT);
-        if constexpr (TB == 2) {
+        if constexpr (XB) {
+          const float4 c1 = ld_uniform4(c1row, t * BT);
+          bwd_w_tile_bf4<K, NPL, ACT, RA, true>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t,
+                                                c1, addr, w, bias, dw, dbv, mw);
+        } else if constexpr (TB == 2) {
           const float2 c1 = ld_uniform2(c1row, t * 2);
           bwd_w_tile2<K, NPL, ACT, RA, true>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t, c1,
                                              addr, w, bias, dw, dbv, mw);
@@ -1019,6 +1086,7 @@ void edge_layout(int D, int G, int S, int K, EdgeHeader* h, size_t* total) {
 template <int K, int NPL, int WAVES, int ACT, int RA>
 static int launch_bwd_w(const BwK& k, hipStream_t s) {
   auto fn = k.win ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, true>
+                  : k.xb ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true, false, false, BT, true>
                   : k.tb == 2 ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true, false, false, 2>
                   : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true>
                                      : (k.D <= XTILE_SB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false>
@@ -1155,8 +1223,15 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     int ww = 0, npw = 0;
     const bool dense = !smooth && !a->winner;
     const bool win = dense && window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &ww, &npw);
-    const int tb = dense && !win && tiles_of_two(a->D) ? 2 : BT;
-    GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles * BT / tb, xt, s, tb));
+    const bool wide = dense && !win && tiles_of_two(a->D);
+    // bf16 X keeps its bf16 values, 4 tokens per 8-byte slot (C4 dW 114.3 -> 90.2 ms against
+    // two-token fp32 tiles: half the gathers and tile overheads per token for one widening per value)
+    const bool xb = wide && a->x_dtype == GL_DTYPE_BF16;
+    const int tb = wide && !xb ? 2 : BT;
+    if (xb)
+      GL_TRY(launch_tile_x_bf16x4(a->X, a->sxb, a->B, a->D, b0, n_tiles, xt, s));
+    else
+      GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles * BT / tb, xt, s, tb));
     if (smooth) {  // coefficients, recompute pass (dW, db, dz), dX from dz
       float* c2t = (float*)(ws + q.xt_bytes + q.c1_bytes + q.part_bytes);
       float* c3t = (float*)((char*)c2t + q.c1_bytes);
@@ -1202,7 +1277,7 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     const long long NS = (long long)a->G * a->S;
     BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, a->sched, nullptr, q.n_chunks, NS,
            a->D, a->S, q.cpg, n_tiles * BT / tb, cap, 2 * T, ceil_div(a->S, SCHED_WIN), a->G, ww, npw, a->rec_shift,
-           sps, gs, tb};
+           sps, gs, tb, xb ? 1 : 0};
     if (win) bk.win = a->win;
     GL_TRY(launch_bwd_w_any(a->K, a->act, bk, s));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),

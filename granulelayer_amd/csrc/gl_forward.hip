@@ -69,7 +69,7 @@ static int launch_tile_x_tb(const void* X, long long sxb, int x_dtype, int B, in
 }
 
 // bf16 X only: 4-token tiles of raw bf16 (8-byte slots)
-static int launch_tile_x_bf16x4(const void* X, long long sxb, int B, int D, int b0, int n_tiles, void* xt,
+int launch_tile_x_bf16x4(const void* X, long long sxb, int B, int D, int b0, int n_tiles, void* xt,
                                 hipStream_t s) {
   long long total = (long long)n_tiles * D;
   dim3 grid((unsigned)ceil_div(total, 256));

@@ -38,6 +38,10 @@ bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, i
 int launch_tile_x(const void* X, long long sxb, int x_dtype, int B, int D, int b0, int n_tiles, float4* xt,
                   hipStream_t s, int tb = 4);
 
+// bf16 X rows [b0, b0 + 4 n_tiles) -> 4-token tiles [n_tiles][D] of raw bf16 bits in 8 bytes
+// (word 0 = token 1 << 16 | token 0, word 1 = token 3 << 16 | token 2; +0 past B).
+int launch_tile_x_bf16x4(const void* X, long long sxb, int B, int D, int b0, int n_tiles, void* xt, hipStream_t s);
+
 // Two-token tiles (tb = 2) for the inputs past one 16-byte-slot buffer: XTILE_DB < D <= 2 XTILE_DB, D even.
 inline bool tiles_of_two(int D) { return D > XTILE_DB && D <= 2 * XTILE_DB && D % 2 == 0; }
 

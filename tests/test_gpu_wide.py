@@ -192,16 +192,23 @@ def test_two_token_tiles_give_the_bits_of_four_token_tiles():
 
 
 def test_bf16_tiles_give_the_bits_of_fp32_tiles():
-    """bf16 X at 4096 < D <= 8192 runs the forward over 4-token tiles of raw bf16 values (each
-    widened exactly before its FMA); the same values given as fp32 X run two-token fp32 tiles.
-    pre is bit-identical, and matches the oracle; ragged B."""
+    """bf16 X at 4096 < D <= 8192 runs the forward and dW over 4-token tiles of raw bf16 values
+    (each widened exactly before use); the same values given as fp32 X run two-token fp32 tiles.
+    pre, dW, db and dX are bit-identical (same values, same order of every sum), and pre matches
+    the oracle; ragged B."""
     L, idx, w, b, x, dy = make_case(8192, 12000, 12, 8, 45, x_dtype=torch.bfloat16, seed=13)
     rt = _rt(L, idx, LevelSpec("mean", activation="relu"))
     wd, bd = w.to(DEV), b.to(DEV)
-    pre_b = rt.forward(x.to(DEV), wd, bd)["pre"]
-    pre_f = rt.forward(x.float().to(DEV), wd, bd)["pre"]
-    assert torch.equal(pre_b, pre_f)
+    outs = []
+    for xd in (x.to(DEV), x.float().to(DEV)):
+        pre = rt.forward(xd, wd, bd)["pre"]
+        dw = torch.zeros(L.weight_shape, device=DEV)
+        db = torch.zeros(L.bias_shape, device=DEV)
+        dx = rt.backward(xd, wd, bd, dy.to(DEV), {}, "minimal_stats", dw, db)
+        outs.append((pre.cpu(), dw.cpu(), db.cpu(), dx.float().cpu()))
+    for a, c in zip(*outs):
+        assert torch.equal(a, c)
     fi, fw, fb = flat(L, idx, w, b)
     counts = L.counts_tensor("cpu").numpy()
     want, mag = O.forward(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, "relu", "mean", with_mag=True)
-    assert_parity(pre_b.cpu().numpy(), want, mag, what="pre")
+    assert_parity(outs[0][0].numpy(), want, mag, what="pre")
