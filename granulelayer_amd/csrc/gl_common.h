@@ -187,31 +187,42 @@ struct WinLayout {
 // A stage is WS_TILES * npw runs (one tile's window of one pool, ww slots); wave w copies runs
 // w, w + waves, ...  (taking its own runs directly: walking every 64-slot group of the stage in
 // each wave cost ~25% of the kernel in scalar instructions)
+// IB: bytes per input of the tiles (16: 4 fp32 tokens; 8: 4 raw bf16 tokens, where the window
+// starts at the even input at or below lo so every copied 16-byte slot is a whole slot of the tile).
+template <int IB = 16>
 __device__ __forceinline__ void dma_window_stage(const float4* __restrict__ xt, float4* region, int t0, int n_tiles,
                                                  int D, const WinLayout& L, int waves) {
+  constexpr int IPS = 16 / IB;  // inputs per 16-byte slot
   const unsigned lane = threadIdx.x & 63u;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const char* xb = uniform_ptr(xt);
   const unsigned r0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)region);
+  const int nsl = L.ww / IPS, last = D / IPS - 1;  // slots per run; the tile's last slot (D even when IPS = 2)
   for (int run = wave; run < WS_TILES * L.npw; run += waves) {
     const int tt = run / L.npw, k = run - tt * L.npw;
     const int t = t0 + tt < n_tiles ? t0 + tt : n_tiles - 1;
     const int g = L.g_first + k < L.G ? L.g_first + k : L.G - 1;
-    const int lo = (int)__builtin_amdgcn_readfirstlane(L.win[g]);
-    const char* sb = xb + (size_t)t * D * 16;
-    for (int i0 = 0; i0 < L.ww; i0 += 64) {
-      const int col = lo + i0 + (int)lane < D - 1 ? lo + i0 + (int)lane : D - 1;
-      const unsigned m0v = r0 + (unsigned)(run * L.ww + i0) * 16u;
+    const int lo = (int)__builtin_amdgcn_readfirstlane(L.win[g]) / IPS;  // first slot of the window
+    const char* sb = xb + (size_t)t * D * IB;
+    for (int i0 = 0; i0 < nsl; i0 += 64) {
+      // nsl is a multiple of 64 for 16-byte inputs, of 32 for 8-byte ones: lanes past the run
+      // write nothing
+      if (i0 + (int)lane >= nsl) continue;
+      const int col = lo + i0 + (int)lane < last ? lo + i0 + (int)lane : last;
+      const unsigned m0v = r0 + (unsigned)(run * nsl + i0) * 16u;
       asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
                    :: "v"((unsigned)col * 16u), "s"(m0v), "s"(sb) : "memory", "m0");
     }
   }
 }
 // LDS byte address of input d of a neuron in pool slot k of the workgroup whose window starts at lo
+// (IB bytes per input; with IB = 8 the staged window starts at the even input lo & ~1)
+template <int IB = 16>
 __device__ __forceinline__ unsigned win_addr(int d, int k, int lo, int ww) {
+  if constexpr (IB == 8) lo &= ~1;
   int i = d - lo;
   i = i < 0 ? 0 : (i >= ww ? ww - 1 : i);  // the host validated the widths; clamp keeps LDS reads in bounds
-  return (unsigned)(k * ww + i) * 16u;
+  return (unsigned)(k * ww + i) * (unsigned)IB;
 }
 
 // Four consecutive floats at a wave-uniform address, read through the constant address space so

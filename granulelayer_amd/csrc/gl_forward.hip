@@ -604,8 +604,8 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   // mean: D x 8 bytes per buffer)
   // XB: 4-token tiles of raw bf16 (8-byte slots, bf16 X), one buffer (SMALL) or two
   static_assert(TB == BT || (TB == 2 && DBUF && !WS && !XG && PK == PK_SUM), "two-token tiles: sum / mean, two buffers");
-  static_assert(!XB || (TB == BT && (DBUF || SMALL) && !WS && !XG && PK == PK_SUM), "bf16 tiles: sum / mean");
-  constexpr unsigned SLOT = XB ? 8u : 4u * TB;  // bytes per input of a tile
+  static_assert(!XB || (TB == BT && (DBUF || SMALL || WS) && !XG && PK == PK_SUM), "bf16 tiles: sum / mean");
+  constexpr int SLOT = XB ? 8 : 4 * TB;  // bytes per input of a tile or stage
   __shared__ float4 xa[WS ? (SMALL ? XTILE_DB : 2 * XTILE_DB) : (XG ? 1 : (DBUF || SMALL ? XTILE_DB : XTILE_SB))];
   __shared__ float4 xb[DBUF ? XTILE_DB : 1];
   const int lane = threadIdx.x & 63;
@@ -639,7 +639,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       const int k = sched_k<K>(order, ks);  // the pooled sum does not depend on the visiting order
       int d = rec_index(p.idx, n, k, K, p.rs);
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-      addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * SLOT;
+      addr[j][ks] = WS ? win_addr<SLOT>(d, pk, lo, p.ww) : (unsigned)d * SLOT;
       const float wl = p.W[n * K + k];
       w[j][ks] = valid ? wl : 0.f;
     }
@@ -660,22 +660,28 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   int* oslot = (PK == PK_MAX || PK == PK_TOPK) ? p.pslot + chunk * p.b_pad * kp : nullptr;
   const bool store = active;
   if constexpr (WS) {
-    // window staging: WS_TILES tiles per stage and barrier; tile t at slot (t mod 2 WS_TILES) * nsl
+    // window staging: WS_TILES tiles per stage and barrier; tile t at input (t mod 2 WS_TILES) * nsl
+    // of the stage regions (IB bytes per input)
     const WinLayout L{p.win, p.ww, p.npw, g_first, p.G};
     const int nsl = p.npw * p.ww;
-    const unsigned tstep = (unsigned)nsl * 16u;
-    dma_window_stage(p.xt, xa, 0, p.n_tiles, p.D, L, WAVES);
+    const unsigned tstep = (unsigned)nsl * (unsigned)SLOT;
+    const int rslots = WS_TILES * nsl * (int)SLOT / 16;  // 16-byte slots per region
+    dma_window_stage<SLOT>(p.xt, xa, 0, p.n_tiles, p.D, L, WAVES);
     stage_wait();
     __syncthreads();
     for (int t0 = 0; t0 < p.n_tiles; t0 += WS_TILES) {
       const int r = (t0 / WS_TILES) & 1;
       // region r ^ 1 was last read in the previous stage, which every wave finished before the barrier
-      if (t0 + WS_TILES < p.n_tiles) dma_window_stage(p.xt, xa + (r ^ 1) * WS_TILES * nsl, t0 + WS_TILES, p.n_tiles, p.D, L, WAVES);
+      if (t0 + WS_TILES < p.n_tiles)
+        dma_window_stage<SLOT>(p.xt, xa + (r ^ 1) * rslots, t0 + WS_TILES, p.n_tiles, p.D, L, WAVES);
       const int tn = p.n_tiles - t0 < WS_TILES ? p.n_tiles - t0 : WS_TILES;
       for (int tt = 0; tt < tn; ++tt) {
         const int t = t0 + tt;
-        fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
-                                                  out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
+        if constexpr (XB)
+          fwd_tile_bf4<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
+        else
+          fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
+                                                    out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
         // next tile's slot; after the last tile of region 1 back to region 0
         const unsigned step = (t & (2 * WS_TILES - 1)) == 2 * WS_TILES - 1 ? tstep - 2u * WS_TILES * tstep : tstep;
 #pragma unroll
@@ -1041,9 +1047,29 @@ template <int ACT, int K, int PK>
 static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
   constexpr int W = fwd_waves(K, PK);
   if (k.win) {
+    if (k.xb) {  // bf16 windows (sum / mean)
+      if constexpr (PK == PK_SUM && W % 8 == 0)
+        return k.ws_small ? launch_fwd<K, FWD_NPL, W / 2, ACT, false, true, PK, false, true, BT, true>(k, s)
+                          : launch_fwd<K, FWD_NPL, W, ACT, false, true, PK, false, false, BT, true>(k, s);
+      return GL_ERR_UNSUPPORTED;
+    }
     if constexpr (W % 8 == 0 && !pk_smooth(PK))
       if (k.ws_small) return launch_fwd<K, FWD_NPL, W / 2, ACT, false, true, PK, false, true>(k, s);
     return launch_fwd<K, FWD_NPL, W, ACT, false, true, PK>(k, s);
+  }
+  // 8-byte-slot tiles (sum / mean, the host chose the format):
+  // - bf16 X (even D <= 2 XTILE_DB): 4-token tiles of raw bf16 (64 KiB at D = 8192), one per
+  //   workgroup and two workgroups per CU (C4 forward 81.8 -> 51.5 ms; two buffers in one
+  //   workgroup: 56.3 ms);
+  // - fp32 X, XTILE_DB < D <= 2 XTILE_DB: two-token tiles, two 64-KiB buffers in one workgroup of W waves (at C4, 81.7 ms
+  //   against 83.7 ms for two workgroups of W / 2 waves with one tile each: the copy of the next
+  //   tile overlaps the gathers, and the tile is shared by twice the neurons)
+  if (k.xb || k.tb == 2) {
+    if constexpr (PK == PK_SUM && W % 8 == 0) {
+      if (k.xb) return launch_fwd<K, FWD_NPL, W / 2, ACT, false, false, PK, false, true, BT, true>(k, s);
+      return launch_fwd<K, FWD_NPL, W, ACT, true, false, PK, false, false, 2>(k, s);
+    }
+    return GL_ERR_UNSUPPORTED;
   }
   if (D > XTILE_SB) return launch_fwd<K, FWD_NPL, W, ACT, false, false, PK, true>(k, s);
   // D <= XTILE_DB: two workgroups of W / 2 waves per CU, each with one 64-KiB tile, when W / 2 waves
@@ -1052,15 +1078,6 @@ static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
   // mean and top-k at C2; the smooth pools measured even)
   if constexpr (W % 8 == 0 && !pk_smooth(PK))
     if (D <= XTILE_DB) return launch_fwd<K, FWD_NPL, W / 2, ACT, false, false, PK, false, true>(k, s);
-  // two-token tiles (sum / mean, XTILE_DB < D <= 2 XTILE_DB): two 64-KiB buffers in one workgroup
-  // of W waves (at C4, 81.7 ms against 83.7 ms for two workgroups of W / 2 waves with one tile each:
-  // the copy of the next tile overlaps the gathers, and the tile is shared by twice the neurons)
-  if constexpr (PK == PK_SUM)
-    if (k.tb == 2) return launch_fwd<K, FWD_NPL, W, ACT, true, false, PK, false, false, 2>(k, s);
-  // bf16 X at those widths: 4-token tiles of raw bf16 (64 KiB at D = 8192), one per workgroup and
-  // two workgroups per CU (C4 forward 81.8 -> 51.5 ms; two buffers in one workgroup: 56.3 ms)
-  if constexpr (PK == PK_SUM && W % 8 == 0)
-    if (k.xb) return launch_fwd<K, FWD_NPL, W / 2, ACT, false, false, PK, false, true, BT, true>(k, s);
   return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true, false, PK>(k, s)
                        : launch_fwd<K, FWD_NPL, W, ACT, false, false, PK>(k, s);
 }
@@ -1078,13 +1095,14 @@ static int launch_fwd_any(int act, int K, int D, const FwdK& k, hipStream_t s) {
 // Window staging applies when the staged windows of a workgroup's pools (npw of them, each ww
 // inputs) fit a stage tile (<= WS_SLOTS) and are narrower than the full input width.
 bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, int G, int* ww, int* npw,
-                    int max_slots) {
+                    int max_slots, int in_bytes) {
   if (!win || width < 1) return false;
-  const int w = (int)round_up(width, 64);
+  // 8-byte inputs: a staged window starts at the even input at or below the pool's first, one more
+  const int w = (int)round_up(in_bytes == 8 ? width + 1 : width, 64);
   // pools spanned by `waves` consecutive chunks (cpg chunks per pool)
   int n = waves % cpg == 0 ? waves / cpg : (waves - 1) / cpg + 2;
   if (n > G) n = G;
-  if ((long long)n * w > max_slots || (long long)n * w >= D) return false;
+  if ((long long)n * w * in_bytes > (long long)max_slots * 16 || (long long)n * w >= D) return false;
   *ww = w;
   *npw = n;
   return true;
@@ -1155,20 +1173,22 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
            smooth_scale(a->pool, a->pool_param), a->pool_param, smooth_pint(a->pool, a->pool_param)};
     k.sps = a->sps > 1 ? a->sps : 1;
     k.gs = a->sps > 1 ? a->gs : a->S;
+    // sum / mean with bf16 X (even D <= 2 XTILE_DB) keeps X's bf16 values, 4 tokens per 8-byte slot,
+    // in full tiles or windows: half the LDS bytes per gathered token for one exact widening per
+    // value (C4 forward 81.8 -> 51.5 ms; at D = 4096 full tiles 16.4 -> 14.4 ms)
+    k.xb = pool_kind(a->pool) == PK_SUM && a->x_dtype == GL_DTYPE_BF16 && a->D % 2 == 0 && a->D <= 2 * XTILE_DB;
+    const int ib = k.xb ? 8 : 16;  // bytes per staged input
     // window staging: two workgroups of half the waves per CU when their windows fit half the slots
     // (the rule of the full-tile kernels: wave counts that spread evenly, not the smooth pools)
     if (q.waves % 8 == 0 && !pool_smooth(a->pool) &&
-        window_staging(a->win, a->win_width, a->D, q.waves / 2, q.cpg, a->G, &k.ww, &k.npw, WS_SLOTS / 2)) {
+        window_staging(a->win, a->win_width, a->D, q.waves / 2, q.cpg, a->G, &k.ww, &k.npw, WS_SLOTS / 2, ib)) {
       k.win = a->win;
       k.ws_small = 1;
-    } else if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw)) {
+    } else if (window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &k.ww, &k.npw, WS_SLOTS, ib)) {
       k.win = a->win;
     }
-    // sum / mean over full tiles of 4097..8192 inputs: bf16 X keeps its bf16 values, 4 tokens per
-    // 8-byte slot; fp32 X goes to two-token tiles (8-byte slots of 2 fp32 tokens)
-    const bool wide = pool_kind(a->pool) == PK_SUM && !k.win && tiles_of_two(a->D);
-    k.xb = wide && a->x_dtype == GL_DTYPE_BF16;
-    k.tb = wide && !k.xb ? 2 : BT;
+    // fp32 X, sum / mean over full tiles of 4097..8192 inputs: two-token tiles (8-byte slots)
+    k.tb = !k.xb && pool_kind(a->pool) == PK_SUM && !k.win && tiles_of_two(a->D) ? 2 : BT;
     k.n_tiles = b_pad / k.tb;
     if (k.xb)
       GL_TRY(launch_tile_x_bf16x4(a->X, a->sxb, a->B, a->D, b0, k.n_tiles, xt, s));

@@ -29,9 +29,10 @@ int check_geometry(int G, int S, int32_t* sps, int32_t* gs);
 
 // Window staging for a kernel whose workgroups hold `waves` chunks of cpg per pool: true (with the
 // padded width *ww and pools per workgroup *npw) when the pools' windows fit a stage tile.
-// max_slots: the 16-byte slots one token tile of the stage may take (WS_SLOTS: two regions fill 128 KiB).
+// max_slots: the 16-byte slots one token tile of the stage may take (WS_SLOTS: two regions fill 128 KiB);
+// in_bytes: bytes per staged input (16: 4 fp32 tokens; 8: 4 bf16 tokens, windows from an even input).
 bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, int G, int* ww, int* npw,
-                    int max_slots = WS_SLOTS);
+                    int max_slots = WS_SLOTS, int in_bytes = 16);
 
 // X rows [b0, b0 + n_tiles*tb) -> token tiles [n_tiles][D] of tb floats (zero past B): float4
 // slots (tb = 4) or the two-token float2 slots (tb = 2).  The same bytes either way.

@@ -97,12 +97,12 @@ def test_backward_matches_oracle(case, pool, act):
     assert not dw.cpu().numpy().reshape(-1, K)[~valid].any()
 
 
-def make_window_case(D, H, G, K, B, width, seed=0):
+def make_window_case(D, H, G, K, B, width, seed=0, x_dtype=torch.float32):
     """The C3 index structure: every pool draws its inputs from one contiguous window of `width`
     inputs at a seeded offset (padded slots keep index 0)."""
     from granulelayer_amd.layout import sample_distinct
 
-    L, idx, w, b, x, dy = make_case(D, H, G, K, B, seed=seed)
+    L, idx, w, b, x, dy = make_case(D, H, G, K, B, seed=seed, x_dtype=x_dtype)
     S = L.slots_per_group
     gen = torch.Generator().manual_seed(seed + 7)
     off = torch.randint(0, D - width + 1, (G,), generator=gen)
@@ -115,14 +115,16 @@ def make_window_case(D, H, G, K, B, width, seed=0):
 WIN_CASES = [(2048, 8192, 8, 8, 37, 256), (1536, 4800, 16, 8, 70, 120), (2048, 2048, 4, 16, 33, 200)]
 
 
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("case", WIN_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}w{c[5]}")
-def test_window_staging_matches_full_staging_and_oracle(case):
+def test_window_staging_matches_full_staging_and_oracle(case, x_dtype):
     """Pool-window staging (gl_window_build_host) runs the window kernels and gives bit-identical
-    results to full-width staging, within the oracle's bar."""
+    results to full-width staging, within the oracle's bar.  bf16 X stages 4 raw bf16 tokens per
+    8-byte input (windows from an even input) in the forward, fp32 X 16-byte inputs."""
     from granulelayer_amd import _native as N
 
     D, H, G, K, B, width = case
-    L, idx, w, b, x, dy = make_window_case(D, H, G, K, B, width)
+    L, idx, w, b, x, dy = make_window_case(D, H, G, K, B, width, x_dtype=x_dtype)
     be = HipBackend.get()
     outs = {}
     try:
