@@ -62,7 +62,7 @@ def algorithmic(kernel: str, B: int, N: int, K: int, D: int, G: int, x_bytes: in
     if kernel == "bwd_w_kernel":
         # idx + W + bias, X once, dW/db read-modify-write, mask bits written
         return 4 * E + 4 * E + 4 * N + B * D * x_bytes + 8 * E + 8 * N + N * B // 8, 4 * B * E
-    if kernel == "dx_kernel":
+    if kernel in ("dx_kernel", "dx_dma_kernel"):
         # per edge: record, weight and the neuron's B mask bits; dX written once
         return E * (4 + 4 + B // 8) + 4 * B * D, 2 * B * E
     if kernel == "adam_kernel":

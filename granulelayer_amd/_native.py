@@ -68,7 +68,8 @@ EXPORTS = ("gl_abi_version", "gl_struct_layout", "gl_error_string", "gl_fwd_work
 KERNEL_NAMES = {1: "tile_x_kernel", 2: "fwd_kernel", 3: "fwd_finalize_kernel", 4: "c1t_kernel", 5: "bwd_w_kernel",
                 6: "dx_kernel", 7: "dx_reduce_kernel", 8: "adam_kernel", 9: "edges_build", 10: "fwd_kernel_win",
                 11: "bwd_w_kernel_win", 12: "max_events_dw_kernel", 13: "max_events_dx_kernel",
-                14: "cover_select_kernel", 15: "sched_build_kernel", 16: "dx_dense_kernel"}
+                14: "cover_select_kernel", 15: "sched_build_kernel", 16: "dx_dense_kernel",
+                17: "dx_dma_kernel"}
 
 
 class NativeError(RuntimeError):

@@ -676,6 +676,218 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
   }
 }
 
+// The 256-token slice kernel (T = 4) with the chunk's gathers copied to LDS by the memory
+// pipeline (global_load_lds): per edge the weight (one dword) and the neuron's 8 mask words (two
+// 16-byte halves) land in a double buffer with no VGPR round trip and no staging stores, so the
+// wave holds 64 VGPRs and a SIMD runs 8 waves instead of 6.  The arithmetic is dx_kernel's, in
+// the same order.  LDS per wave: two buffers of [2 halves][64 edges] 16-byte mask quads and
+// [64] weights, and the 16-entry bits-to-floats table.  A half holds 65 rows: row i of half 1 then
+// sits 4 banks past row i of half 0, so the two half-waves' reads of one edge (lanes 0-31 words
+// 0-3, lanes 32-63 words 4-7) never share a bank.
+struct __align__(16) DxDma {
+  uint4 m[2][2][65];
+  float w[2][64];
+  float lut[16][4];
+};
+
+// the chunk's weights and mask rows -> buffer buf (lanes past the chunk copy the first edge's)
+template <int K>
+__device__ __forceinline__ void dx_dma(const DxK& p, const uint32_t* mask_tc, const DxChunk& c, unsigned rec,
+                                       DxDma& st, int buf) {
+  const long long nb = pool_base(c.u / p.P, p.S, p.sps, p.gs) + (long long)(c.u % p.P) * US;  // first neuron of the unit
+  const unsigned woff = rec & REC_OFF_MASK;  // byte offset of W[n, k] in the unit
+  const unsigned mo = (woff >> (K == 8 ? 5 : 6)) * 32u;  // byte offset of the neuron's mask row
+  const char* ws = uniform_ptr(p.W + nb * K);
+  const char* ms = uniform_ptr(mask_tc + nb * 8);
+  const unsigned lw = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&st.w[buf][0]);
+  const unsigned l0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&st.m[buf][0][0]);
+  const unsigned l1 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&st.m[buf][1][0]);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, %2"
+               :: "v"(woff), "s"(lw), "s"(ws) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
+               :: "v"(mo), "s"(l0), "s"(ms) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
+               :: "v"(mo + 16u), "s"(l1), "s"(ms) : "memory", "m0");
+}
+
+// dx_run over the DMA layout: mrow = the lane's mask word of edge 0 (rows 16 bytes apart); wl =
+// the weight of the lane's own edge, edge i's weight taken from lane i (v_readlane, one VALU
+// instead of one more LDS read per edge)
+template <int X>
+__device__ __forceinline__ void dx_run_dma(const unsigned* mrow, float wl, const float (*lut)[4], int i0, int i1,
+                                           unsigned bit, const float (&c1)[4], float (&acc)[FW][4]) {
+  int len = i1 - i0;
+  asm volatile("" : "+s"(len));
+  if (len <= 0) return;
+  const unsigned* m = mrow + 4 * i0;
+  float s[4];
+  {
+    const unsigned v = __builtin_amdgcn_ubfe(*m, bit, 4u);
+    const float4 t = *reinterpret_cast<const float4*>(&lut[v][0]);
+    const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), i0));
+    s[0] = t.x * wv, s[1] = t.y * wv, s[2] = t.z * wv, s[3] = t.w * wv;
+  }
+  for (int i = i0 + 1; i < i1; ++i) {
+    m += 4;
+    const unsigned v = __builtin_amdgcn_ubfe(*m, bit, 4u);
+    const float4 t = *reinterpret_cast<const float4*>(&lut[v][0]);
+    const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), i));
+    s[0] = __builtin_fmaf(t.x, wv, s[0]);
+    s[1] = __builtin_fmaf(t.y, wv, s[1]);
+    s[2] = __builtin_fmaf(t.z, wv, s[2]);
+    s[3] = __builtin_fmaf(t.w, wv, s[3]);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[X][j] = __builtin_fmaf(c1[j], s[j], acc[X][j]);
+}
+
+template <int X>
+__device__ __forceinline__ void dx_runs_dma(const unsigned* mrow, float wl, const float (*lut)[4],
+                                            const int (&b)[FW + 1], unsigned bit, const float (&c1)[4],
+                                            float (&acc)[FW][4]) {
+  dx_run_dma<X>(mrow, wl, lut, b[X], b[X + 1], bit, c1, acc);
+  if constexpr (X + 1 < FW) dx_runs_dma<X + 1>(mrow, wl, lut, b, bit, c1, acc);
+}
+
+// dx_next with the segment table read one step ahead: (pe, pu) hold the end and the unit of
+// segment c.si + 1, loaded by the step that entered segment c.si; their loads land by the next
+// loop-top wait, so no wait for them sits behind a chunk copy
+__device__ __forceinline__ void dx_seg_ahead(const DxK& p, int si, int hi, unsigned& pe, unsigned& pu) {
+  if (si + 1 < hi) {
+    pe = p.seg_begin[si + 2];
+    pu = (unsigned)p.seg_unit[si + 1];
+  }
+}
+__device__ __forceinline__ void dx_next_ahead(const DxK& p, DxChunk& c, int hi, unsigned& pe, unsigned& pu) {
+  if (c.e + 64 < c.end) {
+    c.e += 64;
+  } else {
+    c.si += 1;
+    if (c.si < hi) {
+      c.e = c.end;
+      c.end = __builtin_amdgcn_readfirstlane(pe);
+      c.u = __builtin_amdgcn_readfirstlane((int)pu);
+      dx_seg_ahead(p, c.si, hi, pe, pu);
+    }
+  }
+}
+
+// c1 of the lane's 4 tokens for the pool of unit u: a uniform row base (scalar registers) plus the
+// lane's 32-bit offset (no 64-bit vector address to keep live)
+__device__ __forceinline__ void dx_load_c1_u(const DxK& p, int u, int slice0, int lane, float (&c1)[4]) {
+  const uint4 v = ld_uniform_u128(p.c1t + (long long)(u / p.P) * p.cap + slice0, (unsigned)lane * 16u);
+  c1[0] = __uint_as_float(v.x), c1[1] = __uint_as_float(v.y), c1[2] = __uint_as_float(v.z), c1[3] = __uint_as_float(v.w);
+}
+
+template <int K>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) dx_dma_kernel(DxK p) {
+  constexpr int T = 4;
+  const int lane = threadIdx.x;
+  // block order as dx_kernel: all feature ranges of a unit range side by side on one XCD
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7;
+  const int loc = bid >> 3;
+  const int F = loc % p.FR;
+  const int rest = loc / p.FR;
+  const int ql = rest % p.QL;
+  const int tc = rest / p.QL;
+  const int q = ql * 8 + xcd;
+  const int u_lo = q * p.UQ;
+  const int u_hi = min(u_lo + p.UQ, p.U);
+  int lo = (int)p.seg_ptr[F], hi = (int)p.seg_ptr[F + 1];
+  {
+    int a = lo, b = hi;
+    while (a < b) {
+      int mid = (a + b) >> 1;
+      if (p.seg_unit[mid] < u_lo) a = mid + 1; else b = mid;
+    }
+    lo = a;
+    b = hi;
+    while (a < b) {
+      int mid = (a + b) >> 1;
+      if (p.seg_unit[mid] < u_hi) a = mid + 1; else b = mid;
+    }
+    hi = a;
+  }
+  float acc[FW][T];
+#pragma unroll
+  for (int f = 0; f < FW; ++f)
+#pragma unroll
+    for (int j = 0; j < T; ++j) acc[f][j] = 0.f;
+
+  const int tok0 = tc * 64 * T + T * lane;
+  const unsigned bit = (unsigned)(T * lane) & 31u;
+  const int word = (T * lane) >> 5;  // the lane's word of a mask row: half word / 4, dword word % 4
+  const uint32_t* mask_tc = p.mask + (long long)tc * p.NS * (2 * T);
+  __shared__ DxDma st;
+  if (lane < 16) {
+#pragma unroll
+    for (int j = 0; j < T; ++j) st.lut[lane][j] = (lane >> j) & 1 ? 1.0f : 0.0f;
+  }
+  if (lo < hi) {
+    DxChunk cc{lo, p.seg_begin[lo], p.seg_begin[lo + 1], p.seg_unit[lo]};
+    unsigned pe = 0u, pu = 0u;
+    dx_seg_ahead(p, lo, hi, pe, pu);
+    DxChunk cn = cc;
+    dx_next_ahead(p, cn, hi, pe, pu);
+    const unsigned rc0 = dx_load_rec(p, cc, lane);
+    unsigned rn = cn.si < hi ? dx_load_rec(p, cn, lane) : 0u;
+    dx_dma<K>(p, mask_tc, cc, rc0, st, 0);
+    unsigned rc = rc0;
+    float c1[T];
+    dx_load_c1_u(p, cc.u, tc * 64 * T, lane, c1);
+    int cur = 0;
+    for (;;) {
+      // every copy, load and LDS read so far is done: buffer cur holds chunk cc, and buffer
+      // cur ^ 1 (read by the previous chunk) may be refilled
+      __builtin_amdgcn_s_waitcnt(0);
+      const bool more = cn.si < hi;
+      float c1n[T];
+#pragma unroll
+      for (int j = 0; j < T; ++j) c1n[j] = c1[j];
+      DxChunk cnn = cn;
+      unsigned rnn = 0u;
+      if (more) {
+        // the segment table before the copy: a wait for those loads after it would also wait for
+        // the copy (the counter is in order); their values were loaded one step ago
+        dx_next_ahead(p, cnn, hi, pe, pu);
+        if (cnn.si < hi) rnn = dx_load_rec(p, cnn, lane);
+        dx_dma<K>(p, mask_tc, cn, rn, st, cur ^ 1);
+        if (cn.si != cc.si) dx_load_c1_u(p, cn.u, tc * 64 * T, lane, c1n);
+      }
+      {
+        const int n = (int)min(cc.end - cc.e, 64u);
+        const int f = lane < n ? (int)((rc >> REC_F_SHIFT) & REC_F_MASK) : FW;
+        int b[FW + 1];
+        b[0] = 0;
+#pragma unroll
+        for (int x = 1; x <= FW; ++x)
+          b[x] = __builtin_amdgcn_readfirstlane((int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(f < x)));
+        const unsigned* mrow = reinterpret_cast<const unsigned*>(&st.m[opaque(cur)][word >> 2][0]) + (word & 3);
+        const float wl = st.w[opaque(cur)][lane];
+        dx_runs_dma<0>(mrow, wl, st.lut, b, bit, c1, acc);
+      }
+      if (!more) break;
+      cc = cn;
+      rc = rn;
+#pragma unroll
+      for (int j = 0; j < T; ++j) c1[j] = c1n[j];
+      cn = cnn;
+      rn = rnn;
+      cur ^= 1;
+    }
+  }
+  float* out = p.part + (long long)q * p.D * p.cap;
+#pragma unroll
+  for (int f = 0; f < FW; ++f) {
+    const int d = F * FW + f;
+    if (d < p.D) {
+#pragma unroll
+      for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j] = acc[f][j];
+    }
+  }
+}
+
 // dX[b0 + b, d] = sum_q part[q, d, b]  (fixed order, q ascending), transposed to [B, D] through
 // LDS.  A thread sums 4 adjacent tokens of one input with 16-byte loads, 8 partials in flight
 // (the add order per element is unchanged); 32 inputs x 32 tokens per workgroup.
@@ -1109,20 +1321,23 @@ static int launch_bwd_w_any(int K, int act, const BwK& k, hipStream_t s) {
 }
 
 template <int K, int T>
-static int launch_dx_kt(const DxK& k, hipStream_t s) {
-  auto fn = dx_kernel<K, T>;
-  GL_LAUNCH(GL_KERNEL_DX, fn, dim3((unsigned)(8LL * k.FR * k.QL * k.n_tc)), dim3(64), 0, s, k);
+static int launch_dx_kt(const DxK& k, hipStream_t s, bool dma) {
+  auto fn = T == 4 && dma ? dx_dma_kernel<K> : dx_kernel<K, T>;
+  GL_LAUNCH(T == 4 && dma ? GL_KERNEL_DX_DMA : GL_KERNEL_DX, fn, dim3((unsigned)(8LL * k.FR * k.QL * k.n_tc)), dim3(64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;
 }
 
 template <int K>
-static int launch_dx_k(int T, const DxK& k, hipStream_t s) {
-  return T == 1 ? launch_dx_kt<K, 1>(k, s) : (T == 2 ? launch_dx_kt<K, 2>(k, s) : launch_dx_kt<K, 4>(k, s));
+static int launch_dx_k(int T, const DxK& k, hipStream_t s, bool dma) {
+  return T == 1 ? launch_dx_kt<K, 1>(k, s, dma) : (T == 2 ? launch_dx_kt<K, 2>(k, s, dma) : launch_dx_kt<K, 4>(k, s, dma));
 }
 
-static int launch_dx(int K, int T, const DxK& k, hipStream_t s) {
-  return K == 8 ? launch_dx_k<8>(T, k, s) : launch_dx_k<16>(T, k, s);
+// dma: the LDS-copy kernel (8 waves per SIMD) for short segments; long segments (narrow pool
+// windows) keep dx_kernel, whose 6 waves per SIMD thrash the L2 less when every wave streams
+// long runs of many units (C3: 15.5 ms against 20.5, with 45% against 27% L2 hits)
+static int launch_dx(int K, int T, const DxK& k, hipStream_t s, bool dma) {
+  return K == 8 ? launch_dx_k<8>(T, k, s, dma) : launch_dx_k<16>(T, k, s, dma);
 }
 
 template <int K, int ACT, int OP>
@@ -1166,6 +1381,14 @@ static float smooth_scale_b(int pool, float param) {
 }  // namespace gl
 
 using namespace gl;
+
+// Average edges per dX segment (one unit's edges into FW features): S K FW / (inputs a unit
+// reaches), the pool window's width when the layer has windows (a->win), else D.  Short segments
+// (C2: 16, C4: 8, C5: 16) run the LDS-copy dX kernel; a segment of a 256-wide window holds 256.
+static bool dx_short_segments(const GlBwdArgs* a) {
+  const long long reach = a->win && a->win_width > 0 && a->win_width < a->D ? a->win_width : a->D;
+  return (long long)a->S * a->K * FW < 64 * reach;
+}
 
 extern "C" int gl_bwd_workspace(const GlBwdArgs* a, size_t* bytes) {
   if (!a || !bytes) return GL_ERR_ARG;
@@ -1283,7 +1506,7 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
            (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, a->W, part,
            NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * T), sps, gs};
-    GL_TRY(launch_dx(a->K, T, dk, s));
+    GL_TRY(launch_dx(a->K, T, dk, s, dx_short_segments(a)));
     GL_LAUNCH(GL_KERNEL_DX_REDUCE, dx_reduce_kernel, dim3((unsigned)ceil_div(a->D, 32), (unsigned)ceil_div(Bc, 32)), dim3(256), 0,
                        s, part, a->dX, a->D, cap, q.Q, b0, Bc);
     GL_CHECK_LAUNCH();

@@ -123,7 +123,7 @@ class SparsePoolingLayer(nn.Module):
             return out
         rt = self._runtime()
         out.update(rt.describe_execution(), forward={"backend": "hip", "kernel": "fwd_kernel (neuron-stationary)"},
-                   backward={"backend": "hip", "kernels": ["bwd_w_kernel", "dx_kernel", "dx_reduce_kernel"]},
+                   backward={"backend": "hip", "kernels": ["bwd_w_kernel", "dx_kernel or dx_dma_kernel", "dx_reduce_kernel"]},
                    batch=batch)
         return out
 

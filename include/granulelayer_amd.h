@@ -275,7 +275,8 @@ enum {
   GL_KERNEL_MAX_EV_DW = 12, GL_KERNEL_MAX_EV_DX = 13, /* max-pooling backward: winner events */
   GL_KERNEL_COVER = 14,                                /* Cover-TopK support selection */
   GL_KERNEL_SCHED = 15,                                /* gather schedule / pool windows on the GPU */
-  GL_KERNEL_DX_DENSE = 16                              /* dX of the smooth pools from per-neuron dz */
+  GL_KERNEL_DX_DENSE = 16,                             /* dX of the smooth pools from per-neuron dz */
+  GL_KERNEL_DX_DMA = 17                                /* dX of 256-token slices, short segments */
 };
 
 /* Launch trace for benchmarks and tests (process-wide, not for concurrent callers): after

@@ -111,8 +111,11 @@ def make_window_case(D, H, G, K, B, width, seed=0, x_dtype=torch.float32):
     return L, rec.view(L.index_shape).to(idx.dtype), w, b, x, dy
 
 
-# (D, H, G, K, B, window): pools of 1024 (4 per forward workgroup), of 300 (8 per workgroup), K = 16
-WIN_CASES = [(2048, 8192, 8, 8, 37, 256), (1536, 4800, 16, 8, 70, 120), (2048, 2048, 4, 16, 33, 200)]
+# (D, H, G, K, B, window): pools of 1024 (4 per forward workgroup), of 300 (8 per workgroup), K = 16;
+# 300 tokens: dX in 256-token slices, by dx_kernel with the windows (long segments) and by
+# dx_dma_kernel without them (segments of 32 edges)
+WIN_CASES = [(2048, 8192, 8, 8, 37, 256), (1536, 4800, 16, 8, 70, 120), (2048, 2048, 4, 16, 33, 200),
+             (2048, 8192, 8, 8, 300, 256)]
 
 
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
@@ -138,6 +141,8 @@ def test_window_staging_matches_full_staging_and_oracle(case, x_dtype):
                 dx = rt.backward(x.to(DEV), w.to(DEV), b.to(DEV), dy.to(DEV), {}, "minimal_stats", dw, db)
             names = set(tr.times_ms())
             want = {"fwd_kernel_win", "bwd_w_kernel_win"} if ws else {"fwd_kernel", "bwd_w_kernel"}
+            if B > 128:
+                want.add("dx_kernel" if ws else "dx_dma_kernel")
             assert want <= names, f"window_staging={ws}: ran {sorted(names)}"
             outs[ws] = [t.cpu() for t in (pre, dw, db, dx)]
     finally:
@@ -442,7 +447,7 @@ def test_max_backward_matches_oracle(case, act):
         dx = rt.backward(xd, wd, bd, dy.to(DEV), stats, "save_winners", dw, db).cpu().numpy()
     # the winner-event kernels ran, not the dense dW / dX passes
     names = set(tr.times_ms())
-    assert {"max_events_dw_kernel", "max_events_dx_kernel"} <= names and "dx_kernel" not in names, sorted(names)
+    assert {"max_events_dw_kernel", "max_events_dx_kernel"} <= names and not {"dx_kernel", "dx_dma_kernel"} & names, sorted(names)
     # deterministic: a second backward gives the same bits
     dw2, db2 = torch.zeros_like(dw), torch.zeros_like(db)
     dx2 = rt.backward(xd, wd, bd, dy.to(DEV), stats, "save_winners", dw2, db2).cpu().numpy()
@@ -539,7 +544,7 @@ def test_topk_backward_matches_oracle(case, act, k):
     with N.KernelTrace() as tr:
         dx = rt.backward(xd, wd, bd, dy.to(DEV), stats, "save_winners", dw, db).cpu().numpy()
     names = set(tr.times_ms())
-    assert {"max_events_dw_kernel", "max_events_dx_kernel"} <= names and "dx_kernel" not in names, sorted(names)
+    assert {"max_events_dw_kernel", "max_events_dx_kernel"} <= names and not {"dx_kernel", "dx_dma_kernel"} & names, sorted(names)
     dw2, db2 = torch.zeros_like(dw), torch.zeros_like(db)
     dx2 = rt.backward(xd, wd, bd, dy.to(DEV), stats, "save_winners", dw2, db2).cpu().numpy()
     assert np.array_equal(dx, dx2) and torch.equal(dw, dw2) and torch.equal(db, db2)
