@@ -34,21 +34,34 @@ constexpr int WIN = 128;
 constexpr int SETS = WIN / 16;
 constexpr int KS = 8;
 
-// One window of 128 slots.  The same code runs on the host (gl_sched_build_host, one thread per
-// range of windows) and on the GPU (gl_sched_build, one lane per window), so both builders give
-// the same schedule bit for bit.
-struct Window {
-  int8_t res[WIN][KS];    // residue of edge k of slot p (-1: invalid slot)
-  uint8_t hist[WIN][16];  // multiplicity of each residue among slot p's edges
-  bool valid[WIN];
+// One window of 128 slots: the residues of its edges and the working arrays of the schedule, in one
+// struct of narrow types.  The same code runs on the host (gl_sched_build_host, one struct per
+// thread) and on the GPU (gl_sched_build, one struct per lane in LDS), so both builders give the
+// same schedule bit for bit.  A slot is invalid (past the pool's n_g) when its res row is -1.
+struct WinWork {
+  int8_t res[WIN][KS];     // residue of edge k of slot p (-1: invalid slot)
+  uint8_t order[WIN];      // balance: slots by most repeated residue, then slot
+  uint8_t mxv[WIN];        // balance: multiplicity of slot p's most repeated residue
+  uint8_t H[SETS][16];     // balance: residue counts of each set (<= 128)
+  uint8_t members[SETS][16];
+  uint8_t cnt[SETS];
+  int8_t rem[16][KS];      // match: residue of each lane's unused edge k (-1 = used)
+  uint8_t kperm[16][KS];   // match: visiting order
+  uint32_t cand[16];       // matcher: residues of lane l's unused edges
+  int8_t ord[16];          // matcher: residues, most remaining edges first
+  int8_t owner[16];        // matcher: lane holding residue r (-1: free)
+  uint8_t deg[16], ndist[16], lord[16], used[16];
+  int8_t lane_res[16];
+  int8_t st_lane[17], st_pos[17], st_tried[17];  // matcher: depth-first stack
+  uint8_t pad[7];          // 2036 bytes: an odd number of dwords, so lanes' structs start on different banks
 };
 
 // stable insertion sort of v[0..n) by key (larger first when desc): the order std::stable_sort
 // gives for the same comparator
-template <typename KeyF>
-__host__ __device__ inline void stable_sort_by(int* v, int n, KeyF key, bool desc) {
+template <typename T, typename KeyF>
+__host__ __device__ inline void stable_sort_by(T* v, int n, KeyF key, bool desc) {
   for (int i = 1; i < n; ++i) {
-    const int x = v[i];
+    const T x = v[i];
     const int kx = key(x);
     int j = i - 1;
     while (j >= 0 && (desc ? key(v[j]) < kx : key(v[j]) > kx)) {
@@ -59,39 +72,56 @@ __host__ __device__ inline void stable_sort_by(int* v, int n, KeyF key, bool des
   }
 }
 
+// slot p's distinct residues in ascending order (bit r of the mask) and multiplicity of residue r
+__host__ __device__ inline unsigned slot_mask(const WinWork& W, int p) {
+  unsigned m = 0u;
+  for (int k = 0; k < KS; ++k)
+    if (W.res[p][k] >= 0) m |= 1u << W.res[p][k];
+  return m;
+}
+__host__ __device__ inline int slot_mult(const WinWork& W, int p, int r) {
+  int c = 0;
+  for (int k = 0; k < KS; ++k) c += W.res[p][k] == r;
+  return c;
+}
+
 // greedy balance: slots with the most repeated residue first; each goes to the set (with room)
 // whose sum over residues of (count - 8)^2 for counts above 8 grows least (ties: lower set)
-__host__ __device__ inline void balance(const Window& W, uint8_t members[SETS][16]) {
-  int order[WIN], mx[WIN];
+__host__ __device__ inline void balance(WinWork& W) {
   for (int p = 0; p < WIN; ++p) {
-    order[p] = p;
-    mx[p] = 0;
-    for (int r = 0; r < 16; ++r) mx[p] = mx[p] > W.hist[p][r] ? mx[p] : W.hist[p][r];
+    W.order[p] = (uint8_t)p;
+    int mx = 0;
+    for (int k = 0; k < KS; ++k)
+      if (W.res[p][k] >= 0) {
+        const int c = slot_mult(W, p, W.res[p][k]);
+        mx = mx > c ? mx : c;
+      }
+    W.mxv[p] = (uint8_t)mx;
   }
-  stable_sort_by(order, WIN, [&](int a) { return mx[a]; }, true);
-  int H[SETS][16];
-  int cnt[SETS];
+  stable_sort_by(W.order, WIN, [&](uint8_t a) { return (int)W.mxv[a]; }, true);
   for (int set = 0; set < SETS; ++set) {
-    cnt[set] = 0;
-    for (int r = 0; r < 16; ++r) H[set][r] = 0;
+    W.cnt[set] = 0;
+    for (int r = 0; r < 16; ++r) W.H[set][r] = 0;
   }
   for (int oi = 0; oi < WIN; ++oi) {
-    const int p = order[oi];
-    int rs[KS], hs[KS], nr = 0;  // distinct residues of slot p and their multiplicities
-    for (int r = 0; r < 16; ++r)
-      if (W.hist[p][r]) rs[nr] = r, hs[nr++] = W.hist[p][r];
+    const int p = W.order[oi];
+    const unsigned m = slot_mask(W, p);  // the distinct residues of slot p, ascending
     int best = -1, best_cost = 0;
     for (int set = 0; set < SETS; ++set) {
-      if (cnt[set] == 16) continue;
+      if (W.cnt[set] == 16) continue;
       int c = 0;
-      for (int i = 0; i < nr; ++i) {
-        const int before = H[set][rs[i]] - 8, after = before + hs[i];
+      for (unsigned b = m; b; b &= b - 1) {
+        const int r = __builtin_ctz(b), h = slot_mult(W, p, r);
+        const int before = W.H[set][r] - 8, after = before + h;
         c += (after > 0 ? after * after : 0) - (before > 0 ? before * before : 0);
       }
       if (best < 0 || c < best_cost) best = set, best_cost = c;
     }
-    for (int i = 0; i < nr; ++i) H[best][rs[i]] += hs[i];
-    members[best][cnt[best]++] = (uint8_t)p;
+    for (unsigned b = m; b; b &= b - 1) {
+      const int r = __builtin_ctz(b);
+      W.H[best][r] = (uint8_t)(W.H[best][r] + slot_mult(W, p, r));
+    }
+    W.members[best][W.cnt[best]++] = (uint8_t)p;
   }
 }
 
@@ -99,131 +129,117 @@ __host__ __device__ inline void balance(const Window& W, uint8_t members[SETS][1
 // edges, tried in the round's residue order (most remaining edges first).  Depth-first search with
 // an explicit stack: frame f holds its lane, the next residue position to try and the residue it
 // is trying; a free residue found at depth d gives every frame on the path its residue.
-struct Matcher {
-  uint32_t cand[16];
-  int ord[16];
-  int owner[16];
-
-  __host__ __device__ bool try_lane(int l0) {
-    int lane[17], pos[17], tried[17];
-    uint32_t seen = 0;
-    int d = 0;
-    lane[0] = l0;
-    pos[0] = 0;
-    for (;;) {
-      const int l = lane[d];
-      bool pushed = false;
-      while (pos[d] < 16) {
-        const int r = ord[pos[d]++];
-        if (!((cand[l] >> r) & 1u) || ((seen >> r) & 1u)) continue;
-        seen |= 1u << r;
-        if (owner[r] < 0) {
-          owner[r] = l;
-          for (int f = d - 1; f >= 0; --f) owner[tried[f]] = lane[f];
-          return true;
-        }
-        tried[d] = r;
-        lane[d + 1] = owner[r];
-        pos[d + 1] = 0;
-        ++d;
-        pushed = true;
-        break;
+__host__ __device__ inline bool try_lane(WinWork& W, int l0) {
+  uint32_t seen = 0;
+  int d = 0;
+  W.st_lane[0] = (int8_t)l0;
+  W.st_pos[0] = 0;
+  for (;;) {
+    const int l = W.st_lane[d];
+    bool pushed = false;
+    while (W.st_pos[d] < 16) {
+      const int r = W.ord[W.st_pos[d]];
+      W.st_pos[d] = (int8_t)(W.st_pos[d] + 1);
+      if (!((W.cand[l] >> r) & 1u) || ((seen >> r) & 1u)) continue;
+      seen |= 1u << r;
+      if (W.owner[r] < 0) {
+        W.owner[r] = (int8_t)l;
+        for (int f = d - 1; f >= 0; --f) W.owner[W.st_tried[f]] = W.st_lane[f];
+        return true;
       }
-      if (pushed) continue;
-      if (d == 0) return false;
-      --d;  // the child found no augmenting path: continue this frame's residues
+      W.st_tried[d] = (int8_t)r;
+      W.st_lane[d + 1] = W.owner[r];
+      W.st_pos[d + 1] = 0;
+      ++d;
+      pushed = true;
+      break;
     }
+    if (pushed) continue;
+    if (d == 0) return false;
+    --d;  // the child found no augmenting path: continue this frame's residues
   }
-};
+}
 
-// visiting order kperm[lane][round] of the set's lanes; invalid lanes keep the identity
-__host__ __device__ inline void match_set(const Window& W, const uint8_t mem[16], uint8_t kperm[16][KS]) {
-  int8_t rem[16][KS];  // residue of each lane's unused edge k (-1 = used)
-  bool live[16];
+// visiting order W.kperm[lane][round] of set `set`'s lanes; invalid lanes keep the identity
+__host__ __device__ inline void match_set(WinWork& W, int set) {
+  unsigned live = 0u;  // bit l: lane l's slot is valid
   for (int l = 0; l < 16; ++l) {
-    live[l] = W.valid[mem[l]];
+    const int p = W.members[set][l];
+    if (W.res[p][0] >= 0) live |= 1u << l;
     for (int k = 0; k < KS; ++k) {
-      rem[l][k] = live[l] ? W.res[mem[l]][k] : (int8_t)-1;
-      kperm[l][k] = (uint8_t)k;
+      W.rem[l][k] = (live >> l) & 1u ? W.res[p][k] : (int8_t)-1;
+      W.kperm[l][k] = (uint8_t)k;
     }
   }
-  Matcher M;
   for (int round = 0; round < KS; ++round) {
-    int deg[16];
-    int ndist[16];
-    for (int r = 0; r < 16; ++r) deg[r] = 0;
+    for (int r = 0; r < 16; ++r) W.deg[r] = 0;
     for (int l = 0; l < 16; ++l) {
-      M.cand[l] = 0;
+      unsigned c = 0u;
       for (int k = 0; k < KS; ++k)
-        if (rem[l][k] >= 0) deg[rem[l][k]]++, M.cand[l] |= 1u << rem[l][k];
-      ndist[l] = __builtin_popcount(M.cand[l]);
+        if (W.rem[l][k] >= 0) W.deg[W.rem[l][k]]++, c |= 1u << W.rem[l][k];
+      W.cand[l] = c;
+      W.ndist[l] = (uint8_t)__builtin_popcount(c);
     }
-    for (int r = 0; r < 16; ++r) M.ord[r] = r, M.owner[r] = -1;
-    stable_sort_by(M.ord, 16, [&](int a) { return deg[a]; }, true);
-    int order[16];
-    for (int l = 0; l < 16; ++l) order[l] = l;
-    stable_sort_by(order, 16, [&](int a) { return ndist[a]; }, false);
+    for (int r = 0; r < 16; ++r) W.ord[r] = (int8_t)r, W.owner[r] = -1;
+    stable_sort_by(W.ord, 16, [&](int8_t a) { return (int)W.deg[a]; }, true);
+    for (int l = 0; l < 16; ++l) W.lord[l] = (uint8_t)l;
+    stable_sort_by(W.lord, 16, [&](uint8_t a) { return (int)W.ndist[a]; }, false);
     for (int i = 0; i < 16; ++i) {
-      const int l = order[i];
-      if (!live[l]) continue;
-      M.try_lane(l);
+      const int l = W.lord[i];
+      if (!((live >> l) & 1u)) continue;
+      try_lane(W, l);
     }
-    int lane_res[16], used[16];
-    for (int l = 0; l < 16; ++l) lane_res[l] = -1, used[l] = 0;
+    for (int l = 0; l < 16; ++l) W.lane_res[l] = -1, W.used[l] = 0;
     for (int r = 0; r < 16; ++r)
-      if (M.owner[r] >= 0) lane_res[M.owner[r]] = r, used[r]++;
+      if (W.owner[r] >= 0) W.lane_res[W.owner[r]] = (int8_t)r, W.used[r]++;
     for (int l = 0; l < 16; ++l) {  // unmatched lanes: the residue this round uses least
-      if (!live[l] || lane_res[l] >= 0) continue;
+      if (!((live >> l) & 1u) || W.lane_res[l] >= 0) continue;
       int best = -1;
       for (int k = 0; k < KS; ++k) {
-        const int r = rem[l][k];
+        const int r = W.rem[l][k];
         if (r < 0) continue;
-        if (best < 0 || used[r] < used[best] ||
-            (used[r] == used[best] && (deg[r] > deg[best] || (deg[r] == deg[best] && r < best))))
+        if (best < 0 || W.used[r] < W.used[best] ||
+            (W.used[r] == W.used[best] && (W.deg[r] > W.deg[best] || (W.deg[r] == W.deg[best] && r < best))))
           best = r;
       }
-      lane_res[l] = best;
-      used[best]++;
+      W.lane_res[l] = (int8_t)best;
+      W.used[best]++;
     }
     for (int l = 0; l < 16; ++l) {
-      if (!live[l]) continue;
+      if (!((live >> l) & 1u)) continue;
       for (int k = 0; k < KS; ++k)  // the lowest unused edge with that residue
-        if (rem[l][k] == lane_res[l]) {
-          kperm[l][round] = (uint8_t)k;
-          rem[l][k] = -1;
+        if (W.rem[l][k] == W.lane_res[l]) {
+          W.kperm[l][round] = (uint8_t)k;
+          W.rem[l][k] = -1;
           break;
         }
     }
   }
 }
 
-// slot p's residues and histogram (window w of group g)
-__host__ __device__ inline void load_slot(Window& W, const int32_t* idx, int D, long long nb, int w, int n_g, int p) {
+// slot p's residues (window w of group g)
+__host__ __device__ inline void load_slot(WinWork& W, const int32_t* idx, int D, long long nb, int w, int n_g, int p) {
   const int s = w * WIN + p;
-  W.valid[p] = s < n_g;
-  for (int r = 0; r < 16; ++r) W.hist[p][r] = 0;
+  const bool valid = s < n_g;
   for (int k = 0; k < KS; ++k) {
     int r = -1;
-    if (W.valid[p]) {
+    if (valid) {
       int d = idx[(nb + s) * KS + k];
       d = d < 0 ? 0 : (d >= D ? D - 1 : d);
       r = d & 15;
-      W.hist[p][r]++;
     }
     W.res[p][k] = (int8_t)r;
   }
 }
 
 // the 128 records of one loaded window
-__host__ __device__ inline void schedule_window(const Window& W, uint32_t* out) {
-  uint8_t members[SETS][16];
-  balance(W, members);
+__host__ __device__ inline void schedule_window(WinWork& W, uint32_t* out) {
+  balance(W);
   for (int set = 0; set < SETS; ++set) {
-    uint8_t kperm[16][KS];
-    match_set(W, members[set], kperm);
+    match_set(W, set);
     for (int l = 0; l < 16; ++l) {
-      uint32_t rec = (uint32_t)members[set][l];
-      for (int ks = 0; ks < KS - 1; ++ks) rec |= (uint32_t)kperm[l][ks] << (7 + 3 * ks);
+      uint32_t rec = (uint32_t)W.members[set][l];
+      for (int ks = 0; ks < KS - 1; ++ks) rec |= (uint32_t)W.kperm[l][ks] << (7 + 3 * ks);
       out[set * 16 + l] = rec;
     }
   }
@@ -232,7 +248,7 @@ __host__ __device__ inline void schedule_window(const Window& W, uint32_t* out) 
 void build_range(const int32_t* idx, const int32_t* counts, int D, int S, int sps, int gs, long long w_begin,
                  long long w_end, uint32_t* sched) {
   const int nwin = ceil_div(S, WIN);
-  Window W;
+  WinWork W;
   for (long long gw = w_begin; gw < w_end; ++gw) {
     const long long g = gw / nwin;
     const int w = (int)(gw % nwin);
@@ -243,19 +259,24 @@ void build_range(const int32_t* idx, const int32_t* counts, int D, int S, int sp
   }
 }
 
-// GPU builder: one window per lane (the windows of a wave run the same code on different data;
-// their private arrays are interleaved per lane, so the lanes' accesses to them coalesce)
-__global__ void __launch_bounds__(64) sched_build_kernel(const int32_t* __restrict__ idx,
-                                                         const int32_t* __restrict__ counts, int D, int S, int sps,
-                                                         int gs, int nwin, long long nw, uint32_t* __restrict__ sched) {
-  const long long gw = (long long)blockIdx.x * 64 + threadIdx.x;
+// GPU builder: one window per lane, its working struct (2036 bytes) in the lane's private memory,
+// 128 VGPRs so a SIMD runs 4 waves.  The walk is latency-bound, so waves count: the C2 layer's
+// schedule took 1.45 s with the earlier per-lane arrays (a 16-bit histogram per slot, int locals:
+// ~6 KB per lane), 0.72 s with the compact struct at 2 waves per SIMD and 0.54 s at 4; with the 64
+// structs of a workgroup in LDS (one wave per CU) 2.3 s.
+constexpr int SCHED_LANES = 64;
+static_assert(sizeof(WinWork) == 2036, "WinWork: an odd number of dwords");
+__global__ void __launch_bounds__(SCHED_LANES) __attribute__((amdgpu_waves_per_eu(4, 4)))
+sched_build_kernel(const int32_t* __restrict__ idx, const int32_t* __restrict__ counts, int D, int S, int sps, int gs,
+                   int nwin, long long nw, uint32_t* __restrict__ sched) {
+  const long long gw = (long long)blockIdx.x * SCHED_LANES + threadIdx.x;
   if (gw >= nw) return;
   const long long g = gw / nwin;
   const int w = (int)(gw % nwin);
   const int ext = pool_ext((int)g, S, sps, gs);
   const int n_g = counts[g] < ext ? counts[g] : ext;
   const long long nb = pool_base((int)g, S, sps, gs);
-  Window W;
+  WinWork W;
   for (int p = 0; p < WIN; ++p) load_slot(W, idx, D, nb, w, n_g, p);
   schedule_window(W, sched + gw * WIN);
 }
@@ -370,7 +391,8 @@ extern "C" int gl_sched_build(const int32_t* idx, const int32_t* counts, int32_t
   if (K != 8) return GL_ERR_UNSUPPORTED;
   const long long nw = (long long)G * ceil_div(S, WIN);
   if (nw >= (1LL << 31)) return GL_ERR_UNSUPPORTED;
-  GL_LAUNCH(GL_KERNEL_SCHED, sched_build_kernel, dim3((unsigned)ceil_div(nw, 64)), dim3(64), 0, (hipStream_t)stream, idx,
+  GL_LAUNCH(GL_KERNEL_SCHED, sched_build_kernel, dim3((unsigned)ceil_div(nw, SCHED_LANES)), dim3(SCHED_LANES), 0,
+            (hipStream_t)stream, idx,
             counts, D, S, sps, gs, ceil_div(S, WIN), nw, sched);
   GL_CHECK_LAUNCH();
   return 0;
