@@ -336,7 +336,6 @@ __device__ __forceinline__ float cand_value(cand_t c) {
   const unsigned o = (unsigned)(c >> 32);
   return __uint_as_float((o & 0x80000000u) ? (o ^ 0x80000000u) : ~o);
 }
-__device__ __forceinline__ int cand_slot(cand_t c) { return (int)~(unsigned)c; }
 // the key of (-inf, slot 0x7fffffff): below every candidate a wave holds
 constexpr cand_t CAND_NONE = (0x007fffffull << 32) | 0x80000000u;
 
@@ -348,47 +347,34 @@ __device__ __forceinline__ void cand_cmpex(cand_t& a, cand_t& b) {
   b = swap ? t : b;
 }
 
-// drop the list's head when it is the round's winner w
-__device__ __forceinline__ void cand_pop(cand_t (&c)[4], cand_t w) {
-  const bool take = c[0] == w;
-#pragma unroll
-  for (int i = 0; i < 3; ++i) c[i] = take ? c[i + 1] : c[i];
-  c[3] = take ? CAND_NONE : c[3];
-}
-
+// 32-bit wave_max4 (the same reduce-scatter as wave_sum4): every lane ends with the maximum of
+// token wave_sum4_token(lane) over the wave
 template <int CTRL>
-__device__ __forceinline__ cand_t dppk(cand_t v) {
-  const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)v, CTRL, 0xf, 0xf, false);
-  const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(v >> 32), CTRL, 0xf, 0xf, false);
-  return ((cand_t)hi << 32) | lo;
+__device__ __forceinline__ unsigned dppu(unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
-__device__ __forceinline__ cand_t kmax(cand_t a, cand_t b) { return b > a ? b : a; }
-__device__ __forceinline__ cand_t permlane16_max(cand_t c) {
-  const auto l = __builtin_amdgcn_permlane16_swap((unsigned)c, (unsigned)c, false, false);
-  const auto h = __builtin_amdgcn_permlane16_swap((unsigned)(c >> 32), (unsigned)(c >> 32), false, false);
-  return kmax(((cand_t)h[0] << 32) | l[0], ((cand_t)h[1] << 32) | l[1]);
-}
-__device__ __forceinline__ cand_t permlane32_max(cand_t c) {
-  const auto l = __builtin_amdgcn_permlane32_swap((unsigned)c, (unsigned)c, false, false);
-  const auto h = __builtin_amdgcn_permlane32_swap((unsigned)(c >> 32), (unsigned)(c >> 32), false, false);
-  return kmax(((cand_t)h[0] << 32) | l[0], ((cand_t)h[1] << 32) | l[1]);
-}
-
-// wave_max4 over keys: the same reduce-scatter (lanes 0, 2, 1, 3 end with tokens 0, 1, 2, 3)
-__device__ __forceinline__ cand_t wave_max4_key(cand_t a0, cand_t a1, cand_t a2, cand_t a3, int lane) {
+__device__ __forceinline__ unsigned umax(unsigned a, unsigned b) { return a > b ? a : b; }
+__device__ __forceinline__ unsigned wave_max4_u32(unsigned a0, unsigned a1, unsigned a2, unsigned a3, int lane) {
   const bool odd = lane & 1, hi = lane & 2;
-  const cand_t b0 = kmax(odd ? a2 : a0, dppk<0xB1>(odd ? a0 : a2));  // quad_perm(1,0,3,2)
-  const cand_t b1 = kmax(odd ? a3 : a1, dppk<0xB1>(odd ? a1 : a3));
-  cand_t c = kmax(hi ? b1 : b0, dppk<0x4E>(hi ? b0 : b1));           // quad_perm(2,3,0,1)
-  c = kmax(c, dppk<0x124>(c));                                          // row_ror:4
-  c = kmax(c, dppk<0x128>(c));                                          // row_ror:8
-  return permlane32_max(permlane16_max(c));
+  const unsigned b0 = umax(odd ? a2 : a0, dppu<0xB1>(odd ? a0 : a2));  // quad_perm(1,0,3,2)
+  const unsigned b1 = umax(odd ? a3 : a1, dppu<0xB1>(odd ? a1 : a3));
+  unsigned c = umax(hi ? b1 : b0, dppu<0x4E>(hi ? b0 : b1));           // quad_perm(2,3,0,1)
+  c = umax(c, dppu<0x124>(c));                                          // row_ror:4
+  c = umax(c, dppu<0x128>(c));                                          // row_ror:8
+  const auto p16 = __builtin_amdgcn_permlane16_swap(c, c, false, false);
+  c = umax(p16[0], p16[1]);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  return umax(p32[0], p32[1]);
 }
 
 // Top-k tile (top-k mean pooling, pytorch_reference.py:68-77): per token the k largest raw z of the
 // wave's neurons with their slots (ties to the smaller slot), best first.  Every lane sorts its 4
-// candidates per token; then k rounds take the wave's best head (wave_max4_key) and drop it from
-// the lane that holds it.  Lanes 0-3 store each round's pair; the finalize merges the pool's chunks.
+// candidates per token (64-bit keys: value order, then ~slot); then k rounds take the wave's best
+// head and drop it from the lane that holds it.  A round finds the best head in two 32-bit steps:
+// the largest value order, then among the heads of that value the largest ~slot (the smallest
+// slot); the winner is the 64-bit maximum, as one 64-bit reduction would give, at a third of its
+// VALU (a 64-bit compare and two selects per reduction step become one v_max_u32).  Lanes 0-3
+// store each round's pair; the finalize merges the pool's chunks.
 template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
 __device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                               const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
@@ -424,6 +410,7 @@ __device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NP
       for (int kk = 0; kk < RA; ++kk) xc[kk] = xn[kk];
     }
   }
+  unsigned o[4][4], sl[4][4];  // the sorted lists as value-order and ~slot words
 #pragma unroll
   for (int t = 0; t < 4; ++t) {  // sorting network for 4
     cand_cmpex(c[t][0], c[t][1]);
@@ -431,22 +418,33 @@ __device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NP
     cand_cmpex(c[t][0], c[t][2]);
     cand_cmpex(c[t][1], c[t][3]);
     cand_cmpex(c[t][1], c[t][2]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[t][i] = (unsigned)(c[t][i] >> 32), sl[t][i] = (unsigned)c[t][i];
   }
+  constexpr unsigned NONE_O = (unsigned)(CAND_NONE >> 32), NONE_S = (unsigned)CAND_NONE;
   const int tok = wave_sum4_token(lane);
   for (int r = 0; r < k; ++r) {
-    const cand_t m = wave_max4_key(c[0][0], c[1][0], c[2][0], c[3][0], lane);
+    const unsigned mo = wave_max4_u32(o[0][0], o[1][0], o[2][0], o[3][0], lane);
+    unsigned mot[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)  // lanes 0, 2, 1, 3 hold tokens 0, 1, 2, 3
+      mot[t] = (unsigned)__builtin_amdgcn_readlane((int)mo, (t == 1) ? 2 : (t == 2) ? 1 : t);
+    unsigned es[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) es[t] = o[t][0] == mot[t] ? sl[t][0] : 0u;  // real ~slots are > 0
+    const unsigned ms = wave_max4_u32(es[0], es[1], es[2], es[3], lane);
     if (store && lane < 4) {
-      out[tok * k + r] = cand_value(m);
-      oslot[tok * k + r] = cand_slot(m);
+      out[tok * k + r] = cand_value(((cand_t)mo << 32) | ms);
+      oslot[tok * k + r] = (int)~ms;
     }
-    // lanes 0, 2, 1, 3 hold the winners of tokens 0, 1, 2, 3
-    const unsigned mlo = (unsigned)m, mhi = (unsigned)(m >> 32);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int src = (t == 1) ? 2 : (t == 2) ? 1 : t;
-      const cand_t wt = ((cand_t)(unsigned)__builtin_amdgcn_readlane((int)mhi, src) << 32) |
-                        (unsigned)__builtin_amdgcn_readlane((int)mlo, src);
-      cand_pop(c[t], wt);
+      const unsigned mst = (unsigned)__builtin_amdgcn_readlane((int)ms, (t == 1) ? 2 : (t == 2) ? 1 : t);
+      const bool take = o[t][0] == mot[t] && sl[t][0] == mst;  // drop the winner from its list
+#pragma unroll
+      for (int i = 0; i < 3; ++i) o[t][i] = take ? o[t][i + 1] : o[t][i], sl[t][i] = take ? sl[t][i + 1] : sl[t][i];
+      o[t][3] = take ? NONE_O : o[t][3];
+      sl[t][3] = take ? NONE_S : sl[t][3];
     }
   }
 }
