@@ -1172,30 +1172,41 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
         st[lane] = make_uint2(rec, __float_as_uint(wv));
       }
       __syncthreads();
-      for (int i = 0; i < n; ++i) {
-        uint2 e = st[i];
-        e.x = __builtin_amdgcn_readfirstlane(e.x);  // the same edge in every lane
-        e.y = __builtin_amdgcn_readfirstlane(e.y);
-        const int f = (int)((e.x >> REC_F_SHIFT) & REC_F_MASK);
-        const long long nn = nb + ((e.x & REC_OFF_MASK) >> (K == 8 ? 5 : 6));
-        const float wv = __uint_as_float(e.y);
-        const float* row = dz + nn * p.cap + tok0;
-        float v[T];
-        if constexpr (T == 4) {
-          const float4 x = *reinterpret_cast<const float4*>(row);
-          v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
-        } else if constexpr (T == 2) {
-          const float2 x = *reinterpret_cast<const float2*>(row);
-          v[0] = x.x, v[1] = x.y;
-        } else {
-          v[0] = row[0];
+      // DB edges at a time: their dz rows are loaded together (DB loads in flight per wave, where
+      // one dependent load per edge exposed each load's latency), then added in edge order; 16
+      // floats in flight per lane keep the kernel within 64 VGPRs (8 waves per SIMD)
+      constexpr int DB = T == 4 ? 4 : 8;
+      for (int i0 = 0; i0 < n; i0 += DB) {
+        float v[DB][T], wv[DB];
+        int f[DB];
+#pragma unroll
+        for (int u = 0; u < DB; ++u) {
+          const int i = i0 + u < n ? i0 + u : n - 1;  // past the chunk: the last edge again, not added
+          uint2 e = st[i];
+          e.x = __builtin_amdgcn_readfirstlane(e.x);  // the same edge in every lane
+          e.y = __builtin_amdgcn_readfirstlane(e.y);
+          f[u] = i0 + u < n ? (int)((e.x >> REC_F_SHIFT) & REC_F_MASK) : FW;
+          const long long nn = nb + ((e.x & REC_OFF_MASK) >> (K == 8 ? 5 : 6));
+          wv[u] = __uint_as_float(e.y);
+          const float* row = dz + nn * p.cap + tok0;
+          if constexpr (T == 4) {
+            const float4 x = *reinterpret_cast<const float4*>(row);
+            v[u][0] = x.x, v[u][1] = x.y, v[u][2] = x.z, v[u][3] = x.w;
+          } else if constexpr (T == 2) {
+            const float2 x = *reinterpret_cast<const float2*>(row);
+            v[u][0] = x.x, v[u][1] = x.y;
+          } else {
+            v[u][0] = row[0];
+          }
         }
 #pragma unroll
-        for (int x = 0; x < FW; ++x)  // f is wave-uniform: one branch taken, accumulators stay in registers
-          if (x == f) {
+        for (int u = 0; u < DB; ++u)
 #pragma unroll
-            for (int j = 0; j < T; ++j) acc[x][j] = __builtin_fmaf(wv, v[j], acc[x][j]);
-          }
+          for (int x = 0; x < FW; ++x)  // f is wave-uniform: one branch taken, accumulators stay in registers
+            if (x == f[u]) {
+#pragma unroll
+              for (int j = 0; j < T; ++j) acc[x][j] = __builtin_fmaf(wv[u], v[u][j], acc[x][j]);
+            }
       }
       __syncthreads();
     }
