@@ -1011,8 +1011,11 @@ struct BsK {
 // Neuron-stationary recompute pass of a smooth pool: per token tile z, dz = c1 f(z, c2, c3), db and dW
 // accumulated in registers over the chunk's tokens and added to the caller's buffers once; dz of
 // every valid neuron stored for the dX pass.  Token tiles stream through LDS as in bwd_w_kernel.
-template <int K, int NPL, int WAVES, int ACT, int OP, bool DBUF, bool XG = false>
+template <int K, int NPL, int WAVES, int ACT, int OP, bool DBUF, bool XG = false, int SB = 1>
 __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
+  // SB tiles of dz per neuron are held in registers and stored as one 16·SB-byte run: a lone
+  // 16-byte piece of a row (rows are cap·4 bytes apart) is a partial line write
+  static_assert(SB == 1 || SB == 2 || SB == 4 || SB == 8, "SB divides the 16 tiles of any cap");
   // XG (D > XTILE_SB): no LDS tile, the lanes gather from the token tiles in global memory
   __shared__ float4 xs[DBUF ? 2 * XTILE_DB : (XG ? 1 : XTILE_SB)];
   const int lane = threadIdx.x & 63;
@@ -1056,7 +1059,16 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
     stage_wait();
     __syncthreads();
   }
-  for (int t = 0; t < p.n_tiles; ++t) {
+  float4 dzb[NPL][SB];
+  for (int t0 = 0; t0 < p.n_tiles; t0 += SB) {
+#pragma unroll
+   for (int tt = 0; tt < SB; ++tt) {
+    const int t = t0 + tt;
+    if (t >= p.n_tiles) {  // past the last tile: zeros complete the run (cap is a multiple of 64 tokens)
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) dzb[j][tt] = make_float4(0.f, 0.f, 0.f, 0.f);
+      continue;
+    }
     const char* xb = nullptr;
     const XBuf xg = xbuf(p.xt + (long long)t * p.D, p.D);  // XG: the tile in global memory
     if constexpr (XG) {
@@ -1100,13 +1112,20 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
         a = __builtin_fmaf(d3, xc[k].w, a);
         dw[j][k] = a;
       }
-      if (active && v)
-        *reinterpret_cast<float4*>(p.dz + (nb + slot[j]) * (long long)p.cap + t * BT) = make_float4(d0, d1, d2, d3);
+      dzb[j][tt] = make_float4(d0, d1, d2, d3);
     }
     if constexpr (DBUF) {
       stage_wait();
       __syncthreads();
     }
+   }
+#pragma unroll
+    for (int j = 0; j < NPL; ++j)
+      if (active && slot[j] >= 0) {
+        float4* dst = reinterpret_cast<float4*>(p.dz + (nb + slot[j]) * (long long)p.cap + t0 * BT);
+#pragma unroll
+        for (int tt = 0; tt < SB; ++tt) dst[tt] = dzb[j][tt];
+      }
   }
   if (!active) return;
 #pragma unroll
@@ -1228,9 +1247,12 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
 // chunks of 128 slots cover pools of 512 exactly, where 3 per lane (chunks of 192) left 11% of the
 // lanes idle (C5 dW 53.8 -> 52.8 ms)
 constexpr int bwd_npl(int K) { return K == 8 ? 4 : 2; }
-// the smooth pools' recompute pass keeps every gathered x of a neuron live across dz: fewer neurons
-// per lane at K = 16 keep it in registers
-constexpr int smooth_npl(int K) { return K == 8 ? 4 : 2; }
+// The smooth pools' recompute pass keeps every gathered x of a neuron live across dz, and holds
+// smooth_sb tiles of dz per neuron to store them as one 64-byte (K = 8) or 32-byte (K = 16) run:
+// 2 neurons per lane.  At K = 8, 4 per lane with 16-byte stores ran 28.5 ms per 64-token C2
+// chunk, 2 per lane with 64-byte runs 22.0 ms (4 per lane with 32-byte runs spills).
+constexpr int smooth_npl(int K) { return 2; }
+constexpr int smooth_sb(int K) { return K == 8 ? 4 : 2; }
 constexpr int bwd_waves(int K) { return K == 8 ? 12 : 8; }
 
 struct BwdPlan {
@@ -1356,10 +1378,10 @@ static int launch_dx(int K, int T, const DxK& k, hipStream_t s, bool dma) {
 template <int K, int ACT, int OP>
 static int launch_bwd_smooth_k(const BsK& k, hipStream_t s) {
   // neurons per lane: the plan's (its cpg chunks of 64 NPL slots cover every pool exactly)
-  constexpr int NPL = smooth_npl(K), WAVES = 8;
-  auto fn = k.D <= XTILE_DB ? bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, true>
-                            : (k.D <= XTILE_SB ? bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, false>
-                                               : bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, false, true>);
+  constexpr int NPL = smooth_npl(K), WAVES = 8, SB = smooth_sb(K);
+  auto fn = k.D <= XTILE_DB ? bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, true, false, SB>
+                            : (k.D <= XTILE_SB ? bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, false, false, SB>
+                                               : bwd_smooth_kernel<K, NPL, WAVES, ACT, OP, false, true, SB>);
   GL_LAUNCH(GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)), dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;
