@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgranulelayer_amd.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 GL_ACT = {"identity": 0, "relu": 1}
 GL_POOL = {"mean": 0, "sum": 1, "max": 2, "topk_mean": 3, "logmeanexp": 4, "power_mean": 5, "softmax_weighted": 6}
@@ -37,7 +37,7 @@ class GlBwdArgs(ctypes.Structure):
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("g_pre", _P), ("winner", _P), ("pool_param", _F),
                 ("pre", _P), ("lse", _P), ("dW", _P), ("db", _P),
                 ("dX", _P), ("edges", _P), ("edges_bytes", _SZ),
-                ("ws", _P), ("ws_bytes", _SZ)]
+                ("ws", _P), ("ws_bytes", _SZ), ("dz_budget", _SZ)]
 
 
 class GlEdgeArgs(ctypes.Structure):

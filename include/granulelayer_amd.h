@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 10
+#define GL_ABI_VERSION 11
 
 enum {
   GL_OK = 0,
@@ -133,6 +133,11 @@ typedef struct GlBwdArgs {
   size_t edges_bytes;
   void* ws;               /* workspace of gl_bwd_workspace() bytes */
   size_t ws_bytes;
+  size_t dz_budget;       /* smooth pools (GL_POOL_LME / POWER / SOFTMAX): bytes of the per-neuron dz
+                             of one backward token chunk, [G*S, chunk] fp32 (0: 8 GiB).  Chunks are of
+                             64 to 1024 tokens, at least 64 whatever the budget; larger chunks run
+                             fewer recompute and dX passes per token (the workspace query includes
+                             it).  dW / db sum over the chunks, so their rounding depends on it */
 } GlBwdArgs;
 
 /* Input-major (transposed) edge list of a layer, built once per index tensor.  It has no

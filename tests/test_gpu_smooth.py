@@ -129,3 +129,31 @@ def test_smooth_backward_chunks_and_wide_inputs(case, pool, param, act):
     assert_parity(dx, wdX, mX, what="dX")
     assert_parity(dw.cpu().numpy().reshape(-1, L.fan_in), wdW, mW, what="dW")
     assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, what="db")
+
+
+@pytest.mark.parametrize("pool,param,act", [OPS[0], OPS[3], OPS[4]], ids=lambda v: str(v))
+def test_smooth_backward_dz_budget_sets_the_token_chunks(pool, param, act):
+    """The dz budget only chunks the tokens: a budget below one 64-token chunk runs B = 200 as four
+    chunks (64, 64, 64, 8) with a smaller workspace, and both runs give the oracle's gradients;
+    dX of a token never crosses a chunk."""
+    L, idx, w, b, x, dy = _case((512, 6000, 6, 8, 200, torch.float32), seed=5)
+    xd, wd, bd, dyd = x.to(DEV), w.to(DEV), b.to(DEV), dy.to(DEV)
+    fi, fw, fb = _flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    wdW, wdb, wdX, (mW, mb, mX) = O.backward_smooth(x.numpy(), fi, fw, fb, counts, L.slots_per_group, dy.numpy(), pool,
+                                                    param, act)
+    info = []
+    for budget in (1, 2**30):
+        rt = Level1Runtime(L, idx.to(DEV), _spec(pool, param, act), PhysicalPlan(), workspace_budget=budget)
+        out = rt.forward(xd, wd, bd)
+        dw = torch.zeros(L.weight_shape, device=DEV)
+        db = torch.zeros(L.bias_shape, device=DEV)
+        dx = rt.backward(xd, wd, bd, dyd, out, "minimal_stats", dw, db).cpu().numpy()
+        assert_parity(dx, wdX, mX, what=f"dX at budget {budget}")
+        assert_parity(dw.cpu().numpy().reshape(-1, L.fan_in), wdW, mW, what=f"dW at budget {budget}")
+        assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, what=f"db at budget {budget}")
+        info.append(rt.last_info["backward_workspace_bytes"])
+    # one 64-token chunk of dz against the whole B = 200 (cap 256) at once
+    assert info[0] < info[1]
+    assert info[1] - info[0] >= L.groups * L.slots_per_group * (256 - 64) * 4
+
