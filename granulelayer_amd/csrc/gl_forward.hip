@@ -484,43 +484,12 @@ __device__ __forceinline__ void wave_merge4(const float (&m)[4], const float (&s
   mo = cm, so = cs, to = ct;
 }
 
-// Smooth pooling tile (LogMeanExp, power mean, softmax-weighted; pytorch_reference.py:80-100): z of
-// the lane's neurons for the tile's 4 tokens, then per token the lane's state over its valid neurons
-// (vmask bit j: neuron j valid) -- the largest u (or a), the sum of 2^(u - m) (or (a / m)^p) and, for
-// softmax-weighted, of 2^(u - m) a -- merged over the wave; lanes 0-3 store (m, s, t) per token.
-template <int K, int NPL, int ACT, bool FAR, int OP, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
-__device__ __forceinline__ void fwd_tile_smooth(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
-                                                const float (&bias)[NPL], unsigned vmask, float* out, bool store,
-                                                int lane, float scale, float p, int pint) {
-  float z[NPL][4];
-  float4 xc[K];
-#pragma unroll
-  for (int k = 0; k < RA; ++k) xc[k] = gather_x<FAR>(xsb, addr[0][k]);
-#pragma unroll
-  for (int j = 0; j < NPL; ++j) {
-#pragma unroll
-    for (int k = RA; k < K; ++k) xc[k] = gather_x<FAR>(xsb, addr[j][k]);
-    float4 xn[RA];
-    if (j + 1 < NPL) {
-#pragma unroll
-      for (int k = 0; k < RA; ++k) xn[k] = gather_x<FAR>(xsb, addr[j + 1][k]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
-      z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
-      z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
-      z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
-    }
-    z[j][0] = z0, z[j][1] = z1, z[j][2] = z2, z[j][3] = z3;
-    __builtin_amdgcn_sched_barrier(0);
-    if (j + 1 < NPL) {
-#pragma unroll
-      for (int k = 0; k < RA; ++k) xc[k] = xn[k];
-    }
-  }
+// Per token the lane's smooth state over its valid neurons (vmask bit j: neuron j valid) -- the
+// largest u (or a), the sum of 2^(u - m) (or (a / m)^p) and, for softmax-weighted, of 2^(u - m) a --
+// merged over the wave: every lane ends with the merged state of token wave_sum4_token(lane).
+template <int OP, int NPL, int ACT = GL_ACT_RELU>
+__device__ __forceinline__ void smooth_reduce(const float (&z)[NPL][4], unsigned vmask, int lane, float scale, float p,
+                                              int pint, float& mo, float& so, float& to) {
   float m[4], s[4], t[4];
   const float ninf = -__builtin_inff();
 #pragma unroll
@@ -558,8 +527,59 @@ __device__ __forceinline__ void fwd_tile_smooth(SRC xsb, const unsigned (&addr)[
       m[tk] = mx, s[tk] = acc, t[tk] = acct;
     }
   }
-  float mo, so, to;
   wave_merge4<OP>(m, s, t, lane, p, pint, mo, so, to);
+}
+
+// Smooth pooling tile (LogMeanExp, power mean, softmax-weighted; pytorch_reference.py:80-100): z of
+// the lane's neurons for the tile's 4 tokens, their states merged over the wave (smooth_reduce);
+// lanes 0-3 store (m, s, t) per token.
+template <int K, int NPL, int ACT, bool FAR, int OP, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
+__device__ __forceinline__ void fwd_tile_smooth(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
+                                                const float (&bias)[NPL], unsigned vmask, float* out, bool store,
+                                                int lane, float scale, float p, int pint) {
+  float z[NPL][4];
+  float4 xc[K];
+#pragma unroll
+  for (int k = 0; k < RA; ++k) xc[k] = gather_x<FAR>(xsb, addr[0][k]);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+#pragma unroll
+    for (int k = RA; k < K; ++k) xc[k] = gather_x<FAR>(xsb, addr[j][k]);
+    float4 xn[RA];
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xn[k] = gather_x<FAR>(xsb, addr[j + 1][k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
+      z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
+      z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
+      z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
+    }
+    z[j][0] = z0, z[j][1] = z1, z[j][2] = z2, z[j][3] = z3;
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 1 < NPL) {
+#pragma unroll
+      for (int k = 0; k < RA; ++k) xc[k] = xn[k];
+    }
+  }
+  float mo, so, to;
+  if constexpr (OP == SM_POW) {
+    // p as a literal where it is 1, 2, 4 or 8: the inlined powers then fold to products (with p
+    // read at run time the branches of every power cost 63.5 against 33.0 ms per C2 forward)
+    switch (pint) {
+      case 1: smooth_reduce<OP, NPL>(z, vmask, lane, scale, p, 1, mo, so, to); break;
+      case 2: smooth_reduce<OP, NPL>(z, vmask, lane, scale, p, 2, mo, so, to); break;
+      case 4: smooth_reduce<OP, NPL>(z, vmask, lane, scale, p, 4, mo, so, to); break;
+      case 8: smooth_reduce<OP, NPL>(z, vmask, lane, scale, p, 8, mo, so, to); break;
+      default: smooth_reduce<OP, NPL>(z, vmask, lane, scale, p, 0, mo, so, to); break;
+    }
+  } else {
+    smooth_reduce<OP, NPL, ACT>(z, vmask, lane, scale, p, pint, mo, so, to);
+  }
   if (store && lane < 4) {
     float* o = out + wave_sum4_token(lane) * 3;
     o[0] = mo, o[1] = so, o[2] = to;
