@@ -1,7 +1,8 @@
 """LogMeanExp, power mean and softmax-weighted pooling on the GPU (pytorch_reference.py:80-100;
 backward kernels/ops.py:242-262, triton_fused.py:364-399) against the float64 oracle on identical
 seeded inputs: forward pre and the log-normaliser L2, backward dX / dW / db, the layer's autograd
-under its checkpoint policies, bitwise determinism, two backward token chunks and D > 4096.
+under its checkpoint policies, bitwise determinism, two backward token chunks and D > 4096, the
+power mean at every integer p the kernels take as a literal, and the dz budget's token chunks.
 
 fp32 bar: conftest.assert_parity with the oracle's error scales (elementwise 1e-6 + 1e-5 * mag and
 a whole-tensor relative error <= 1e-5)."""
@@ -157,3 +158,27 @@ def test_smooth_backward_dz_budget_sets_the_token_chunks(pool, param, act):
     assert info[0] < info[1]
     assert info[1] - info[0] >= L.groups * L.slots_per_group * (256 - 64) * 4
 
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[2]], ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}")
+@pytest.mark.parametrize("p", [1.0, 4.0, 8.0])
+def test_power_mean_integer_p(case, p):
+    """The power mean's integer p (1, 4, 8; 2 in the main test) runs kernels where p is a literal:
+    forward pre and backward dX / dW / db against the oracle."""
+    L, idx, w, b, x, dy = _case(case, seed=9)
+    rt = Level1Runtime(L, idx.to(DEV), _spec("power_mean", p, "relu"), PhysicalPlan())
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    out = rt.forward(xd, wd, bd)
+    fi, fw, fb = _flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    xn = x.float().numpy()
+    want, _, mag = O.forward_smooth(xn, fi, fw, fb, counts, L.slots_per_group, "power_mean", p, "relu")
+    assert_parity(out["pre"].cpu().numpy(), want, mag, what=f"p {p} pre")
+    dw = torch.zeros(L.weight_shape, device=DEV)
+    db = torch.zeros(L.bias_shape, device=DEV)
+    dx = rt.backward(xd, wd, bd, dy.to(DEV), out, "minimal_stats", dw, db).cpu().numpy()
+    wdW, wdb, wdX, (mW, mb, mX) = O.backward_smooth(xn, fi, fw, fb, counts, L.slots_per_group, dy.numpy(),
+                                                    "power_mean", p, "relu")
+    assert_parity(dx, wdX, mX, what=f"p {p} dX")
+    assert_parity(dw.cpu().numpy().reshape(-1, L.fan_in), wdW, mW, what=f"p {p} dW")
+    assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, what=f"p {p} db")
