@@ -1144,7 +1144,10 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
 
 // dX of a smooth pool: dX[b, d] = sum over edges (n, k) -> d of dz[b, n] W[n, k], walking the
 // input-major edges like dx_kernel (one wave per feature range, unit range and token slice); per
-// edge every lane reads its T tokens of the neuron's dz row.
+// edge every lane reads its T (<= 2) tokens of the neuron's dz row.  A segment's edges are sorted
+// by feature, so consecutive edges into one feature are summed in registers (a run) and the run is
+// added to that feature's sums in LDS when the feature changes: one uniform branch per run where
+// selecting one of FW register accumulators per edge cost FW * T multiply-adds and selects.
 template <int K, int T>
 __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __restrict__ dz) {
   const int lane = threadIdx.x;
@@ -1173,13 +1176,19 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
     }
     hi = a;
   }
-  float acc[FW][T];
-#pragma unroll
-  for (int f = 0; f < FW; ++f)
-#pragma unroll
-    for (int j = 0; j < T; ++j) acc[f][j] = 0.f;
   const int tok0 = tc * 64 * T + T * lane;
   __shared__ uint2 st[64];  // (record, weight bits) of the chunk's edges
+  // per feature of the range, every lane's T sums: lane-major rows of T floats (no bank conflicts)
+  __shared__ float sums[FW][64 * T];
+#pragma unroll
+  for (int x = 0; x < FW; ++x)
+#pragma unroll
+    for (int j = 0; j < T; ++j) sums[x][T * lane + j] = 0.f;
+  float r[T];  // the open run: its feature fc (wave-uniform; -1 before the first edge)
+#pragma unroll
+  for (int j = 0; j < T; ++j) r[j] = 0.f;
+  int fc = -1;
+  const unsigned lo8 = (unsigned)tok0 * 4u;  // the lane's byte offset in a dz row
   for (int si = lo; si < hi; ++si) {
     const int u = p.seg_unit[si];
     const long long nb = pool_base(u / p.P, p.S, p.sps, p.gs) + (long long)(u % p.P) * US;  // first neuron of the unit
@@ -1194,8 +1203,7 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
       }
       __syncthreads();
       // DB edges at a time: their dz rows are loaded together (DB loads in flight per wave, where
-      // one dependent load per edge exposed each load's latency), then added in edge order; 16
-      // floats in flight per lane keep the kernel within 64 VGPRs (8 waves per SIMD)
+      // one dependent load per edge exposed each load's latency), then added in edge order
       constexpr int DB = T == 4 ? 4 : 8;
       for (int i0 = 0; i0 < n; i0 += DB) {
         float v[DB][T], wv[DB];
@@ -1209,36 +1217,48 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
           f[u] = i0 + u < n ? (int)((e.x >> REC_F_SHIFT) & REC_F_MASK) : FW;
           const long long nn = nb + ((e.x & REC_OFF_MASK) >> (K == 8 ? 5 : 6));
           wv[u] = __uint_as_float(e.y);
-          const float* row = dz + nn * p.cap + tok0;
+          const float* row = dz + nn * p.cap;  // scalar row base (buffer resource), the lane's 32-bit offset
           if constexpr (T == 4) {
-            const float4 x = *reinterpret_cast<const float4*>(row);
-            v[u][0] = x.x, v[u][1] = x.y, v[u][2] = x.z, v[u][3] = x.w;
+            const uint4 x = ld_uniform_u128(row, lo8);
+            v[u][0] = __uint_as_float(x.x), v[u][1] = __uint_as_float(x.y);
+            v[u][2] = __uint_as_float(x.z), v[u][3] = __uint_as_float(x.w);
           } else if constexpr (T == 2) {
-            const float2 x = *reinterpret_cast<const float2*>(row);
-            v[u][0] = x.x, v[u][1] = x.y;
+            const uint2 x = ld_uniform_u64(row, lo8);
+            v[u][0] = __uint_as_float(x.x), v[u][1] = __uint_as_float(x.y);
           } else {
-            v[u][0] = row[0];
+            v[u][0] = __uint_as_float(ld_uniform_u32(row, lo8));
           }
         }
 #pragma unroll
-        for (int u = 0; u < DB; ++u)
+        for (int u = 0; u < DB; ++u) {
+          if (f[u] >= FW) break;  // past the chunk (uniform)
+          if (f[u] != fc) {       // the run ends: add it to its feature's sums
+            if (fc >= 0) {
 #pragma unroll
-          for (int x = 0; x < FW; ++x)  // f is wave-uniform: one branch taken, accumulators stay in registers
-            if (x == f[u]) {
-#pragma unroll
-              for (int j = 0; j < T; ++j) acc[x][j] = __builtin_fmaf(wv[u], v[u][j], acc[x][j]);
+              for (int j = 0; j < T; ++j) sums[fc][T * lane + j] += r[j];
             }
+            fc = f[u];
+#pragma unroll
+            for (int j = 0; j < T; ++j) r[j] = 0.f;
+          }
+#pragma unroll
+          for (int j = 0; j < T; ++j) r[j] = __builtin_fmaf(wv[u], v[u][j], r[j]);
+        }
       }
       __syncthreads();
     }
   }
+  if (fc >= 0) {
+#pragma unroll
+    for (int j = 0; j < T; ++j) sums[fc][T * lane + j] += r[j];
+  }
   float* out = p.part + (long long)q * p.D * p.cap;
 #pragma unroll
-  for (int f = 0; f < FW; ++f) {
-    const int d = F * FW + f;
+  for (int x = 0; x < FW; ++x) {
+    const int d = F * FW + x;
     if (d < p.D) {
 #pragma unroll
-      for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j] = acc[f][j];
+      for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j] = sums[x][T * lane + j];
     }
   }
 }
@@ -1522,10 +1542,11 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
                    sps, gs};
       GL_TRY(a->K == 8 ? launch_bwd_smooth_kk<8>(a->pool, a->act, bk, s) : launch_bwd_smooth_kk<16>(a->pool, a->act, bk, s));
       const long long NS = (long long)a->G * a->S;
+      const int Td = T;
       DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
              (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, nullptr, a->W, part,
-             NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * T), sps, gs};
-      GL_TRY(launch_dx_dense(a->K, T, dk, dz, s));
+             NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * Td), sps, gs};
+      GL_TRY(launch_dx_dense(a->K, Td, dk, dz, s));
       GL_LAUNCH(GL_KERNEL_DX_REDUCE, dx_reduce_kernel, dim3((unsigned)ceil_div(a->D, 32), (unsigned)ceil_div(Bc, 32)),
                 dim3(256), 0, s, part, a->dX, a->D, cap, q.Q, b0, Bc);
       GL_CHECK_LAUNCH();
