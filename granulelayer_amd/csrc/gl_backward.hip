@@ -1270,11 +1270,13 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
 // lanes idle (C5 dW 53.8 -> 52.8 ms)
 constexpr int bwd_npl(int K) { return K == 8 ? 4 : 2; }
 // The smooth pools' recompute pass keeps every gathered x of a neuron live across dz, and holds
-// smooth_sb tiles of dz per neuron to store them as one 64-byte (K = 8) or 32-byte (K = 16) run:
+// smooth_sb tiles of dz per neuron to store them as one 128-byte (K = 8) or 32-byte (K = 16) run:
 // 2 neurons per lane.  At K = 8, 4 per lane with 16-byte stores ran 28.5 ms per 64-token C2
-// chunk, 2 per lane with 64-byte runs 22.0 ms (4 per lane with 32-byte runs spills).
+// chunk, 2 per lane with 64-byte runs 22.0 ms, with 128-byte runs 22.6 ms (4 per lane with 32-byte
+// runs spills); per 128-token chunk (the layer's default dz budget) 64-byte runs 37.6 ms,
+// 128-byte runs 35.5 ms.
 constexpr int smooth_npl(int K) { return 2; }
-constexpr int smooth_sb(int K) { return K == 8 ? 4 : 2; }
+constexpr int smooth_sb(int K) { return K == 8 ? 8 : 2; }
 constexpr int bwd_waves(int K) { return K == 8 ? 12 : 8; }
 
 struct BwdPlan {
