@@ -26,8 +26,8 @@ import torch
 from . import _native as N
 
 # Default dz budget of the smooth pools' backward: 64 GiB of MI355X's 288 GB HBM.  100.6 M neurons
-# (C2) then run 128-token chunks: 267 ms per LogMeanExp train step against 355 ms with the
-# library's own 8 GiB (64-token chunks).
+# (C2) then run 128-token chunks instead of the library default's 64, and the recompute and dense
+# dX passes cost less per token in longer chunks.
 DZ_BUDGET = 64 * 2**30
 
 
@@ -190,7 +190,7 @@ class HipBackend:
     @staticmethod
     def part_budget(rt) -> int:
         """Bytes of per-chunk forward partials one pass may hold: the layer's ``workspace_budget``
-        when the caller set one, else 0 (the library's default of 4 GiB, which runs the BASELINE
+        when the caller set one, else 0 (the library's default of 8 GiB, which runs the BASELINE
         shapes' sum / mean forward in one pass).  The forward runs token chunks within it."""
         from .config import DEFAULT_WORKSPACE_BUDGET
 

@@ -1007,8 +1007,9 @@ static int smooth_pint(int pool, float param) {
 // Forward plan: the forward runs over token chunks of bf tokens (a multiple of BT) whose per-chunk
 // partials (part_bytes + slot_bytes) fit the caller's part budget; every pass reloads the chunk
 // parameters once and streams its own token tiles.  The per-token results do not depend on the
-// chunking (same waves, same order), so any budget gives the same bits.
-constexpr size_t FWD_PART_BUDGET_DEFAULT = 4ull << 30;
+// chunking (same waves, same order), so any budget gives the same bits.  The default 8 GiB runs
+// C2's top-8 mean in one pass of 256 tokens (67.2 ms) where 4 GiB took two (2 x 34.4 ms).
+constexpr size_t FWD_PART_BUDGET_DEFAULT = 8ull << 30;
 
 struct FwdPlan {
   int npl, waves, cpg, bf, n_passes;

@@ -93,7 +93,7 @@ typedef struct GlFwdArgs {
                              reference's "L2" statistic, kernels/ops.py:201-209) */
   void* ws;               /* workspace of gl_fwd_workspace() bytes */
   size_t ws_bytes;
-  size_t part_budget;     /* bytes of per-chunk partial results one pass may hold (0: 4 GiB).  The
+  size_t part_budget;     /* bytes of per-chunk partial results one pass may hold (0: 8 GiB).  The
                              forward runs over token chunks whose partials fit it, so the workspace
                              stays bounded as B grows (the reference keeps its split states within
                              workspace_budget, sparse_pooling/kernels/ops.py:82-98) */

@@ -99,7 +99,7 @@ def test_pool_limits_are_refused_by_the_size_query():
 
 
 def test_forward_workspace_is_bounded_as_the_batch_grows():
-    """The forward runs token chunks whose partial results fit part_budget (default 4 GiB), so its
+    """The forward runs token chunks whose partial results fit part_budget (default 8 GiB), so its
     workspace stops growing with B: at the C2 shape with top-16 mean, B = 8192 needs no more than
     B = 1024; sum pooling at B = 256 (the headline) still runs as one pass.  Host-side size query
     only (placeholder pointers, never dereferenced)."""
@@ -113,9 +113,9 @@ def test_forward_workspace_is_bounded_as_the_batch_grows():
         return out.value
 
     tk = [ws(B, "topk_mean", 16) for B in (1024, 8192, 65536)]
-    assert tk[0] == tk[1] == tk[2] <= (4 << 30) + 1024 * 4096 * 4 + 512
+    assert tk[0] == tk[1] == tk[2] <= (8 << 30) + 1024 * 4096 * 4 + 512
     assert ws(256, "sum") == 256 * 4096 * 4 + 98_304 * 4 * 256 * 4  # X tiles + one pass of partials
-    assert ws(1 << 20, "max") <= (4 << 30) + (1 << 20) * 4096 * 4
+    assert ws(1 << 20, "max") <= (8 << 30) + (1 << 20) * 4096 * 4
     small = ws(1 << 16, "sum", budget=64 << 20)
     assert small <= (64 << 20) + (1 << 16) * 4096 * 4
     # a budget below one token tile's partials still runs (one tile per pass)
