@@ -13,9 +13,9 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgranulelayer_amd.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
-GL_ACT = {"identity": 0, "relu": 1}
+GL_ACT = {"identity": 0, "relu": 1, "gelu": 2}
 GL_POOL = {"mean": 0, "sum": 1, "max": 2, "topk_mean": 3, "logmeanexp": 4, "power_mean": 5, "softmax_weighted": 6}
 GL_DTYPE_F32, GL_DTYPE_BF16 = 0, 1
 GL_ERR_SCRATCH = -8
@@ -28,7 +28,7 @@ class GlFwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
                 ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("rec_shift", _I32), ("sps", _I32), ("gs", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("pre", _P), ("winner", _P), ("pool_param", _F),
-                ("lse", _P), ("ws", _P), ("ws_bytes", _SZ), ("part_budget", _SZ)]
+                ("lse", _P), ("ws", _P), ("ws_bytes", _SZ), ("part_budget", _SZ), ("w_dtype", _I32)]
 
 
 class GlBwdArgs(ctypes.Structure):
@@ -37,7 +37,7 @@ class GlBwdArgs(ctypes.Structure):
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("g_pre", _P), ("winner", _P), ("pool_param", _F),
                 ("pre", _P), ("lse", _P), ("dW", _P), ("db", _P),
                 ("dX", _P), ("edges", _P), ("edges_bytes", _SZ),
-                ("ws", _P), ("ws_bytes", _SZ), ("dz_budget", _SZ)]
+                ("ws", _P), ("ws_bytes", _SZ), ("dz_budget", _SZ), ("w_dtype", _I32)]
 
 
 class GlEdgeArgs(ctypes.Structure):

@@ -18,7 +18,7 @@ from typing import Dict, Optional
 
 import torch
 
-from .config import DEFAULT_WORKSPACE_BUDGET, LevelSpec, PhysicalPlan, resolve_reduction
+from .config import LevelSpec, PhysicalPlan, check_workspace_budget, resolve_reduction
 from .layout import SparseLayout
 
 AUTO_POLICY = {"max": "save_winners", "topk_mean": "save_winners", "mean": "minimal_stats",
@@ -127,7 +127,7 @@ class Level1Runtime:
     """Executes the fused level-1 kernels for one layer (sparse_pooling/autograd.py:68-300)."""
 
     def __init__(self, layout: SparseLayout, idx: torch.Tensor, level: LevelSpec, plan: PhysicalPlan,
-                 nps: Optional[int] = None, workspace_budget: int = DEFAULT_WORKSPACE_BUDGET,
+                 nps: Optional[int] = None, workspace_budget: Optional[int] = None,
                  backend: Optional[object] = None):
         reason = level.hip_reason()
         if reason:
@@ -147,7 +147,7 @@ class Level1Runtime:
         # valid neurons per pooling unit (the groups, or the level-1 shards), as the kernels read them
         self.unit_counts_i32 = (self.counts_i32 if nps is None
                                 else self.units.counts.to(torch.int32).contiguous())
-        self.workspace_budget = workspace_budget
+        self.workspace_budget = check_workspace_budget(workspace_budget)
         if backend is None and idx.is_cuda:
             from .backend import backend_for
 
@@ -204,18 +204,20 @@ class Level1Runtime:
 
 
 def _compute_operands(x, w, b, compute_dtype):
-    """Operands of the kernels (autograd.py:349-354).  The HIP kernels compute in fp32 with fp32
-    weights and accept fp32 or bf16 inputs; a bf16 compute dtype rounds x, W and b to bf16 first,
-    as the reference's cast does, then runs the same fp32 arithmetic."""
+    """Operands of the kernels (autograd.py:349-354).  The HIP kernels read x, W and b as fp32 or
+    bf16 and compute in fp32 (bf16 values are widened in the kernel, as the reference's kernels
+    widen W, triton_fused.py:257).  A bf16 compute dtype rounds x, W and b to bf16 as the
+    reference's cast does; parameters already stored in bf16 (the reference's default layer dtype)
+    are passed as they are, with no copy."""
     if compute_dtype == torch.bfloat16:
         xc = x.to(torch.bfloat16).contiguous()
-        wc = w.to(torch.bfloat16).to(torch.float32)
-        bc = b.to(torch.bfloat16).to(torch.float32)
+        wc = w if w.dtype == torch.bfloat16 else w.to(torch.bfloat16)
+        bc = b if b.dtype == torch.bfloat16 else b.to(torch.bfloat16)
     elif compute_dtype == torch.float32:
         xc = x if x.dtype in (torch.float32, torch.bfloat16) else x.to(torch.float32)
         xc = xc.contiguous()
-        wc = w if w.dtype == torch.float32 else w.to(torch.float32)
-        bc = b if b.dtype == torch.float32 else b.to(torch.float32)
+        wc = w if w.dtype in (torch.float32, torch.bfloat16) else w.to(torch.float32)
+        bc = b if b.dtype in (torch.float32, torch.bfloat16) else b.to(torch.float32)
     else:
         raise NotImplementedError(f"compute dtype {compute_dtype} (the MI355X path computes fp32 or bf16 operands)")
     return xc, wc.contiguous(), bc.contiguous()

@@ -54,6 +54,20 @@ def _x_operand(x: torch.Tensor):
     return x, code, x.stride(0)
 
 
+def _params(w: torch.Tensor, b: torch.Tensor):
+    """(W, bias, dtype code) as the kernels read them: fp32 or bf16 (widened in the kernels), both
+    of one dtype (a bf16 / fp32 mix is widened to fp32, exactly), contiguous, W 4-byte aligned."""
+    for name, t in (("weight", w), ("bias", b)):
+        if t.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError(f"{name} must be float32 or bfloat16 (got {t.dtype})")
+    if w.dtype != b.dtype:
+        w, b = w.float(), b.float()
+    w, b = w.contiguous(), b.contiguous()
+    if w.data_ptr() % 4:  # a bf16 view at an odd element offset: the dX kernels read 32-bit words
+        w = w.clone()
+    return w, b, N.GL_DTYPE_BF16 if w.dtype == torch.bfloat16 else N.GL_DTYPE_F32
+
+
 def _f32(t: torch.Tensor, name: str) -> torch.Tensor:
     if t.dtype != torch.float32:
         raise TypeError(f"{name} must be float32 (got {t.dtype})")
@@ -144,7 +158,7 @@ class HipBackend:
         G, S, sps, gs, counts = self._pools(rt)
         act, pool = self._codes(rt)
         x, xcode, sxb = _x_operand(x)
-        w, b = _f32(w, "weight"), _f32(b, "bias")
+        w, b, wcode = _params(w, b)
         B = x.shape[0]
         pre = torch.empty((B, G), device=x.device, dtype=torch.float32)
         # with track_ids, the selected slots: max pooling's "winner" [B, U] and top-k mean's
@@ -171,7 +185,7 @@ class HipBackend:
                         counts=_ptr(counts),
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, pre=_ptr(pre),
                         winner=_ptr(winner), pool_param=self.pool_param(rt), lse=_ptr(lse),
-                        part_budget=self.part_budget(rt))
+                        part_budget=self.part_budget(rt), w_dtype=wcode)
         with torch.cuda.device(x.device):
             need = self.lib.size_query("gl_fwd_workspace", a)
             ws = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)
@@ -190,12 +204,11 @@ class HipBackend:
     @staticmethod
     def part_budget(rt) -> int:
         """Bytes of per-chunk forward partials one pass may hold: the layer's ``workspace_budget``
-        when the caller set one, else 0 (the library's default of 8 GiB, which runs the BASELINE
-        shapes' sum / mean forward in one pass).  The forward runs token chunks within it."""
-        from .config import DEFAULT_WORKSPACE_BUDGET
-
-        wb = getattr(rt, "workspace_budget", DEFAULT_WORKSPACE_BUDGET)
-        return 0 if wb == DEFAULT_WORKSPACE_BUDGET else int(wb)
+        when the caller set one (any value, the reference's 512 MiB default included), else 0 (the
+        library's default of 8 GiB, which runs the BASELINE shapes' sum / mean forward in one
+        pass).  The forward runs token chunks within it."""
+        wb = getattr(rt, "workspace_budget", None)
+        return 0 if wb is None else int(wb)
 
     @staticmethod
     def dz_budget(rt) -> int:
@@ -203,10 +216,8 @@ class HipBackend:
         softmax-weighted) may hold: the layer's ``workspace_budget`` when the caller set one, else
         DZ_BUDGET.  A fixed figure, not one taken from the free memory, because the chunking sets
         the order in which dW and db sum over the tokens."""
-        from .config import DEFAULT_WORKSPACE_BUDGET
-
-        wb = getattr(rt, "workspace_budget", DEFAULT_WORKSPACE_BUDGET)
-        return DZ_BUDGET if wb == DEFAULT_WORKSPACE_BUDGET else int(wb)
+        wb = getattr(rt, "workspace_budget", None)
+        return DZ_BUDGET if wb is None else int(wb)
 
     # ------------------------------------------------------------------ gather schedule
     def schedule(self, rt) -> Optional[torch.Tensor]:
@@ -284,7 +295,7 @@ class HipBackend:
         G, S, sps, gs, counts = self._pools(rt)
         act, pool = self._codes(rt)
         x, xcode, sxb = _x_operand(x)
-        w, b = _f32(w, "weight"), _f32(b, "bias")
+        w, b, wcode = _params(w, b)
         g_pre = _f32(g_pre, "g_pre")
         B, D = x.shape
         if tuple(g_pre.shape) != (B, G):
@@ -323,7 +334,7 @@ class HipBackend:
                         sched=_ptr(self.schedule(rt)), win=_ptr(win_lo), win_width=win_width, g_pre=_ptr(g_pre),
                         winner=_ptr(winner), pool_param=self.pool_param(rt), pre=_ptr(pre), lse=_ptr(lse),
                         dW=_ptr(dw_buf), db=_ptr(db_buf), dX=_ptr(dx), edges=_ptr(edges),
-                        edges_bytes=edges.numel(), dz_budget=self.dz_budget(rt))
+                        edges_bytes=edges.numel(), dz_budget=self.dz_budget(rt), w_dtype=wcode)
         with torch.cuda.device(x.device):
             need = self.lib.size_query("gl_bwd_workspace", a)
             ws = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)

@@ -2,10 +2,12 @@
 
 ``LevelSpec`` / ``PoolingConfig`` / ``PhysicalPlan`` keep the reference's names, fields, defaults
 and validation (sparse_pooling/config.py:22-224, 240-421) so existing call sites construct
-them unchanged.  The MI355X path executes single-level Mean pooling with a ReLU or identity neuron activation,
+them unchanged.  The MI355X path executes every level-1 operator of the reference -- Mean,
 ``"sum"`` (Mean x n_g, BASELINE's "sum pooling"), Max, Top-K mean, LogMeanExp, power mean and
-softmax-weighted pooling; two-level hierarchies and the GELU activation parse exactly as in the
-reference but are refused by the runtime with a clear error.
+softmax-weighted -- with identity, ReLU or exact (erf) GELU neuron activations (power mean: ReLU,
+as the reference defines it), and the semantic two-level hierarchies (level 1 on the HIP kernels,
+level 2 in PyTorch).  What it does not run (Mode B block-shared records, input-supergroup
+connectivity) parses exactly as in the reference and is refused at run time with a clear error.
 """
 from __future__ import annotations
 
@@ -22,7 +24,7 @@ ACT_ID = {name: i for i, name in enumerate(ACTIVATIONS)}
 
 # operators executed by the HIP path (everything else parses but is refused at run time)
 HIP_POOLS = ("mean", "sum", "max", "topk_mean", "logmeanexp", "power_mean", "softmax_weighted")
-HIP_ACTIVATIONS = ("identity", "relu")
+HIP_ACTIVATIONS = ("identity", "relu", "gelu")
 
 _DEFAULT_ACT = {"max": "identity", "topk_mean": "identity", "mean": "relu", "logmeanexp": "identity",
                 "power_mean": "relu", "softmax_weighted": "identity", "sum": "relu"}
@@ -93,7 +95,7 @@ class LevelSpec:
         if self.type not in HIP_POOLS:
             return f"pooling {self.type!r} is not on the MI355X path (supported: {', '.join(HIP_POOLS)})"
         if self.activation not in HIP_ACTIVATIONS:
-            return f"activation {self.activation!r} is not on the MI355X path (supported: relu, identity)"
+            return f"activation {self.activation!r} is not on the MI355X path (supported: {', '.join(HIP_ACTIVATIONS)})"
         # out_activation is applied to pre by the autograd layer (torch): identity, relu and gelu
         if self.neurons_per_shard is not None and self.neurons_per_shard % 32 != 0:
             return "neurons_per_shard must be a multiple of 4*C = 32"
@@ -163,7 +165,18 @@ class PoolingConfig:
 
 
 REDUCTIONS = ("auto", "fast", "deterministic")
+# the reference's default workspace_budget (sparse_pooling/config.py); a layer built here without a
+# budget (None) uses the library's larger defaults instead, an explicit value is always honoured
 DEFAULT_WORKSPACE_BUDGET = 512 * 2**20
+
+
+def check_workspace_budget(budget):
+    """None (no budget: the library's defaults) or a positive number of bytes."""
+    if budget is None:
+        return None
+    if isinstance(budget, bool) or int(budget) != budget or int(budget) <= 0:
+        raise ValueError(f"workspace_budget must be None or a positive number of bytes (got {budget!r})")
+    return int(budget)
 
 
 @dataclass

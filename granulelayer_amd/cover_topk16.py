@@ -41,7 +41,7 @@ from torch import nn
 
 from . import _native as N
 from .autograd import Level1Runtime, SparsePoolFunction, resolve_policy
-from .config import DEFAULT_WORKSPACE_BUDGET, PhysicalPlan, PoolingConfig
+from .config import PhysicalPlan, PoolingConfig, check_workspace_budget
 
 POLICY = "Cover-TopK"
 FAN_IN = 16
@@ -260,7 +260,7 @@ class CoverTopK16Layer(nn.Module):
 
     def __init__(self, input_dim: int, hidden_dim: int, output_dim: int, slots_per_group: int, *,
                  pooling: Union[str, dict, PoolingConfig] = "mean", checkpoint_policy: str = "auto",
-                 plan: Optional[PhysicalPlan] = None, workspace_budget: int = DEFAULT_WORKSPACE_BUDGET, device=None):
+                 plan: Optional[PhysicalPlan] = None, workspace_budget: Optional[int] = None, device=None):
         super().__init__()
         if slots_per_group % 16:
             raise ValueError("slots_per_group must be a multiple of 16")
@@ -276,7 +276,7 @@ class CoverTopK16Layer(nn.Module):
         if reason:
             raise NotImplementedError(reason)
         self.plan = plan or PhysicalPlan()
-        self.workspace_budget = workspace_budget
+        self.workspace_budget = check_workspace_budget(workspace_budget)
         self.compute_dtype = torch.float32
         L = self.layout
         dev = device or "cpu"

@@ -80,6 +80,7 @@ struct BwK {
   int sps, gs;            // pool geometry (pool_base)
   int tb;                 // tokens per tile: 4, or 2 (two-token tiles; n_tiles counts those)
   int xb;                 // 4-token tiles of raw bf16 (8-byte slots; bf16 X)
+  int wbf;                // W and bias stored as bf16 (widened in the kernel)
 };
 
 // One token tile of the dW pass (LDS at xsb): recompute z, form dz = c1 * act'(z), accumulate
@@ -281,11 +282,11 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
       int d = rec_index(p.idx, n, k, K, p.rs);
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
       addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * SLOT;
-      const float wl = p.W[n * K + k];
+      const float wl = ld_param(p.W, p.wbf, n * K + k);
       w[j][ks] = valid ? wl : 0.f;
       dw[j][ks] = 0.f;
     }
-    const float bl = p.bias[n];
+    const float bl = ld_param(p.bias, p.wbf, n);
     bias[j] = valid ? bl : 0.f;
     dbv[j] = 0.f;
   }
@@ -415,6 +416,7 @@ struct DxK {
   long long NS;
   int D, S, P, U, QL, UQ, FR, cap, n_tc;
   int sps, gs;  // pool geometry (pool_base)
+  int wbf;      // W stored as bf16: the edge's weight is the half of the 32-bit word at (offset / 2) & ~3
 };
 
 // ---- dX ----------------------------------------------------------------------------------------
@@ -477,7 +479,12 @@ __device__ __forceinline__ void dx_gather(const DxK& p, const uint32_t* mask_tc,
   g.rec = rec;
   // the unit's weight and mask rows start at wave-uniform addresses (scalar registers); each lane
   // adds a 32-bit offset (< 64 KiB), so the gathers need no 64-bit vector address arithmetic
-  g.w = __uint_as_float(ld_uniform_u32(p.W + nb * K, woff));
+  if (p.wbf) {
+    const unsigned boff = woff >> 1;
+    g.w = bf16_half(ld_uniform_u32(reinterpret_cast<const unsigned short*>(p.W) + nb * K, boff & ~3u), boff);
+  } else {
+    g.w = __uint_as_float(ld_uniform_u32(p.W + nb * K, woff));
+  }
   const uint32_t* mb = mask_tc + nb * (2 * T);
   const unsigned mo = nl * (unsigned)(2 * T * 4);
   if constexpr (T == 1) {
@@ -697,13 +704,15 @@ __device__ __forceinline__ void dx_dma(const DxK& p, const uint32_t* mask_tc, co
   const long long nb = pool_base(c.u / p.P, p.S, p.sps, p.gs) + (long long)(c.u % p.P) * US;  // first neuron of the unit
   const unsigned woff = rec & REC_OFF_MASK;  // byte offset of W[n, k] in the unit
   const unsigned mo = (woff >> (K == 8 ? 5 : 6)) * 32u;  // byte offset of the neuron's mask row
-  const char* ws = uniform_ptr(p.W + nb * K);
+  // bf16 W: the 32-bit word holding the weight (its half is taken when the chunk is read)
+  const unsigned wo = p.wbf ? (woff >> 1) & ~3u : woff;
+  const char* ws = p.wbf ? uniform_ptr(reinterpret_cast<const unsigned short*>(p.W) + nb * K) : uniform_ptr(p.W + nb * K);
   const char* ms = uniform_ptr(mask_tc + nb * 8);
   const unsigned lw = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&st.w[buf][0]);
   const unsigned l0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&st.m[buf][0][0]);
   const unsigned l1 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&st.m[buf][1][0]);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, %2"
-               :: "v"(woff), "s"(lw), "s"(ws) : "memory", "m0");
+               :: "v"(wo), "s"(lw), "s"(ws) : "memory", "m0");
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
                :: "v"(mo), "s"(l0), "s"(ms) : "memory", "m0");
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
@@ -864,7 +873,8 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))
         for (int x = 1; x <= FW; ++x)
           b[x] = __builtin_amdgcn_readfirstlane((int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(f < x)));
         const unsigned* mrow = reinterpret_cast<const unsigned*>(&st.m[opaque(cur)][word >> 2][0]) + (word & 3);
-        const float wl = st.w[opaque(cur)][lane];
+        float wl = st.w[opaque(cur)][lane];
+        if (p.wbf) wl = bf16_half(__float_as_uint(wl), (rc & REC_OFF_MASK) >> 1);
         dx_runs_dma<0>(mrow, wl, st.lut, b, bit, c1, acc);
       }
       if (!more) break;
@@ -924,6 +934,7 @@ __global__ void __launch_bounds__(256) dx_reduce_kernel(const float* __restrict_
 
 // ---- smooth pools (LogMeanExp, power mean, softmax-weighted) ------------------------------------
 // Per (pool, token) coefficients (kernels/ops.py:242-262), transposed to [G][cap] like c1t:
+//   sum / mean (GELU neurons): c1 = g_pre (/ n_g for mean)
 //   LogMeanExp:       c1 = g_pre, c2 = L2 (from lse, or recovered as pre * scale + log2 n_g)
 //   power mean:       c1 = g_pre / n_g, c2 = 1 / pre (both 0 when pre <= 0)
 //   softmax-weighted: c1 = g_pre, c2 = L2, c3 = pre
@@ -952,7 +963,9 @@ __global__ void __launch_bounds__(256) coef_smooth_kernel(const float* __restric
     const float n = (float)counts[g];
     float c1 = 0.f, c2 = 0.f, c3 = 0.f;
     if (b < Bc) {
-      if (pool == GL_POOL_POWER) {
+      if (pool == GL_POOL_MEAN || pool == GL_POOL_SUM) {  // GELU neurons: c1t_kernel's c1
+        c1 = pool == GL_POOL_MEAN ? gp / n : gp;
+      } else if (pool == GL_POOL_POWER) {
         c1 = pv > 0.f ? gp / n : 0.f;
         c2 = pv > 0.f ? 1.f / pv : 0.f;
       } else {
@@ -966,10 +979,13 @@ __global__ void __launch_bounds__(256) coef_smooth_kernel(const float* __restric
   }
 }
 
-// dL/dz of one (token, neuron) of a smooth pool (triton_fused.py:364-399 _dz_from_z)
+// dL/dz of one (token, neuron) of a smooth pool (triton_fused.py:364-399 _dz_from_z), or of sum /
+// mean pooling with GELU (SM_LIN: c1 act'(z), triton_fused.py:364-374 for the mean coefficients)
 template <int OP, int ACT>
 __device__ __forceinline__ float smooth_dz(float z, float c1, float c2, float c3, float scale, float p, int pint) {
-  if constexpr (OP == SM_POW) {
+  if constexpr (OP == SM_LIN) {
+    return c1 * dact_f<ACT>(z);
+  } else if constexpr (OP == SM_POW) {
     if (!(z > 0.f)) return 0.f;
     const float q = z * c2;  // a / pre
     float qp;  // q^(p - 1)
@@ -980,8 +996,8 @@ __device__ __forceinline__ float smooth_dz(float z, float c1, float c2, float c3
     else qp = q > 0.f ? __builtin_amdgcn_exp2f((p - 1.f) * __builtin_amdgcn_logf(q)) : 0.f;
     return c1 * qp;
   } else {
-    const float a = ACT == GL_ACT_RELU ? __builtin_fmaxf(z, 0.f) : z;
-    const float da = ACT == GL_ACT_RELU ? (z > 0.f ? 1.f : 0.f) : 1.f;
+    const float a = act_f<ACT>(z);
+    const float da = dact_f<ACT>(z);
     const float pw = __builtin_amdgcn_exp2f(a * scale - c2);
     if constexpr (OP == SM_SW) return c1 * pw * (1.f + p * (a - c3)) * da;
     return c1 * pw * da;
@@ -1006,6 +1022,7 @@ struct BsK {
   float scale, pparam;
   int pint;
   int sps, gs;  // pool geometry (pool_base)
+  int wbf;      // W and bias stored as bf16 (widened in the kernel)
 };
 
 // Neuron-stationary recompute pass of a smooth pool: per token tile z, dz = c1 f(z, c2, c3), db and dW
@@ -1046,10 +1063,10 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
       int d = rec_index(p.idx, n, k, K, p.rs);
       d = (d < 0 || s >= n_g) ? 0 : (d >= p.D ? p.D - 1 : d);
       addr[j][ks] = (unsigned)d * 16u;
-      w[j][ks] = s < n_g ? p.W[n * K + k] : 0.f;
+      w[j][ks] = s < n_g ? ld_param(p.W, p.wbf, n * K + k) : 0.f;
       dw[j][ks] = 0.f;
     }
-    bias[j] = s < n_g ? p.bias[n] : 0.f;
+    bias[j] = s < n_g ? ld_param(p.bias, p.wbf, n) : 0.f;
     dbv[j] = 0.f;
   }
   const float* c1row = p.c1t + g * p.cap;
@@ -1144,7 +1161,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
 
 // dX of a smooth pool: dX[b, d] = sum over edges (n, k) -> d of dz[b, n] W[n, k], walking the
 // input-major edges like dx_kernel (one wave per feature range, unit range and token slice); per
-// edge every lane reads its T (<= 2) tokens of the neuron's dz row.  A segment's edges are sorted
+// edge every lane reads its T tokens of the neuron's dz row (T = 1, 2 or 4 for token chunks of up
+// to 64, 128 or 256 tokens; test_gpu_smooth's B = 130 case runs T = 4).  A segment's edges are sorted
 // by feature, so consecutive edges into one feature are summed in registers (a run) and the run is
 // added to that feature's sums in LDS when the feature changes: one uniform branch per run where
 // selecting one of FW register accumulators per edge cost FW * T multiply-adds and selects.
@@ -1197,8 +1215,7 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
       const int n = (int)min(e_end - e0, 64u);
       if (lane < n) {
         const unsigned rec = p.rec[e0 + lane];
-        const float wv = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.W + nb * K) +
-                                                          (rec & REC_OFF_MASK));
+        const float wv = ld_param(p.W, p.wbf, nb * K + (long long)((rec & REC_OFF_MASK) >> 2));
         st[lane] = make_uint2(rec, __float_as_uint(wv));
       }
       __syncthreads();
@@ -1291,6 +1308,11 @@ struct BwdPlan {
 // 0.29 + 0.60, 256-token chunks 0.33 + 0.52
 constexpr size_t SMOOTH_DZ_BUDGET = 8ull << 30;
 static bool is_smooth(int pool) { return pool == GL_POOL_LME || pool == GL_POOL_POWER || pool == GL_POOL_SOFTMAX; }
+// backward through a per-neuron dz (recompute pass + dense dX): the smooth pools, and sum / mean
+// pooling of GELU neurons (dz = c1 gelu'(z) is not a 0 / 1 mask times c1)
+static bool dense_dz(int pool, int act) {
+  return is_smooth(pool) || (act == GL_ACT_GELU && (pool == GL_POOL_MEAN || pool == GL_POOL_SUM));
+}
 
 static BwdPlan bwd_plan(int B, int D, int G, int S, int K, bool smooth = false, size_t dz_budget = 0) {
   BwdPlan q;
@@ -1424,12 +1446,19 @@ static int launch_bwd_smooth_k(const BsK& k, hipStream_t s) {
   return 0;
 }
 
+template <int K, int OP>
+static int launch_bwd_smooth_op(int act, const BsK& k, hipStream_t s) {
+  if (act == GL_ACT_GELU) return launch_bwd_smooth_k<K, GL_ACT_GELU, OP>(k, s);
+  if constexpr (OP == SM_LIN) return GL_ERR_UNSUPPORTED;  // relu / identity sum and mean take the mask path
+  else return act == GL_ACT_RELU ? launch_bwd_smooth_k<K, GL_ACT_RELU, OP>(k, s) : launch_bwd_smooth_k<K, GL_ACT_IDENTITY, OP>(k, s);
+}
+
 template <int K>
 static int launch_bwd_smooth_kk(int pool, int act, const BsK& k, hipStream_t s) {
   if (pool == GL_POOL_POWER) return launch_bwd_smooth_k<K, GL_ACT_RELU, SM_POW>(k, s);
-  if (pool == GL_POOL_LME)
-    return act == GL_ACT_RELU ? launch_bwd_smooth_k<K, GL_ACT_RELU, SM_LME>(k, s) : launch_bwd_smooth_k<K, GL_ACT_IDENTITY, SM_LME>(k, s);
-  return act == GL_ACT_RELU ? launch_bwd_smooth_k<K, GL_ACT_RELU, SM_SW>(k, s) : launch_bwd_smooth_k<K, GL_ACT_IDENTITY, SM_SW>(k, s);
+  if (pool == GL_POOL_LME) return launch_bwd_smooth_op<K, SM_LME>(act, k, s);
+  if (pool == GL_POOL_SOFTMAX) return launch_bwd_smooth_op<K, SM_SW>(act, k, s);
+  return launch_bwd_smooth_op<K, SM_LIN>(act, k, s);
 }
 
 template <int K, int T>
@@ -1465,8 +1494,8 @@ static bool dx_short_segments(const GlBwdArgs* a) {
 extern "C" int gl_bwd_workspace(const GlBwdArgs* a, size_t* bytes) {
   if (!a || !bytes) return GL_ERR_ARG;
   GL_TRY(check_layer(a->B, a->D, a->G, a->S, a->K, a->act, a->pool, a->X, a->idx, a->W, a->bias, a->counts,
-                     a->x_dtype));
-  const bool smooth = is_smooth(a->pool);
+                     a->x_dtype, a->w_dtype));
+  const bool smooth = dense_dz(a->pool, a->act);
   BwdPlan q = bwd_plan(a->B, a->D, a->G, a->S, a->K, smooth, a->dz_budget);
   GL_TRY(check_topk(a->pool, a->topk, a->S));
   GL_TRY(check_rec_shift(a->rec_shift, a->S, a->sched));
@@ -1496,8 +1525,8 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
   edge_layout(a->D, a->G, a->S, a->K, &h, &edge_bytes);
   if (a->edges_bytes < edge_bytes) return GL_ERR_EDGES;
   hipStream_t s = (hipStream_t)stream;
-  const bool smooth = is_smooth(a->pool);
-  if (smooth && (!a->pre && !(a->pool == GL_POOL_LME && a->lse))) return GL_ERR_ARG;  // coefficients need pre
+  const bool smooth = dense_dz(a->pool, a->act);
+  if (is_smooth(a->pool) && (!a->pre && !(a->pool == GL_POOL_LME && a->lse))) return GL_ERR_ARG;  // coefficients need pre
   if (a->pool == GL_POOL_SOFTMAX && !a->lse) return GL_ERR_ARG;
   BwdPlan q = bwd_plan(a->B, a->D, a->G, a->S, a->K, smooth, a->dz_budget);
   const int sps = a->sps > 1 ? a->sps : 1, gs = a->sps > 1 ? a->gs : a->S;  // checked by gl_bwd_workspace
@@ -1508,6 +1537,10 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
   float* part = (float*)(ws + q.xt_bytes + q.c1_bytes + q.mask_bytes);
   int32_t* wint = a->winner ? (int32_t*)(ws + q.xt_bytes + q.c1_bytes + q.mask_bytes + q.part_bytes) : nullptr;
   const char* eb = (const char*)a->edges;
+  // W and bias in their stored dtype (bf16: widened in the kernels)
+  const float* W = (const float*)a->W;
+  const float* bias = (const float*)a->bias;
+  const int wbf = a->w_dtype == GL_DTYPE_BF16;
 
   for (int b0 = 0; b0 < a->B; b0 += q.bc_max) {
     const int Bc = a->B - b0 < q.bc_max ? a->B - b0 : q.bc_max;
@@ -1527,7 +1560,7 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
       GL_TRY(launch_tile_x_bf16x4(a->X, a->sxb, a->B, a->D, b0, n_tiles, xt, s));
     else
       GL_TRY(launch_tile_x(a->X, a->sxb, a->x_dtype, a->B, a->D, b0, n_tiles * BT / tb, xt, s, tb));
-    if (smooth) {  // coefficients, recompute pass (dW, db, dz), dX from dz
+    if (smooth) {  // coefficients, recompute pass (dW, db, dz), dX from dz (smooth pools, GELU sum / mean)
       float* c2t = (float*)(ws + q.xt_bytes + q.c1_bytes + q.part_bytes);
       float* c3t = (float*)((char*)c2t + q.c1_bytes);
       float* dz = (float*)((char*)c3t + q.c1_bytes);
@@ -1539,15 +1572,17 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
                                (a->pool_param == 1.f || a->pool_param == 2.f || a->pool_param == 4.f || a->pool_param == 8.f)
                            ? (int)a->pool_param
                            : 0;
-      const BsK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, c2t, c3t, a->dW, a->db, dz, a->sched, q.n_chunks, a->D,
-                   a->S, q.cpg, n_tiles, cap, ceil_div(a->S, SCHED_WIN), a->rec_shift, scale, a->pool_param, pint,
-                   sps, gs};
+      BsK bk{xt, a->idx, W, bias, a->counts, c1t, c2t, c3t, a->dW, a->db, dz, a->sched, q.n_chunks, a->D,
+             a->S, q.cpg, n_tiles, cap, ceil_div(a->S, SCHED_WIN), a->rec_shift, scale, a->pool_param, pint,
+             sps, gs};
+      bk.wbf = wbf;
       GL_TRY(a->K == 8 ? launch_bwd_smooth_kk<8>(a->pool, a->act, bk, s) : launch_bwd_smooth_kk<16>(a->pool, a->act, bk, s));
       const long long NS = (long long)a->G * a->S;
       const int Td = T;
       DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
-             (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, nullptr, a->W, part,
+             (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, nullptr, W, part,
              NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * Td), sps, gs};
+      dk.wbf = wbf;
       GL_TRY(launch_dx_dense(a->K, Td, dk, dz, s));
       GL_LAUNCH(GL_KERNEL_DX_REDUCE, dx_reduce_kernel, dim3((unsigned)ceil_div(a->D, 32), (unsigned)ceil_div(Bc, 32)),
                 dim3(256), 0, s, part, a->dX, a->D, cap, q.Q, b0, Bc);
@@ -1565,20 +1600,23 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
                   dim3(256), 0, s, a->winner, wint, a->G, b0, Bc, cap, kpe);
         GL_CHECK_LAUNCH();
       }
-      const MaxEvKArgs ev{xt, a->idx, a->W, a->bias, a->counts, c1t, wint, a->g_pre, a->winner, a->dW, a->db, a->dX,
-                          a->D, a->G, a->S, cap, Bc, b0, kpe, a->rec_shift, a->pool == GL_POOL_TOPK_MEAN, sps, gs};
+      MaxEvKArgs ev{xt, a->idx, W, bias, a->counts, c1t, wint, a->g_pre, a->winner, a->dW, a->db, a->dX,
+                    a->D, a->G, a->S, cap, Bc, b0, kpe, a->rec_shift, a->pool == GL_POOL_TOPK_MEAN, sps, gs};
+      ev.wbf = wbf;
       GL_TRY(launch_max_events(a->K, a->act, ev, s));
       continue;
     }
     const long long NS = (long long)a->G * a->S;
-    BwK bk{xt, a->idx, a->W, a->bias, a->counts, c1t, a->dW, a->db, mask, a->sched, nullptr, q.n_chunks, NS,
+    BwK bk{xt, a->idx, W, bias, a->counts, c1t, a->dW, a->db, mask, a->sched, nullptr, q.n_chunks, NS,
            a->D, a->S, q.cpg, n_tiles * BT / tb, cap, 2 * T, ceil_div(a->S, SCHED_WIN), a->G, ww, npw, a->rec_shift,
            sps, gs, tb, xb ? 1 : 0};
+    bk.wbf = wbf;
     if (win) bk.win = a->win;
     GL_TRY(launch_bwd_w_any(a->K, a->act, bk, s));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
-           (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, a->W, part,
+           (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, W, part,
            NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * T), sps, gs};
+    dk.wbf = wbf;
     GL_TRY(launch_dx(a->K, T, dk, s, dx_short_segments(a)));
     GL_LAUNCH(GL_KERNEL_DX_REDUCE, dx_reduce_kernel, dim3((unsigned)ceil_div(a->D, 32), (unsigned)ceil_div(Bc, 32)), dim3(256), 0,
                        s, part, a->dX, a->D, cap, q.Q, b0, Bc);

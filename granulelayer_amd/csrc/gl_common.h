@@ -94,6 +94,46 @@ __device__ __forceinline__ int rec_index(const int32_t* __restrict__ idx, long l
   return idx[(n >> rs) * K + k];
 }
 
+// ---- parameters stored as fp32 or bf16 ------------------------------------------------------------
+// W and bias are read in their stored dtype and widened in the kernel (bf16 -> fp32 is exact: the
+// 16 bits become the high half of the fp32 pattern), as the reference's kernels load W[nk] and
+// widen it (triton_fused.py:257).  With bf, p points at bf16 elements.
+__device__ __forceinline__ float ld_param(const float* p, bool bf, long long i) {
+  if (bf) return __uint_as_float((unsigned)reinterpret_cast<const unsigned short*>(p)[i] << 16);
+  return p[i];
+}
+// the fp32 value of a weight whose 32-bit word w32 was loaded from byte offset (boff & ~3) of bf16
+// storage (boff = the element's byte offset): its half of the word
+__device__ __forceinline__ float bf16_half(unsigned w32, unsigned boff) {
+  return __uint_as_float((boff & 2u) ? (w32 & 0xffff0000u) : (w32 << 16));
+}
+
+// ---- the neuron activation and its derivative (triton_fused.py:29-45 _act / _dact) -------------
+// GELU is the exact (erf) form, 0.5 z (1 + erf(z / sqrt 2)), with derivative Phi(z) + z phi(z).
+// -inf (the max tile's padded-slot sentinel) stays -inf under every activation.
+template <int ACT>
+__device__ __forceinline__ float act_f(float z) {
+  if constexpr (ACT == GL_ACT_RELU) {
+    return __builtin_fmaxf(z, 0.f);
+  } else if constexpr (ACT == GL_ACT_GELU) {
+    const float g = 0.5f * z * (1.f + erff(z * 0.70710678118654752f));
+    return z == -__builtin_inff() ? z : g;
+  } else {
+    return z;
+  }
+}
+template <int ACT>
+__device__ __forceinline__ float dact_f(float z) {
+  if constexpr (ACT == GL_ACT_RELU) {
+    return z > 0.f ? 1.f : 0.f;
+  } else if constexpr (ACT == GL_ACT_GELU) {
+    const float cdf = 0.5f * (1.f + erff(z * 0.70710678118654752f));
+    return __builtin_fmaf(z * 0.39894228040143268f, expf(-0.5f * z * z), cdf);
+  } else {
+    return 1.f;
+  }
+}
+
 // Tokens of one dX wave: 64 lanes x T slots, T in {1, 2, 4}, for a chunk of B tokens.
 inline int dx_slots(int B) { return B <= 64 ? 1 : (B <= 128 ? 2 : 4); }
 inline int dx_cap(int B) { return (int)round_up(B, 64 * dx_slots(B)); }
@@ -384,6 +424,9 @@ __device__ __forceinline__ void wave_max4(float a0, float a1, float a2, float a3
 // Two states merge by rescaling to the larger m (kernels/triton_fused.py:180-222 restated as a
 // pairwise merge); an empty state has m = -inf (exp2 forms) or m = 0 (power).
 constexpr int SM_LME = 0, SM_POW = 1, SM_SW = 2;
+// the dense-dz backward of sum / mean pooling with a GELU neuron activation (dz = c1 gelu'(z), no
+// 0 / 1 mask): SM_LIN is its operator in the smooth pools' recompute kernel
+constexpr int SM_LIN = 3;
 
 // q^p for q >= 0: exact products for p in {1, 2, 4, 8} (pint), else exp2(p log2 q)
 __device__ __forceinline__ float pow_p(float q, float p, int pint) {

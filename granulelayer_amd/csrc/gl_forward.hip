@@ -106,6 +106,7 @@ struct FwdK {
   int tb;                 // tokens per tile: 4, or 2 (two-token tiles; n_tiles counts those)
   int ws_small;           // window staging in workgroups of half the waves (two per CU, 64 KiB of stages)
   int xb;                 // 4-token tiles of raw bf16 (8-byte slots; bf16 X, sum / mean)
+  int wbf;                // W and bias stored as bf16 (widened in the kernel)
 };
 
 // One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
@@ -137,12 +138,10 @@ __device__ __forceinline__ void fwd_tile(SRC xsb, const unsigned (&addr)[NPL][K]
       z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
       z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
     }
-    if (ACT == GL_ACT_RELU) {
-      z0 = __builtin_fmaxf(z0, 0.f);
-      z1 = __builtin_fmaxf(z1, 0.f);
-      z2 = __builtin_fmaxf(z2, 0.f);
-      z3 = __builtin_fmaxf(z3, 0.f);
-    }
+    z0 = act_f<ACT>(z0);
+    z1 = act_f<ACT>(z1);
+    z2 = act_f<ACT>(z2);
+    z3 = act_f<ACT>(z3);
     a0 += z0;
     a1 += z1;
     a2 += z2;
@@ -189,12 +188,10 @@ __device__ __forceinline__ void fwd_tile_bf4(const char* xsb, const unsigned (&a
       z2 = __builtin_fmaf(__uint_as_float(xc[k].y << 16), w[j][k], z2);
       z3 = __builtin_fmaf(__uint_as_float(xc[k].y & 0xffff0000u), w[j][k], z3);
     }
-    if (ACT == GL_ACT_RELU) {
-      z0 = __builtin_fmaxf(z0, 0.f);
-      z1 = __builtin_fmaxf(z1, 0.f);
-      z2 = __builtin_fmaxf(z2, 0.f);
-      z3 = __builtin_fmaxf(z3, 0.f);
-    }
+    z0 = act_f<ACT>(z0);
+    z1 = act_f<ACT>(z1);
+    z2 = act_f<ACT>(z2);
+    z3 = act_f<ACT>(z3);
     a0 += z0;
     a1 += z1;
     a2 += z2;
@@ -233,10 +230,8 @@ __device__ __forceinline__ void fwd_tile2(const char* xsb, const unsigned (&addr
       z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
       z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
     }
-    if (ACT == GL_ACT_RELU) {
-      z0 = __builtin_fmaxf(z0, 0.f);
-      z1 = __builtin_fmaxf(z1, 0.f);
-    }
+    z0 = act_f<ACT>(z0);
+    z1 = act_f<ACT>(z1);
     a0 += z0;
     a1 += z1;
     __builtin_amdgcn_sched_barrier(0);
@@ -280,12 +275,10 @@ __device__ __forceinline__ void fwd_tile_max(SRC xsb, const unsigned (&addr)[NPL
       z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
       z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
     }
-    if (ACT == GL_ACT_RELU) {
-      z0 = __builtin_fmaxf(z0, 0.f);
-      z1 = __builtin_fmaxf(z1, 0.f);
-      z2 = __builtin_fmaxf(z2, 0.f);
-      z3 = __builtin_fmaxf(z3, 0.f);
-    }
+    z0 = act_f<ACT>(z0);
+    z1 = act_f<ACT>(z1);
+    z2 = act_f<ACT>(z2);
+    z3 = act_f<ACT>(z3);
     // A lane's neurons 2i and 2i + 1 share a 128-slot window (sched_slot), later pairs lie in later
     // windows: slot[2i] exceeds every slot before it, so a strict compare keeps ties on the
     // smaller slot there; inside a pair the order is free and the full pair compare decides.
@@ -511,7 +504,7 @@ __device__ __forceinline__ void smooth_reduce(const float (&z)[NPL][4], unsigned
 #pragma unroll
       for (int j = 0; j < NPL; ++j) {
         const bool v = (vmask >> j) & 1u;
-        const float aj = ACT == GL_ACT_RELU ? __builtin_fmaxf(z[j][tk], 0.f) : z[j][tk];
+        const float aj = act_f<ACT>(z[j][tk]);
         a[j] = v ? aj : 0.f;
         u[j] = v ? aj * scale : ninf;
         mx = __builtin_fmaxf(mx, u[j]);
@@ -658,10 +651,10 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       int d = rec_index(p.idx, n, k, K, p.rs);
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
       addr[j][ks] = WS ? win_addr<SLOT>(d, pk, lo, p.ww) : (unsigned)d * SLOT;
-      const float wl = p.W[n * K + k];
+      const float wl = ld_param(p.W, p.wbf, n * K + k);
       w[j][ks] = valid ? wl : 0.f;
     }
-    const float bl = p.bias[n];
+    const float bl = ld_param(p.bias, p.wbf, n);
     bias[j] = valid ? bl : ((PK == PK_MAX || PK == PK_TOPK) ? -__builtin_inff() : 0.f);
     slot[j] = s;
     vmask |= (unsigned)valid << j;
@@ -867,7 +860,7 @@ __global__ void __launch_bounds__(256) fwd_finalize_topk_kernel(const float* __r
     }
 #pragma unroll
     for (int c = 0; c < FWD_TOPK_CPG; ++c) ptr[c] += c == best;
-    sum += ACT == GL_ACT_RELU ? __builtin_fmaxf(bv, 0.f) : bv;
+    sum += act_f<ACT>(bv);
     if (topk_slot) topk_slot[i * k + j] = bs;
   }
   if (topk_slot)
@@ -924,7 +917,7 @@ __global__ void __launch_bounds__(256) fwd_finalize_top8_kernel(const float* __r
       bc = tk ? c : bc, bv = tk ? v[c][0] : bv, bs = tk ? s[c][0] : bs;
     }
     out[j] = j < kk ? bs : -1;
-    if (j < kk) sum += ACT == GL_ACT_RELU ? __builtin_fmaxf(bv, 0.f) : bv;
+    if (j < kk) sum += act_f<ACT>(bv);
     // drop the head of the list it came from; after j + 1 picks a list is read at most up to
     // position KP - 2 - j, and a list popped p <= j times still holds valid entries to KP - 1 - p
 #pragma unroll
@@ -1108,6 +1101,7 @@ static int launch_fwd_act(int K, int D, const FwdK& k, hipStream_t s) {
 
 template <int PK>
 static int launch_fwd_any(int act, int K, int D, const FwdK& k, hipStream_t s) {
+  if (act == GL_ACT_GELU) return launch_fwd_act<GL_ACT_GELU, PK>(K, D, k, s);
   return act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU, PK>(K, D, k, s) : launch_fwd_act<GL_ACT_IDENTITY, PK>(K, D, k, s);
 }
 
@@ -1127,12 +1121,14 @@ bool window_staging(const uint32_t* win, int width, int D, int waves, int cpg, i
   return true;
 }
 
-int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const float* W,
-                const float* bias, const int32_t* counts, int x_dtype) {
+int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const void* W,
+                const void* bias, const int32_t* counts, int x_dtype, int w_dtype) {
   if (!X || !idx || !W || !bias || !counts) return GL_ERR_ARG;
+  if (w_dtype != GL_DTYPE_F32 && w_dtype != GL_DTYPE_BF16) return GL_ERR_UNSUPPORTED;
+  if (((uintptr_t)W & 3) != 0) return GL_ERR_ARG;  // the dX kernels read bf16 weights as 32-bit words
   if (B < 1 || D < 1 || G < 1 || S < 1) return GL_ERR_ARG;
   if (K != 8 && K != 16) return GL_ERR_UNSUPPORTED;
-  if (act != GL_ACT_IDENTITY && act != GL_ACT_RELU) return GL_ERR_UNSUPPORTED;
+  if (act != GL_ACT_IDENTITY && act != GL_ACT_RELU && act != GL_ACT_GELU) return GL_ERR_UNSUPPORTED;
   if (pool < GL_POOL_MEAN || pool > GL_POOL_SOFTMAX) return GL_ERR_UNSUPPORTED;
   if (x_dtype != GL_DTYPE_F32 && x_dtype != GL_DTYPE_BF16) return GL_ERR_UNSUPPORTED;
   if ((long long)G * S > (1LL << 31) / 16) return GL_ERR_UNSUPPORTED;
@@ -1187,11 +1183,12 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
     const int b_pad = (int)round_up(Bc, BT);
     float* pre = a->pre + (long long)b0 * a->G;
     int32_t* winner = a->winner ? a->winner + (long long)b0 * a->G * kpe : nullptr;
-    FwdK k{xt, a->idx, a->W, a->bias, a->counts, part, pslot, kpe, a->sched, nullptr, q.n_chunks, a->D, a->S, q.cpg,
+    FwdK k{xt, a->idx, (const float*)a->W, (const float*)a->bias, a->counts, part, pslot, kpe, a->sched, nullptr, q.n_chunks, a->D, a->S, q.cpg,
            b_pad / BT, b_pad, ceil_div(a->S, SCHED_WIN), a->G, 0, 0, a->rec_shift,
            smooth_scale(a->pool, a->pool_param), a->pool_param, smooth_pint(a->pool, a->pool_param)};
     k.sps = a->sps > 1 ? a->sps : 1;
     k.gs = a->sps > 1 ? a->gs : a->S;
+    k.wbf = a->w_dtype == GL_DTYPE_BF16;
     // sum / mean with bf16 X (even D <= 2 XTILE_DB) keeps X's bf16 values, 4 tokens per 8-byte slot,
     // in full tiles or windows: half the LDS bytes per gathered token for one exact widening per
     // value (C4 forward 81.8 -> 51.5 ms; at D = 4096 full tiles 16.4 -> 14.4 ms)
@@ -1225,11 +1222,17 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
       if (top8 && a->act == GL_ACT_RELU)
         GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_top8_kernel<GL_ACT_RELU>, g1, dim3(256), 0, s, part, pslot,
                   a->counts, pre, winner, Bc, a->G, q.cpg, b_pad);
+      else if (top8 && a->act == GL_ACT_GELU)
+        GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_top8_kernel<GL_ACT_GELU>, g1, dim3(256), 0, s, part, pslot,
+                  a->counts, pre, winner, Bc, a->G, q.cpg, b_pad);
       else if (top8)
         GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_top8_kernel<GL_ACT_IDENTITY>, g1, dim3(256), 0, s, part, pslot,
                   a->counts, pre, winner, Bc, a->G, q.cpg, b_pad);
       else if (a->act == GL_ACT_RELU)
         GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_topk_kernel<GL_ACT_RELU>, g1, dim3(256), 0, s, part, pslot,
+                  a->counts, pre, winner, Bc, a->G, q.cpg, b_pad, a->topk);
+      else if (a->act == GL_ACT_GELU)
+        GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_topk_kernel<GL_ACT_GELU>, g1, dim3(256), 0, s, part, pslot,
                   a->counts, pre, winner, Bc, a->G, q.cpg, b_pad, a->topk);
       else
         GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_topk_kernel<GL_ACT_IDENTITY>, g1, dim3(256), 0, s, part, pslot,
@@ -1271,21 +1274,26 @@ static __device__ __align__(256) unsigned char scratch[GL_FWD_STATIC_SCRATCH_BYT
 namespace {
 constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxScratchDevices];  // per device; null until resolved
+void* g_scratch_ptr[kMaxScratchDevices];       // per device; null until resolved
+hipEvent_t g_scratch_last[kMaxScratchDevices];  // per device: recorded after the last use's launches
+bool g_scratch_used[kMaxScratchDevices];
 }  // namespace
 
-// the address of this device's scratch (resolved once per device, with the device current)
-static int scratch_address(void** out) {
+// the address of this device's scratch and its "last use" event (resolved once per device, with
+// the device current); call with g_scratch_mu held
+static int scratch_address(int* dev_out, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return GL_ERR_DEVICE;
-  std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return (int)e;
     if (!p) return GL_ERR_DEVICE;
+    e = hipEventCreateWithFlags(&g_scratch_last[dev], hipEventDisableTiming);
+    if (e != hipSuccess) return (int)e;
     g_scratch_ptr[dev] = p;
   }
+  *dev_out = dev;
   *out = g_scratch_ptr[dev];
   return 0;
 }
@@ -1305,7 +1313,7 @@ using namespace gl;
 extern "C" int gl_fwd_workspace(const GlFwdArgs* a, size_t* bytes) {
   if (!a || !bytes) return GL_ERR_ARG;
   GL_TRY(check_layer(a->B, a->D, a->G, a->S, a->K, a->act, a->pool, a->X, a->idx, a->W, a->bias, a->counts,
-                     a->x_dtype));
+                     a->x_dtype, a->w_dtype));
   GL_TRY(check_topk(a->pool, a->topk, a->S));
   GL_TRY(check_rec_shift(a->rec_shift, a->S, a->sched));
   GL_TRY(check_smooth(a->pool, a->pool_param, a->act));
@@ -1335,7 +1343,28 @@ extern "C" int gl_fwd_static(const GlFwdArgs* a, void* stream) {
   if (bf < BT) return GL_ERR_SCRATCH;
   const FwdPlan q = fwd_plan(a, bf);
   if (q.xt_bytes + q.part_bytes + q.slot_bytes > (size_t)GL_FWD_STATIC_SCRATCH_BYTES) return GL_ERR_SCRATCH;
+  // Calls on one GPU share its scratch.  A call waits on the device's "last use" event before its
+  // launches and records it after them, so calls on different streams of one GPU run one after
+  // the other instead of overwriting each other's tiles.  Under graph capture the event is left
+  // alone: the captured graph's own dependencies order its nodes.
+  const hipStream_t s = (hipStream_t)stream;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  int dev = -1;
   void* ws = nullptr;
-  GL_TRY(scratch_address(&ws));
-  return fwd_run(a, ws, q, (hipStream_t)stream);
+  GL_TRY(scratch_address(&dev, &ws));
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &cap);
+  if (e != hipSuccess) return (int)e;
+  const bool order = cap == hipStreamCaptureStatusNone;
+  if (order && g_scratch_used[dev]) {
+    e = hipStreamWaitEvent(s, g_scratch_last[dev], 0);
+    if (e != hipSuccess) return (int)e;
+  }
+  GL_TRY(fwd_run(a, ws, q, s));
+  if (order) {
+    e = hipEventRecord(g_scratch_last[dev], s);
+    if (e != hipSuccess) return (int)e;
+    g_scratch_used[dev] = true;
+  }
+  return 0;
 }

@@ -10,8 +10,8 @@ size_t max_lds_bytes();
 // Raise a kernel's dynamic-LDS limit when it needs more than the 64 KiB default.
 int set_lds_limit(const void* kernel, size_t bytes);
 
-int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const float* W,
-                const float* bias, const int32_t* counts, int x_dtype);
+int check_layer(int B, int D, int G, int S, int K, int act, int pool, const void* X, const int32_t* idx, const void* W,
+                const void* bias, const int32_t* counts, int x_dtype, int w_dtype);
 
 // GL_POOL_TOPK_MEAN arguments (k, pool size); 0 for other pools
 int check_topk(int pool, int topk, int S);
@@ -67,6 +67,7 @@ struct MaxEvKArgs {
   int rs;     // log2 slots per shared index record
   bool topk;  // coef = g_pre / min(n_g, kpe) (top-k mean) instead of g_pre
   int sps, gs;  // pool geometry (pool_base)
+  int wbf;      // W and bias stored as bf16
 };
 int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s);
 

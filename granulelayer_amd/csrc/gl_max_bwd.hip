@@ -39,6 +39,7 @@ struct MaxEvK {
   bool topk;  // coef = g_pre / min(n_g, kpe)
   int sps, gs;  // pool geometry (pool_base)
   int dblk;     // dX: inputs per block (D when the token's row, bounds and accumulators fit the LDS)
+  int wbf;      // W and bias stored as bf16 (widened in the kernel)
 };
 
 // x[b, d] of the chunk's token b from the token tiles
@@ -51,16 +52,17 @@ __device__ __forceinline__ float tile_x(const float4* xt, int D, int b, int d) {
 template <int K, int ACT, typename XF>
 __device__ __forceinline__ float event_dz(const MaxEvK& p, long long n, float c1, XF xat, float (&xk)[K],
                                           float (&wk)[K], int (&dk)[K]) {
-  float z = p.bias[n];
+  float z = ld_param(p.bias, p.wbf, n);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     int d = rec_index(p.idx, n, k, K, p.rs);
     d = d < 0 ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps reads in bounds
     dk[k] = d;
-    wk[k] = p.W[n * K + k];
+    wk[k] = ld_param(p.W, p.wbf, n * K + k);
     xk[k] = xat(d);
     z = __builtin_fmaf(xk[k], wk[k], z);
   }
+  if constexpr (ACT == GL_ACT_GELU) return c1 * dact_f<ACT>(z);
   return ACT == GL_ACT_RELU ? (z > 0.f ? c1 : 0.f) : c1;
 }
 
@@ -161,8 +163,9 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
     for (int d = threadIdx.x; d < p.D; d += blockDim.x) xrow[d] = tile_x(p.xt, p.D, b, d);
   if (threadIdx.x == 0) tokmax = 0u;
   __syncthreads();
-  // pass 1: every term |dz * W[n*, k]| is at most |g_pre| * |W[n*, k]| (act' <= 1); the bits of
-  // non-negative floats order like the values, so an integer maximum is the float maximum
+  // pass 1: every term |dz * W[n*, k]| is at most |g_pre| * |W[n*, k]| * max |act'| (1 for
+  // identity and relu, < 1.13 for GELU, bounded by 2 below); the bits of non-negative floats order
+  // like the values, so an integer maximum is the float maximum
   float m = 0.f;
   for (int e = threadIdx.x; e < p.G * p.kpe; e += blockDim.x) {
     const int g = e / p.kpe;
@@ -171,14 +174,15 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
     const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
     float wm = 0.f;
 #pragma unroll
-    for (int k = 0; k < K; ++k) wm = __builtin_fmaxf(wm, __builtin_fabsf(p.W[n * K + k]));
+    for (int k = 0; k < K; ++k) wm = __builtin_fmaxf(wm, __builtin_fabsf(ld_param(p.W, p.wbf, n * K + k)));
     m = __builtin_fmaxf(m, __builtin_fabsf(p.g_pre[row + g]) * wm);
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
   if ((threadIdx.x & 63) == 0) atomicMax(&tokmax, __float_as_uint(m));
   __syncthreads();
-  const double bound = (double)__uint_as_float(tokmax) * ((double)p.G * (double)p.kpe * (double)K);
+  const double bound = (double)__uint_as_float(tokmax) * ((double)p.G * (double)p.kpe * (double)K) *
+                       (ACT == GL_ACT_GELU ? 2.0 : 1.0);
   const int e2 = bound > 0.0 ? (int)((__double_as_longlong(bound) >> 52) & 0x7ff) - 1023 : 0;
   const int sh = 61 - e2 + 32;
   const double scale = pow2(sh), unscale = pow2(-sh);
@@ -268,7 +272,8 @@ int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s) {
   int npow2 = 1;
   while (npow2 < tsub * a.kpe) npow2 <<= 1;
   const MaxEvK k{a.xt, a.idx, a.W, a.bias, a.counts, a.c1t, a.wint, a.g_pre, a.winner, a.dW, a.db, a.dX,
-                 a.D, a.G, a.S, a.cap, a.Bc, a.b0, npow2, a.kpe, tsub, a.rs, a.topk, a.sps, a.gs, a.D};
+                 a.D, a.G, a.S, a.cap, a.Bc, a.b0, npow2, a.kpe, tsub, a.rs, a.topk, a.sps, a.gs, a.D, a.wbf};
+  if (act == GL_ACT_GELU) return K == 8 ? launch_max_events_k<8, GL_ACT_GELU>(k, s) : launch_max_events_k<16, GL_ACT_GELU>(k, s);
   if (K == 8) return act == GL_ACT_RELU ? launch_max_events_k<8, GL_ACT_RELU>(k, s) : launch_max_events_k<8, GL_ACT_IDENTITY>(k, s);
   return act == GL_ACT_RELU ? launch_max_events_k<16, GL_ACT_RELU>(k, s) : launch_max_events_k<16, GL_ACT_IDENTITY>(k, s);
 }

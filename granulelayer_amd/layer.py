@@ -18,7 +18,7 @@ from torch import nn
 
 from .autograd import Level1Runtime, SparsePoolFunction, resolve_policy
 from .semantic import SemanticPoolFunction
-from .config import DEFAULT_WORKSPACE_BUDGET, PhysicalPlan, PoolingConfig
+from .config import PhysicalPlan, PoolingConfig, check_workspace_budget
 from .layout import SparseLayout, check_indices, init_parameters
 
 
@@ -37,7 +37,7 @@ class SparsePoolingLayer(nn.Module):
         checkpoint_policy: str = "auto",
         dtype: torch.dtype = torch.bfloat16,
         plan: Optional[PhysicalPlan] = None,
-        workspace_budget: int = DEFAULT_WORKSPACE_BUDGET,
+        workspace_budget: Optional[int] = None,
         device=None,
         seed: int = 0,
         bias_std: float = 0.0,
@@ -65,7 +65,9 @@ class SparsePoolingLayer(nn.Module):
         self.compute_dtype = dtype
         self.plan = plan or PhysicalPlan()
         self.backend_name = backend
-        self.workspace_budget = workspace_budget
+        # None: the library's own defaults (8 GiB of forward partials, 64 GiB of smooth-pool dz);
+        # any explicit value, the reference's 512 MiB default included, bounds both workspaces
+        self.workspace_budget = check_workspace_budget(workspace_budget)
         self.connectivity = None
         idx, w, b = init_parameters(self.layout, device or "cpu", dtype=dtype, seed=seed, bias_std=bias_std)
         self.register_buffer("indices", idx)

@@ -21,8 +21,8 @@ from typing import Dict, List
 
 import torch
 
-from .autograd import (Level1Runtime, _compute_operands, _grad_buffers, _level1_backward, _saved_stats, act_torch,
-                       fit_policy)
+from .autograd import (CHECKPOINT_BUDGET, Level1Runtime, _compute_operands, _grad_buffers, _ids_per_token,
+                       _level1_backward, _saved_stats, act_torch, fit_policy)
 from .config import LevelSpec, PoolingConfig
 
 
@@ -134,9 +134,13 @@ class SemanticPoolFunction(torch.autograd.Function):
         l1 = rt.level
         xc, wc, bc = _compute_operands(x, w, b, ctx.compute_dtype)
         rebuilt = "pre" not in saved
-        if rebuilt:  # level1_checkpoint="recompute": rebuild the level-1 features
-            saved.update(rt.forward(xc, wc, bc))
         B = x.shape[0]
+        if rebuilt:
+            # level1_checkpoint="recompute": rebuild the level-1 features, with the selected slots a
+            # max / top-k level 1 needs when they fit the checkpoint budget (otherwise the level-1
+            # backward recomputes them one token chunk at a time)
+            track = l1.type in ("max", "topk_mean") and B * _ids_per_token(rt) * 4 <= CHECKPOINT_BUDGET
+            saved.update(rt.forward(xc, wc, bc, track_ids=track))
         G, S = rt.layout.groups, rt.units.S
         pre = saved["pre"]
         with torch.enable_grad():

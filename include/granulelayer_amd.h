@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 11
+#define GL_ABI_VERSION 12
 
 enum {
   GL_OK = 0,
@@ -44,7 +44,9 @@ enum {
  * D <= 4096 stages two token tiles in LDS, D <= 10112 one; wider layers gather X from the token
  * tiles in global memory (same results). */
 #define GL_MAX_INPUTS 65536
-enum { GL_ACT_IDENTITY = 0, GL_ACT_RELU = 1 };
+/* neuron activation: identity, relu, exact (erf) GELU 0.5 z (1 + erf(z / sqrt 2)) (the reference's
+ * ACTIVATIONS and _act / _dact, sparse_pooling/config.py:33, kernels/triton_fused.py:29-45) */
+enum { GL_ACT_IDENTITY = 0, GL_ACT_RELU = 1, GL_ACT_GELU = 2 };
 /* max: pytorch_reference.py:61-67 (winner = first maximum of act(z) over the pool's valid
  * slots), merged as kernels/ops.py:189-195; top-k mean: pytorch_reference.py:68-77 (the k largest
  * raw z, ties to the smaller slot, mean of act(z) over min(n_g, k) of them), ops.py:212-228 */
@@ -77,8 +79,8 @@ typedef struct GlFwdArgs {
                              (sps - 1) * S < gs <= sps * S; tensors below indexed by neuron then have
                              G / sps * gs rows instead of G*S, and rec_shift must be 0 */
   const int32_t* idx;     /* [G*S >> rec_shift, K] input indices in [0, D) */
-  const float* W;         /* [G*S, K] */
-  const float* bias;      /* [G*S] */
+  const void* W;          /* [G*S, K], dtype w_dtype (4-byte aligned) */
+  const void* bias;       /* [G*S], dtype w_dtype */
   const int32_t* counts;  /* [G] valid neurons per pool, 1 <= counts[g] <= S (and inside its group) */
   const uint32_t* sched;  /* gather schedule from gl_sched_build_host (K = 8), or NULL */
   const uint32_t* win;    /* [G] first input of each pool's window (gl_window_build_host), or NULL */
@@ -97,6 +99,9 @@ typedef struct GlFwdArgs {
                              forward runs over token chunks whose partials fit it, so the workspace
                              stays bounded as B grows (the reference keeps its split states within
                              workspace_budget, sparse_pooling/kernels/ops.py:82-98) */
+  int32_t w_dtype;        /* W and bias: GL_DTYPE_F32, or GL_DTYPE_BF16 read and widened in the kernels
+                             (the reference's kernels load W in its stored dtype and widen it,
+                             sparse_pooling/kernels/triton_fused.py:257) */
 } GlFwdArgs;
 
 /* Backward arguments.  Replaces the reference's BwdArgs + sp_bwd (sparse_pool_bwd.cuh:45-66,
@@ -112,8 +117,8 @@ typedef struct GlBwdArgs {
   int32_t rec_shift;      /* as GlFwdArgs.rec_shift */
   int32_t sps, gs;        /* as GlFwdArgs.sps / gs */
   const int32_t* idx;
-  const float* W;
-  const float* bias;
+  const void* W;          /* as GlFwdArgs.W / bias (dtype w_dtype) */
+  const void* bias;
   const int32_t* counts;
   const uint32_t* sched;  /* gather schedule from gl_sched_build_host (K = 8), or NULL */
   const uint32_t* win;    /* as GlFwdArgs.win / win_width */
@@ -138,6 +143,7 @@ typedef struct GlBwdArgs {
                              64 to 1024 tokens, at least 64 whatever the budget; larger chunks run
                              fewer recompute and dX passes per token (the workspace query includes
                              it).  dW / db sum over the chunks, so their rounding depends on it */
+  int32_t w_dtype;        /* as GlFwdArgs.w_dtype; dW and db are fp32 whatever it is */
 } GlBwdArgs;
 
 /* Input-major (transposed) edge list of a layer, built once per index tensor.  It has no
@@ -225,8 +231,10 @@ int gl_fwd(const GlFwdArgs* a, void* stream);
  * call on that GPU until the process ends); a->ws, a->ws_bytes are ignored.  The forward runs as
  * many token passes as the array needs, with the results of gl_fwd; layers whose partials for one
  * 4-token tile exceed the array are refused with GL_ERR_SCRATCH.  Every call on a GPU shares that
- * GPU's array: calls that overlap on one GPU (different streams, different threads) race and must
- * be serialized by the caller.  Nothing in it needs zeroing between calls. */
+ * GPU's array.  Outside graph capture, calls on different streams of one GPU are ordered by a
+ * per-device "last use" event (each call's launches wait for the previous call's); under graph
+ * capture the caller's graph must order the calls that share a GPU, or they race.  Nothing in it
+ * needs zeroing between calls. */
 #define GL_FWD_STATIC_SCRATCH_BYTES (64u << 20)
 int gl_fwd_static(const GlFwdArgs* a, void* stream);
 

@@ -10,7 +10,7 @@
  *   z[b,n]  = sum_k x[b, idx[n,k]] * w[n,k] + bias[n]
  *             sparse_pooling/reference/pytorch_reference.py:29-47 (Mode-A branch :43-46),
  *             sparse_pooling/kernels/triton_fused.py:253-264 (_tile_z Mode A)
- *   a       = act(z)                 pytorch_reference.py:19-26 (identity | relu)
+ *   a       = act(z)                 pytorch_reference.py:19-26 (identity | relu | exact GELU)
  *   pre[b,g]= scale_g * sum_{s < n_g} a[b, g*S+s]
  *             mean: scale_g = 1/n_g   pytorch_reference.py:78-79, kernels/ops.py:198-199
  *             sum : scale_g = 1       (mean * n_g; BASELINE's "sum pooling")
@@ -53,8 +53,16 @@
 #include <stdlib.h>
 #include <string.h>
 
-static inline double act_f(double z, int act) { return act == 1 ? (z > 0.0 ? z : 0.0) : z; }
-static inline double dact_f(double z, int act) { return act == 1 ? (z > 0.0 ? 1.0 : 0.0) : 1.0; }
+/* act 0 identity, 1 relu, 2 exact (erf) GELU: 0.5 z (1 + erf(z / sqrt 2)), derivative
+ * Phi(z) + z phi(z) (triton_fused.py:29-45 _act / _dact, pytorch_reference.py:19-26 F.gelu) */
+static inline double act_f(double z, int act) {
+  if (act == 2) return 0.5 * z * (1.0 + erf(z * 0.70710678118654752440));
+  return act == 1 ? (z > 0.0 ? z : 0.0) : z;
+}
+static inline double dact_f(double z, int act) {
+  if (act == 2) return 0.5 * (1.0 + erf(z * 0.70710678118654752440)) + z * 0.39894228040143267794 * exp(-0.5 * z * z);
+  return act == 1 ? (z > 0.0 ? 1.0 : 0.0) : 1.0;
+}
 
 /* Pre-activation of neuron n for token row xb (float64 accumulation in k order); *mag receives
  * sum_k |x w| + |bias|, the scale of the fp32 rounding error of z. */
@@ -72,7 +80,8 @@ static inline double neuron_z(const float* xb, const int32_t* idx, const float* 
 
 /*
  * Forward.  x [B, D] fp32 (bf16 inputs are widened exactly by the caller); idx/w [G*S, K];
- * bias [G*S]; counts [G]; pool 0 = mean, 1 = sum (max: glo_forward_max_f64); act 0 = identity, 1 = relu.
+ * bias [G*S]; counts [G]; pool 0 = mean, 1 = sum (max: glo_forward_max_f64); act 0 = identity, 1 = relu,
+ * 2 = GELU.
  * pre [B, G] float64.  mag (optional, [B, G]): scale_g * sum_s (sum_k |x w| + |bias|), the
  * magnitude the rounding error of an fp32 evaluation of pre is proportional to.
  */

@@ -305,7 +305,7 @@ def adam_bf16(p_bits, g, m, v, lr, b1, b2, eps, wd, step, moments_bf16=False, ma
                           bc2, int(moments_bf16), int(stochastic), seed)
 
 
-_ACT = {"identity": 0, "relu": 1}
+_ACT = {"identity": 0, "relu": 1, "gelu": 2}
 _POOL = {"mean": 0, "sum": 1, "max": 2}
 
 

@@ -147,3 +147,46 @@ def test_pool_geometry_is_validated_by_the_size_queries():
     assert q(3, 600, G=16) == -1  # G not a multiple of sps
     assert q(-1, 0) == -1
     assert q(2, 384, S=256, rec_shift=4) == -2  # shared index records are not sharded
+
+
+def test_an_explicit_workspace_budget_is_honoured():
+    """workspace_budget=None leaves the library its defaults (8 GiB of forward partials, 64 GiB of
+    smooth-pool dz); any explicit value, the reference's own 512 MiB default included, is what the
+    launches are given, and it bounds gl_bwd_workspace of a smooth pool at the C2 shape.  Host-side
+    only (CPU runtime objects, placeholder pointers never dereferenced)."""
+    import torch
+
+    from granulelayer_amd import backend as BK
+    from granulelayer_amd.autograd import Level1Runtime
+    from granulelayer_amd.config import DEFAULT_WORKSPACE_BUDGET, LevelSpec, PhysicalPlan
+    from granulelayer_amd.layout import SparseLayout
+
+    L = SparseLayout(256, 4096, 4, 8, 8, False)
+    idx = torch.zeros(L.index_shape, dtype=torch.int32)
+    lv = LevelSpec(type="logmeanexp")
+    default = Level1Runtime(L, idx, lv, PhysicalPlan())
+    explicit = Level1Runtime(L, idx, lv, PhysicalPlan(), workspace_budget=DEFAULT_WORKSPACE_BUDGET)
+    assert BK.HipBackend.part_budget(default) == 0 and BK.HipBackend.dz_budget(default) == BK.DZ_BUDGET
+    assert BK.HipBackend.part_budget(explicit) == DEFAULT_WORKSPACE_BUDGET
+    assert BK.HipBackend.dz_budget(explicit) == DEFAULT_WORKSPACE_BUDGET
+    for bad in (0, -1, 1.5, True):
+        with pytest.raises(ValueError):
+            Level1Runtime(L, idx, lv, PhysicalPlan(), workspace_budget=bad)
+
+    lib = N.library()
+    out = ctypes.c_size_t()
+
+    def bwd_ws(dz_budget, B=1024):
+        # 1,048,576 neurons: 4 MiB of dz per token
+        a = N.GlBwdArgs(X=16, idx=16, W=16, bias=16, counts=16, g_pre=16, pre=16, lse=16, dW=16, db=16, dX=16,
+                        edges=16, B=B, D=1024, G=4096, S=256, K=8, act=N.GL_ACT["identity"],
+                        pool=N.GL_POOL["logmeanexp"], pool_param=1.0, dz_budget=dz_budget)
+        assert lib.lib.gl_bwd_workspace(ctypes.byref(a), ctypes.byref(out)) == 0
+        return out.value
+
+    big, small = bwd_ws(BK.DZ_BUDGET), bwd_ws(DEFAULT_WORKSPACE_BUDGET)
+    # 1024-token chunks (4 GiB of dz) without a budget, 128-token chunks (512 MiB) with 512 MiB;
+    # the rest of the workspace (X tiles, coefficients, dX partials) scales with the chunk too
+    assert big - small >= (1024 - 128) * (4 << 20)
+    assert small - bwd_ws(DEFAULT_WORKSPACE_BUDGET, B=128) < (1 << 20)  # B = 128: the same one chunk
+    assert bwd_ws(DEFAULT_WORKSPACE_BUDGET // 2) < small

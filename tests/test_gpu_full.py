@@ -246,3 +246,35 @@ def test_selection_backward_over_the_checkpoint_budget(pooling, monkeypatch):
     assert_parity(x.grad.cpu().numpy(), wdX, mX, what="dx")
     assert_parity(lay.weight.grad.cpu().numpy().reshape(-1, K), wdW, mW, what="dW")
     assert_parity(lay.bias.grad.cpu().numpy().reshape(-1), wdb, mb, what="db")
+
+
+def test_adam_at_the_c4_size_matches_the_oracle_on_a_sample():
+    """gl_adam over C4's 805,306,368-element weight stream (3.2 GB per array, byte offsets past 2^31
+    and 2^32): two steps, then a seeded sample of elements -- the first and last 4096, 4096 around
+    element 2^29 (byte 2^31) and 2^30 (byte 2^32), 65,536 random -- against oracle.adam on the same
+    elements (the update is elementwise, so a sample evolves on its own)."""
+    from granulelayer_amd.backend import HipBackend
+    from oracle import oracle as O
+
+    n = 805_306_368
+    gen = torch.Generator(device=DEV).manual_seed(21)
+    p = torch.randn(n, generator=gen, device=DEV)
+    m = torch.randn(n, generator=gen, device=DEV) * 0.01
+    v = torch.rand(n, generator=gen, device=DEV) * 1e-4
+    rng = np.random.default_rng(5)
+    parts = [np.arange(4096), np.arange(n - 4096, n), np.arange((1 << 29) - 2048, (1 << 29) + 2048),
+             np.arange((1 << 30) - 2048, (1 << 30) + 2048), rng.integers(0, n, 65536)]
+    sample = torch.as_tensor(np.unique(np.concatenate(parts)), device=DEV)
+    po, mo, vo = (t[sample].cpu().numpy().copy() for t in (p, m, v))
+    be = HipBackend.get()
+    for t in (1, 2):
+        g = torch.randn(n, generator=gen, device=DEV)
+        go = g[sample].cpu().numpy().copy()
+        be.adam(p, g, m, v, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1 - 0.9 ** t, 1 - 0.999 ** t)
+        O.adam(po, go, mo, vo, 1e-3, 0.9, 0.999, 1e-8, 0.01, t)
+        assert float(g[sample].abs().max()) == 0.0 and float(g[-4096:].abs().max()) == 0.0, "fused zero_grad"
+        del g
+    for name, got, want in (("p", p, po), ("m", m, mo), ("v", v, vo)):
+        gs = got[sample].cpu().numpy()
+        assert_close(gs, want, what=f"adam {name} (C4 size, sampled)")
+        print(f"adam C4 size {name}: {(gs == want).mean() * 100:.3f}% of the sample bitwise equal to the oracle")

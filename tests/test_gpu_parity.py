@@ -52,7 +52,8 @@ FWD_CASES = [
 
 
 @pytest.mark.parametrize("case", FWD_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
-@pytest.mark.parametrize("pool,act", [("mean", "relu"), ("sum", "relu"), ("mean", "identity"), ("sum", "identity")])
+@pytest.mark.parametrize("pool,act", [("mean", "relu"), ("sum", "relu"), ("mean", "identity"), ("sum", "identity"),
+                                      ("mean", "gelu"), ("sum", "gelu")])
 def test_forward_matches_oracle(case, pool, act):
     D, H, G, K, B, xdt = case
     L, idx, w, b, x, _ = make_case(D, H, G, K, B, x_dtype=xdt)
@@ -76,7 +77,8 @@ BWD_CASES = [
 
 
 @pytest.mark.parametrize("case", BWD_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
-@pytest.mark.parametrize("pool,act", [("mean", "relu"), ("sum", "relu"), ("sum", "identity")])
+@pytest.mark.parametrize("pool,act", [("mean", "relu"), ("sum", "relu"), ("sum", "identity"), ("mean", "gelu"),
+                                      ("sum", "gelu")])
 def test_backward_matches_oracle(case, pool, act):
     D, H, G, K, B, xdt = case
     L, idx, w, b, x, dy = make_case(D, H, G, K, B, x_dtype=xdt)
@@ -407,7 +409,7 @@ def _max_oracle(L, idx, w, b, x, act):
 
 
 @pytest.mark.parametrize("case", MAX_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
-@pytest.mark.parametrize("act", ["identity", "relu"])
+@pytest.mark.parametrize("act", ["identity", "relu", "gelu"])
 def test_max_forward_matches_oracle(case, act):
     D, H, G, K, B, xdt = case
     L, idx, w, b, x, _ = make_case(D, H, G, K, B, x_dtype=xdt)
@@ -430,7 +432,7 @@ def test_max_forward_matches_oracle(case, act):
 
 
 @pytest.mark.parametrize("case", MAX_CASES[:4], ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
-@pytest.mark.parametrize("act", ["identity", "relu"])
+@pytest.mark.parametrize("act", ["identity", "relu", "gelu"])
 def test_max_backward_matches_oracle(case, act):
     D, H, G, K, B, xdt = case
     L, idx, w, b, x, dy = make_case(D, H, G, K, B, x_dtype=xdt)
@@ -505,7 +507,8 @@ def _runtime_topk(L, idx, act, k):
 
 
 @pytest.mark.parametrize("case", TOPK_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
-@pytest.mark.parametrize("act,k", [("identity", 1), ("identity", 8), ("relu", 8), ("identity", 64)])
+@pytest.mark.parametrize("act,k", [("identity", 1), ("identity", 8), ("relu", 8), ("identity", 64), ("gelu", 8),
+                                   ("gelu", 16)])
 def test_topk_forward_matches_oracle(case, act, k):
     D, H, G, K, B, xdt = case
     L, idx, w, b, x, _ = make_case(D, H, G, K, B, x_dtype=xdt)
@@ -528,7 +531,7 @@ def test_topk_forward_matches_oracle(case, act, k):
 
 
 @pytest.mark.parametrize("case", TOPK_CASES[:3], ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}{str(c[5])[6:]}")
-@pytest.mark.parametrize("act,k", [("identity", 8), ("relu", 4), ("identity", 64)])
+@pytest.mark.parametrize("act,k", [("identity", 8), ("relu", 4), ("identity", 64), ("gelu", 8)])
 def test_topk_backward_matches_oracle(case, act, k):
     """The selection events of the HIP forward, checked against the oracle's backward of the same
     selection (which equals its top-k backward, test_oracle.py), plus determinism."""

@@ -85,7 +85,14 @@ def test_two_level_layer_matches_oracle(l1, l2, ckpt):
     x = torch.randn(32, 64, generator=gen).to(DEV).requires_grad_(True)
     dy = torch.randn(32, 8, generator=gen).to(DEV)
     y = lay(x)
+    # the backward reruns level 1 once under "recompute" (with the selected slots a max / top-k
+    # level 1 needs) and never under "save"
+    rt, calls = lay._runtime(), []
+    fwd = rt.forward
+    rt.forward = lambda *a, **k: (calls.append(k.get("track_ids", False)), fwd(*a, **k))[1]
     (y * dy).sum().backward()
+    del rt.forward
+    assert len(calls) == (1 if ckpt == "recompute" else 0), calls
     wy, wdW, wdb, wdX, wdt = _oracle_two_level(lay, x, dy)
     K = lay.layout.fan_in
     got = {"y": y.detach(), "dX": x.grad, "dW": lay.weight.grad.reshape(-1, K), "db": lay.bias.grad.reshape(-1)}

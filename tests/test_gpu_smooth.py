@@ -21,13 +21,14 @@ from oracle import oracle as O  # noqa: E402
 DEV = "cuda"
 
 OPS = [("logmeanexp", 1.0, "identity"), ("logmeanexp", 0.5, "relu"), ("power_mean", 2.0, "relu"),
-       ("power_mean", 3.0, "relu"), ("softmax_weighted", 1.0, "identity"), ("softmax_weighted", 2.0, "relu")]
+       ("power_mean", 3.0, "relu"), ("softmax_weighted", 1.0, "identity"), ("softmax_weighted", 2.0, "relu"),
+       ("logmeanexp", 0.7, "gelu"), ("softmax_weighted", 1.5, "gelu")]
 CASES = [
     # D, H, G, K, B, x dtype
     (64, 3000, 8, 8, 37, torch.float32),
     (1024, 20011, 16, 8, 64, torch.bfloat16),
     (96, 5000, 7, 16, 33, torch.float32),
-    (1024, 65536, 64, 8, 130, torch.float32),
+    (1024, 65536, 64, 8, 130, torch.float32),  # one 130-token chunk: the dense dX at 4 tokens per lane
 ]
 
 

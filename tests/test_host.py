@@ -88,7 +88,10 @@ def test_config_parsing_matches_reference_semantics():
     assert LevelSpec("mean", neurons_per_shard=64).hip_reason() == ""  # level-1 shards of two-level pooling
     assert LevelSpec("mean", neurons_per_shard=48).hip_reason()  # not a multiple of 4*C = 32
     assert LevelSpec("mean", out_activation="gelu").hip_reason() == ""  # applied to pre in torch
-    assert LevelSpec("mean", activation="gelu").hip_reason()  # the neuron activation runs in the kernels
+    for t in ("mean", "sum", "max", "topk_mean", "logmeanexp", "softmax_weighted"):  # GELU neurons run in the kernels
+        assert LevelSpec(t, activation="gelu").hip_reason() == ""
+    with pytest.raises(ValueError):
+        LevelSpec("power_mean", activation="gelu")  # the reference defines the power mean on relu only
     with pytest.raises(ValueError):
         LevelSpec("topk_mean", k=3)
     with pytest.raises(ValueError):
@@ -98,8 +101,7 @@ def test_config_parsing_matches_reference_semantics():
 
 @pytest.mark.parametrize("kwargs,exc", [
     (dict(shared_neurons=8, pooling="mean"), NotImplementedError),
-    (dict(shared_neurons=None, pooling={"type": "mean", "activation": "gelu"}), NotImplementedError),
-    (dict(shared_neurons=None, pooling={"type": "mean", "activation": "gelu"}), NotImplementedError),
+    (dict(shared_neurons=None, pooling="mean", connectivity=object()), NotImplementedError),
     (dict(shared_neurons=None, pooling="mean", backend="triton"), ValueError),
     (dict(shared_neurons=None, pooling="mean", weight_layout="packed"), ValueError),
 ])

@@ -31,6 +31,15 @@ def random_problem(rng, B, D, G, S, K, ragged=True, bias_std=0.3):
     return x, idx, w, b, counts
 
 
+def _act(z, act):
+    """The neuron activation through torch's own ops: relu, exact (erf) GELU, identity."""
+    if act == "relu":
+        return torch.relu(z)
+    if act == "gelu":
+        return torch.nn.functional.gelu(z, approximate="none")
+    return z
+
+
 def dense_forward(x, idx, w, b, counts, S, act, pool):
     """float64 torch formulation through a dense [N, D] weight matrix and torch.matmul."""
     x = torch.as_tensor(x, dtype=torch.float64)
@@ -42,13 +51,13 @@ def dense_forward(x, idx, w, b, counts, S, act, pool):
     Wd.scatter_(1, torch.as_tensor(idx, dtype=torch.int64), torch.as_tensor(w, dtype=torch.float64))
     Wd = Wd * valid[:, None]
     z = torch.matmul(x, Wd.T) + torch.as_tensor(b, dtype=torch.float64) * valid
-    a = torch.relu(z) if act == "relu" else z
+    a = _act(z, act)
     a = a * valid
     s = a.reshape(x.shape[0], G, S).sum(-1)
     return s / torch.as_tensor(counts, dtype=torch.float64) if pool == "mean" else s
 
 
-@pytest.mark.parametrize("act", ["relu", "identity"])
+@pytest.mark.parametrize("act", ["relu", "identity", "gelu"])
 @pytest.mark.parametrize("pool", ["mean", "sum"])
 @pytest.mark.parametrize("B,D,G,S,K", [(3, 16, 2, 32, 8), (5, 40, 3, 64, 8), (2, 64, 2, 32, 16)])
 def test_forward_matches_dense_gemm(oracle, act, pool, B, D, G, S, K):
@@ -107,7 +116,7 @@ def test_mean_is_sum_over_count_and_padding_is_masked(oracle):
     assert np.array_equal(oracle.forward(x, idx2, w2, b2, counts, S, "relu", "sum"), s)
 
 
-@pytest.mark.parametrize("act", ["relu", "identity"])
+@pytest.mark.parametrize("act", ["relu", "identity", "gelu"])
 @pytest.mark.parametrize("pool", ["mean", "sum"])
 def test_backward_matches_autograd(oracle, act, pool):
     rng = np.random.default_rng(4)
@@ -123,7 +132,7 @@ def test_backward_matches_autograd(oracle, act, pool):
     bt = torch.tensor(b, dtype=torch.float64, requires_grad=True)
     Wd = torch.zeros(N, D, dtype=torch.float64).scatter(1, torch.as_tensor(idx, dtype=torch.int64), wt)
     z = torch.matmul(xt, (Wd * valid[:, None]).T) + bt * valid
-    a = (torch.relu(z) if act == "relu" else z) * valid
+    a = (_act(z, act)) * valid
     s = a.reshape(B, G, S).sum(-1)
     y = s / torch.as_tensor(counts, dtype=torch.float64) if pool == "mean" else s
     (y * torch.as_tensor(dy, dtype=torch.float64)).sum().backward()
@@ -144,14 +153,14 @@ def dense_z(x, idx, w, b, counts, S):
     return z.reshape(x.shape[0], G, S), valid
 
 
-@pytest.mark.parametrize("act", ["identity", "relu"])
+@pytest.mark.parametrize("act", ["identity", "relu", "gelu"])
 @pytest.mark.parametrize("B,D,G,S,K", [(4, 16, 3, 32, 8), (3, 40, 2, 64, 16)])
 def test_forward_max_matches_torch_argmax(oracle, act, B, D, G, S, K):
     # pytorch_reference.py:61-67: am = where(mask, act(z), -inf); winner = argmax (first maximum)
     rng = np.random.default_rng(11)
     x, idx, w, b, counts = random_problem(rng, B, D, G, S, K)
     z, valid = dense_z(x, idx, w, b, counts, S)
-    a = torch.relu(z) if act == "relu" else z
+    a = _act(z, act)
     am = torch.where(valid[None], a, torch.tensor(float("-inf"), dtype=torch.float64))
     want_pre, want_win = am.max(-1).values.numpy(), am.argmax(-1).numpy()
     pre, win, gap = oracle.forward_max(x, idx, w, b, counts, S, act)
@@ -176,7 +185,7 @@ def test_forward_max_ties_go_to_the_smaller_slot(oracle):
     assert pre[0, 0] == 0.0 and win[0, 0] == 0
 
 
-@pytest.mark.parametrize("act", ["identity", "relu"])
+@pytest.mark.parametrize("act", ["identity", "relu", "gelu"])
 def test_backward_max_matches_autograd(oracle, act):
     # the gradient reaches only the winner (autograd of am.gather(winner), pytorch_reference.py:61-67)
     rng = np.random.default_rng(12)
@@ -187,7 +196,7 @@ def test_backward_max_matches_autograd(oracle, act):
     wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
     bt = torch.tensor(b, dtype=torch.float64, requires_grad=True)
     z = (xt[:, torch.as_tensor(idx, dtype=torch.int64)] * wt).sum(-1) + bt  # [B, N]
-    a = torch.relu(z) if act == "relu" else z
+    a = _act(z, act)
     valid = (torch.arange(S)[None, :] < torch.as_tensor(counts)[:, None]).reshape(-1)
     am = torch.where(valid[None], a, torch.tensor(float("-inf"), dtype=torch.float64)).reshape(B, G, S)
     win = am.detach().argmax(-1, keepdim=True)
@@ -207,7 +216,7 @@ def _topk_reference(x, idx, w, b, counts, S, k, act):
     wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
     bt = torch.tensor(b, dtype=torch.float64, requires_grad=True)
     z = ((xt[:, torch.as_tensor(idx, dtype=torch.int64)] * wt).sum(-1) + bt).reshape(B, G, S)
-    a = torch.relu(z) if act == "relu" else z
+    a = _act(z, act)
     mask = (torch.arange(S)[None, :] < torch.as_tensor(counts)[:, None])[None].expand_as(z)
     count = mask.sum(-1).to(z.dtype)
     zm = torch.where(mask, z, torch.tensor(float("-inf"), dtype=torch.float64))
@@ -219,7 +228,7 @@ def _topk_reference(x, idx, w, b, counts, S, k, act):
     return pooled, torch.where(sel_valid, order, torch.full_like(order, -1)), (xt, wt, bt)
 
 
-@pytest.mark.parametrize("act", ["identity", "relu"])
+@pytest.mark.parametrize("act", ["identity", "relu", "gelu"])
 @pytest.mark.parametrize("k", [1, 4, 16, 64])
 def test_forward_topk_matches_reference_formula(oracle, act, k):
     rng = np.random.default_rng(13)
@@ -249,7 +258,7 @@ def test_forward_topk_ties_go_to_the_smaller_slot(oracle):
     assert gap[0, 0] == 0.0  # slot 0 and slot 3 tie at the boundary
 
 
-@pytest.mark.parametrize("act", ["identity", "relu"])
+@pytest.mark.parametrize("act", ["identity", "relu", "gelu"])
 @pytest.mark.parametrize("k", [2, 8])
 def test_backward_topk_matches_autograd(oracle, act, k):
     rng = np.random.default_rng(14)
@@ -264,7 +273,7 @@ def test_backward_topk_matches_autograd(oracle, act, k):
     assert_close(dX, xt.grad.numpy(), rtol=1e-12, atol=1e-12, what="dX")
 
 
-@pytest.mark.parametrize("act", ["identity", "relu"])
+@pytest.mark.parametrize("act", ["identity", "relu", "gelu"])
 def test_backward_events_of_the_own_selection_is_the_pooling_backward(oracle, act):
     rng = np.random.default_rng(15)
     B, D, G, S, K = 4, 32, 3, 40, 8
@@ -418,7 +427,7 @@ def _dense_pool_torch(x, idx, w, b, counts, S, pool, param, act):
     xg = x[:, torch.as_tensor(idx, dtype=torch.long)]
     z = (xg * w).sum(-1) + b  # [B, G*S]
     z = z.view(x.shape[0], G, S)
-    a = torch.relu(z) if (act == "relu" or pool == "power_mean") else z
+    a = _act(z, "relu" if pool == "power_mean" else act)
     mask = torch.arange(S)[None, :] < torch.as_tensor(counts)[:, None]
     n = torch.as_tensor(counts, dtype=torch.float64)
     if pool == "logmeanexp":
@@ -435,8 +444,10 @@ def _dense_pool_torch(x, idx, w, b, counts, S, pool, param, act):
 
 
 @pytest.mark.parametrize("pool,param,act", [("logmeanexp", 1.0, "identity"), ("logmeanexp", 0.3, "relu"),
+                                            ("logmeanexp", 0.7, "gelu"),
                                             ("power_mean", 2.0, "relu"), ("power_mean", 3.5, "relu"),
-                                            ("softmax_weighted", 1.0, "identity"), ("softmax_weighted", 2.5, "relu")])
+                                            ("softmax_weighted", 1.0, "identity"), ("softmax_weighted", 2.5, "relu"),
+                                            ("softmax_weighted", 1.5, "gelu")])
 def test_smooth_pools_match_torch_formulas_and_autograd(oracle, pool, param, act):
     """Forward against the reference's pooling formulas in float64 torch, backward against torch
     autograd of them (dW, db, dX), on ragged pools (padded slots)."""

@@ -68,6 +68,37 @@ def test_static_forward_equals_gl_fwd_on_two_calls(pool, k):
             assert torch.equal(w1, w2), "topk_slot differs"
 
 
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a ROCm GPU")
+def test_static_forward_orders_calls_on_two_streams():
+    """Two calls on two streams of one GPU, issued back to back with no host synchronisation,
+    share the static scratch; the library orders them (the second waits for the first's launches),
+    so each gives gl_fwd's result."""
+    lib = N.library()
+    spec = LevelSpec("sum", activation="relu")
+    cases = [_case(1024, 400_000, 400, 256, 3), _case(1024, 400_000, 400, 256, 4)]
+    want, got = [], []
+    for L, idx, w, b, x in cases:
+        rt = Level1Runtime(L, idx, spec, PhysicalPlan())
+        pre = torch.empty((x.shape[0], L.groups), device=DEV)
+        a = _args(rt, x, w, b, pre)
+        need = lib.size_query("gl_fwd_workspace", a)
+        ws = torch.empty(need, device=DEV, dtype=torch.uint8)
+        a.ws, a.ws_bytes = _ptr(ws), need
+        assert lib.lib.gl_fwd(ctypes.byref(a), ctypes.c_void_p(_stream(x.device))) == 0
+        want.append(pre)
+        got.append((rt, x, w, b, torch.full_like(pre, float("nan"))))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s, (rt, x, w, b, pre) in zip(streams, got):
+        a = _args(rt, x, w, b, pre)
+        rc = lib.lib.gl_fwd_static(ctypes.byref(a), ctypes.c_void_p(s.cuda_stream))
+        assert rc == 0, lib.error(rc)
+    torch.cuda.synchronize()
+    for (_, _, _, _, pre), ref in zip(got, want):
+        assert torch.equal(pre, ref)
+
+
 def test_static_forward_refuses_layers_beyond_the_scratch():
     """Host-side refusal (placeholder pointers never dereferenced): top-64 lists of 40,000 pools of
     256 slots take 2 KiB per chunk and 4-token tile, 78 MiB > 64 MiB."""
