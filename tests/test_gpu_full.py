@@ -249,10 +249,11 @@ def test_selection_backward_over_the_checkpoint_budget(pooling, monkeypatch):
 
 
 def test_adam_at_the_c4_size_matches_the_oracle_on_a_sample():
-    """gl_adam over C4's 805,306,368-element weight stream (3.2 GB per array, byte offsets past 2^31
-    and 2^32): two steps, then a seeded sample of elements -- the first and last 4096, 4096 around
-    element 2^29 (byte 2^31) and 2^30 (byte 2^32), 65,536 random -- against oracle.adam on the same
-    elements (the update is elementwise, so a sample evolves on its own)."""
+    """gl_adam over C4's 805,306,368-element weight stream (3.2 GB per array, byte offsets past
+    2^31): two steps, then a seeded sample of elements -- the first and last 4096, 4096 around
+    element 2^29 (byte 2^31), 65,536 random -- against oracle.adam on the same elements (the update
+    is elementwise, so a sample evolves on its own).  Every sampled index is checked to lie in
+    [0, n) on the host before it reaches the device."""
     from granulelayer_amd.backend import HipBackend
     from oracle import oracle as O
 
@@ -263,8 +264,10 @@ def test_adam_at_the_c4_size_matches_the_oracle_on_a_sample():
     v = torch.rand(n, generator=gen, device=DEV) * 1e-4
     rng = np.random.default_rng(5)
     parts = [np.arange(4096), np.arange(n - 4096, n), np.arange((1 << 29) - 2048, (1 << 29) + 2048),
-             np.arange((1 << 30) - 2048, (1 << 30) + 2048), rng.integers(0, n, 65536)]
-    sample = torch.as_tensor(np.unique(np.concatenate(parts)), device=DEV)
+             rng.integers(0, n, 65536)]
+    idx = np.unique(np.concatenate(parts))
+    assert idx.min() >= 0 and idx.max() < n
+    sample = torch.as_tensor(idx, device=DEV)
     po, mo, vo = (t[sample].cpu().numpy().copy() for t in (p, m, v))
     be = HipBackend.get()
     for t in (1, 2):
