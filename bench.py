@@ -12,6 +12,12 @@ value = useful edge-MACs per second of the whole step (B * N * 8 / step time, on
 reference's useful_tflops(passes=1), sparse_pooling/benchmarks/common.py:80-82).
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-cpu-baseline] [--no-extra]
+                      [--relu-bits keep|recompute]
+
+The layers run with PhysicalPlan(relu_bits="keep") by default: the forward keeps one ReLU bit per
+(token, neuron) (1/32 of the hidden tensor's fp32 bytes) and the backward's dW pass reads it
+instead of recomputing z, with the same results bit for bit.  The same step with the reference's
+recompute (relu_bits="recompute") is timed beside it ("other_relu_bits").
 
 Beside the headline the line carries: the C1 train step on the GPU, the C4
 full training step (configs[3], 3 timed steps), the one-time layer setup, and cpu_baseline = the
@@ -51,15 +57,18 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def algorithmic(kernel: str, B: int, N: int, K: int, D: int, G: int, x_bytes: int = 4):
+def algorithmic(kernel: str, B: int, N: int, K: int, D: int, G: int, x_bytes: int = 4, relu_bits: bool = False):
     """(bytes, flops) of one training step's launches of a kernel (one launch each, except the
     AdamW kernel: one launch for the weights, one for the bias): every input read once, every
-    output written once."""
+    output written once.  relu_bits: the forward also writes the ReLU bits (N B / 8 bytes) and the
+    dW pass reads them instead of W, bias and the z recompute (its flops are dW's 2 B E alone)."""
     E = N * K
     if kernel == "fwd_kernel":
-        # idx + W + bias, X once, pooled output
-        return 4 * E + 4 * E + 4 * N + B * D * x_bytes + 4 * B * G, 2 * B * E
+        # idx + W + bias, X once, pooled output (+ the ReLU bits)
+        return 4 * E + 4 * E + 4 * N + B * D * x_bytes + 4 * B * G + (N * B // 8 if relu_bits else 0), 2 * B * E
     if kernel == "bwd_w_kernel":
+        if relu_bits:  # idx, X once, the forward's bits, dW/db read-modify-write, mask bits written
+            return 4 * E + B * D * x_bytes + N * B // 8 + 8 * E + 8 * N + N * B // 8, 2 * B * E
         # idx + W + bias, X once, dW/db read-modify-write, mask bits written
         return 4 * E + 4 * E + 4 * N + B * D * x_bytes + 8 * E + 8 * N + N * B // 8, 4 * B * E
     if kernel in ("dx_kernel", "dx_dma_kernel"):
@@ -108,6 +117,7 @@ def run_config(name: str, steps: int, warmup: int):
     G = N // pool
     t0 = time.time()
     lay = SparsePoolingLayer(D, N, G, fan_in=K, shared_neurons=None, pooling="sum", dtype=torch.float32, device=dev,
+                             plan=_plan(),
                              seed=0)
     if c["indices"] != "uniform":  # locality windows (C3) or top-16 of 64 candidates (C5)
         pr = make_problem(name, device=dev, seed=0)
@@ -162,6 +172,17 @@ def _med_iqr(v):
     return round(q2 * 1e3, 2), round((q3 - q1) * 1e3, 2)
 
 
+# PhysicalPlan.relu_bits of every layer the bench builds ("keep": the forward keeps its ReLU bits
+# for the backward's dW pass; "recompute": the reference's O(B x G) checkpoint); --relu-bits
+RELU_BITS = "keep"
+
+
+def _plan():
+    from granulelayer_amd import PhysicalPlan
+
+    return PhysicalPlan(relu_bits=RELU_BITS)
+
+
 def c1_problem():
     """BASELINE configs[0] (the reference's CPU-runnable case): B=64, D=1024, N=1,048,576, fan-in 8,
     pools of 256, seed 0, generated on the CPU so the GPU and the CPU path see the same bits."""
@@ -179,7 +200,7 @@ def c1_gpu(pr, steps: int, warmup: int):
 
     L = pr.layout
     dev = torch.device("cuda", 0)
-    lay = SparsePoolingLayer(L.input_dim, L.hidden_dim, L.groups, fan_in=L.fan_in, shared_neurons=None,
+    lay = SparsePoolingLayer(L.input_dim, L.hidden_dim, L.groups, fan_in=L.fan_in, shared_neurons=None, plan=_plan(),
                              pooling="sum", dtype=torch.float32, device=dev, seed=0)
     with torch.no_grad():
         lay.indices.copy_(pr.idx.to(dev))
@@ -259,6 +280,7 @@ def c4_step(steps: int, warmup: int):
     G = N // pool
     dev = torch.device("cuda", 0)
     lay = SparsePoolingLayer(D, N, G, fan_in=K, shared_neurons=None, pooling="sum", dtype=torch.float32, device=dev,
+                             plan=_plan(),
                              seed=0)
     lay.enable_main_grad()
     opt = FusedAdamW(lay.parameters(), lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, moments="fp32")
@@ -341,7 +363,9 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=4, help="timed steps of the C1 CPU baseline")
+    ap.add_argument("--relu-bits", choices=("keep", "recompute"), default="keep",
+                    help="PhysicalPlan.relu_bits of the timed layers (the other mode's step is timed beside it)")
+    ap.add_argument("--cpu-steps", type=int, default=5, help="timed steps of the C1 CPU baseline (after one untimed)")
     ap.add_argument("--no-extra", action="store_true", help="skip the C1 and C4 extra measurements")
     ap.add_argument("--config", choices=sorted(CONFIG_WORK), default=None,
                     help="time one BASELINE config's own work at full size instead of the headline step")
@@ -353,6 +377,8 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
+    global RELU_BITS
+    RELU_BITS = args.relu_bits
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build measures one MI355X (--gpus {args.gpus} requested); "
               "nothing in it shards across GPUs", file=sys.stderr)
@@ -386,7 +412,7 @@ def main():
     t0 = time.time()
     log(f"building layer N={N:,} K={K} D={D} G={G:,} on {torch.cuda.get_device_name(0)}")
     pooling = POOLINGS[args.pooling][0]
-    lay = SparsePoolingLayer(D, N, G, fan_in=K, shared_neurons=None, pooling=pooling, dtype=torch.float32,
+    lay = SparsePoolingLayer(D, N, G, fan_in=K, shared_neurons=None, pooling=pooling, dtype=torch.float32, plan=_plan(),
                              device=dev, seed=0)
     lay.enable_main_grad()
     opt = FusedAdamW(lay.parameters(), lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0, moments="fp32")
@@ -421,6 +447,22 @@ def main():
     ms_step = ev0.elapsed_time(ev1) / args.steps
     ktimes = tr.times_ms()
     log(f"timed {args.steps} steps: {ms_step:.3f} ms/step (wall {wall / args.steps * 1e3:.3f} ms)")
+    # the same step with the other relu_bits mode, for comparison (same layer, same inputs)
+    other = "recompute" if RELU_BITS == "keep" else "keep"
+    lay.plan.relu_bits = other
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    with KernelTrace(max_launches=32 * args.steps) as tr2:
+        ev0.record()
+        for _ in range(args.steps):
+            step()
+        ev1.record()
+        torch.cuda.synchronize()
+    other_ms = ev0.elapsed_time(ev1) / args.steps
+    other_k = {k: round(sum(v) / len(v), 4) for k, v in tr2.times_ms().items()}
+    lay.plan.relu_bits = RELU_BITS
+    log(f"relu_bits={other}: {other_ms:.3f} ms/step")
 
     # forward only (BASELINE C2 headline), same layer
     with torch.no_grad():
@@ -442,7 +484,7 @@ def main():
     kernels = {}
     for name, ts in ktimes.items():
         step_ms = sum(ts) / args.steps  # all launches of the kernel in one step
-        by, fl = algorithmic(name, B, N, K, D, G)
+        by, fl = algorithmic(name, B, N, K, D, G, relu_bits=RELU_BITS == "keep")
         rec = {"ms": round(sum(ts) / len(ts), 4), "launches_per_step": len(ts) // args.steps,
                "ms_per_step": round(step_ms, 4)}
         if by is not None:
@@ -453,7 +495,7 @@ def main():
     dom = max(ktimes, key=lambda n: sum(ktimes[n]))
     dom_ms = sum(ktimes[dom]) / args.steps
     dom_launch_ms = sum(ktimes[dom]) / len(ktimes[dom])
-    by, fl = algorithmic(dom, B, N, K, D, G)
+    by, fl = algorithmic(dom, B, N, K, D, G, relu_bits=RELU_BITS == "keep")
     prof = read_profile(os.path.join(ROOT, "profiles", "pmc_c2_train_step.txt")).get(dom, {})
     if dom == "adam_kernel":
         roof = {"bound": "hbm", "achieved": round(by / (dom_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
@@ -493,7 +535,9 @@ def main():
         "config": {"workload": "C2-shaped train step: fwd + recompute bwd (dX, dW, db) + fused AdamW",
                    "neurons": N, "fan_in": K, "d_in": D, "batch": B, "pool": pool, "groups": G,
                    "pooling": POOLINGS[args.pooling][1], "x_dtype": "f32", "moments": "f32",
-                   "parallelism": "single GPU"},
+                   "relu_bits": RELU_BITS, "parallelism": "single GPU"},
+        "other_relu_bits": {"relu_bits": other, "ms_per_step": round(other_ms, 3),
+                            "G_edge_macs_per_s": round(B * E / (other_ms * 1e-3) / 1e9, 2), "kernels_ms": other_k},
         "fwd_ms": round(fwd_ms, 3),
         "fwd_G_edge_macs_per_s": round(B * E / (fwd_ms * 1e-3) / 1e9, 2),
         "setup": setup,

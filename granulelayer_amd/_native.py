@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libgranulelayer_amd.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 GL_ACT = {"identity": 0, "relu": 1, "gelu": 2}
 GL_POOL = {"mean": 0, "sum": 1, "max": 2, "topk_mean": 3, "logmeanexp": 4, "power_mean": 5, "softmax_weighted": 6}
@@ -28,7 +28,8 @@ class GlFwdArgs(ctypes.Structure):
     _fields_ = [("X", _P), ("sxb", _I64), ("x_dtype", _I32), ("B", _I32), ("D", _I32), ("G", _I32), ("S", _I32),
                 ("K", _I32), ("act", _I32), ("pool", _I32), ("topk", _I32), ("rec_shift", _I32), ("sps", _I32), ("gs", _I32), ("idx", _P), ("W", _P), ("bias", _P), ("counts", _P),
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("pre", _P), ("winner", _P), ("pool_param", _F),
-                ("lse", _P), ("ws", _P), ("ws_bytes", _SZ), ("part_budget", _SZ), ("w_dtype", _I32)]
+                ("lse", _P), ("ws", _P), ("ws_bytes", _SZ), ("part_budget", _SZ), ("w_dtype", _I32),
+                ("relu_mask", _P)]
 
 
 class GlBwdArgs(ctypes.Structure):
@@ -37,7 +38,8 @@ class GlBwdArgs(ctypes.Structure):
                 ("sched", _P), ("win", _P), ("win_width", _I32), ("g_pre", _P), ("winner", _P), ("pool_param", _F),
                 ("pre", _P), ("lse", _P), ("dW", _P), ("db", _P),
                 ("dX", _P), ("edges", _P), ("edges_bytes", _SZ),
-                ("ws", _P), ("ws_bytes", _SZ), ("dz_budget", _SZ), ("w_dtype", _I32)]
+                ("ws", _P), ("ws_bytes", _SZ), ("dz_budget", _SZ), ("w_dtype", _I32),
+                ("relu_mask", _P)]
 
 
 class GlEdgeArgs(ctypes.Structure):
@@ -61,6 +63,7 @@ class GlCoverArgs(ctypes.Structure):
 STRUCTS = (GlFwdArgs, GlBwdArgs, GlEdgeArgs, GlAdamArgs, GlCoverArgs)  # gl_struct_layout ids 0..4
 # every symbol include/granulelayer_amd.h declares
 EXPORTS = ("gl_abi_version", "gl_struct_layout", "gl_error_string", "gl_fwd_workspace", "gl_fwd", "gl_fwd_static",
+           "gl_fwd_mask_bytes",
            "gl_edges_size",
            "gl_edges_build", "gl_bwd_workspace", "gl_bwd", "gl_adam", "gl_sched_size", "gl_sched_build_host",
            "gl_sched_build", "gl_window_build_host", "gl_window_build", "gl_cover_select", "gl_trace_begin",

@@ -181,12 +181,14 @@ class Level1Runtime:
         return out
 
     # ---------------------------------------------------------------- forward
-    def forward(self, x: torch.Tensor, w, b, track_ids: bool = False) -> Dict[str, torch.Tensor]:
-        """Merged statistics: {'pre': [B, U]} (the pooled value before the out-activation)."""
+    def forward(self, x: torch.Tensor, w, b, track_ids: bool = False, relu_mask: bool = False) -> Dict[str, torch.Tensor]:
+        """Merged statistics: {'pre': [B, U]} (the pooled value before the out-activation); with
+        relu_mask, also the ReLU bits the HIP backward can use instead of recomputing z."""
         self.check_devices(x, w, b)
         self._require_backend()
         self.resolve_reduction(x.shape[0])
-        out = self.backend.forward(self, x, w, b, track_ids)
+        out = (self.backend.forward(self, x, w, b, track_ids, relu_mask=True) if relu_mask
+               else self.backend.forward(self, x, w, b, track_ids))
         self.last_info["forward_backend"] = "hip"
         return out
 
@@ -238,6 +240,8 @@ def _saved_stats(level: LevelSpec, out: Dict[str, torch.Tensor], policy: str) ->
     if policy == "recompute_stats":
         return {}
     keep = {"pre": out["pre"]}
+    if "relu_mask" in out:  # the forward's ReLU bits (1/32 of the hidden tensor): dW skips the recompute
+        keep["relu_mask"] = out["relu_mask"]
     for key in ("winner", "topk_slot"):
         if policy == "save_winners" and key in out:
             keep[key] = out[key]
@@ -291,7 +295,11 @@ class SparsePoolFunction(torch.autograd.Function):
         policy = fit_policy(rt, policy, x.shape[0])
         xc, wc, bc = _compute_operands(x, w, b, compute_dtype)
         lv = rt.level
-        out = rt.forward(xc, wc, bc, track_ids=(policy == "save_winners"))
+        # the ReLU bits (PhysicalPlan.relu_bits="keep") only when a backward will run and the
+        # policy keeps statistics
+        keep_bits = (getattr(rt.plan, "relu_bits", "recompute") == "keep" and policy != "recompute_stats"
+                     and any(ctx.needs_input_grad[:3]))
+        out = rt.forward(xc, wc, bc, track_ids=(policy == "save_winners"), relu_mask=keep_bits)
         pre = out["pre"]
         y = act_torch(pre, lv.out_activation)
         saved = _saved_stats(lv, out, policy)

@@ -30,6 +30,11 @@ from . import _native as N
 # dX passes cost less per token in longer chunks.
 DZ_BUDGET = 64 * 2**30
 
+# The forward's ReLU bits kept for the backward (GlFwdArgs.relu_mask): one bit per (token, neuron),
+# 1/32 of the [B, N] hidden tensor's fp32 bytes (3.2 GB at C2, 12.9 GB at C4).  With them the
+# backward's dW pass does not recompute z.  Kept only up to this size; larger layers recompute.
+RELU_MASK_BUDGET = 16 * 2**30
+
 
 def _ptr(t: Optional[torch.Tensor]) -> int:
     return 0 if t is None else t.data_ptr()
@@ -152,7 +157,10 @@ class HipBackend:
             raise ValueError("weight / bias shapes do not match the layout")
 
     # ------------------------------------------------------------------ forward
-    def forward(self, rt, x, w, b, track_ids: bool = False) -> Dict[str, torch.Tensor]:
+    def forward(self, rt, x, w, b, track_ids: bool = False, relu_mask: bool = False) -> Dict[str, torch.Tensor]:
+        """The reference's backend forward (sparse_pooling/autograd.py:220-223).  relu_mask: also
+        return the ReLU bits of every (token, neuron) as "relu_mask" when the layer has them
+        (ReLU sum / mean at fan-in 8) and they fit RELU_MASK_BUDGET, for the backward."""
         self._check(rt, x, w, b)
         L, _, _, K = self._layer(rt)
         G, S, sps, gs, counts = self._pools(rt)
@@ -187,6 +195,11 @@ class HipBackend:
                         winner=_ptr(winner), pool_param=self.pool_param(rt), lse=_ptr(lse),
                         part_budget=self.part_budget(rt), w_dtype=wcode)
         with torch.cuda.device(x.device):
+            if relu_mask:
+                mb = self.lib.size_query("gl_fwd_mask_bytes", a)
+                if 0 < mb <= RELU_MASK_BUDGET:
+                    out["relu_mask"] = torch.empty(mb, device=x.device, dtype=torch.uint8)
+                    a.relu_mask = _ptr(out["relu_mask"])
             need = self.lib.size_query("gl_fwd_workspace", a)
             ws = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)
             a.ws, a.ws_bytes = _ptr(ws), need
@@ -335,6 +348,15 @@ class HipBackend:
                         winner=_ptr(winner), pool_param=self.pool_param(rt), pre=_ptr(pre), lse=_ptr(lse),
                         dW=_ptr(dw_buf), db=_ptr(db_buf), dX=_ptr(dx), edges=_ptr(edges),
                         edges_bytes=edges.numel(), dz_budget=self.dz_budget(rt), w_dtype=wcode)
+        # the forward's ReLU bits, when it kept them: the dW pass then skips the recompute of z
+        rm = stats.get("relu_mask")
+        if rm is not None:
+            fa = N.GlFwdArgs(B=B, D=D, G=G, S=S, K=K, act=act, pool=pool, rec_shift=self.rec_shift(rt), x_dtype=xcode)
+            want = self.lib.size_query("gl_fwd_mask_bytes", fa)
+            if rm.dtype != torch.uint8 or rm.numel() != want or want == 0 or rm.device != x.device:
+                raise ValueError("relu_mask does not come from this layer's forward of this batch")
+            a.relu_mask = _ptr(rm)
+        rt.last_info["backward_relu_mask"] = rm is not None
         with torch.cuda.device(x.device):
             need = self.lib.size_query("gl_bwd_workspace", a)
             ws = torch.empty(max(need, 1), device=x.device, dtype=torch.uint8)

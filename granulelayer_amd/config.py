@@ -189,6 +189,12 @@ class PhysicalPlan:
     accepted for source compatibility and ignored: the HIP kernels pick their own tiles.  Every
     HIP reduction has a fixed owner and order, so ``reduction="fast"`` and ``"deterministic"``
     both run deterministic kernels.
+
+    ``relu_bits`` is this build's own: ``"recompute"`` (default, the reference's behaviour) keeps
+    only the pooled statistics between forward and backward and the backward recomputes z;
+    ``"keep"`` also keeps the forward's ReLU bit of every (token, neuron) -- 1/32 of the [B, N]
+    hidden tensor's fp32 bytes -- for ReLU mean / sum layers at fan-in 8, so the backward's dW
+    pass skips the recompute (same results, bit for bit).
     """
 
     phys_splits: int = 0
@@ -227,6 +233,7 @@ class PhysicalPlan:
     cuda_grouped_merge: str = "atomic"
     reduction: str = "auto"
     deterministic_workspace_bytes: int = 0
+    relu_bits: str = "recompute"
 
     def __post_init__(self):
         if self.input_layout not in ("feature_major", "token_major"):
@@ -239,6 +246,8 @@ class PhysicalPlan:
             raise ValueError(f"reduction must be one of {REDUCTIONS} (got {self.reduction!r})")
         if self.deterministic_workspace_bytes < 0:
             raise ValueError("deterministic_workspace_bytes must be >= 0")
+        if self.relu_bits not in ("recompute", "keep"):
+            raise ValueError(f"relu_bits must be 'recompute' or 'keep' (got {self.relu_bits!r})")
 
 
 def resolve_reduction(plan: PhysicalPlan):

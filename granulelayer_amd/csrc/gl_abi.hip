@@ -96,7 +96,7 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
                        OFF(S, S), OFF(S, K), OFF(S, act), OFF(S, pool), OFF(S, topk), OFF(S, rec_shift), OFF(S, sps), OFF(S, gs), OFF(S, idx), OFF(S, W),
                        OFF(S, bias), OFF(S, counts), OFF(S, sched), OFF(S, win), OFF(S, win_width), OFF(S, pre), OFF(S, winner),
                        OFF(S, pool_param), OFF(S, lse), OFF(S, ws),
-                       OFF(S, ws_bytes), OFF(S, part_budget), OFF(S, w_dtype)};
+                       OFF(S, ws_bytes), OFF(S, part_budget), OFF(S, w_dtype), OFF(S, relu_mask)};
       for (long long x : t) v[c++] = x;
       break;
     }
@@ -107,7 +107,8 @@ extern "C" int gl_struct_layout(int which, long long* out, int n) {
                        OFF(S, bias), OFF(S, counts), OFF(S, sched), OFF(S, win), OFF(S, win_width), OFF(S, g_pre), OFF(S, winner),
                        OFF(S, pool_param), OFF(S, pre), OFF(S, lse), OFF(S, dW),
                        OFF(S, db), OFF(S, dX), OFF(S, edges),
-                       OFF(S, edges_bytes), OFF(S, ws), OFF(S, ws_bytes), OFF(S, dz_budget), OFF(S, w_dtype)};
+                       OFF(S, edges_bytes), OFF(S, ws), OFF(S, ws_bytes), OFF(S, dz_budget), OFF(S, w_dtype),
+                       OFF(S, relu_mask)};
       for (long long x : t) v[c++] = x;
       break;
     }

@@ -81,15 +81,20 @@ struct BwK {
   int tb;                 // tokens per tile: 4, or 2 (two-token tiles; n_tiles counts those)
   int xb;                 // 4-token tiles of raw bf16 (8-byte slots; bf16 X)
   int wbf;                // W and bias stored as bf16 (widened in the kernel)
+  const uint16_t* fm;     // the forward's ReLU bits ([n_chunks][fm_tiles][64] 16-bit words) or null
+  int fm_tiles, fm_t0;    // 4-token tiles of the whole batch; the backward chunk's first tile
 };
 
 // One token tile of the dW pass (LDS at xsb): recompute z, form dz = c1 * act'(z), accumulate
 // db, dW and the tile's 4 mask bits (bit 4 (t % 8) + i of word mw for token i of tile t).  The
 // first RA LDS reads of neuron j + 1 are issued before the arithmetic of neuron j.
-template <int K, int NPL, int ACT, int RA, bool FAR, typename SRC = const char*>
+// FM: the tile's mask bits come from the forward (fb: bit 15 - (4 j + i) = token i of neuron j): no z
+// recompute, no W or bias; dz = c1 where the bit is set, else +0 (the bit sign-extended and ANDed
+// with c1's pattern is the select below, bit for bit), and the bits go into mw as the recompute's.
+template <int K, int NPL, int ACT, int RA, bool FAR, typename SRC = const char*, bool FM = false>
 __device__ __forceinline__ void bwd_w_tile(SRC xsb, int t, const float4 c1, const unsigned (&addr)[NPL][K],
                                            const float (&w)[NPL][K], const float (&bias)[NPL], float (&dw)[NPL][K],
-                                           float (&dbv)[NPL], unsigned (&mw)[NPL]) {
+                                           float (&dbv)[NPL], unsigned (&mw)[NPL], unsigned fb) {
   float4 xc[K];
 #pragma unroll
   for (int k = 0; k < RA; ++k) xc[k] = gather_x<FAR>(xsb, addr[0][k]);
@@ -103,17 +108,27 @@ __device__ __forceinline__ void bwd_w_tile(SRC xsb, int t, const float4 c1, cons
       for (int k = 0; k < RA; ++k) xn[k] = gather_x<FAR>(xsb, addr[j + 1][k]);
     }
     __builtin_amdgcn_sched_barrier(0);
-    float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+    float d0, d1, d2, d3;
+    if constexpr (FM) {  // token i of neuron j is bit 15 - (4 j + i) of fb
+      d0 = __uint_as_float((unsigned)__builtin_amdgcn_sbfe((int)fb, 15u - 4u * j, 1u) & __float_as_uint(c1.x));
+      d1 = __uint_as_float((unsigned)__builtin_amdgcn_sbfe((int)fb, 14u - 4u * j, 1u) & __float_as_uint(c1.y));
+      d2 = __uint_as_float((unsigned)__builtin_amdgcn_sbfe((int)fb, 13u - 4u * j, 1u) & __float_as_uint(c1.z));
+      d3 = __uint_as_float((unsigned)__builtin_amdgcn_sbfe((int)fb, 12u - 4u * j, 1u) & __float_as_uint(c1.w));
+      mw[j] |= ((unsigned)__builtin_bitreverse32(fb) >> (16u + 4u * j) & 15u) << ((t & 7) * 4);
+    } else {
+      float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
-      z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
-      z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
-      z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
+      for (int k = 0; k < K; ++k) {
+        z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
+        z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
+        z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
+        z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
+      }
+      const bool m0 = ACT != GL_ACT_RELU || z0 > 0.f, m1 = ACT != GL_ACT_RELU || z1 > 0.f;
+      const bool m2 = ACT != GL_ACT_RELU || z2 > 0.f, m3 = ACT != GL_ACT_RELU || z3 > 0.f;
+      d0 = m0 ? c1.x : 0.f, d1 = m1 ? c1.y : 0.f, d2 = m2 ? c1.z : 0.f, d3 = m3 ? c1.w : 0.f;
+      mw[j] |= ((unsigned)m0 | ((unsigned)m1 << 1) | ((unsigned)m2 << 2) | ((unsigned)m3 << 3)) << ((t & 7) * 4);
     }
-    const bool m0 = ACT != GL_ACT_RELU || z0 > 0.f, m1 = ACT != GL_ACT_RELU || z1 > 0.f;
-    const bool m2 = ACT != GL_ACT_RELU || z2 > 0.f, m3 = ACT != GL_ACT_RELU || z3 > 0.f;
-    const float d0 = m0 ? c1.x : 0.f, d1 = m1 ? c1.y : 0.f, d2 = m2 ? c1.z : 0.f, d3 = m3 ? c1.w : 0.f;
     dbv[j] = dbv[j] + d0 + d1 + d2 + d3;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -124,7 +139,6 @@ __device__ __forceinline__ void bwd_w_tile(SRC xsb, int t, const float4 c1, cons
       a = __builtin_fmaf(d3, xc[k].w, a);
       dw[j][k] = a;
     }
-    mw[j] |= ((unsigned)m0 | ((unsigned)m1 << 1) | ((unsigned)m2 << 2) | ((unsigned)m3 << 3)) << ((t & 7) * 4);
     __builtin_amdgcn_sched_barrier(0);
     if (j + 1 < NPL) {
 #pragma unroll
@@ -135,10 +149,10 @@ __device__ __forceinline__ void bwd_w_tile(SRC xsb, int t, const float4 c1, cons
 
 // The same over a 4-token tile of raw bf16 values (8-byte slots): the gathers keep the packed
 // words, which are widened (exactly) once after the read-ahead and used for both z and dW.
-template <int K, int NPL, int ACT, int RA, bool FAR>
+template <int K, int NPL, int ACT, int RA, bool FAR, bool FM = false>
 __device__ __forceinline__ void bwd_w_tile_bf4(const char* xsb, int t, const float4 c1, const unsigned (&addr)[NPL][K],
                                                const float (&w)[NPL][K], const float (&bias)[NPL], float (&dw)[NPL][K],
-                                               float (&dbv)[NPL], unsigned (&mw)[NPL]) {
+                                               float (&dbv)[NPL], unsigned (&mw)[NPL], unsigned fb) {
   uint2 xr[K];
   auto ld = [&](unsigned a) {
     if constexpr (FAR) asm volatile("" : "+v"(a));
@@ -161,17 +175,27 @@ __device__ __forceinline__ void bwd_w_tile_bf4(const char* xsb, int t, const flo
     for (int k = 0; k < K; ++k)
       xc[k] = make_float4(__uint_as_float(xr[k].x << 16), __uint_as_float(xr[k].x & 0xffff0000u),
                           __uint_as_float(xr[k].y << 16), __uint_as_float(xr[k].y & 0xffff0000u));
-    float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
+    float d0, d1, d2, d3;
+    if constexpr (FM) {  // token i of neuron j is bit 15 - (4 j + i) of fb
+      d0 = __uint_as_float((unsigned)__builtin_amdgcn_sbfe((int)fb, 15u - 4u * j, 1u) & __float_as_uint(c1.x));
+      d1 = __uint_as_float((unsigned)__builtin_amdgcn_sbfe((int)fb, 14u - 4u * j, 1u) & __float_as_uint(c1.y));
+      d2 = __uint_as_float((unsigned)__builtin_amdgcn_sbfe((int)fb, 13u - 4u * j, 1u) & __float_as_uint(c1.z));
+      d3 = __uint_as_float((unsigned)__builtin_amdgcn_sbfe((int)fb, 12u - 4u * j, 1u) & __float_as_uint(c1.w));
+      mw[j] |= ((unsigned)__builtin_bitreverse32(fb) >> (16u + 4u * j) & 15u) << ((t & 7) * 4);
+    } else {
+      float z0 = bias[j], z1 = bias[j], z2 = bias[j], z3 = bias[j];
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
-      z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
-      z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
-      z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
+      for (int k = 0; k < K; ++k) {
+        z0 = __builtin_fmaf(xc[k].x, w[j][k], z0);
+        z1 = __builtin_fmaf(xc[k].y, w[j][k], z1);
+        z2 = __builtin_fmaf(xc[k].z, w[j][k], z2);
+        z3 = __builtin_fmaf(xc[k].w, w[j][k], z3);
+      }
+      const bool m0 = ACT != GL_ACT_RELU || z0 > 0.f, m1 = ACT != GL_ACT_RELU || z1 > 0.f;
+      const bool m2 = ACT != GL_ACT_RELU || z2 > 0.f, m3 = ACT != GL_ACT_RELU || z3 > 0.f;
+      d0 = m0 ? c1.x : 0.f, d1 = m1 ? c1.y : 0.f, d2 = m2 ? c1.z : 0.f, d3 = m3 ? c1.w : 0.f;
+      mw[j] |= ((unsigned)m0 | ((unsigned)m1 << 1) | ((unsigned)m2 << 2) | ((unsigned)m3 << 3)) << ((t & 7) * 4);
     }
-    const bool m0 = ACT != GL_ACT_RELU || z0 > 0.f, m1 = ACT != GL_ACT_RELU || z1 > 0.f;
-    const bool m2 = ACT != GL_ACT_RELU || z2 > 0.f, m3 = ACT != GL_ACT_RELU || z3 > 0.f;
-    const float d0 = m0 ? c1.x : 0.f, d1 = m1 ? c1.y : 0.f, d2 = m2 ? c1.z : 0.f, d3 = m3 ? c1.w : 0.f;
     dbv[j] = dbv[j] + d0 + d1 + d2 + d3;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -182,7 +206,6 @@ __device__ __forceinline__ void bwd_w_tile_bf4(const char* xsb, int t, const flo
       a = __builtin_fmaf(d3, xc[k].w, a);
       dw[j][k] = a;
     }
-    mw[j] |= ((unsigned)m0 | ((unsigned)m1 << 1) | ((unsigned)m2 << 2) | ((unsigned)m3 << 3)) << ((t & 7) * 4);
     __builtin_amdgcn_sched_barrier(0);
     if (j + 1 < NPL) {
 #pragma unroll
@@ -241,13 +264,15 @@ __device__ __forceinline__ void bwd_w_tile2(const char* xsb, int t, const float2
 // load, wait, read.  The wave index goes through readfirstlane so the chunk's parameters and the
 // c1 row are addressed with scalar registers.
 template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF, bool WS = false, bool XG = false, int TB = BT,
-          bool XB = false>
+          bool XB = false, bool FM = false>
 __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   // XG (D > XTILE_SB): no LDS tile, the lanes gather from the token tiles in global memory.
   // TB: tokens per tile, 4 or 2 (two-token tiles in the two buffers of DBUF: D <= 2 XTILE_DB)
   static_assert(TB == BT || (TB == 2 && DBUF && !WS && !XG), "two-token tiles: double-buffered only");
   // XB: 4-token tiles of raw bf16 (8-byte slots, bf16 X), double-buffered
   static_assert(!XB || (TB == BT && DBUF && !WS && !XG), "bf16 tiles: double-buffered only");
+  // FM: the mask bits come from the forward (p.fm): no z recompute, W and bias are not read
+  static_assert(!FM || (TB == BT && ACT == GL_ACT_RELU), "forward ReLU bits: 4-token tiles, ReLU");
   constexpr unsigned SLOT = XB ? 8u : 4u * TB;  // bytes per input of a tile
   __shared__ float4 xs[DBUF || WS ? 2 * XTILE_DB : (XG ? 1 : XTILE_SB)];
   const int lane = threadIdx.x & 63;
@@ -282,12 +307,20 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
       int d = rec_index(p.idx, n, k, K, p.rs);
       d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
       addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * SLOT;
-      const float wl = ld_param(p.W, p.wbf, n * K + k);
-      w[j][ks] = valid ? wl : 0.f;
+      if constexpr (!FM) {
+        const float wl = ld_param(p.W, p.wbf, n * K + k);
+        w[j][ks] = valid ? wl : 0.f;
+      } else {
+        w[j][ks] = 0.f;
+      }
       dw[j][ks] = 0.f;
     }
-    const float bl = ld_param(p.bias, p.wbf, n);
-    bias[j] = valid ? bl : 0.f;
+    if constexpr (!FM) {
+      const float bl = ld_param(p.bias, p.wbf, n);
+      bias[j] = valid ? bl : 0.f;
+    } else {
+      bias[j] = 0.f;
+    }
     dbv[j] = 0.f;
   }
   const float* c1row = p.c1t + g * p.cap;
@@ -312,6 +345,14 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
   // after it is done, and the pair is stored as one 8-byte write: each store writes a separate
   // 32-byte memory sector, so pairs halve the mask's write traffic.
   unsigned mwe[NPL];
+  // FM: the forward's 16 bits of this lane for tile t (coalesced 128 bytes per wave), loaded a tile ahead
+  const uint16_t* fsrc = FM ? p.fm + (chunk * p.fm_tiles + p.fm_t0) * 64 + lane : nullptr;
+  unsigned fbn = FM ? fsrc[0] : 0u;
+  auto fbits = [&](int t) {
+    const unsigned b = fbn;
+    if (FM && t + 1 < p.n_tiles) fbn = fsrc[(long long)(t + 1) * 64];
+    return b;
+  };
   for (int t0 = 0; t0 < p.n_tiles; t0 += TPW) {
     unsigned mw[NPL];
 #pragma unroll
@@ -327,7 +368,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
         for (int tt = 0; tt < tn; ++tt) {
           const int t = ts0 + tt;
           const float4 c1 = ld_uniform4(c1row, t * BT);
-          bwd_w_tile<K, NPL, ACT, RA, false>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw, dbv, mw);
+          bwd_w_tile<K, NPL, ACT, RA, false, const char*, FM>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias,
+                                                             dw, dbv, mw, fbits(t));
           // next tile's slot; after the last tile of region 1 back to region 0 (uniform step, no branch)
           const unsigned step = (t & (2 * WS_TILES - 1)) == 2 * WS_TILES - 1 ? tstep - 2u * WS_TILES * tstep : tstep;
 #pragma unroll
@@ -342,23 +384,25 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
     for (int t = t0; t < t1 && !WS; ++t) {
       if constexpr (XG) {
         const float4 c1 = ld_uniform4(c1row, t * BT);
-        bwd_w_tile<K, NPL, ACT, RA, false>(xbuf(p.xt + (long long)t * p.D, p.D), t, c1, addr, w, bias, dw, dbv, mw);
+        bwd_w_tile<K, NPL, ACT, RA, false, decltype(xbuf(p.xt, p.D)), FM>(xbuf(p.xt + (long long)t * p.D, p.D), t, c1,
+                                                                          addr, w, bias, dw, dbv, mw, fbits(t));
       } else if constexpr (DBUF) {
         // buffer cur ^ 1 was last read in tile t - 1, which every wave finished before the barrier
         const int cur = t & 1;
         if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * ns, xs + (cur ^ 1) * XTILE_DB, ns, NT);
         if constexpr (XB) {
           const float4 c1 = ld_uniform4(c1row, t * BT);
-          bwd_w_tile_bf4<K, NPL, ACT, RA, true>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t,
-                                                c1, addr, w, bias, dw, dbv, mw);
+          bwd_w_tile_bf4<K, NPL, ACT, RA, true, FM>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16),
+                                                    t, c1, addr, w, bias, dw, dbv, mw, fbits(t));
         } else if constexpr (TB == 2) {
           const float2 c1 = ld_uniform2(c1row, t * 2);
           bwd_w_tile2<K, NPL, ACT, RA, true>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t, c1,
                                              addr, w, bias, dw, dbv, mw);
         } else {
           const float4 c1 = ld_uniform4(c1row, t * BT);
-          bwd_w_tile<K, NPL, ACT, RA, true>(reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t, c1,
-                                            addr, w, bias, dw, dbv, mw);
+          bwd_w_tile<K, NPL, ACT, RA, true, const char*, FM>(
+              reinterpret_cast<const char*>(xs) + opaque(cur) * (XTILE_DB * 16), t, c1, addr, w, bias, dw, dbv, mw,
+              fbits(t));
         }
         stage_wait();  // tile t + 1 is in LDS for this wave's copies; the barrier publishes every wave's
         __syncthreads();
@@ -368,7 +412,8 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
         const float4 c1 = ld_uniform4(c1row, t * BT);
         stage_wait();
         __syncthreads();
-        bwd_w_tile<K, NPL, ACT, RA, false>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw, dbv, mw);
+        bwd_w_tile<K, NPL, ACT, RA, false, const char*, FM>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw,
+                                                           dbv, mw, fbits(t));
       }
     }
     const int word = t0 / TPW;
@@ -1286,6 +1331,7 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
 // chunks of 128 slots cover pools of 512 exactly, where 3 per lane (chunks of 192) left 11% of the
 // lanes idle (C5 dW 53.8 -> 52.8 ms)
 constexpr int bwd_npl(int K) { return K == 8 ? 4 : 2; }
+static_assert(bwd_npl(8) == RELU_MASK_NPL, "the dW pass reads the forward's ReLU bits chunk by chunk");
 // The smooth pools' recompute pass keeps every gathered x of a neuron live across dz, and holds
 // smooth_sb tiles of dz per neuron to store them as one 128-byte (K = 8) or 32-byte (K = 16) run:
 // 2 neurons per lane.  At K = 8, 4 per lane with 16-byte stores ran 28.5 ms per 64-token C2
@@ -1295,6 +1341,12 @@ constexpr int bwd_npl(int K) { return K == 8 ? 4 : 2; }
 constexpr int smooth_npl(int K) { return 2; }
 constexpr int smooth_sb(int K) { return K == 8 ? 8 : 2; }
 constexpr int bwd_waves(int K) { return K == 8 ? 12 : 8; }
+#ifndef BWD_FM_WAVES
+#define BWD_FM_WAVES 16
+#endif
+#ifndef BWD_FM_RA
+#define BWD_FM_RA 1
+#endif
 
 struct BwdPlan {
   int bc_max, npl, waves, cpg, tiles_max, cap_max, rs_max, FR, P, U, Q, QL, UQ;
@@ -1337,12 +1389,15 @@ static BwdPlan bwd_plan(int B, int D, int G, int S, int K, bool smooth = false, 
   // the XCD's L2 when the next of them gathers from it (measured at C2: QL 8 -> 32 cut the dX
   // kernel by 8% for 0.3 ms more partial-sum reduction).  About 256K waves in total, at most
   // QL = 32 and at least 128 units per range, so the [Q, D, tokens] partials (and their
-  // reduction) stay small next to the layer.
+  // reduction) stay small next to the layer -- except that small layers get shorter ranges until
+  // they have 16K waves (two per wave slot of the chip): at C1 (4096 units) 4 ranges per XCD left
+  // 4096 waves walking 128 units each, a latency-bound 0.29 ms against 0.20 ms with 16.
   const int n_tc = q.cap_max / (64 * dx_slots(q.bc_max));
   const long long waves_wanted = 262144;
   long long ql = (waves_wanted + 8LL * q.FR * n_tc - 1) / (8LL * q.FR * n_tc);
   if (ql > 32) ql = 32;
-  if (ql > q.U / 1024) ql = q.U / 1024;
+  const long long ql_fill = (16384 + 8LL * q.FR * n_tc - 1) / (8LL * q.FR * n_tc);
+  if (ql > q.U / 1024 && ql > ql_fill) ql = q.U / 1024 > ql_fill ? q.U / 1024 : ql_fill;
   if (ql < 1) ql = 1;
   if (8 * ql > q.U) ql = ceil_div(q.U, 8);
   q.QL = (int)ql;
@@ -1386,6 +1441,23 @@ static int launch_bwd_w(const BwK& k, hipStream_t s) {
                   : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true>
                                      : (k.D <= XTILE_SB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false>
                                                         : bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, false, true>));
+
+  GL_LAUNCH(k.win ? GL_KERNEL_BWD_W_WIN : GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)),
+            dim3(WAVES * 64), 0, s, k);
+  GL_CHECK_LAUNCH();
+  return 0;
+}
+
+// With the forward's ReLU bits (gl_bwd checked the format) the dW pass holds neither W nor bias
+// and fits 128 VGPRs: 16 waves per workgroup, 4 per SIMD.
+template <int K, int NPL, int WAVES, int RA>
+static int launch_bwd_w_fm(const BwK& k, hipStream_t s) {
+  constexpr int A = GL_ACT_RELU;
+  auto fn = k.win ? bwd_w_kernel<K, NPL, WAVES, A, RA, false, true, false, BT, false, true>
+            : k.xb ? bwd_w_kernel<K, NPL, WAVES, A, RA, true, false, false, BT, true, true>
+            : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, A, RA, true, false, false, BT, false, true>
+                               : (k.D <= XTILE_SB ? bwd_w_kernel<K, NPL, WAVES, A, RA, false, false, false, BT, false, true>
+                                                  : bwd_w_kernel<K, NPL, WAVES, A, RA, false, false, true, BT, false, true>));
   GL_LAUNCH(k.win ? GL_KERNEL_BWD_W_WIN : GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)),
             dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
@@ -1395,6 +1467,8 @@ static int launch_bwd_w(const BwK& k, hipStream_t s) {
 // read-ahead of 2 LDS reads (more would spill)
 template <int ACT>
 static int launch_bwd_w_act(int K, const BwK& k, hipStream_t s) {
+  if constexpr (ACT == GL_ACT_RELU)
+    if (K == 8 && k.fm) return launch_bwd_w_fm<8, bwd_npl(8), BWD_FM_WAVES, BWD_FM_RA>(k, s);
   if (K == 8) return launch_bwd_w<8, bwd_npl(8), bwd_waves(8), ACT, 2>(k, s);
   return launch_bwd_w<16, bwd_npl(16), bwd_waves(16), ACT, 2>(k, s);
 }
@@ -1517,6 +1591,7 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
   const bool sel = a->pool == GL_POOL_MAX || a->pool == GL_POOL_TOPK_MEAN;
   if (sel != (a->winner != nullptr)) return GL_ERR_ARG;  // selected slots exactly for max / top-k
   if (a->winner && a->S >= (1 << 21)) return GL_ERR_UNSUPPORTED;  // the event sort keys hold slot << 11
+  if (a->relu_mask && !relu_mask_layer(a->act, a->pool, a->K, a->rec_shift, a->x_dtype, a->D)) return GL_ERR_ARG;
   size_t need = 0;
   GL_TRY(gl_bwd_workspace(a, &need));
   if (!a->ws || a->ws_bytes < need) return GL_ERR_WORKSPACE;
@@ -1550,7 +1625,10 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     // the dense dW pass over full tiles of 4097..8192 inputs reads two-token tiles (two 64-KiB buffers)
     int ww = 0, npw = 0;
     const bool dense = !smooth && !a->winner;
-    const bool win = dense && window_staging(a->win, a->win_width, a->D, q.waves, q.cpg, a->G, &ww, &npw);
+    // the staged windows cover the pools of one workgroup: size them for the dW launch that runs
+    // (16 waves with the forward's ReLU bits, else bwd_waves)
+    const int dw_waves = a->relu_mask && a->K == 8 ? BWD_FM_WAVES : q.waves;
+    const bool win = dense && window_staging(a->win, a->win_width, a->D, dw_waves, q.cpg, a->G, &ww, &npw);
     const bool wide = dense && !win && tiles_of_two(a->D);
     // bf16 X keeps its bf16 values, 4 tokens per 8-byte slot (C4 dW 114.3 -> 90.2 ms against
     // two-token fp32 tiles: half the gathers and tile overheads per token for one widening per value)
@@ -1612,6 +1690,12 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
            sps, gs, tb, xb ? 1 : 0};
     bk.wbf = wbf;
     if (win) bk.win = a->win;
+    if (a->relu_mask) {  // the forward's bits, per 4-token tile of the batch
+      if (tb != BT) return GL_ERR_ARG;
+      bk.fm = (const uint16_t*)a->relu_mask;
+      bk.fm_tiles = ceil_div(a->B, BT);
+      bk.fm_t0 = b0 / BT;
+    }
     GL_TRY(launch_bwd_w_any(a->K, a->act, bk, s));
     DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
            (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, mask, W, part,

@@ -10,6 +10,7 @@
 // kernel merges the chunks of a group in a fixed order (reference: fwd_pool_kernel +
 // merge_finalize, sparse_pooling/kernels/triton_fused.py:289-358, kernels/ops.py:182-199).
 #include <mutex>
+#include <type_traits>
 
 #include "gl_common.h"
 #include "gl_internal.h"
@@ -107,15 +108,45 @@ struct FwdK {
   int ws_small;           // window staging in workgroups of half the waves (two per CU, 64 KiB of stages)
   int xb;                 // 4-token tiles of raw bf16 (8-byte slots; bf16 X, sum / mean)
   int wbf;                // W and bias stored as bf16 (widened in the kernel)
+  uint16_t* fm;           // ReLU bits for the backward ([n_chunks][fm_tiles][64] 16-bit words) or null
+  int fm_tiles, fm_t0;    // 4-token tiles of the whole batch; the pass's first tile
 };
+
+// ReLU activation bits of a lane's neurons for the backward, shifted in as they are decided: after
+// a tile, bit 15 - (4 j + i) of the 16-bit word is token i of the tile for the lane's neuron j.  The
+// kernel stores each tile's word (64 lanes x 2 bytes, one coalesced store), so no state is held
+// across tiles.  With them the backward's dW pass skips the recompute of z.  NoBits is the sink of
+// the kernels that keep none.
+struct NoBits {};
+struct ReluBits {
+  unsigned bits;
+};
+template <typename MB>
+__device__ __forceinline__ void relu_bits(MB&, int, float, float, float, float) {}
+// bits = 2 bits + (a > 0): the compare's lane mask is the carry-in of one add (two VALU per bit
+// where compare, select and or took three), issued here rather than sunk to the end of the tile,
+// which kept 16 activations live and spilled at 128 VGPRs
+__device__ __forceinline__ void relu_bit(unsigned& bits, float a) {
+  unsigned long long c;
+  asm volatile("v_cmp_lt_f32_e64 %1, 0, %2\n\tv_addc_co_u32_e64 %0, %1, %0, %0, %1"
+               : "+v"(bits), "=&s"(c)
+               : "v"(a));
+}
+__device__ __forceinline__ void relu_bits(ReluBits& m, int, float a0, float a1, float a2, float a3) {
+  relu_bit(m.bits, a0);
+  relu_bit(m.bits, a1);
+  relu_bit(m.bits, a2);
+  relu_bit(m.bits, a3);
+}
 
 // One token tile (4 tokens per 16-byte LDS entry at xsb): z = bias + sum_k w * x[idx], activation,
 // pooled over the wave's neurons and lanes (wave_sum4; lanes 0-3 store the 4 token sums).  The
 // first RA LDS reads of neuron j + 1 are issued before the arithmetic of neuron j, so up to K + RA
 // reads are in flight per wave (the compiler's own schedule keeps two).
-template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
+template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8), typename SRC = const char*,
+          typename MB = NoBits>
 __device__ __forceinline__ void fwd_tile(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
-                                         const float (&bias)[NPL], float* out, bool store, int lane) {
+                                         const float (&bias)[NPL], float* out, bool store, int lane, MB& mb) {
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
   float4 xc[K];
 #pragma unroll
@@ -142,6 +173,7 @@ __device__ __forceinline__ void fwd_tile(SRC xsb, const unsigned (&addr)[NPL][K]
     z1 = act_f<ACT>(z1);
     z2 = act_f<ACT>(z2);
     z3 = act_f<ACT>(z3);
+    relu_bits(mb, j, z0, z1, z2, z3);
     a0 += z0;
     a1 += z1;
     a2 += z2;
@@ -159,9 +191,9 @@ __device__ __forceinline__ void fwd_tile(SRC xsb, const unsigned (&addr)[NPL][K]
 // The sum / mean tile over a 4-token tile of raw bf16 values (8-byte slots, ds_read_b64): the gathers
 // keep the packed words (the read-ahead holds 2 registers per slot, not 4) and each value is
 // widened (shift or mask: exact) right before its FMA.  The arithmetic is fwd_tile's.
-template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8)>
+template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8), typename MB = NoBits>
 __device__ __forceinline__ void fwd_tile_bf4(const char* xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
-                                             const float (&bias)[NPL], float* out, bool store, int lane) {
+                                             const float (&bias)[NPL], float* out, bool store, int lane, MB& mb) {
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
   uint2 xc[K];
   auto ld = [&](unsigned a) {
@@ -192,6 +224,7 @@ __device__ __forceinline__ void fwd_tile_bf4(const char* xsb, const unsigned (&a
     z1 = act_f<ACT>(z1);
     z2 = act_f<ACT>(z2);
     z3 = act_f<ACT>(z3);
+    relu_bits(mb, j, z0, z1, z2, z3);
     a0 += z0;
     a1 += z1;
     a2 += z2;
@@ -585,30 +618,33 @@ constexpr bool pk_smooth(int pk) { return pk >= PK_LME; }
 constexpr int pk_sm_op(int pk) { return pk == PK_LME ? SM_LME : (pk == PK_POW ? SM_POW : SM_SW); }
 
 // sum / mean, max or top-k tile
-template <int K, int NPL, int ACT, bool FAR, int PK, typename SRC = const char*>
+template <int K, int NPL, int ACT, bool FAR, int PK, typename SRC = const char*, typename MB = NoBits>
 __device__ __forceinline__ void fwd_tile_any(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                              const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
-                                             int k, bool store, int lane) {
+                                             int k, bool store, int lane, MB& mb) {
   if constexpr (PK == PK_MAX) fwd_tile_max<K, NPL, ACT, FAR>(xsb, addr, w, bias, slot, out, oslot, store, lane);
   else if constexpr (PK == PK_TOPK) fwd_tile_topk<K, NPL, ACT, FAR>(xsb, addr, w, bias, slot, out, oslot, k, store, lane);
-  else fwd_tile<K, NPL, ACT, FAR>(xsb, addr, w, bias, out, store, lane);
+  else
+    fwd_tile<K, NPL, ACT, FAR>(xsb, addr, w, bias, out, store, lane, mb);
 }
 
 // smooth pools: the tile needs the validity bits and the operator's parameters
-template <int K, int NPL, int ACT, bool FAR, int PK, typename SRC = const char*>
+template <int K, int NPL, int ACT, bool FAR, int PK, typename SRC = const char*, typename MB = NoBits>
 __device__ __forceinline__ void fwd_tile_dispatch(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                                   const float (&bias)[NPL], const int (&slot)[NPL], unsigned vmask,
-                                                  float* out, int* oslot, int k, bool store, int lane, const FwdK& p) {
+                                                  float* out, int* oslot, int k, bool store, int lane, const FwdK& p,
+                                                  MB& mb) {
   if constexpr (pk_smooth(PK))
     fwd_tile_smooth<K, NPL, ACT, FAR, pk_sm_op(PK)>(xsb, addr, w, bias, vmask, out, store, lane, p.scale, p.pparam,
                                                     p.pint);
   else
-    fwd_tile_any<K, NPL, ACT, FAR, PK>(xsb, addr, w, bias, slot, out, oslot, k, store, lane);
+    fwd_tile_any<K, NPL, ACT, FAR, PK>(xsb, addr, w, bias, slot, out, oslot, k, store, lane, mb);
 }
 
 template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, int PK = PK_SUM, bool XG = false,
-          bool SMALL = false, int TB = BT, bool XB = false>
-__global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
+          bool SMALL = false, int TB = BT, bool XB = false, bool FM = false>
+// SMALL: two workgroups share a CU, so a wave must fit 128 VGPRs (4 waves per SIMD)
+__global__ void __launch_bounds__(WAVES * 64, SMALL ? 16 / WAVES * WAVES / 4 : 1) fwd_kernel(FwdK p) {
   // WS: xa holds both stage regions (2 * WS_TILES * nsl <= 2 * XTILE_DB slots, XTILE_DB with
   // SMALL); XG: no LDS tile; SMALL: one single-buffered tile of at most XTILE_DB 16-byte slots, so
   // two workgroups share a CU.  TB: tokens per tile (4, or 2 for the two-token tiles of DBUF sum /
@@ -616,6 +652,7 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   // XB: 4-token tiles of raw bf16 (8-byte slots, bf16 X), one buffer (SMALL) or two
   static_assert(TB == BT || (TB == 2 && DBUF && !WS && !XG && PK == PK_SUM), "two-token tiles: sum / mean, two buffers");
   static_assert(!XB || (TB == BT && (DBUF || SMALL || WS) && !XG && PK == PK_SUM), "bf16 tiles: sum / mean");
+  static_assert(!FM || (TB == BT && PK == PK_SUM && ACT == GL_ACT_RELU), "ReLU bits: 4-token tiles, sum / mean");
   constexpr int SLOT = XB ? 8 : 4 * TB;  // bytes per input of a tile or stage
   __shared__ float4 xa[WS ? (SMALL ? XTILE_DB : 2 * XTILE_DB) : (XG ? 1 : (DBUF || SMALL ? XTILE_DB : XTILE_SB))];
   __shared__ float4 xb[DBUF ? XTILE_DB : 1];
@@ -670,6 +707,17 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
   float* out = p.part + chunk * p.b_pad * kp;
   int* oslot = (PK == PK_MAX || PK == PK_TOPK) ? p.pslot + chunk * p.b_pad * kp : nullptr;
   const bool store = active;
+  // FM: every tile's ReLU bits go out as one 16-bit word per lane (128 contiguous bytes per wave)
+  static_assert(!FM || NPL == 4, "16 bits per lane and tile");
+  std::conditional_t<FM, ReluBits, NoBits> mb{};
+  // the chunk's row of words as a scalar base; a tile's store adds a 32-bit offset
+  char* const fmb = FM ? const_cast<char*>(uniform_ptr(p.fm + (chunk * p.fm_tiles + p.fm_t0) * 64)) : nullptr;
+  auto bits_done = [&](int t) {
+    if constexpr (FM) {
+      if (store) *reinterpret_cast<uint16_t*>(fmb + ((unsigned)t * 128u + (unsigned)lane * 2u)) = (uint16_t)mb.bits;
+      mb.bits = 0u;
+    }
+  };
   if constexpr (WS) {
     // window staging: WS_TILES tiles per stage and barrier; tile t at input (t mod 2 WS_TILES) * nsl
     // of the stage regions (IB bytes per input)
@@ -689,10 +737,12 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       for (int tt = 0; tt < tn; ++tt) {
         const int t = t0 + tt;
         if constexpr (XB)
-          fwd_tile_bf4<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
+          fwd_tile_bf4<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane,
+                                           mb);
         else
           fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
-                                                    out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
+                                                    out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p, mb);
+        bits_done(t);
         // next tile's slot; after the last tile of region 1 back to region 0
         const unsigned step = (t & (2 * WS_TILES - 1)) == 2 * WS_TILES - 1 ? tstep - 2u * WS_TILES * tstep : tstep;
 #pragma unroll
@@ -707,9 +757,11 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
     // D too wide for an LDS tile: the lanes gather their 16-byte slots straight from the token tile
     // in global memory with buffer loads (D x 16 bytes, L2-resident while the workgroups of the
     // launch read it), with no staging and no barriers
-    for (int t = 0; t < p.n_tiles; ++t)
+    for (int t = 0; t < p.n_tiles; ++t) {
       fwd_tile_dispatch<K, NPL, ACT, false, PK>(xbuf(p.xt + (long long)t * p.D, p.D), addr, w, bias, slot, vmask,
-                                                out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
+                                                out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p, mb);
+      bits_done(t);
+    }
   } else if constexpr (DBUF) {
     const int ns = (int)((long long)p.D * SLOT / 16);  // 16-byte slots per tile
     dma_tile(p.xt, xa, ns, NT);
@@ -718,24 +770,28 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       __syncthreads();  // tile t is in xa; every wave is done with xb (tile t - 1)
       if (t + 1 < p.n_tiles) dma_tile(p.xt + (long long)(t + 1) * ns, xb, ns, NT);
       if constexpr (XB)
-        fwd_tile_bf4<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
+        fwd_tile_bf4<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane,
+                                         mb);
       else if constexpr (TB == 2)
         fwd_tile2<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * 2, store, lane);
       else
         fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
-                                                  out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
+                                                  out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p, mb);
+      bits_done(t);
       if (t + 1 < p.n_tiles) {
         stage_wait();
         __syncthreads();  // tile t + 1 is in xb; every wave is done with xa
         if (t + 2 < p.n_tiles) dma_tile(p.xt + (long long)(t + 2) * ns, xa, ns, NT);
         if constexpr (XB)
           fwd_tile_bf4<K, NPL, ACT, true>(reinterpret_cast<const char*>(xb), addr, w, bias, out + (t + 1) * BT, store,
-                                          lane);
+                                          lane, mb);
         else if constexpr (TB == 2)
           fwd_tile2<K, NPL, ACT, true>(reinterpret_cast<const char*>(xb), addr, w, bias, out + (t + 1) * 2, store, lane);
         else
           fwd_tile_dispatch<K, NPL, ACT, true, PK>(reinterpret_cast<const char*>(xb), addr, w, bias, slot, vmask,
-                                                   out + (t + 1) * BT * kp, oslot + (t + 1) * BT * kp, kp, store, lane, p);
+                                                   out + (t + 1) * BT * kp, oslot + (t + 1) * BT * kp, kp, store, lane, p,
+                                                   mb);
+        bits_done(t + 1);
       }
     }
   } else {
@@ -746,10 +802,12 @@ __global__ void __launch_bounds__(WAVES * 64) fwd_kernel(FwdK p) {
       stage_wait();
       __syncthreads();
       if constexpr (XB)
-        fwd_tile_bf4<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane);
+        fwd_tile_bf4<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane,
+                                         mb);
       else
         fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
-                                                  out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p);
+                                                  out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p, mb);
+      bits_done(t);
     }
   }
 }
@@ -971,6 +1029,7 @@ __global__ void __launch_bounds__(256) fwd_finalize_smooth_kernel(const float* _
 // keeps a slot per neuron and a (value, slot) pair per token: 12 waves at K = 8, 4 at K = 16;
 // top-k keeps a sorted list of 4 pairs per token: 8 waves at K = 8, 4 at K = 16.
 constexpr int FWD_NPL = 4;
+static_assert(FWD_NPL == RELU_MASK_NPL, "the forward writes the ReLU bits chunk by chunk");
 constexpr int fwd_waves(int K, int pk = PK_SUM) {
   return K == 8 ? (pk == PK_SUM ? 16 : (pk == PK_MAX ? 12 : 8)) : (pk == PK_SUM ? 8 : 4);
 }
@@ -1046,6 +1105,8 @@ template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS, int PK, bool X
           int TB = BT, bool XB = false>
 static int launch_fwd(const FwdK& k, hipStream_t s) {
   auto fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, PK, XG, SMALL, TB, XB>;
+  if constexpr (PK == PK_SUM && ACT == GL_ACT_RELU && K == 8 && TB == BT)
+    if (k.fm) fn = fwd_kernel<K, NPL, WAVES, ACT, DBUF, WS, PK, XG, SMALL, TB, XB, true>;
   dim3 grid((unsigned)ceil_div(k.n_chunks, WAVES));
   GL_LAUNCH(WS ? GL_KERNEL_FWD_WIN : GL_KERNEL_FWD, fn, grid, dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
@@ -1189,6 +1250,11 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
     k.sps = a->sps > 1 ? a->sps : 1;
     k.gs = a->sps > 1 ? a->gs : a->S;
     k.wbf = a->w_dtype == GL_DTYPE_BF16;
+    if (a->relu_mask) {
+      k.fm = (uint16_t*)a->relu_mask;
+      k.fm_tiles = ceil_div(a->B, BT);
+      k.fm_t0 = b0 / BT;
+    }
     // sum / mean with bf16 X (even D <= 2 XTILE_DB) keeps X's bf16 values, 4 tokens per 8-byte slot,
     // in full tiles or windows: half the LDS bytes per gathered token for one exact widening per
     // value (C4 forward 81.8 -> 51.5 ms; at D = 4096 full tiles 16.4 -> 14.4 ms)
@@ -1325,8 +1391,17 @@ extern "C" int gl_fwd_workspace(const GlFwdArgs* a, size_t* bytes) {
   return 0;
 }
 
+extern "C" int gl_fwd_mask_bytes(const GlFwdArgs* a, size_t* bytes) {
+  if (!a || !bytes) return GL_ERR_ARG;
+  *bytes = relu_mask_layer(a->act, a->pool, a->K, a->rec_shift, a->x_dtype, a->D) && a->B > 0 && a->G > 0 && a->S > 0
+               ? relu_mask_bytes(a->G, a->S, a->B)
+               : 0;
+  return 0;
+}
+
 extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
   if (!a || !a->pre) return GL_ERR_ARG;
+  if (a->relu_mask && !relu_mask_layer(a->act, a->pool, a->K, a->rec_shift, a->x_dtype, a->D)) return GL_ERR_ARG;
   size_t need = 0;
   GL_TRY(gl_fwd_workspace(a, &need));
   if (!a->ws || a->ws_bytes < need) return GL_ERR_WORKSPACE;
@@ -1336,6 +1411,7 @@ extern "C" int gl_fwd(const GlFwdArgs* a, void* stream) {
 
 extern "C" int gl_fwd_static(const GlFwdArgs* a, void* stream) {
   if (!a || !a->pre) return GL_ERR_ARG;
+  if (a->relu_mask && !relu_mask_layer(a->act, a->pool, a->K, a->rec_shift, a->x_dtype, a->D)) return GL_ERR_ARG;
   size_t need = 0;
   GL_TRY(gl_fwd_workspace(a, &need));  // argument checks; ws / ws_bytes are ignored
   if (a->sched && a->K != 8) return GL_ERR_UNSUPPORTED;

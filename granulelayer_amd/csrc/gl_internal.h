@@ -46,6 +46,21 @@ int launch_tile_x_bf16x4(const void* X, long long sxb, int B, int D, int b0, int
 // Two-token tiles (tb = 2) for the inputs past one 16-byte-slot buffer: XTILE_DB < D <= 2 XTILE_DB, D even.
 inline bool tiles_of_two(int D) { return D > XTILE_DB && D <= 2 * XTILE_DB && D % 2 == 0; }
 
+// The forward's ReLU bits for the backward (GlFwdArgs / GlBwdArgs.relu_mask): ReLU mean / sum at
+// K = 8, where the forward and the dW pass both give a wave a chunk of RELU_MASK_NPL x 64 slots of
+// one pool with the same lane / slot assignment (sched_slot), one record per slot, and 4-token X
+// tiles in both passes (fp32 X over 4097..8192 inputs runs two-token tiles).  Layout: per chunk
+// and 4-token tile of the batch, 64 16-bit words (one per lane), bit 15 - (4 j + i) = token i of
+// the tile for the lane's neuron j.
+constexpr int RELU_MASK_NPL = 4;
+inline bool relu_mask_layer(int act, int pool, int K, int rec_shift, int x_dtype, int D) {
+  return act == GL_ACT_RELU && (pool == GL_POOL_MEAN || pool == GL_POOL_SUM) && K == 8 && rec_shift == 0 &&
+         !(x_dtype == GL_DTYPE_F32 && tiles_of_two(D));
+}
+inline size_t relu_mask_bytes(int G, int S, int B) {
+  return (size_t)G * (size_t)ceil_div(S, 64 * RELU_MASK_NPL) * (size_t)ceil_div(B, 4) * 64 * 2;
+}
+
 // Max / top-k pooling backward as selection events (gl_max_bwd.hip): dW / db / dX of one token
 // chunk [b0, b0 + Bc) from the chunk's token tiles, transposed coef / slots (c1t_kernel,
 // events_transpose_kernel) and the row-major g_pre / selected slots.

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define GL_ABI_VERSION 12
+#define GL_ABI_VERSION 13
 
 enum {
   GL_OK = 0,
@@ -102,6 +102,13 @@ typedef struct GlFwdArgs {
   int32_t w_dtype;        /* W and bias: GL_DTYPE_F32, or GL_DTYPE_BF16 read and widened in the kernels
                              (the reference's kernels load W in its stored dtype and widen it,
                              sparse_pooling/kernels/triton_fused.py:257) */
+  void* relu_mask;        /* out or NULL: the ReLU bit (z > 0) of every (token, neuron), in the kernels'
+                             own order, for GlBwdArgs.relu_mask; gl_fwd_mask_bytes() bytes.  Only for
+                             the layers that query gives a non-zero size (GL_ACT_RELU with
+                             GL_POOL_MEAN / GL_POOL_SUM, K = 8, rec_shift 0, 4-token X tiles).  The
+                             reference keeps no such statistic: its backward recomputes z
+                             (sparse_pooling/kernels/triton_fused.py:364-374); 1/32 of the [B, N]
+                             hidden tensor's bytes buys the backward's dW pass that recompute */
 } GlFwdArgs;
 
 /* Backward arguments.  Replaces the reference's BwdArgs + sp_bwd (sparse_pool_bwd.cuh:45-66,
@@ -144,6 +151,9 @@ typedef struct GlBwdArgs {
                              fewer recompute and dX passes per token (the workspace query includes
                              it).  dW / db sum over the chunks, so their rounding depends on it */
   int32_t w_dtype;        /* as GlFwdArgs.w_dtype; dW and db are fp32 whatever it is */
+  const void* relu_mask;  /* or NULL: the bits gl_fwd wrote into GlFwdArgs.relu_mask for the same X,
+                             idx, W, bias, counts, sched and B; the dW pass then reads them instead of
+                             recomputing z (results identical bit for bit) */
 } GlBwdArgs;
 
 /* Input-major (transposed) edge list of a layer, built once per index tensor.  It has no
@@ -223,6 +233,10 @@ const char* gl_error_string(int code);
 /* Forward.  gl_fwd_workspace writes the workspace size for these arguments to *bytes. */
 int gl_fwd_workspace(const GlFwdArgs* a, size_t* bytes);
 int gl_fwd(const GlFwdArgs* a, void* stream);
+/* Bytes of GlFwdArgs.relu_mask for these arguments, 0 when the layer has no ReLU bits (then
+ * relu_mask must be NULL).  No counterpart in the reference (whose backward recomputes z,
+ * sparse_pooling/kernels/triton_fused.py:364-374). */
+int gl_fwd_mask_bytes(const GlFwdArgs* a, size_t* bytes);
 
 /* Forward that allocates nothing and takes no workspace.  No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph capture, tight serving

@@ -190,3 +190,25 @@ def test_an_explicit_workspace_budget_is_honoured():
     assert big - small >= (1024 - 128) * (4 << 20)
     assert small - bwd_ws(DEFAULT_WORKSPACE_BUDGET, B=128) < (1 << 20)  # B = 128: the same one chunk
     assert bwd_ws(DEFAULT_WORKSPACE_BUDGET // 2) < small
+
+
+def test_relu_bit_sizes_follow_the_layer():
+    """gl_fwd_mask_bytes: G x ceil(S / 256) chunks x ceil(B / 4) tiles x 64 lanes x 2 bytes for ReLU
+    mean / sum at fan-in 8 with 4-token tiles; 0 for the layers without bits (fp32 X over
+    4097..8192 inputs runs two-token tiles, fan-in 16, other activations or pools, shared records)."""
+    lib = N.library()
+
+    def size(**kw):
+        a = N.GlFwdArgs(**{"B": 300, "D": 1024, "G": 64, "S": 1024, "K": 8, "act": N.GL_ACT["relu"],
+                           "pool": N.GL_POOL["sum"], **kw})
+        return lib.size_query("gl_fwd_mask_bytes", a)
+
+    assert size() == 64 * 4 * 75 * 128
+    assert size(B=301, S=1000) == 64 * 4 * 76 * 128
+    assert size(pool=N.GL_POOL["mean"], D=6000, x_dtype=N.GL_DTYPE_BF16) == 64 * 4 * 75 * 128
+    assert size(D=12000) == 64 * 4 * 75 * 128
+    assert size(D=6000) == 0
+    assert size(K=16) == 0
+    assert size(act=N.GL_ACT["gelu"]) == 0
+    assert size(pool=N.GL_POOL["max"]) == 0
+    assert size(rec_shift=4) == 0
