@@ -155,6 +155,7 @@ class Level1Runtime:
         self.backend = backend
         self.last_info: Dict = {}
         self.det = False
+        self.grad_call = True  # set per call by the layer: grad mode was on (a backward can follow)
 
     def check_devices(self, *tensors):
         dev = self.idx.device
@@ -190,6 +191,7 @@ class Level1Runtime:
         out = (self.backend.forward(self, x, w, b, track_ids, relu_mask=True) if relu_mask
                else self.backend.forward(self, x, w, b, track_ids))
         self.last_info["forward_backend"] = "hip"
+        self.last_info["forward_relu_mask"] = "relu_mask" in out
         return out
 
     # --------------------------------------------------------------- backward
@@ -295,10 +297,11 @@ class SparsePoolFunction(torch.autograd.Function):
         policy = fit_policy(rt, policy, x.shape[0])
         xc, wc, bc = _compute_operands(x, w, b, compute_dtype)
         lv = rt.level
-        # the ReLU bits (PhysicalPlan.relu_bits="keep") only when a backward will run and the
-        # policy keeps statistics
+        # the ReLU bits (PhysicalPlan.relu_bits="keep") only when a backward can run (grad mode on
+        # at the call, recorded by rt.grad_call: inside forward it is always off) and the policy
+        # keeps statistics
         keep_bits = (getattr(rt.plan, "relu_bits", "recompute") == "keep" and policy != "recompute_stats"
-                     and any(ctx.needs_input_grad[:3]))
+                     and getattr(rt, "grad_call", True) and any(ctx.needs_input_grad[:3]))
         out = rt.forward(xc, wc, bc, track_ids=(policy == "save_winners"), relu_mask=keep_bits)
         pre = out["pre"]
         y = act_torch(pre, lv.out_activation)

@@ -428,7 +428,9 @@ class CoverTopK16Layer(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         lead = x.shape[:-1]
         x2 = x.reshape(-1, x.shape[-1])
-        y = SparsePoolFunction.apply(x2, self.weight, self.bias, self._runtime(), self.effective_policy,
+        rt = self._runtime()
+        rt.grad_call = torch.is_grad_enabled()
+        y = SparsePoolFunction.apply(x2, self.weight, self.bias, rt, self.effective_policy,
                                      self.compute_dtype)
         return y.reshape(*lead, y.shape[-1])
 

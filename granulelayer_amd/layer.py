@@ -154,6 +154,7 @@ class SparsePoolingLayer(nn.Module):
             y = SemanticPoolFunction.apply(x2, self.weight, self.bias, rt, self.cfg, self.effective_policy,
                                            self.compute_dtype, self._tnames, *tparams)
         else:
+            rt.grad_call = torch.is_grad_enabled()
             y = SparsePoolFunction.apply(x2, self.weight, self.bias, rt, self.effective_policy, self.compute_dtype)
         return y.reshape(*lead, y.shape[-1])
 

@@ -120,6 +120,10 @@ def test_layer_with_relu_bits_matches_oracle(pool):
     assert_parity(lay.weight.main_grad.cpu().numpy().reshape(-1, K), wdW, mW, uW, what="dW")
     assert_parity(lay.bias.main_grad.cpu().numpy().reshape(-1), wdb, mb, ub, what="db")
 
+    with torch.no_grad():  # no backward can follow: no bits
+        lay(x)
+    assert not lay.last_info["forward_relu_mask"]
+
     dflt = SparsePoolingLayer(D, H, G, shared_neurons=None, pooling=pool, dtype=torch.float32, device=DEV, seed=3)
     dflt.enable_main_grad()
     dflt(x).sum().backward()
