@@ -264,17 +264,19 @@ __device__ __forceinline__ void bwd_w_tile2(const char* xsb, int t, const float2
 // load, wait, read.  The wave index goes through readfirstlane so the chunk's parameters and the
 // c1 row are addressed with scalar registers.
 template <int K, int NPL, int WAVES, int ACT, int RA, bool DBUF, bool WS = false, bool XG = false, int TB = BT,
-          bool XB = false, bool FM = false>
-__global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
+          bool XB = false, bool FM = false, bool SMALL = false>
+__global__ void __launch_bounds__(WAVES * 64, SMALL ? 4 : 1) bwd_w_kernel(BwK p) {
   // XG (D > XTILE_SB): no LDS tile, the lanes gather from the token tiles in global memory.
   // TB: tokens per tile, 4 or 2 (two-token tiles in the two buffers of DBUF: D <= 2 XTILE_DB)
   static_assert(TB == BT || (TB == 2 && DBUF && !WS && !XG), "two-token tiles: double-buffered only");
   // XB: 4-token tiles of raw bf16 (8-byte slots, bf16 X), double-buffered
-  static_assert(!XB || (TB == BT && DBUF && !WS && !XG), "bf16 tiles: double-buffered only");
+  static_assert(!XB || (TB == BT && (DBUF || SMALL) && !WS && !XG), "bf16 tiles: double- or small-buffered");
+  // SMALL: one single-buffered 64-KiB tile per workgroup, two workgroups per CU (128 VGPRs at most)
+  static_assert(!SMALL || (!DBUF && !WS && !XG && TB == BT), "small: one 4-token tile per workgroup");
   // FM: the mask bits come from the forward (p.fm): no z recompute, W and bias are not read
   static_assert(!FM || (TB == BT && ACT == GL_ACT_RELU), "forward ReLU bits: 4-token tiles, ReLU");
   constexpr unsigned SLOT = XB ? 8u : 4u * TB;  // bytes per input of a tile
-  __shared__ float4 xs[DBUF || WS ? 2 * XTILE_DB : (XG ? 1 : XTILE_SB)];
+  __shared__ float4 xs[DBUF || WS ? 2 * XTILE_DB : (XG ? 1 : (SMALL ? XTILE_DB : XTILE_SB))];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   long long chunk = (long long)blockIdx.x * WAVES + wave;
@@ -408,12 +410,16 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_w_kernel(BwK p) {
         __syncthreads();
       } else {
         __syncthreads();  // every wave is done with tile t - 1
-        dma_tile(p.xt + (long long)t * p.D, xs, p.D, NT);
+        dma_tile(p.xt + (long long)t * ns, xs, ns, NT);
         const float4 c1 = ld_uniform4(c1row, t * BT);
         stage_wait();
         __syncthreads();
-        bwd_w_tile<K, NPL, ACT, RA, false, const char*, FM>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw,
-                                                           dbv, mw, fbits(t));
+        if constexpr (XB)
+          bwd_w_tile_bf4<K, NPL, ACT, RA, false, FM>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw, dbv,
+                                                     mw, fbits(t));
+        else
+          bwd_w_tile<K, NPL, ACT, RA, false, const char*, FM>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias,
+                                                             dw, dbv, mw, fbits(t));
       }
     }
     const int word = t0 / TPW;
@@ -728,79 +734,95 @@ __global__ void __launch_bounds__(64) dx_kernel(DxK p) {
   }
 }
 
-// The 256-token slice kernel (T = 4) with the chunk's gathers copied to LDS by the memory
-// pipeline (global_load_lds): per edge the weight (one dword) and the neuron's 8 mask words (two
-// 16-byte halves) land in a double buffer with no VGPR round trip and no staging stores, so the
-// wave holds 64 VGPRs and a SIMD runs 8 waves instead of 6.  The arithmetic is dx_kernel's, in
-// the same order.  LDS per wave: two buffers of [2 halves][64 edges] 16-byte mask quads and
-// [64] weights, and the 16-entry bits-to-floats table.  A half holds 65 rows: row i of half 1 then
-// sits 4 banks past row i of half 0, so the two half-waves' reads of one edge (lanes 0-31 words
-// 0-3, lanes 32-63 words 4-7) never share a bank.
+// The slice kernel (T = 4 tokens per lane and slice) with the chunk's gathers copied to LDS by the
+// memory pipeline (global_load_lds): per edge the weight (one dword) and, for each of the wave's NS
+// slices of 256 tokens, the neuron's 8 mask words of that slice (two 16-byte halves) land in a
+// double buffer with no VGPR round trip and no staging stores.  NS = 1 holds 64 VGPRs (8 waves per
+// SIMD); NS = 2 (512-token layers and up) walks each edge once for two slices, so the record, the
+// weight, the run bounds and the per-chunk control are paid once per 512 tokens (4 waves per SIMD).
+// The arithmetic of every token is dx_kernel's, in the same order.  LDS per wave: two buffers of
+// [2 NS halves][64 edges] 16-byte mask quads and [64] weights, and the 16-entry bits-to-floats
+// table.  A half holds 65 rows: row i of half h + 1 then sits 4 banks past row i of half h, so the
+// two half-waves' reads of one edge (lanes 0-31 words 0-3, lanes 32-63 words 4-7) never share a bank.
+template <int NS>
 struct __align__(16) DxDma {
-  uint4 m[2][2][65];
+  uint4 m[2][2 * NS][65];
   float w[2][64];
   float lut[16][4];
 };
+// words between slice s and slice s + 1 of one half of a buffer
+constexpr int DX_SLICE_WORDS = 2 * 65 * 4;
 
-// the chunk's weights and mask rows -> buffer buf (lanes past the chunk copy the first edge's)
-template <int K>
-__device__ __forceinline__ void dx_dma(const DxK& p, const uint32_t* mask_tc, const DxChunk& c, unsigned rec,
-                                       DxDma& st, int buf) {
+// the chunk's weights and the NS slices' mask rows -> buffer buf (lanes past the chunk copy the
+// first edge's); slice s reads slab tc0 + s of the mask
+template <int K, int NS>
+__device__ __forceinline__ void dx_dma(const DxK& p, int tc0, const DxChunk& c, unsigned rec, DxDma<NS>& st, int buf) {
   const long long nb = pool_base(c.u / p.P, p.S, p.sps, p.gs) + (long long)(c.u % p.P) * US;  // first neuron of the unit
   const unsigned woff = rec & REC_OFF_MASK;  // byte offset of W[n, k] in the unit
   const unsigned mo = (woff >> (K == 8 ? 5 : 6)) * 32u;  // byte offset of the neuron's mask row
   // bf16 W: the 32-bit word holding the weight (its half is taken when the chunk is read)
   const unsigned wo = p.wbf ? (woff >> 1) & ~3u : woff;
   const char* ws = p.wbf ? uniform_ptr(reinterpret_cast<const unsigned short*>(p.W) + nb * K) : uniform_ptr(p.W + nb * K);
-  const char* ms = uniform_ptr(mask_tc + nb * 8);
   const unsigned lw = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&st.w[buf][0]);
-  const unsigned l0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&st.m[buf][0][0]);
-  const unsigned l1 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&st.m[buf][1][0]);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, %2"
                :: "v"(wo), "s"(lw), "s"(ws) : "memory", "m0");
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
-               :: "v"(mo), "s"(l0), "s"(ms) : "memory", "m0");
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
-               :: "v"(mo + 16u), "s"(l1), "s"(ms) : "memory", "m0");
+#pragma unroll
+  for (int sl = 0; sl < NS; ++sl) {
+    const char* ms = uniform_ptr(p.mask + ((long long)(tc0 + sl) * p.NS + nb) * 8);
+    const unsigned l0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&st.m[buf][2 * sl][0]);
+    const unsigned l1 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)&st.m[buf][2 * sl + 1][0]);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
+                 :: "v"(mo), "s"(l0), "s"(ms) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
+                 :: "v"(mo + 16u), "s"(l1), "s"(ms) : "memory", "m0");
+  }
 }
 
-// dx_run over the DMA layout: mrow = the lane's mask word of edge 0 (rows 16 bytes apart); wl =
-// the weight of the lane's own edge, edge i's weight taken from lane i (v_readlane, one VALU
-// instead of one more LDS read per edge)
-template <int X>
+// dx_run over the DMA layout: mrow = the lane's mask word of edge 0 in slice 0 (rows 16 bytes
+// apart, slice s DX_SLICE_WORDS further); wl = the weight of the lane's own edge, edge i's weight
+// taken from lane i (v_readlane, one VALU instead of one more LDS read per edge)
+template <int X, int NS>
 __device__ __forceinline__ void dx_run_dma(const unsigned* mrow, float wl, const float (*lut)[4], int i0, int i1,
-                                           unsigned bit, const float (&c1)[4], float (&acc)[FW][4]) {
+                                           unsigned bit, const float (&c1)[NS][4], float (&acc)[NS][FW][4]) {
   int len = i1 - i0;
   asm volatile("" : "+s"(len));
   if (len <= 0) return;
   const unsigned* m = mrow + 4 * i0;
-  float s[4];
+  float s[NS][4];
   {
-    const unsigned v = __builtin_amdgcn_ubfe(*m, bit, 4u);
-    const float4 t = *reinterpret_cast<const float4*>(&lut[v][0]);
     const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), i0));
-    s[0] = t.x * wv, s[1] = t.y * wv, s[2] = t.z * wv, s[3] = t.w * wv;
+#pragma unroll
+    for (int sl = 0; sl < NS; ++sl) {
+      const unsigned v = __builtin_amdgcn_ubfe(m[sl * DX_SLICE_WORDS], bit, 4u);
+      const float4 t = *reinterpret_cast<const float4*>(&lut[v][0]);
+      s[sl][0] = t.x * wv, s[sl][1] = t.y * wv, s[sl][2] = t.z * wv, s[sl][3] = t.w * wv;
+    }
   }
   for (int i = i0 + 1; i < i1; ++i) {
     m += 4;
-    const unsigned v = __builtin_amdgcn_ubfe(*m, bit, 4u);
-    const float4 t = *reinterpret_cast<const float4*>(&lut[v][0]);
     const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), i));
-    s[0] = __builtin_fmaf(t.x, wv, s[0]);
-    s[1] = __builtin_fmaf(t.y, wv, s[1]);
-    s[2] = __builtin_fmaf(t.z, wv, s[2]);
-    s[3] = __builtin_fmaf(t.w, wv, s[3]);
+#pragma unroll
+    for (int sl = 0; sl < NS; ++sl) {
+      const unsigned v = __builtin_amdgcn_ubfe(m[sl * DX_SLICE_WORDS], bit, 4u);
+      const float4 t = *reinterpret_cast<const float4*>(&lut[v][0]);
+      s[sl][0] = __builtin_fmaf(t.x, wv, s[sl][0]);
+      s[sl][1] = __builtin_fmaf(t.y, wv, s[sl][1]);
+      s[sl][2] = __builtin_fmaf(t.z, wv, s[sl][2]);
+      s[sl][3] = __builtin_fmaf(t.w, wv, s[sl][3]);
+    }
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[X][j] = __builtin_fmaf(c1[j], s[j], acc[X][j]);
+  for (int sl = 0; sl < NS; ++sl)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[sl][X][j] = __builtin_fmaf(c1[sl][j], s[sl][j], acc[sl][X][j]);
 }
 
-template <int X>
+template <int X, int NS>
 __device__ __forceinline__ void dx_runs_dma(const unsigned* mrow, float wl, const float (*lut)[4],
-                                            const int (&b)[FW + 1], unsigned bit, const float (&c1)[4],
-                                            float (&acc)[FW][4]) {
-  dx_run_dma<X>(mrow, wl, lut, b[X], b[X + 1], bit, c1, acc);
-  if constexpr (X + 1 < FW) dx_runs_dma<X + 1>(mrow, wl, lut, b, bit, c1, acc);
+                                            const int (&b)[FW + 1], unsigned bit, const float (&c1)[NS][4],
+                                            float (&acc)[NS][FW][4]) {
+  dx_run_dma<X, NS>(mrow, wl, lut, b[X], b[X + 1], bit, c1, acc);
+  if constexpr (X + 1 < FW) dx_runs_dma<X + 1, NS>(mrow, wl, lut, b, bit, c1, acc);
 }
 
 // dx_next with the segment table read one step ahead: (pe, pu) hold the end and the unit of
@@ -826,15 +848,21 @@ __device__ __forceinline__ void dx_next_ahead(const DxK& p, DxChunk& c, int hi, 
   }
 }
 
-// c1 of the lane's 4 tokens for the pool of unit u: a uniform row base (scalar registers) plus the
-// lane's 32-bit offset (no 64-bit vector address to keep live)
-__device__ __forceinline__ void dx_load_c1_u(const DxK& p, int u, int slice0, int lane, float (&c1)[4]) {
-  const uint4 v = ld_uniform_u128(p.c1t + (long long)(u / p.P) * p.cap + slice0, (unsigned)lane * 16u);
-  c1[0] = __uint_as_float(v.x), c1[1] = __uint_as_float(v.y), c1[2] = __uint_as_float(v.z), c1[3] = __uint_as_float(v.w);
+// c1 of the lane's 4 tokens of each of the NS slices for the pool of unit u: a uniform row base
+// (scalar registers) plus the lane's 32-bit offset (no 64-bit vector address to keep live)
+template <int NS>
+__device__ __forceinline__ void dx_load_c1_u(const DxK& p, int u, int slice0, int lane, float (&c1)[NS][4]) {
+#pragma unroll
+  for (int sl = 0; sl < NS; ++sl) {
+    const uint4 v = ld_uniform_u128(p.c1t + (long long)(u / p.P) * p.cap + slice0 + sl * 256, (unsigned)lane * 16u);
+    c1[sl][0] = __uint_as_float(v.x), c1[sl][1] = __uint_as_float(v.y), c1[sl][2] = __uint_as_float(v.z),
+    c1[sl][3] = __uint_as_float(v.w);
+  }
 }
 
-template <int K>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8))) dx_dma_kernel(DxK p) {
+template <int K, int NS>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NS == 1 ? 8 : 4, NS == 1 ? 8 : 4)))
+dx_dma_kernel(DxK p) {
   constexpr int T = 4;
   const int lane = threadIdx.x;
   // block order as dx_kernel: all feature ranges of a unit range side by side on one XCD
@@ -844,7 +872,7 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))
   const int F = loc % p.FR;
   const int rest = loc / p.FR;
   const int ql = rest % p.QL;
-  const int tc = rest / p.QL;
+  const int tc0 = (rest / p.QL) * NS;  // the wave's first 256-token slice
   const int q = ql * 8 + xcd;
   const int u_lo = q * p.UQ;
   const int u_hi = min(u_lo + p.UQ, p.U);
@@ -863,17 +891,17 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))
     }
     hi = a;
   }
-  float acc[FW][T];
+  float acc[NS][FW][T];
 #pragma unroll
-  for (int f = 0; f < FW; ++f)
+  for (int sl = 0; sl < NS; ++sl)
 #pragma unroll
-    for (int j = 0; j < T; ++j) acc[f][j] = 0.f;
+    for (int f = 0; f < FW; ++f)
+#pragma unroll
+      for (int j = 0; j < T; ++j) acc[sl][f][j] = 0.f;
 
-  const int tok0 = tc * 64 * T + T * lane;
   const unsigned bit = (unsigned)(T * lane) & 31u;
   const int word = (T * lane) >> 5;  // the lane's word of a mask row: half word / 4, dword word % 4
-  const uint32_t* mask_tc = p.mask + (long long)tc * p.NS * (2 * T);
-  __shared__ DxDma st;
+  __shared__ DxDma<NS> st;
   if (lane < 16) {
 #pragma unroll
     for (int j = 0; j < T; ++j) st.lut[lane][j] = (lane >> j) & 1 ? 1.0f : 0.0f;
@@ -886,19 +914,21 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))
     dx_next_ahead(p, cn, hi, pe, pu);
     const unsigned rc0 = dx_load_rec(p, cc, lane);
     unsigned rn = cn.si < hi ? dx_load_rec(p, cn, lane) : 0u;
-    dx_dma<K>(p, mask_tc, cc, rc0, st, 0);
+    dx_dma<K, NS>(p, tc0, cc, rc0, st, 0);
     unsigned rc = rc0;
-    float c1[T];
-    dx_load_c1_u(p, cc.u, tc * 64 * T, lane, c1);
+    float c1[NS][T];
+    dx_load_c1_u<NS>(p, cc.u, tc0 * 64 * T, lane, c1);
     int cur = 0;
     for (;;) {
       // every copy, load and LDS read so far is done: buffer cur holds chunk cc, and buffer
       // cur ^ 1 (read by the previous chunk) may be refilled
       __builtin_amdgcn_s_waitcnt(0);
       const bool more = cn.si < hi;
-      float c1n[T];
+      float c1n[NS][T];
 #pragma unroll
-      for (int j = 0; j < T; ++j) c1n[j] = c1[j];
+      for (int sl = 0; sl < NS; ++sl)
+#pragma unroll
+        for (int j = 0; j < T; ++j) c1n[sl][j] = c1[sl][j];
       DxChunk cnn = cn;
       unsigned rnn = 0u;
       if (more) {
@@ -906,8 +936,8 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))
         // the copy (the counter is in order); their values were loaded one step ago
         dx_next_ahead(p, cnn, hi, pe, pu);
         if (cnn.si < hi) rnn = dx_load_rec(p, cnn, lane);
-        dx_dma<K>(p, mask_tc, cn, rn, st, cur ^ 1);
-        if (cn.si != cc.si) dx_load_c1_u(p, cn.u, tc * 64 * T, lane, c1n);
+        dx_dma<K, NS>(p, tc0, cn, rn, st, cur ^ 1);
+        if (cn.si != cc.si) dx_load_c1_u<NS>(p, cn.u, tc0 * 64 * T, lane, c1n);
       }
       {
         const int n = (int)min(cc.end - cc.e, 64u);
@@ -920,13 +950,15 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))
         const unsigned* mrow = reinterpret_cast<const unsigned*>(&st.m[opaque(cur)][word >> 2][0]) + (word & 3);
         float wl = st.w[opaque(cur)][lane];
         if (p.wbf) wl = bf16_half(__float_as_uint(wl), (rc & REC_OFF_MASK) >> 1);
-        dx_runs_dma<0>(mrow, wl, st.lut, b, bit, c1, acc);
+        dx_runs_dma<0, NS>(mrow, wl, st.lut, b, bit, c1, acc);
       }
       if (!more) break;
       cc = cn;
       rc = rn;
 #pragma unroll
-      for (int j = 0; j < T; ++j) c1[j] = c1n[j];
+      for (int sl = 0; sl < NS; ++sl)
+#pragma unroll
+        for (int j = 0; j < T; ++j) c1[sl][j] = c1n[sl][j];
       cn = cnn;
       rn = rnn;
       cur ^= 1;
@@ -934,11 +966,15 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(8, 8)))
   }
   float* out = p.part + (long long)q * p.D * p.cap;
 #pragma unroll
-  for (int f = 0; f < FW; ++f) {
-    const int d = F * FW + f;
-    if (d < p.D) {
+  for (int sl = 0; sl < NS; ++sl) {
+    const int tok0 = (tc0 + sl) * 64 * T + T * lane;
 #pragma unroll
-      for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j] = acc[f][j];
+    for (int f = 0; f < FW; ++f) {
+      const int d = F * FW + f;
+      if (d < p.D) {
+#pragma unroll
+        for (int j = 0; j < T; ++j) out[(long long)d * p.cap + tok0 + j] = acc[sl][f][j];
+      }
     }
   }
 }
@@ -1341,8 +1377,14 @@ static_assert(bwd_npl(8) == RELU_MASK_NPL, "the dW pass reads the forward's ReLU
 constexpr int smooth_npl(int K) { return 2; }
 constexpr int smooth_sb(int K) { return K == 8 ? 8 : 2; }
 constexpr int bwd_waves(int K) { return K == 8 ? 12 : 8; }
+#ifndef DX_DMA_TWO_SLICES
+#define DX_DMA_TWO_SLICES 1
+#endif
 #ifndef BWD_FM_WAVES
 #define BWD_FM_WAVES 16
+#endif
+#ifndef BWD_FM_SMALL
+#define BWD_FM_SMALL 1
 #endif
 #ifndef BWD_FM_RA
 #define BWD_FM_RA 1
@@ -1453,6 +1495,17 @@ static int launch_bwd_w(const BwK& k, hipStream_t s) {
 template <int K, int NPL, int WAVES, int RA>
 static int launch_bwd_w_fm(const BwK& k, hipStream_t s) {
   constexpr int A = GL_ACT_RELU;
+  // full tiles of at most 64 KiB (fp32 D <= 4096, bf16 D <= 8192): two workgroups of WAVES / 2
+  // waves per CU, each with one single-buffered tile, the forward's arrangement: while one waits
+  // at its tile barrier the other computes
+  if (BWD_FM_SMALL && !k.win && (k.xb || k.D <= XTILE_DB)) {
+    constexpr int W2 = WAVES / 2;
+    auto fs = k.xb ? bwd_w_kernel<K, NPL, W2, A, RA, false, false, false, BT, true, true, true>
+                   : bwd_w_kernel<K, NPL, W2, A, RA, false, false, false, BT, false, true, true>;
+    GL_LAUNCH(GL_KERNEL_BWD_W, fs, dim3((unsigned)ceil_div(k.n_chunks, W2)), dim3(W2 * 64), 0, s, k);
+    GL_CHECK_LAUNCH();
+    return 0;
+  }
   auto fn = k.win ? bwd_w_kernel<K, NPL, WAVES, A, RA, false, true, false, BT, false, true>
             : k.xb ? bwd_w_kernel<K, NPL, WAVES, A, RA, true, false, false, BT, true, true>
             : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, A, RA, true, false, false, BT, false, true>
@@ -1479,8 +1532,18 @@ static int launch_bwd_w_any(int K, int act, const BwK& k, hipStream_t s) {
 
 template <int K, int T>
 static int launch_dx_kt(const DxK& k, hipStream_t s, bool dma) {
-  auto fn = T == 4 && dma ? dx_dma_kernel<K> : dx_kernel<K, T>;
-  GL_LAUNCH(T == 4 && dma ? GL_KERNEL_DX_DMA : GL_KERNEL_DX, fn, dim3((unsigned)(8LL * k.FR * k.QL * k.n_tc)), dim3(64), 0, s, k);
+  if constexpr (T == 4) {
+    if (dma) {  // two 256-token slices per wave when the chunk has an even number of them
+      const bool two = k.n_tc % 2 == 0 && DX_DMA_TWO_SLICES;
+      auto fn = two ? dx_dma_kernel<K, 2> : dx_dma_kernel<K, 1>;
+      GL_LAUNCH(GL_KERNEL_DX_DMA, fn, dim3((unsigned)(8LL * k.FR * k.QL * (two ? k.n_tc / 2 : k.n_tc))), dim3(64), 0,
+                s, k);
+      GL_CHECK_LAUNCH();
+      return 0;
+    }
+  }
+  auto fn = dx_kernel<K, T>;
+  GL_LAUNCH(GL_KERNEL_DX, fn, dim3((unsigned)(8LL * k.FR * k.QL * k.n_tc)), dim3(64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;
 }
