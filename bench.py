@@ -183,6 +183,97 @@ def _plan():
     return PhysicalPlan(relu_bits=RELU_BITS)
 
 
+def lds_patterns(bytes_: int, kind: str, rng) -> "np.ndarray":
+    """Byte offsets into a 64-KiB LDS tile for 8 reads x 64 lanes of one gather pattern.
+
+    A bank row is 256 bytes (64 banks of 4 bytes), so a 16-byte slot's residue is slot mod 16 and an
+    8-byte slot's is slot mod 32; `kind` fixes the residue each lane reads, the row is random."""
+    import numpy as np
+
+    nres = 256 // bytes_
+    nrow = 65536 // 256
+    out = np.empty((8, 64), dtype=np.uint32)
+    for r in range(8):
+        if kind == "linear":  # lane l reads slot l: every bank once per 256 bytes
+            res = np.arange(64) % nres
+            rows = np.arange(64) // nres
+        else:
+            rows = rng.integers(0, nrow, 64)
+            if kind == "random":
+                res = rng.integers(0, nres, 64)
+            elif kind == "rows_distinct":  # each 16-lane row a permutation of 16 residues
+                res = np.concatenate([rng.permutation(nres)[:16] for _ in range(4)])
+            elif kind in ("rows_matched", "rows_matched_swapped"):
+                # lanes 16-31 read the residue set of lanes 0-15 per 4-lane block (any order), and
+                # lanes 48-63 that of lanes 32-47; rows distinct
+                res = np.empty(64, dtype=np.int64)
+                for h in (0, 32):
+                    a = rng.permutation(nres)[:16]
+                    b = np.concatenate([rng.permutation(a[4 * k:4 * k + 4]) for k in range(4)])
+                    if kind == "rows_matched_swapped":  # blocks 0 and 1 of the second row trade sets
+                        b = np.concatenate([b[4:8], b[0:4], b[8:]])
+                    res[h:h + 16], res[h + 16:h + 32] = a, b
+            elif kind == "halves_distinct":  # each 32-lane half a permutation of 32 residues
+                res = np.concatenate([rng.permutation(nres)[:32] for _ in range(2)])
+            elif kind == "halves_one_repeat":  # the same with one residue read twice in each half
+                hs = []
+                for _ in range(2):
+                    h = rng.permutation(nres)[:32]
+                    h[31] = h[0]
+                    hs.append(h)
+                res = np.concatenate(hs)
+            elif kind == "rows16_colliding":  # 16-lane rows distinct, both rows of a half the same 16
+                hs = []
+                for _ in range(2):
+                    a = rng.permutation(nres)[:16]
+                    hs += [a, rng.permutation(a)]
+                res = np.concatenate(hs)
+            else:
+                raise ValueError(kind)
+        out[r] = (rows * 256 + res * bytes_).astype(np.uint32)
+    return out
+
+
+def lds_probe(iters: int = 20000):
+    """`bench.py --lds-probe`: one workgroup of 16 waves per CU reads 8 independent patterns per
+    loop iteration with ds_read_b128 (16-byte slots) or ds_read_b64 (8-byte slots); prints bytes
+    per shader clock per CU (median over the workgroups) for each lane-to-bank pattern."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from granulelayer_amd.build import PROBE_LIB
+
+    if not PROBE_LIB.exists():
+        raise SystemExit(f"{PROBE_LIB} is missing: run __graft_entry__.build() first")
+    lib = ctypes.CDLL(str(PROBE_LIB))
+    lib.gl_lds_probe.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                 ctypes.c_void_p]
+    dev = torch.device("cuda", 0)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    rng = np.random.default_rng(0)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    cases = [(16, k) for k in ("linear", "random", "rows_distinct", "rows_matched", "rows_matched_swapped")]
+    cases += [(8, k) for k in ("linear", "random", "halves_distinct", "halves_one_repeat", "rows16_colliding")]
+    rows = []
+    for bytes_, kind in cases:
+        offs = torch.from_numpy(lds_patterns(bytes_, kind, rng).astype(np.int32)).to(dev)
+        cyc = torch.zeros(cus * 16, dtype=torch.int64, device=dev)
+        for _ in range(2):  # the first launch warms up
+            rc = lib.gl_lds_probe(bytes_, offs.data_ptr(), iters, cyc.data_ptr(), cus, stream)
+            if rc != 0:
+                raise SystemExit(f"gl_lds_probe failed ({bytes_}, {kind})")
+        torch.cuda.synchronize()
+        per_wg = cyc.view(cus, 16).max(dim=1).values.double().cpu().numpy()
+        rate = 16 * iters * 8 * 64 * bytes_ / per_wg
+        rows.append({"slot_bytes": bytes_, "pattern": kind, "B_per_clk_per_CU": round(float(np.median(rate)), 1),
+                     "min": round(float(rate.min()), 1), "max": round(float(rate.max()), 1)})
+        print(json.dumps(rows[-1]), flush=True)
+    print(json.dumps({"lds_probe": rows, "cus": cus, "iters": iters, "waves_per_cu": 16, "reads_per_iter": 8}),
+          flush=True)
+
+
 def c1_problem():
     """BASELINE configs[0] (the reference's CPU-runnable case): B=64, D=1024, N=1,048,576, fan-in 8,
     pools of 256, seed 0, generated on the CPU so the GPU and the CPU path see the same bits."""
@@ -376,6 +467,8 @@ def main():
                          "shards of 256, then LogMeanExp over the 4 shard features)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (calibrates rocprofv3 byte counters)")
+    ap.add_argument("--lds-probe", action="store_true",
+                    help="only measure the LDS gather rate (ds_read_b128 / ds_read_b64) of lane-to-bank patterns")
     args = ap.parse_args()
     global RELU_BITS
     RELU_BITS = args.relu_bits
@@ -391,6 +484,9 @@ def main():
         sys.exit(2)
     if args.config:
         run_config(args.config, args.steps, args.warmup)
+        return
+    if args.lds_probe:
+        lds_probe()
         return
     if args.copy_probe:
         n = args.copy_probe * (1 << 20) // 4

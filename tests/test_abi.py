@@ -212,3 +212,20 @@ def test_relu_bit_sizes_follow_the_layer():
     assert size(act=N.GL_ACT["gelu"]) == 0
     assert size(pool=N.GL_POOL["max"]) == 0
     assert size(rec_shift=4) == 0
+
+
+def test_lds_probe_library_is_separate_and_refuses_bad_shapes():
+    """bench.py --lds-probe's kernel lives in its own library: the layer's library does not export
+    it, and the probe refuses an unsupported slot size or launch shape before any device use."""
+    from granulelayer_amd.build import PROBE_LIB
+
+    if not PROBE_LIB.exists():
+        pytest.skip("probe library not built")
+    probe = ctypes.CDLL(str(PROBE_LIB))
+    probe.gl_lds_probe.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                   ctypes.c_void_p]
+    buf = ctypes.create_string_buffer(64)
+    assert probe.gl_lds_probe(4, buf, 1, buf, 1, None) == -1
+    assert probe.gl_lds_probe(16, buf, 0, buf, 1, None) == -1
+    assert probe.gl_lds_probe(16, None, 1, buf, 1, None) == -1
+    assert not hasattr(N.library().lib, "gl_lds_probe")
