@@ -49,16 +49,24 @@ __device__ __forceinline__ float tile_x(const float4* xt, int D, int b, int d) {
 }
 
 // dz of the event (token b, pool g, slot s): g_pre * act'(z), z = bias + sum_k x[idx] w in k order
-template <int K, int ACT, typename XF>
+// W and bias in their stored dtype, chosen at compile time (a run-time dtype test inside the event
+// loops doubled the dX pass)
+template <bool WBF>
+__device__ __forceinline__ float ld_param_t(const float* p, long long i) {
+  if constexpr (WBF) return __uint_as_float((unsigned)reinterpret_cast<const unsigned short*>(p)[i] << 16);
+  return p[i];
+}
+
+template <int K, int ACT, bool WBF, typename XF>
 __device__ __forceinline__ float event_dz(const MaxEvK& p, long long n, float c1, XF xat, float (&xk)[K],
                                           float (&wk)[K], int (&dk)[K]) {
-  float z = ld_param(p.bias, p.wbf, n);
+  float z = ld_param_t<WBF>(p.bias, n);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     int d = rec_index(p.idx, n, k, K, p.rs);
     d = d < 0 ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps reads in bounds
     dk[k] = d;
-    wk[k] = ld_param(p.W, p.wbf, n * K + k);
+    wk[k] = ld_param_t<WBF>(p.W, n * K + k);
     xk[k] = xat(d);
     z = __builtin_fmaf(xk[k], wk[k], z);
   }
@@ -68,7 +76,7 @@ __device__ __forceinline__ float event_dz(const MaxEvK& p, long long n, float c1
 
 // dW / db of one pool's events, tsub tokens (tsub * kpe <= 1024 events) at a time.  LDS: npow2
 // sort keys, then per event its dz and K products.
-template <int K, int ACT>
+template <int K, int ACT, bool WBF>
 __global__ void __launch_bounds__(256) max_events_dw_kernel(MaxEvK p) {
   extern __shared__ unsigned lds[];
   unsigned* keys = lds;
@@ -85,7 +93,7 @@ __global__ void __launch_bounds__(256) max_events_dw_kernel(MaxEvK p) {
           const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
           float xk[K], wk[K];
           int dk[K];
-          const float dz = event_dz<K, ACT>(p, n, p.c1t[(long long)g * p.cap + bl],
+          const float dz = event_dz<K, ACT, WBF>(p, n, p.c1t[(long long)g * p.cap + bl],
                                             [&](int d) { return tile_x(p.xt, p.D, bl, d); }, xk, wk, dk);
           float* e = ev + (long long)i * (K + 1);
           e[0] = dz;
@@ -147,7 +155,7 @@ __device__ __forceinline__ double pow2(int e) {
 // quantum is ~2^-70 of the token's largest term (~2^-38 with one 64-bit word), so inputs fed only
 // by terms many orders below it keep fp32 accuracy.  LDS: dblk pairs of words, then, with a single
 // block, the token's X row (with several, x is read from the token tile in global memory).
-template <int K, int ACT, bool ONE>
+template <int K, int ACT, bool ONE, bool WBF>
 __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
   // ONE is a compile-time choice, so each instantiation reads X from one address space (a run-time
   // choice between the LDS row and the global tile makes the compiler use flat loads for both)
@@ -174,7 +182,7 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
     const long long n = pool_base(g, p.S, p.sps, p.gs) + s;
     float wm = 0.f;
 #pragma unroll
-    for (int k = 0; k < K; ++k) wm = __builtin_fmaxf(wm, __builtin_fabsf(ld_param(p.W, p.wbf, n * K + k)));
+    for (int k = 0; k < K; ++k) wm = __builtin_fmaxf(wm, __builtin_fabsf(ld_param_t<WBF>(p.W, n * K + k)));
     m = __builtin_fmaxf(m, __builtin_fabsf(p.g_pre[row + g]) * wm);
   }
 #pragma unroll
@@ -208,7 +216,7 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
         const int n_g = p.counts[g];
         coef = coef / (float)(n_g < p.kpe ? n_g : p.kpe);
       }
-      const float dz = event_dz<K, ACT>(
+      const float dz = event_dz<K, ACT, WBF>(
           p, n, coef,
           [&](int d) {
             if constexpr (ONE) return xrow[d];
@@ -239,8 +247,8 @@ __global__ void __launch_bounds__(1024) max_events_dx_kernel(MaxEvK p) {
   }
 }
 
-template <int K, int ACT>
-static int launch_max_events_k(MaxEvK k, hipStream_t s) {
+template <int K, int ACT, bool WBF>
+static int launch_max_events_kw(MaxEvK k, hipStream_t s) {
   const size_t dw_lds = (size_t)k.npow2 * 4 + (size_t)k.tsub * k.kpe * (K + 1) * 4;
   // dX: the whole row (20 bytes per input: two accumulator words and x) when it fits, else blocks
   // of 16-byte inputs (the kernel's static LDS word aside)
@@ -252,18 +260,23 @@ static int launch_max_events_k(MaxEvK k, hipStream_t s) {
     dx_lds = (size_t)k.dblk * 16;
   }
   if (dw_lds > max_lds_bytes() || k.dblk < 64) return GL_ERR_LDS;
-  GL_TRY(set_lds_limit((const void*)max_events_dw_kernel<K, ACT>, dw_lds));
+  GL_TRY(set_lds_limit((const void*)max_events_dw_kernel<K, ACT, WBF>, dw_lds));
   const bool one = k.dblk >= k.D;
-  const void* dxk = one ? (const void*)max_events_dx_kernel<K, ACT, true> : (const void*)max_events_dx_kernel<K, ACT, false>;
+  const void* dxk = one ? (const void*)max_events_dx_kernel<K, ACT, true, WBF> : (const void*)max_events_dx_kernel<K, ACT, false, WBF>;
   GL_TRY(set_lds_limit(dxk, dx_lds));
-  GL_LAUNCH(GL_KERNEL_MAX_EV_DW, (max_events_dw_kernel<K, ACT>), dim3((unsigned)k.G), dim3(256), dw_lds, s, k);
+  GL_LAUNCH(GL_KERNEL_MAX_EV_DW, (max_events_dw_kernel<K, ACT, WBF>), dim3((unsigned)k.G), dim3(256), dw_lds, s, k);
   GL_CHECK_LAUNCH();
   if (one)
-    GL_LAUNCH(GL_KERNEL_MAX_EV_DX, (max_events_dx_kernel<K, ACT, true>), dim3((unsigned)k.Bc), dim3(1024), dx_lds, s, k);
+    GL_LAUNCH(GL_KERNEL_MAX_EV_DX, (max_events_dx_kernel<K, ACT, true, WBF>), dim3((unsigned)k.Bc), dim3(1024), dx_lds, s, k);
   else
-    GL_LAUNCH(GL_KERNEL_MAX_EV_DX, (max_events_dx_kernel<K, ACT, false>), dim3((unsigned)k.Bc), dim3(1024), dx_lds, s, k);
+    GL_LAUNCH(GL_KERNEL_MAX_EV_DX, (max_events_dx_kernel<K, ACT, false, WBF>), dim3((unsigned)k.Bc), dim3(1024), dx_lds, s, k);
   GL_CHECK_LAUNCH();
   return 0;
+}
+
+template <int K, int ACT>
+static int launch_max_events_k(const MaxEvK& k, hipStream_t s) {
+  return k.wbf ? launch_max_events_kw<K, ACT, true>(k, s) : launch_max_events_kw<K, ACT, false>(k, s);
 }
 
 int launch_max_events(int K, int act, const MaxEvKArgs& a, hipStream_t s) {
