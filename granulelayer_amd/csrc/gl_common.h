@@ -102,6 +102,13 @@ __device__ __forceinline__ float ld_param(const float* p, bool bf, long long i) 
   if (bf) return __uint_as_float((unsigned)reinterpret_cast<const unsigned short*>(p)[i] << 16);
   return p[i];
 }
+// The same with the dtype fixed at compile time: loops of parameter loads are instantiated once per
+// dtype behind one uniform branch (a dtype test per load keeps the compiler from batching them)
+template <bool BF>
+__device__ __forceinline__ float ld_param_t(const float* p, long long i) {
+  if constexpr (BF) return __uint_as_float((unsigned)reinterpret_cast<const unsigned short*>(p)[i] << 16);
+  return p[i];
+}
 // the fp32 value of a weight whose 32-bit word w32 was loaded from byte offset (boff & ~3) of bf16
 // storage (boff = the element's byte offset): its half of the word
 __device__ __forceinline__ float bf16_half(unsigned w32, unsigned boff) {

@@ -49,14 +49,8 @@ __device__ __forceinline__ float tile_x(const float4* xt, int D, int b, int d) {
 }
 
 // dz of the event (token b, pool g, slot s): g_pre * act'(z), z = bias + sum_k x[idx] w in k order
-// W and bias in their stored dtype, chosen at compile time (a run-time dtype test inside the event
-// loops doubled the dX pass)
-template <bool WBF>
-__device__ __forceinline__ float ld_param_t(const float* p, long long i) {
-  if constexpr (WBF) return __uint_as_float((unsigned)reinterpret_cast<const unsigned short*>(p)[i] << 16);
-  return p[i];
-}
-
+// W and bias in their stored dtype, chosen at compile time (ld_param_t: a run-time dtype test
+// inside the event loops doubled the dX pass)
 template <int K, int ACT, bool WBF, typename XF>
 __device__ __forceinline__ float event_dz(const MaxEvK& p, long long n, float c1, XF xat, float (&xk)[K],
                                           float (&wk)[K], int (&dk)[K]) {
