@@ -297,9 +297,10 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 4 : 1) bwd_w_kernel(BwK p)
   const int g_first = (int)((long long)blockIdx.x * WAVES / p.cpg);
   const int pk = WS ? (int)(g - g_first) : 0;
   const int lo = WS ? (int)__builtin_amdgcn_readfirstlane(p.win[g]) : 0;
-  // one uniform branch on the parameter dtype around the whole set-up (loads issued back to back)
-  auto setup = [&](auto bf) {
-    constexpr bool BF = decltype(bf)::value;
+  // the lane's neurons: LDS addresses of their inputs, weights, bias, slots
+  if constexpr (WS) {
+    // pool windows: the parameter dtype tested per load (the set-up below, written as a generic
+    // lambda, raised these kernels' spills from 8 / 20 to 92 / 148 bytes per lane)
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
       uint32_t order;
@@ -313,9 +314,9 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 4 : 1) bwd_w_kernel(BwK p)
         const int k = sched_k<K>(order, ks);
         int d = rec_index(p.idx, n, k, K, p.rs);
         d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-        addr[j][ks] = WS ? win_addr(d, pk, lo, p.ww) : (unsigned)d * SLOT;
+        addr[j][ks] = win_addr(d, pk, lo, p.ww);
         if constexpr (!FM) {
-          const float wl = ld_param_t<BF>(p.W, n * K + k);
+          const float wl = ld_param(p.W, p.wbf, n * K + k);
           w[j][ks] = valid ? wl : 0.f;
         } else {
           w[j][ks] = 0.f;
@@ -323,16 +324,52 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 4 : 1) bwd_w_kernel(BwK p)
         dw[j][ks] = 0.f;
       }
       if constexpr (!FM) {
-        const float bl = ld_param_t<BF>(p.bias, n);
+        const float bl = ld_param(p.bias, p.wbf, n);
         bias[j] = valid ? bl : 0.f;
       } else {
         bias[j] = 0.f;
       }
       dbv[j] = 0.f;
     }
-  };
-  if (FM || !p.wbf) setup(std::false_type{});
-  else setup(std::true_type{});
+  } else {
+    // one uniform branch on the parameter dtype around the set-up, so the loads of either dtype
+    // issue back to back (a dtype test per load made the compiler wait on each in turn)
+    auto setup = [&](auto bf) {
+      constexpr bool BF = decltype(bf)::value;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        uint32_t order;
+        const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, lane, order);
+        const unsigned s16 = (unsigned)(s < 0xffff ? s : 0xffff);
+        if (j % 2 == 0) slot2[j / 2] = s16; else slot2[j / 2] |= s16 << 16;
+        const bool valid = s < n_g;
+        const long long n = pool_base((int)g, p.S, p.sps, p.gs) + (s < ext ? s : ext - 1);  // in bounds; invalid slots masked
+#pragma unroll
+        for (int ks = 0; ks < K; ++ks) {
+          const int k = sched_k<K>(order, ks);
+          int d = rec_index(p.idx, n, k, K, p.rs);
+          d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
+          addr[j][ks] = (unsigned)d * SLOT;
+          if constexpr (!FM) {
+            const float wl = ld_param_t<BF>(p.W, n * K + k);
+            w[j][ks] = valid ? wl : 0.f;
+          } else {
+            w[j][ks] = 0.f;
+          }
+          dw[j][ks] = 0.f;
+        }
+        if constexpr (!FM) {
+          const float bl = ld_param_t<BF>(p.bias, n);
+          bias[j] = valid ? bl : 0.f;
+        } else {
+          bias[j] = 0.f;
+        }
+        dbv[j] = 0.f;
+      }
+    };
+    if (FM || !p.wbf) setup(std::false_type{});
+    else setup(std::true_type{});
+  }
   const float* c1row = p.c1t + g * p.cap;
   constexpr int NT = WAVES * 64;
   constexpr int TPW = 32 / TB;       // tiles per mask word
@@ -1140,29 +1177,24 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
   float w[NPL][K], dw[NPL][K];
   float bias[NPL], dbv[NPL];
   int slot[NPL];
-  auto setup = [&](auto bf) {  // one uniform branch on the parameter dtype around the set-up
-    constexpr bool BF = decltype(bf)::value;
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-      uint32_t order;
-      const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, lane, order);
-      slot[j] = s < n_g ? s : -1;
-      const long long n = nb + (s < ext ? s : ext - 1);
+  for (int j = 0; j < NPL; ++j) {
+    uint32_t order;
+    const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, lane, order);
+    slot[j] = s < n_g ? s : -1;
+    const long long n = nb + (s < ext ? s : ext - 1);
 #pragma unroll
-      for (int ks = 0; ks < K; ++ks) {
-        const int k = sched_k<K>(order, ks);
-        int d = rec_index(p.idx, n, k, K, p.rs);
-        d = (d < 0 || s >= n_g) ? 0 : (d >= p.D ? p.D - 1 : d);
-        addr[j][ks] = (unsigned)d * 16u;
-        w[j][ks] = s < n_g ? ld_param_t<BF>(p.W, n * K + k) : 0.f;
-        dw[j][ks] = 0.f;
-      }
-      bias[j] = s < n_g ? ld_param_t<BF>(p.bias, n) : 0.f;
-      dbv[j] = 0.f;
+    for (int ks = 0; ks < K; ++ks) {
+      const int k = sched_k<K>(order, ks);
+      int d = rec_index(p.idx, n, k, K, p.rs);
+      d = (d < 0 || s >= n_g) ? 0 : (d >= p.D ? p.D - 1 : d);
+      addr[j][ks] = (unsigned)d * 16u;
+      w[j][ks] = s < n_g ? ld_param(p.W, p.wbf, n * K + k) : 0.f;
+      dw[j][ks] = 0.f;
     }
-  };
-  if (p.wbf) setup(std::true_type{});
-  else setup(std::false_type{});
+    bias[j] = s < n_g ? ld_param(p.bias, p.wbf, n) : 0.f;
+    dbv[j] = 0.f;
+  }
   const float* c1row = p.c1t + g * p.cap;
   const float* c2row = p.c2t + g * p.cap;
   const float* c3row = p.c3t + g * p.cap;

@@ -676,10 +676,10 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 16 / WAVES * WAVES / 4 : 1
   const int g_first = (int)((long long)blockIdx.x * WAVES / p.cpg);
   const int pk = WS ? (int)(g - g_first) : 0;
   const int lo = WS ? (int)__builtin_amdgcn_readfirstlane(p.win[g]) : 0;
-  // the lane's neurons: input addresses, weights, bias, slots (one uniform branch on the parameter
-  // dtype around the whole set-up, so the loads of either dtype are issued back to back)
-  auto setup = [&](auto bf) {
-    constexpr bool BF = decltype(bf)::value;
+  // the lane's neurons: input addresses, weights, bias, slots
+  if constexpr (WS) {
+    // pool windows: the parameter dtype tested per load (the set-up below, written as a generic
+    // lambda, added spills to these kernels)
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
       uint32_t order;
@@ -691,18 +691,44 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 16 / WAVES * WAVES / 4 : 1
         const int k = sched_k<K>(order, ks);  // the pooled sum does not depend on the visiting order
         int d = rec_index(p.idx, n, k, K, p.rs);
         d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-        addr[j][ks] = WS ? win_addr<SLOT>(d, pk, lo, p.ww) : (unsigned)d * SLOT;
-        const float wl = ld_param_t<BF>(p.W, n * K + k);
+        addr[j][ks] = win_addr<SLOT>(d, pk, lo, p.ww);
+        const float wl = ld_param(p.W, p.wbf, n * K + k);
         w[j][ks] = valid ? wl : 0.f;
       }
-      const float bl = ld_param_t<BF>(p.bias, n);
+      const float bl = ld_param(p.bias, p.wbf, n);
       bias[j] = valid ? bl : ((PK == PK_MAX || PK == PK_TOPK) ? -__builtin_inff() : 0.f);
       slot[j] = s;
       vmask |= (unsigned)valid << j;
     }
-  };
-  if (p.wbf) setup(std::true_type{});
-  else setup(std::false_type{});
+  } else {
+    // one uniform branch on the parameter dtype around the set-up, so the loads of either dtype
+    // issue back to back (a dtype test per load made the compiler wait on each in turn)
+    auto setup = [&](auto bf) {
+      constexpr bool BF = decltype(bf)::value;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        uint32_t order;
+        const int s = sched_slot(p.sched, p.nwin, p.S, g, s_lo, j, lane, order);
+        const bool valid = s < n_g;
+        const long long n = nb + (s < ext ? s : ext - 1);  // in-bounds address; invalid slots masked
+#pragma unroll
+        for (int ks = 0; ks < K; ++ks) {
+          const int k = sched_k<K>(order, ks);  // the pooled sum does not depend on the visiting order
+          int d = rec_index(p.idx, n, k, K, p.rs);
+          d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
+          addr[j][ks] = (unsigned)d * SLOT;
+          const float wl = ld_param_t<BF>(p.W, n * K + k);
+          w[j][ks] = valid ? wl : 0.f;
+        }
+        const float bl = ld_param_t<BF>(p.bias, n);
+        bias[j] = valid ? bl : ((PK == PK_MAX || PK == PK_TOPK) ? -__builtin_inff() : 0.f);
+        slot[j] = s;
+        vmask |= (unsigned)valid << j;
+      }
+    };
+    if (p.wbf) setup(std::true_type{});
+    else setup(std::false_type{});
+  }
 
   // Token tiles reach LDS by LDS-DMA (dma_tile).  DBUF: tile t + 1 is loaded into the other
   // buffer while tile t is read, one barrier per tile; tiles alternate xa (even t) and xb (odd t),
