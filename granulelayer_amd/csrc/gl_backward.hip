@@ -1434,6 +1434,14 @@ constexpr int bwd_waves(int K) { return K == 8 ? 12 : 8; }
 #ifndef BWD_FM_RA
 #define BWD_FM_RA 1
 #endif
+// kept bits with pool windows: waves per workgroup and read-ahead (12 waves: 132 VGPRs, where 16
+// waves held to 128 spilled 20 bytes per lane; C3 dW 19.6 -> 18.9 ms)
+#ifndef BWD_FM_WIN_WAVES
+#define BWD_FM_WIN_WAVES 12
+#endif
+#ifndef BWD_FM_WIN_RA
+#define BWD_FM_WIN_RA 1
+#endif
 
 struct BwdPlan {
   int bc_max, npl, waves, cpg, tiles_max, cap_max, rs_max, FR, P, U, Q, QL, UQ;
@@ -1551,13 +1559,18 @@ static int launch_bwd_w_fm(const BwK& k, hipStream_t s) {
     GL_CHECK_LAUNCH();
     return 0;
   }
-  auto fn = k.win ? bwd_w_kernel<K, NPL, WAVES, A, RA, false, true, false, BT, false, true>
-            : k.xb ? bwd_w_kernel<K, NPL, WAVES, A, RA, true, false, false, BT, true, true>
+  if (k.win) {
+    constexpr int WW = BWD_FM_WIN_WAVES;
+    GL_LAUNCH(GL_KERNEL_BWD_W_WIN, (bwd_w_kernel<K, NPL, WW, A, BWD_FM_WIN_RA, false, true, false, BT, false, true>),
+              dim3((unsigned)ceil_div(k.n_chunks, WW)), dim3(WW * 64), 0, s, k);
+    GL_CHECK_LAUNCH();
+    return 0;
+  }
+  auto fn = k.xb ? bwd_w_kernel<K, NPL, WAVES, A, RA, true, false, false, BT, true, true>
             : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, A, RA, true, false, false, BT, false, true>
                                : (k.D <= XTILE_SB ? bwd_w_kernel<K, NPL, WAVES, A, RA, false, false, false, BT, false, true>
                                                   : bwd_w_kernel<K, NPL, WAVES, A, RA, false, false, true, BT, false, true>));
-  GL_LAUNCH(k.win ? GL_KERNEL_BWD_W_WIN : GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)),
-            dim3(WAVES * 64), 0, s, k);
+  GL_LAUNCH(GL_KERNEL_BWD_W, fn, dim3((unsigned)ceil_div(k.n_chunks, WAVES)), dim3(WAVES * 64), 0, s, k);
   GL_CHECK_LAUNCH();
   return 0;
 }
@@ -1735,7 +1748,7 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     const bool dense = !smooth && !a->winner;
     // the staged windows cover the pools of one workgroup: size them for the dW launch that runs
     // (16 waves with the forward's ReLU bits, else bwd_waves)
-    const int dw_waves = a->relu_mask && a->K == 8 ? BWD_FM_WAVES : q.waves;
+    const int dw_waves = a->relu_mask && a->K == 8 ? BWD_FM_WIN_WAVES : q.waves;
     const bool win = dense && window_staging(a->win, a->win_width, a->D, dw_waves, q.cpg, a->G, &ww, &npw);
     const bool wide = dense && !win && tiles_of_two(a->D);
     // bf16 X keeps its bf16 values, 4 tokens per 8-byte slot (C4 dW 114.3 -> 90.2 ms against
