@@ -1063,8 +1063,12 @@ __global__ void __launch_bounds__(256) fwd_finalize_smooth_kernel(const float* _
 // top-k keeps a sorted list of 4 pairs per token: 8 waves at K = 8, 4 at K = 16.
 constexpr int FWD_NPL = 4;
 static_assert(FWD_NPL == RELU_MASK_NPL, "the forward writes the ReLU bits chunk by chunk");
-constexpr int fwd_waves(int K, int pk = PK_SUM) {
-  return K == 8 ? (pk == PK_SUM ? 16 : (pk == PK_MAX ? 12 : 8)) : (pk == PK_SUM ? 8 : 4);
+constexpr int fwd_waves(int K, int pk = PK_SUM, int act = GL_ACT_RELU) {
+  // LogMeanExp and softmax-weighted at fan-in 8 with ReLU or identity neurons: 12 waves (3 per SIMD,
+  // 130-136 VGPRs; C2 LogMeanExp forward 31.4 -> 26.2 ms against 8); the power mean (168 VGPRs
+  // would spill 140-176 bytes per lane) and GELU neurons keep 8
+  const bool sm12 = K == 8 && (pk == PK_LME || pk == PK_SW) && act != GL_ACT_GELU;
+  return K == 8 ? (pk == PK_SUM ? 16 : (pk == PK_MAX || sm12 ? 12 : 8)) : (pk == PK_SUM ? 8 : 4);
 }
 static int pool_kind(int pool) {
   switch (pool) {
@@ -1114,7 +1118,7 @@ static long long fwd_part_per_token(const GlFwdArgs* a, long long n_chunks) {
 static FwdPlan fwd_plan(const GlFwdArgs* a, long long bf_cap = 0) {
   FwdPlan q;
   q.npl = FWD_NPL;
-  q.waves = fwd_waves(a->K, pool_kind(a->pool));
+  q.waves = fwd_waves(a->K, pool_kind(a->pool), a->act);
   q.cpg = ceil_div(a->S, 64 * q.npl);
   q.n_chunks = (long long)a->G * q.cpg;
   const long long kp = a->pool == GL_POOL_TOPK_MEAN ? a->topk : (pool_smooth(a->pool) ? 3 : 1);
@@ -1151,7 +1155,7 @@ static int launch_fwd(const FwdK& k, hipStream_t s) {
 // workgroup per CU
 template <int ACT, int K, int PK>
 static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
-  constexpr int W = fwd_waves(K, PK);
+  constexpr int W = fwd_waves(K, PK, ACT);
   if (k.win) {
     if (k.xb) {  // bf16 windows (sum / mean)
       if constexpr (PK == PK_SUM && W % 8 == 0)
