@@ -150,7 +150,7 @@ def run_config(name: str, steps: int, warmup: int):
         one()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with KernelTrace(max_launches=32 * steps) as tr:
+    with KernelTrace(max_launches=128 * steps) as tr:
         e0.record()
         for _ in range(steps):
             one()
@@ -390,7 +390,7 @@ def c4_step(steps: int, warmup: int):
         step()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with KernelTrace(max_launches=32 * steps) as tr:
+    with KernelTrace(max_launches=128 * steps) as tr:
         e0.record()
         for _ in range(steps):
             step()
@@ -532,7 +532,7 @@ def main():
         log(f"warmup step {i + 1}/{args.warmup} done")
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    with KernelTrace(max_launches=32 * args.steps) as tr:
+    with KernelTrace(max_launches=128 * args.steps) as tr:
         ev0.record()
         w0 = time.perf_counter()
         for _ in range(args.steps):
@@ -549,7 +549,7 @@ def main():
     for _ in range(2):
         step()
     torch.cuda.synchronize()
-    with KernelTrace(max_launches=32 * args.steps) as tr2:
+    with KernelTrace(max_launches=128 * args.steps) as tr2:
         ev0.record()
         for _ in range(args.steps):
             step()

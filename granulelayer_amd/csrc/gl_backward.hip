@@ -513,6 +513,7 @@ struct DxK {
   int D, S, P, U, QL, UQ, FR, cap, n_tc;
   int sps, gs;  // pool geometry (pool_base)
   int wbf;      // W stored as bf16: the edge's weight is the half of the 32-bit word at (offset / 2) & ~3
+  int ql0;      // dx_dense_kernel: the pass's first unit range per XCD (its ranges are ql0 .. ql0 + QL - 1)
 };
 
 // ---- dX ----------------------------------------------------------------------------------------
@@ -1026,14 +1027,25 @@ dx_dma_kernel(DxK p) {
 
 // dX[b0 + b, d] = sum_q part[q, d, b]  (fixed order, q ascending), transposed to [B, D] through
 // LDS.  A thread sums 4 adjacent tokens of one input with 16-byte loads, 8 partials in flight
-// (the add order per element is unchanged); 32 inputs x 32 tokens per workgroup.
+// (the add order per element is unchanged); 32 inputs x 32 tokens per workgroup.  acc: the sum
+// continues from the dX already there (the dense dX's later passes), so P passes over Q / P
+// partials each add in the order of one pass over all Q.
 __global__ void __launch_bounds__(256) dx_reduce_kernel(const float* __restrict__ part, float* __restrict__ dX, int D,
-                                                        int cap, int Q, int b0, int Bc) {
+                                                        int cap, int Q, int b0, int Bc, int acc) {
   __shared__ float tile[32][33];  // [token][input]
   const int d0 = blockIdx.x * 32, bb = blockIdx.y * 32;
   const int dl = threadIdx.x >> 3, q4 = (threadIdx.x & 7) * 4;  // input d0 + dl, tokens bb + q4 .. + 3
   const int d = d0 + dl;
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (acc) {  // the running sums, [B, D] rows in through the tile
+    for (int r = threadIdx.x >> 5; r < 32; r += 8) {
+      const int b = bb + r, dd = d0 + (threadIdx.x & 31);
+      tile[r][threadIdx.x & 31] = dd < D && b < Bc ? dX[(long long)(b0 + b) * D + dd] : 0.f;
+    }
+    __syncthreads();
+    v = make_float4(tile[q4][dl], tile[q4 + 1][dl], tile[q4 + 2][dl], tile[q4 + 3][dl]);
+    __syncthreads();
+  }
   if (d < D && bb + q4 < cap) {  // cap is a multiple of 64: the 4 tokens lie inside the partial rows
     const float4* src = reinterpret_cast<const float4*>(part + (long long)d * cap + bb + q4);
     const long long qs = (long long)D * cap / 4;  // float4 stride between partials
@@ -1302,8 +1314,8 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
   const int rest = loc / p.FR;
   const int ql = rest % p.QL;
   const int tc = rest / p.QL;
-  const int q = ql * 8 + xcd;
-  const int u_lo = q * p.UQ;
+  const int q = ql * 8 + xcd;                        // the pass's partial slot
+  const int u_lo = ((p.ql0 + ql) * 8 + xcd) * p.UQ;  // the layer's unit range (p.ql0 + ql) * 8 + xcd
   const int u_hi = min(u_lo + p.UQ, p.U);
   int lo = (int)p.seg_ptr[F], hi = (int)p.seg_ptr[F + 1];
   {
@@ -1445,6 +1457,7 @@ constexpr int bwd_waves(int K) { return K == 8 ? 12 : 8; }
 
 struct BwdPlan {
   int bc_max, npl, waves, cpg, tiles_max, cap_max, rs_max, FR, P, U, Q, QL, UQ;
+  int QLs, UQs;  // the dense dX: unit ranges per XCD and units per range (passes of QL ranges)
   long long n_chunks, e_max, nseg_max;
   size_t xt_bytes, c1_bytes, mask_bytes, part_bytes, edges_bytes, dz_bytes;
 };
@@ -1498,6 +1511,25 @@ static BwdPlan bwd_plan(int B, int D, int G, int S, int K, bool smooth = false, 
   q.QL = (int)ql;
   q.Q = 8 * q.QL;
   q.UQ = ceil_div(q.U, q.Q);
+  // The dense dX (per-neuron dz) reads a neuron's 4·cap-byte dz row once per edge, and mostly
+  // from HBM unless the feature-range waves that share a unit read it close together in time.
+  // Short unit ranges keep them together: ranges of ~192 KiB of dz rows per wave,
+  // Q = E · 256 T / (FR · 192 KiB) (at C2 LogMeanExp, 128-token chunks: ranges of 24 units,
+  // dX 67.6 -> 57.0 ms per chunk; 12 units 59.4, 48 units 58.4; at the C5 shape 256-token chunks
+  // 189.5 -> 113.6 ms with ranges of 12 units, 133.3 with 24).  The ranges run as passes of QL
+  // ranges per XCD into the same [Q][D][cap] partials, each reduced onto the last.
+  q.QLs = q.QL;
+  q.UQs = q.UQ;
+  if (smooth) {
+    const long long tb = 256LL * dx_slots(q.bc_max);  // dz bytes per edge and 64-lane wave
+    long long qls = (long long)G * S * K * tb / ((long long)q.FR * (192 << 10)) / 8;
+    if (qls > 2048) qls = 2048;
+    if (qls > q.U / 8) qls = q.U / 8;  // at least one unit per range
+    if (qls >= 2 * q.QL) {
+      q.QLs = (int)(qls / q.QL * q.QL);
+      q.UQs = ceil_div(q.U, 8 * q.QLs);
+    }
+  }
   q.xt_bytes = (size_t)round_up((long long)q.tiles_max * D * 16, 256);
   q.c1_bytes = (size_t)round_up((long long)G * q.cap_max * 4, 256);
   q.mask_bytes = (size_t)round_up((long long)G * S * q.rs_max * 4, 256);
@@ -1780,12 +1812,15 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
       const int Td = T;
       DxK dk{(const uint32_t*)(eb + h.off_rec), (const uint32_t*)(eb + h.off_seg_ptr),
              (const int32_t*)(eb + h.off_seg_unit), (const uint32_t*)(eb + h.off_seg_begin), c1t, nullptr, W, part,
-             NS, a->D, a->S, q.P, q.U, q.QL, q.UQ, q.FR, cap, cap / (64 * Td), sps, gs};
+             NS, a->D, a->S, q.P, q.U, q.QL, q.UQs, q.FR, cap, cap / (64 * Td), sps, gs};
       dk.wbf = wbf;
-      GL_TRY(launch_dx_dense(a->K, Td, dk, dz, s));
-      GL_LAUNCH(GL_KERNEL_DX_REDUCE, dx_reduce_kernel, dim3((unsigned)ceil_div(a->D, 32), (unsigned)ceil_div(Bc, 32)),
-                dim3(256), 0, s, part, a->dX, a->D, cap, q.Q, b0, Bc);
-      GL_CHECK_LAUNCH();
+      for (int ql0 = 0; ql0 < q.QLs; ql0 += q.QL) {  // passes of QL unit ranges per XCD
+        dk.ql0 = ql0;
+        GL_TRY(launch_dx_dense(a->K, Td, dk, dz, s));
+        GL_LAUNCH(GL_KERNEL_DX_REDUCE, dx_reduce_kernel, dim3((unsigned)ceil_div(a->D, 32), (unsigned)ceil_div(Bc, 32)),
+                  dim3(256), 0, s, part, a->dX, a->D, cap, q.Q, b0, Bc, ql0 > 0 ? 1 : 0);
+        GL_CHECK_LAUNCH();
+      }
       continue;
     }
     const int kpe = a->pool == GL_POOL_TOPK_MEAN ? a->topk : 1;
@@ -1824,7 +1859,7 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     dk.wbf = wbf;
     GL_TRY(launch_dx(a->K, T, dk, s, dx_short_segments(a)));
     GL_LAUNCH(GL_KERNEL_DX_REDUCE, dx_reduce_kernel, dim3((unsigned)ceil_div(a->D, 32), (unsigned)ceil_div(Bc, 32)), dim3(256), 0,
-                       s, part, a->dX, a->D, cap, q.Q, b0, Bc);
+                       s, part, a->dX, a->D, cap, q.Q, b0, Bc, 0);
     GL_CHECK_LAUNCH();
   }
   return 0;

@@ -160,6 +160,39 @@ def test_smooth_backward_dz_budget_sets_the_token_chunks(pool, param, act):
     assert info[1] - info[0] >= L.groups * L.slots_per_group * (256 - 64) * 4
 
 
+@pytest.mark.parametrize("B,passes", [(128, 2), (200, 4)])
+@pytest.mark.parametrize("pool,param,act", [OPS[1], OPS[3], OPS[4]], ids=lambda v: str(v))
+def test_smooth_dense_dx_in_unit_range_passes(B, passes, pool, param, act):
+    """A layer large enough for the dense dX's short unit ranges (2.1 M edges into 64 inputs, 1024
+    pools): the ranges run as 2 passes at 2 tokens per lane (B = 128) and 4 at 4 (B = 200), each
+    pass's partials reduced onto the previous passes' dX; gradients against the oracle, and a second
+    backward bit-identical."""
+    from granulelayer_amd._native import KernelTrace
+
+    L, idx, w, b, x, dy = _case((64, 262144, 1024, 8, B, torch.float32), seed=11)
+    rt = Level1Runtime(L, idx.to(DEV), _spec(pool, param, act), PhysicalPlan())
+    xd, wd, bd, dyd = x.to(DEV), w.to(DEV), b.to(DEV), dy.to(DEV)
+    out = rt.forward(xd, wd, bd)
+    dw = torch.zeros(L.weight_shape, device=DEV)
+    db = torch.zeros(L.bias_shape, device=DEV)
+    with KernelTrace(max_launches=256) as tr:
+        dx = rt.backward(xd, wd, bd, dyd, out, "minimal_stats", dw, db)
+        torch.cuda.synchronize()
+    launches = {k: len(v) for k, v in tr.times_ms().items()}
+    assert launches.get("dx_dense_kernel") == passes and launches.get("dx_reduce_kernel") == passes, launches
+    dx = dx.cpu().numpy()
+    fi, fw, fb = _flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    wdW, wdb, wdX, (mW, mb, mX) = O.backward_smooth(x.numpy(), fi, fw, fb, counts, L.slots_per_group, dy.numpy(), pool,
+                                                    param, act)
+    assert_parity(dx, wdX, mX, what="dX")
+    assert_parity(dw.cpu().numpy().reshape(-1, L.fan_in), wdW, mW, what="dW")
+    assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, what="db")
+    dw2, db2 = torch.zeros_like(dw), torch.zeros_like(db)
+    dx2 = rt.backward(xd, wd, bd, dyd, out, "minimal_stats", dw2, db2).cpu().numpy()
+    assert np.array_equal(dx, dx2) and torch.equal(dw, dw2) and torch.equal(db, db2)
+
+
 
 @pytest.mark.parametrize("case", [CASES[0], CASES[2]], ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}")
 @pytest.mark.parametrize("p", [1.0, 4.0, 8.0])
