@@ -380,6 +380,7 @@ __device__ __forceinline__ unsigned dppu(unsigned v) {
   return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
 __device__ __forceinline__ unsigned umax(unsigned a, unsigned b) { return a > b ? a : b; }
+__device__ __forceinline__ unsigned umin(unsigned a, unsigned b) { return a < b ? a : b; }
 __device__ __forceinline__ unsigned wave_max4_u32(unsigned a0, unsigned a1, unsigned a2, unsigned a3, int lane) {
   const bool odd = lane & 1, hi = lane & 2;
   const unsigned b0 = umax(odd ? a2 : a0, dppu<0xB1>(odd ? a0 : a2));  // quad_perm(1,0,3,2)
@@ -401,7 +402,25 @@ __device__ __forceinline__ unsigned wave_max4_u32(unsigned a0, unsigned a1, unsi
 // slot); the winner is the 64-bit maximum, as one 64-bit reduction would give, at a third of its
 // VALU (a 64-bit compare and two selects per reduction step become one v_max_u32).  Lanes 0-3
 // store each round's pair; the finalize merges the pool's chunks.
-template <int K, int NPL, int ACT, bool FAR, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
+//
+// Ranked path (TKW > 0 waves per workgroup, k <= 8): no rounds.  A lower bound of every token's
+// k-th largest value comes from windows of 32 candidates (two neighbouring lane quads of a row):
+// of the 16 windows, 8 are disjoint, so the smallest window maximum is at most the 8th largest
+// value.  The candidates at or above the bound (~20 of 256 on random data) are compacted into a
+// per-wave LDS list per token (ballot, mbcnt, zero keys to a multiple of 16); each then counts the
+// list's larger keys (16-key blocks, all reads of a block in flight together) for its rank and
+// stores itself at that position.  Same keys, same order: the output is the rounds' output, bit for
+// bit.  A token with more than 64 candidates at the bound (ties, or a chunk of mostly padded slots
+// at -inf) sends the tile to the rounds.  At C2 (top-8) the ranked tile took the forward from 68.9
+// to 65.5 ms at 8 waves per workgroup, and its 158 VGPRs allow 12 (54.0 ms).
+constexpr int TK_CAP = 64;  // keys per token list
+// the lists of a workgroup of TKW waves (one array per kernel, whichever tiles use it)
+template <int TKW>
+__device__ __forceinline__ cand_t* tk_lists() {
+  __shared__ __align__(16) cand_t tkl[TKW * 4 * TK_CAP];
+  return tkl;
+}
+template <int K, int NPL, int ACT, bool FAR, int TKW = 0, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
 __device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                               const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
                                               int k, bool store, int lane) {
@@ -446,6 +465,81 @@ __device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NP
     cand_cmpex(c[t][1], c[t][2]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[t][i] = (unsigned)(c[t][i] >> 32), sl[t][i] = (unsigned)c[t][i];
+  }
+  if constexpr (TKW > 0) {
+    if (k <= 8) {
+      // the lane's best value order per token, reduce-scattered to quads as in wave_max4_u32: lane l
+      // ends with its quad's maximum for token wave_sum4_token(l)
+      const bool odd = lane & 1, hi2 = lane & 2;
+      const unsigned b0 = umax(odd ? o[2][0] : o[0][0], dppu<0xB1>(odd ? o[0][0] : o[2][0]));
+      const unsigned b1 = umax(odd ? o[3][0] : o[1][0], dppu<0xB1>(odd ? o[1][0] : o[3][0]));
+      unsigned q = umax(hi2 ? b1 : b0, dppu<0x4E>(hi2 ? b0 : b1));
+      q = umax(q, dppu<0x124>(q));  // a window: this quad and its row neighbour (32 candidates)
+      q = umin(q, dppu<0x124>(q));  // the smallest of the row's 4 windows
+      q = umin(q, dppu<0x128>(q));
+      {
+        const auto p16 = __builtin_amdgcn_permlane16_swap(q, q, false, false);
+        q = umin(p16[0], p16[1]);
+        const auto p32 = __builtin_amdgcn_permlane32_swap(q, q, false, false);
+        q = umin(p32[0], p32[1]);
+      }
+      unsigned long long m[4][4];
+      int n[4];
+      bool over = false;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const unsigned bnd = (unsigned)__builtin_amdgcn_readlane((int)q, (t == 1) ? 2 : (t == 2) ? 1 : t);
+        n[t] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // a lane's list is sorted: its survivors are a prefix
+          m[t][i] = __builtin_amdgcn_ballot_w64(o[t][i] >= bnd);
+          n[t] += (int)__builtin_popcountll(m[t][i]);
+        }
+        over |= n[t] > 64;
+      }
+      if (!over) {
+        cand_t* L = tk_lists<TKW>() + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) * (4 * TK_CAP);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          int base = t * TK_CAP;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (m[t][i] == 0) break;
+            const unsigned pos = __builtin_amdgcn_mbcnt_hi((unsigned)(m[t][i] >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((unsigned)m[t][i], 0u));
+            if ((m[t][i] >> lane) & 1) L[base + (int)pos] = c[t][i];
+            base += (int)__builtin_popcountll(m[t][i]);
+          }
+          // zero keys (below every key) up to the next 32-key block
+          const int nb = (n[t] + 15) & ~15;
+          if (lane >= n[t] && lane < nb) L[t * TK_CAP + lane] = 0ull;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const cand_t* Lt = L + t * TK_CAP;
+          const cand_t mine = Lt[lane < n[t] ? lane : 0];
+          unsigned r = 0;
+          for (int j0 = 0; j0 < n[t]; j0 += 16) {  // blocks of 16 keys, all reads issued first
+            ulonglong2 kv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) kv[i] = *reinterpret_cast<const ulonglong2*>(Lt + j0 + 2 * i);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r += (kv[i].x > mine) + (kv[i].y > mine);
+          }
+          if (store && lane < n[t] && r < (unsigned)k) {
+            out[t * k + (int)r] = cand_value(mine);
+            oslot[t * k + (int)r] = (int)~(unsigned)mine;
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the next tile's lists overwrite these
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        return;
+      }
+    }
   }
   constexpr unsigned NONE_O = (unsigned)(CAND_NONE >> 32), NONE_S = (unsigned)CAND_NONE;
   const int tok = wave_sum4_token(lane);
@@ -618,18 +712,19 @@ constexpr bool pk_smooth(int pk) { return pk >= PK_LME; }
 constexpr int pk_sm_op(int pk) { return pk == PK_LME ? SM_LME : (pk == PK_POW ? SM_POW : SM_SW); }
 
 // sum / mean, max or top-k tile
-template <int K, int NPL, int ACT, bool FAR, int PK, typename SRC = const char*, typename MB = NoBits>
+template <int K, int NPL, int ACT, bool FAR, int PK, int TKW, typename SRC = const char*, typename MB = NoBits>
 __device__ __forceinline__ void fwd_tile_any(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                              const float (&bias)[NPL], const int (&slot)[NPL], float* out, int* oslot,
                                              int k, bool store, int lane, MB& mb) {
   if constexpr (PK == PK_MAX) fwd_tile_max<K, NPL, ACT, FAR>(xsb, addr, w, bias, slot, out, oslot, store, lane);
-  else if constexpr (PK == PK_TOPK) fwd_tile_topk<K, NPL, ACT, FAR>(xsb, addr, w, bias, slot, out, oslot, k, store, lane);
+  else if constexpr (PK == PK_TOPK)
+    fwd_tile_topk<K, NPL, ACT, FAR, TKW>(xsb, addr, w, bias, slot, out, oslot, k, store, lane);
   else
     fwd_tile<K, NPL, ACT, FAR>(xsb, addr, w, bias, out, store, lane, mb);
 }
 
 // smooth pools: the tile needs the validity bits and the operator's parameters
-template <int K, int NPL, int ACT, bool FAR, int PK, typename SRC = const char*, typename MB = NoBits>
+template <int K, int NPL, int ACT, bool FAR, int PK, int TKW, typename SRC = const char*, typename MB = NoBits>
 __device__ __forceinline__ void fwd_tile_dispatch(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                                   const float (&bias)[NPL], const int (&slot)[NPL], unsigned vmask,
                                                   float* out, int* oslot, int k, bool store, int lane, const FwdK& p,
@@ -638,7 +733,7 @@ __device__ __forceinline__ void fwd_tile_dispatch(SRC xsb, const unsigned (&addr
     fwd_tile_smooth<K, NPL, ACT, FAR, pk_sm_op(PK)>(xsb, addr, w, bias, vmask, out, store, lane, p.scale, p.pparam,
                                                     p.pint);
   else
-    fwd_tile_any<K, NPL, ACT, FAR, PK>(xsb, addr, w, bias, slot, out, oslot, k, store, lane, mb);
+    fwd_tile_any<K, NPL, ACT, FAR, PK, TKW>(xsb, addr, w, bias, slot, out, oslot, k, store, lane, mb);
 }
 
 template <int K, int NPL, int WAVES, int ACT, bool DBUF, bool WS = false, int PK = PK_SUM, bool XG = false,
@@ -656,6 +751,10 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 16 / WAVES * WAVES / 4 : 1
   constexpr int SLOT = XB ? 8 : 4 * TB;  // bytes per input of a tile or stage
   __shared__ float4 xa[WS ? (SMALL ? XTILE_DB : 2 * XTILE_DB) : (XG ? 1 : (DBUF || SMALL ? XTILE_DB : XTILE_SB))];
   __shared__ float4 xb[DBUF ? XTILE_DB : 1];
+  // top-k: the ranked tile's per-wave candidate lists, where the CU's LDS has room for them
+  constexpr int TKW = PK == PK_TOPK && (SMALL ? 2 : 1) * (sizeof(xa) + sizeof(xb) + WAVES * 4 * TK_CAP * 8) <= 160 * 1024
+                          ? WAVES
+                          : 0;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar chunk addressing
   long long chunk = (long long)blockIdx.x * WAVES + wave;
@@ -773,7 +872,7 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 16 / WAVES * WAVES / 4 : 1
           fwd_tile_bf4<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane,
                                            mb);
         else
-          fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
+          fwd_tile_dispatch<K, NPL, ACT, false, PK, TKW>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
                                                     out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p, mb);
         bits_done(t);
         // next tile's slot; after the last tile of region 1 back to region 0
@@ -791,7 +890,7 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 16 / WAVES * WAVES / 4 : 1
     // in global memory with buffer loads (D x 16 bytes, L2-resident while the workgroups of the
     // launch read it), with no staging and no barriers
     for (int t = 0; t < p.n_tiles; ++t) {
-      fwd_tile_dispatch<K, NPL, ACT, false, PK>(xbuf(p.xt + (long long)t * p.D, p.D), addr, w, bias, slot, vmask,
+      fwd_tile_dispatch<K, NPL, ACT, false, PK, TKW>(xbuf(p.xt + (long long)t * p.D, p.D), addr, w, bias, slot, vmask,
                                                 out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p, mb);
       bits_done(t);
     }
@@ -808,7 +907,7 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 16 / WAVES * WAVES / 4 : 1
       else if constexpr (TB == 2)
         fwd_tile2<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * 2, store, lane);
       else
-        fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
+        fwd_tile_dispatch<K, NPL, ACT, false, PK, TKW>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
                                                   out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p, mb);
       bits_done(t);
       if (t + 1 < p.n_tiles) {
@@ -821,7 +920,7 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 16 / WAVES * WAVES / 4 : 1
         else if constexpr (TB == 2)
           fwd_tile2<K, NPL, ACT, true>(reinterpret_cast<const char*>(xb), addr, w, bias, out + (t + 1) * 2, store, lane);
         else
-          fwd_tile_dispatch<K, NPL, ACT, true, PK>(reinterpret_cast<const char*>(xb), addr, w, bias, slot, vmask,
+          fwd_tile_dispatch<K, NPL, ACT, true, PK, TKW>(reinterpret_cast<const char*>(xb), addr, w, bias, slot, vmask,
                                                    out + (t + 1) * BT * kp, oslot + (t + 1) * BT * kp, kp, store, lane, p,
                                                    mb);
         bits_done(t + 1);
@@ -838,7 +937,7 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 16 / WAVES * WAVES / 4 : 1
         fwd_tile_bf4<K, NPL, ACT, false>(reinterpret_cast<const char*>(xa), addr, w, bias, out + t * BT, store, lane,
                                          mb);
       else
-        fwd_tile_dispatch<K, NPL, ACT, false, PK>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
+        fwd_tile_dispatch<K, NPL, ACT, false, PK, TKW>(reinterpret_cast<const char*>(xa), addr, w, bias, slot, vmask,
                                                   out + t * BT * kp, oslot + t * BT * kp, kp, store, lane, p, mb);
       bits_done(t);
     }
@@ -1060,7 +1159,10 @@ __global__ void __launch_bounds__(256) fwd_finalize_smooth_kernel(const float* _
 // 4 neurons per lane; 16 waves per workgroup at K = 8 (4 waves per SIMD, 128 VGPRs), 8 at K = 16
 // (2 per SIMD: the parameters of 4 neurons of fan-in 16 take twice the registers).  Max pooling
 // keeps a slot per neuron and a (value, slot) pair per token: 12 waves at K = 8, 4 at K = 16;
-// top-k keeps a sorted list of 4 pairs per token: 8 waves at K = 8, 4 at K = 16.
+// top-k keeps a sorted list of 4 keys per token: 12 waves at K = 8 with the ranked tile (158 VGPRs,
+// 16-key blocks; 32-key blocks took 190 VGPRs, 2 waves per SIMD: C2 top-8 forward 54.0 ms against
+// 65.5 ms at 8 waves and 16-key blocks), 8 where the tile is single-buffered (the rounds spill 176
+// bytes at 12), 4 at K = 16.
 constexpr int FWD_NPL = 4;
 static_assert(FWD_NPL == RELU_MASK_NPL, "the forward writes the ReLU bits chunk by chunk");
 constexpr int fwd_waves(int K, int pk = PK_SUM, int act = GL_ACT_RELU) {
@@ -1068,7 +1170,7 @@ constexpr int fwd_waves(int K, int pk = PK_SUM, int act = GL_ACT_RELU) {
   // 130-136 VGPRs; C2 LogMeanExp forward 31.4 -> 26.2 ms against 8); the power mean (168 VGPRs
   // would spill 140-176 bytes per lane) and GELU neurons keep 8
   const bool sm12 = K == 8 && (pk == PK_LME || pk == PK_SW) && act != GL_ACT_GELU;
-  return K == 8 ? (pk == PK_SUM ? 16 : (pk == PK_MAX || sm12 ? 12 : 8)) : (pk == PK_SUM ? 8 : 4);
+  return K == 8 ? (pk == PK_SUM ? 16 : (pk == PK_MAX || pk == PK_TOPK || sm12 ? 12 : 8)) : (pk == PK_SUM ? 8 : 4);
 }
 static int pool_kind(int pool) {
   switch (pool) {
@@ -1188,8 +1290,11 @@ static int launch_fwd_buf(int D, const FwdK& k, hipStream_t s) {
   // mean and top-k at C2; the smooth pools measured even)
   if constexpr (W % 8 == 0 && !pk_smooth(PK))
     if (D <= XTILE_DB) return launch_fwd<K, FWD_NPL, W / 2, ACT, false, false, PK, false, true>(k, s);
+  // top-k over one single-buffered tile: no LDS left for the ranked tile's lists, and the rounds
+  // spill at 12 waves
+  constexpr int W1 = PK == PK_TOPK && K == 8 ? 8 : W;
   return D <= XTILE_DB ? launch_fwd<K, FWD_NPL, W, ACT, true, false, PK>(k, s)
-                       : launch_fwd<K, FWD_NPL, W, ACT, false, false, PK>(k, s);
+                       : launch_fwd<K, FWD_NPL, W1, ACT, false, false, PK>(k, s);
 }
 
 template <int ACT, int PK>

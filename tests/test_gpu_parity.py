@@ -645,6 +645,37 @@ def test_topk_pools_shorter_than_k(k):
     assert_parity(db.cpu().numpy().reshape(-1), wdb, mb, ub, what="db")
 
 
+@pytest.mark.parametrize("act", ["identity", "relu"])
+def test_topk_ranked_tiles_equal_the_rounds(act):
+    """k <= 8 runs the ranked tile (a lower bound of the k-th largest value, the candidates at or
+    above it ranked in an LDS list), k = 16 the extraction rounds: on the same layer the top-8 slots,
+    best first, are the first 8 of the top-16 list, bit for bit, and pre matches the oracle."""
+    D, H, G, K, B = 1024, 65536, 64, 8, 37
+    L, idx, w, b, x, _ = make_case(D, H, G, K, B)
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    s8 = _runtime_topk(L, idx, act, 8).forward(xd, wd, bd, track_ids=True)
+    s16 = _runtime_topk(L, idx, act, 16).forward(xd, wd, bd, track_ids=True)
+    assert torch.equal(s8["topk_slot"].cpu(), s16["topk_slot"].cpu()[..., :8])
+    fi, fw, fb = flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    want, _, _ = O.forward_topk(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, 8, act)
+    assert_close(s8["pre"].cpu().numpy(), want, rtol=1e-5, atol=1e-6, what="top-8 pre")
+
+
+def test_topk_all_tied_takes_the_smallest_slots():
+    """Every z of a pool equal (zero weights, one bias value): all 256 candidates of a chunk reach
+    the ranked tile's bound, more than its 64-entry lists hold, so the tile takes the rounds; the
+    top-8 are the 8 smallest slots of each pool (the reference's stable descending sort)."""
+    D, H, G, K, B = 256, 8192, 8, 8, 9
+    L, idx, w, b, x, _ = make_case(D, H, G, K, B)
+    w = torch.zeros_like(w)
+    b = torch.full_like(b, 0.25)
+    out = _runtime_topk(L, idx, "identity", 8).forward(x.to(DEV), w.to(DEV), b.to(DEV), track_ids=True)
+    slots = out["topk_slot"].cpu().numpy()
+    assert (np.sort(slots, -1) == np.arange(8)[None, None, :]).all()
+    assert torch.equal(out["pre"].cpu(), torch.full((B, G), 0.25))
+
+
 @pytest.mark.parametrize("pooling", ["sum", "mean", "max", {"type": "topk_mean", "k": 8}],
                          ids=["sum", "mean", "max", "topk8"])
 def test_empty_batch(pooling):
