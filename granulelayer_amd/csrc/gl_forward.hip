@@ -653,7 +653,7 @@ __device__ __forceinline__ void smooth_reduce(const float (&z)[NPL][4], unsigned
 // Smooth pooling tile (LogMeanExp, power mean, softmax-weighted; pytorch_reference.py:80-100): z of
 // the lane's neurons for the tile's 4 tokens, their states merged over the wave (smooth_reduce);
 // lanes 0-3 store (m, s, t) per token.
-template <int K, int NPL, int ACT, bool FAR, int OP, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
+template <int K, int NPL, int ACT, bool FAR, int OP, int PI = -1, int RA = (K == 8 ? 4 : 8), typename SRC = const char*>
 __device__ __forceinline__ void fwd_tile_smooth(SRC xsb, const unsigned (&addr)[NPL][K], const float (&w)[NPL][K],
                                                 const float (&bias)[NPL], unsigned vmask, float* out, bool store,
                                                 int lane, float scale, float p, int pint) {
@@ -687,7 +687,10 @@ __device__ __forceinline__ void fwd_tile_smooth(SRC xsb, const unsigned (&addr)[
     }
   }
   float mo, so, to;
-  if constexpr (OP == SM_POW) {
+  if constexpr (OP == SM_POW && PI > 0) {
+    // a kernel of its own per integer p: its registers are those of that power alone
+    smooth_reduce<OP, NPL>(z, vmask, lane, scale, p, PI, mo, so, to);
+  } else if constexpr (OP == SM_POW) {
     // p as a literal where it is 1, 2, 4 or 8: the inlined powers then fold to products (with p
     // read at run time the branches of every power cost 63.5 against 33.0 ms per C2 forward)
     switch (pint) {
@@ -708,8 +711,11 @@ __device__ __forceinline__ void fwd_tile_smooth(SRC xsb, const unsigned (&addr)[
 
 // pool kinds of the forward tile
 constexpr int PK_SUM = 0, PK_MAX = 1, PK_TOPK = 2, PK_LME = 3, PK_POW = 4, PK_SW = 5;
+// the power mean with p = 1, 2, 4 or 8 as a literal: PK_POW_I + p (PK_POW: p read at run time)
+constexpr int PK_POW_I = 8;
 constexpr bool pk_smooth(int pk) { return pk >= PK_LME; }
-constexpr int pk_sm_op(int pk) { return pk == PK_LME ? SM_LME : (pk == PK_POW ? SM_POW : SM_SW); }
+constexpr int pk_pint(int pk) { return pk > PK_POW_I ? pk - PK_POW_I : -1; }
+constexpr int pk_sm_op(int pk) { return pk == PK_LME ? SM_LME : (pk == PK_POW || pk_pint(pk) > 0 ? SM_POW : SM_SW); }
 
 // sum / mean, max or top-k tile
 template <int K, int NPL, int ACT, bool FAR, int PK, int TKW, typename SRC = const char*, typename MB = NoBits>
@@ -730,7 +736,7 @@ __device__ __forceinline__ void fwd_tile_dispatch(SRC xsb, const unsigned (&addr
                                                   float* out, int* oslot, int k, bool store, int lane, const FwdK& p,
                                                   MB& mb) {
   if constexpr (pk_smooth(PK))
-    fwd_tile_smooth<K, NPL, ACT, FAR, pk_sm_op(PK)>(xsb, addr, w, bias, vmask, out, store, lane, p.scale, p.pparam,
+    fwd_tile_smooth<K, NPL, ACT, FAR, pk_sm_op(PK), pk_pint(PK)>(xsb, addr, w, bias, vmask, out, store, lane, p.scale, p.pparam,
                                                     p.pint);
   else
     fwd_tile_any<K, NPL, ACT, FAR, PK, TKW>(xsb, addr, w, bias, slot, out, oslot, k, store, lane, mb);
@@ -1169,7 +1175,10 @@ constexpr int fwd_waves(int K, int pk = PK_SUM, int act = GL_ACT_RELU) {
   // LogMeanExp and softmax-weighted at fan-in 8 with ReLU or identity neurons: 12 waves (3 per SIMD,
   // 130-136 VGPRs; C2 LogMeanExp forward 31.4 -> 26.2 ms against 8); the power mean (168 VGPRs
   // would spill 140-176 bytes per lane) and GELU neurons keep 8
-  const bool sm12 = K == 8 && (pk == PK_LME || pk == PK_SW) && act != GL_ACT_GELU;
+  // the power mean with p = 1, 2 or 4 as a literal: 129-134 VGPRs at 12 waves (p = 8 and p read at
+  // run time spill 88-176 bytes per lane)
+  const bool sm12 = K == 8 && (pk == PK_LME || pk == PK_SW || (pk_pint(pk) > 0 && pk_pint(pk) < 8)) &&
+                    act != GL_ACT_GELU;
   return K == 8 ? (pk == PK_SUM ? 16 : (pk == PK_MAX || pk == PK_TOPK || sm12 ? 12 : 8)) : (pk == PK_SUM ? 8 : 4);
 }
 static int pool_kind(int pool) {
@@ -1183,6 +1192,12 @@ static int pool_kind(int pool) {
   }
 }
 static bool pool_smooth(int pool) { return pool == GL_POOL_LME || pool == GL_POOL_POWER || pool == GL_POOL_SOFTMAX; }
+static int smooth_pint(int pool, float param);
+// the forward kernel's pool kind: the power mean's integer p is part of it
+static int fwd_pool_kind(const GlFwdArgs* a) {
+  const int pi = smooth_pint(a->pool, a->pool_param);
+  return a->pool == GL_POOL_POWER && pi > 0 ? PK_POW_I + pi : pool_kind(a->pool);
+}
 
 // smooth pools: u = a * scale with scale = log2(e) / tau (LogMeanExp) or log2(e) * beta (softmax-weighted),
 // the exact-product power for p in {1, 2, 4, 8}
@@ -1220,7 +1235,7 @@ static long long fwd_part_per_token(const GlFwdArgs* a, long long n_chunks) {
 static FwdPlan fwd_plan(const GlFwdArgs* a, long long bf_cap = 0) {
   FwdPlan q;
   q.npl = FWD_NPL;
-  q.waves = fwd_waves(a->K, pool_kind(a->pool), a->act);
+  q.waves = fwd_waves(a->K, fwd_pool_kind(a), a->act);
   q.cpg = ceil_div(a->S, 64 * q.npl);
   q.n_chunks = (long long)a->G * q.cpg;
   const long long kp = a->pool == GL_POOL_TOPK_MEAN ? a->topk : (pool_smooth(a->pool) ? 3 : 1);
@@ -1304,8 +1319,12 @@ static int launch_fwd_act(int K, int D, const FwdK& k, hipStream_t s) {
 
 template <int PK>
 static int launch_fwd_any(int act, int K, int D, const FwdK& k, hipStream_t s) {
-  if (act == GL_ACT_GELU) return launch_fwd_act<GL_ACT_GELU, PK>(K, D, k, s);
-  return act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU, PK>(K, D, k, s) : launch_fwd_act<GL_ACT_IDENTITY, PK>(K, D, k, s);
+  if constexpr (pk_pint(PK) > 0) {
+    return launch_fwd_act<GL_ACT_RELU, PK>(K, D, k, s);  // the power mean is ReLU only
+  } else {
+    if (act == GL_ACT_GELU) return launch_fwd_act<GL_ACT_GELU, PK>(K, D, k, s);
+    return act == GL_ACT_RELU ? launch_fwd_act<GL_ACT_RELU, PK>(K, D, k, s) : launch_fwd_act<GL_ACT_IDENTITY, PK>(K, D, k, s);
+  }
 }
 
 // Window staging applies when the staged windows of a workgroup's pools (npw of them, each ww
@@ -1453,7 +1472,13 @@ static int fwd_run(const GlFwdArgs* a, void* ws, const FwdPlan& q, hipStream_t s
         GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_smooth_kernel<SM_LME>, g1, dim3(256), 0, s, part, a->counts, pre,
                   lse, Bc, a->G, q.cpg, b_pad, k.scale, k.pparam, k.pint);
       } else if (a->pool == GL_POOL_POWER) {
-        GL_TRY(launch_fwd_any<PK_POW>(a->act, a->K, a->D, k, s));
+        switch (k.pint) {  // a kernel per integer p (12 waves per workgroup at K = 8)
+          case 1: GL_TRY(launch_fwd_any<PK_POW_I + 1>(a->act, a->K, a->D, k, s)); break;
+          case 2: GL_TRY(launch_fwd_any<PK_POW_I + 2>(a->act, a->K, a->D, k, s)); break;
+          case 4: GL_TRY(launch_fwd_any<PK_POW_I + 4>(a->act, a->K, a->D, k, s)); break;
+          case 8: GL_TRY(launch_fwd_any<PK_POW_I + 8>(a->act, a->K, a->D, k, s)); break;
+          default: GL_TRY(launch_fwd_any<PK_POW>(a->act, a->K, a->D, k, s));
+        }
         GL_LAUNCH(GL_KERNEL_FWD_FINALIZE, fwd_finalize_smooth_kernel<SM_POW>, g1, dim3(256), 0, s, part, a->counts, pre,
                   lse, Bc, a->G, q.cpg, b_pad, k.scale, k.pparam, k.pint);
       } else {
