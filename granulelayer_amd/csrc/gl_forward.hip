@@ -404,15 +404,17 @@ __device__ __forceinline__ unsigned wave_max4_u32(unsigned a0, unsigned a1, unsi
 // store each round's pair; the finalize merges the pool's chunks.
 //
 // Ranked path (TKW > 0 waves per workgroup, k <= 8): no rounds.  A lower bound of every token's
-// k-th largest value comes from windows of 32 candidates (two neighbouring lane quads of a row):
-// of the 16 windows, 8 are disjoint, so the smallest window maximum is at most the 8th largest
-// value.  The candidates at or above the bound (~20 of 256 on random data) are compacted into a
+// k-th largest value: the 8th largest of its 16 lane-quad maxima (16 disjoint sets of candidates,
+// so 8 distinct candidates lie at or above it; a bitonic sort across the quads finds it).  The
+// candidates at or above the bound (~10 of 256 on random data) are compacted into a
 // per-wave LDS list per token (ballot, mbcnt, zero keys to a multiple of 16); each then counts the
 // list's larger keys (16-key blocks, all reads of a block in flight together) for its rank and
 // stores itself at that position.  Same keys, same order: the output is the rounds' output, bit for
 // bit.  A token with more than 64 candidates at the bound (ties, or a chunk of mostly padded slots
 // at -inf) sends the tile to the rounds.  At C2 (top-8) the ranked tile took the forward from 68.9
-// to 65.5 ms at 8 waves per workgroup, and its 158 VGPRs allow 12 (54.0 ms).
+// to 65.5 ms at 8 waves per workgroup, and its 158 VGPRs allow 12 (54.0 ms); the quad-maxima
+// bound then took it to 45.4 ms against the smallest maximum of 32-candidate windows (~24
+// survivors per token).
 constexpr int TK_CAP = 64;  // keys per token list
 // the lists of a workgroup of TKW waves (one array per kernel, whichever tiles use it)
 template <int TKW>
@@ -474,21 +476,36 @@ __device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NP
       const unsigned b0 = umax(odd ? o[2][0] : o[0][0], dppu<0xB1>(odd ? o[0][0] : o[2][0]));
       const unsigned b1 = umax(odd ? o[3][0] : o[1][0], dppu<0xB1>(odd ? o[1][0] : o[3][0]));
       unsigned q = umax(hi2 ? b1 : b0, dppu<0x4E>(hi2 ? b0 : b1));
-      q = umax(q, dppu<0x124>(q));  // a window: this quad and its row neighbour (32 candidates)
-      q = umin(q, dppu<0x124>(q));  // the smallest of the row's 4 windows
-      q = umin(q, dppu<0x128>(q));
-      {
-        const auto p16 = __builtin_amdgcn_permlane16_swap(q, q, false, false);
-        q = umin(p16[0], p16[1]);
-        const auto p32 = __builtin_amdgcn_permlane32_swap(q, q, false, false);
-        q = umin(p32[0], p32[1]);
+      // bitonic sort (ascending) of each token's 16 quad maxima across the quads (element i = lane
+      // bits 2-5; partner i ^ jj = lane ^ 4 jj): the 8th largest ends in quad 8.  Each exchange
+      // yields the pair {own, partner} in some order, so min / max of the pair need no direction.
+      const int qi = lane >> 2;
+#pragma unroll
+      for (int kk = 2; kk <= 16; kk <<= 1) {
+#pragma unroll
+        for (int jj = kk >> 1; jj >= 1; jj >>= 1) {
+          unsigned a = q, b;
+          if (jj == 8) {
+            const auto pr = __builtin_amdgcn_permlane32_swap(q, q, false, false);
+            a = pr[0], b = pr[1];
+          } else if (jj == 4) {
+            const auto pr = __builtin_amdgcn_permlane16_swap(q, q, false, false);
+            a = pr[0], b = pr[1];
+          } else if (jj == 2) {
+            b = dppu<0x128>(q);  // row_ror:8 within a 16-lane row: lane ^ 8
+          } else {
+            b = (unsigned)__builtin_amdgcn_ds_swizzle((int)q, 0x101f);  // lane ^ 4
+          }
+          const bool keep_min = ((qi & jj) == 0) == ((qi & kk) == 0);
+          q = keep_min ? umin(a, b) : umax(a, b);
+        }
       }
       unsigned long long m[4][4];
       int n[4];
       bool over = false;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const unsigned bnd = (unsigned)__builtin_amdgcn_readlane((int)q, (t == 1) ? 2 : (t == 2) ? 1 : t);
+        const unsigned bnd = (unsigned)__builtin_amdgcn_readlane((int)q, 32 + ((t == 1) ? 2 : (t == 2) ? 1 : t));
         n[t] = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {  // a lane's list is sorted: its survivors are a prefix
