@@ -414,8 +414,10 @@ __device__ __forceinline__ unsigned wave_max4_u32(unsigned a0, unsigned a1, unsi
 // at -inf) sends the tile to the rounds.  At C2 (top-8) the ranked tile took the forward from 68.9
 // to 65.5 ms at 8 waves per workgroup, and its 158 VGPRs allow 12 (54.0 ms); the quad-maxima
 // bound then took it to 45.4 ms against the smallest maximum of 32-candidate windows (~24
-// survivors per token).
-constexpr int TK_CAP = 64;  // keys per token list
+// survivors per token), and ranking the 4 tokens together to 39.1 ms.
+// keys per token list: 64, and 2 more so that the 4 tokens' lists start 4 banks apart (the
+// 4-token rank reads one 16-byte slot of each list in one ds_read_b128)
+constexpr int TK_CAP = 66;
 // the lists of a workgroup of TKW waves (one array per kernel, whichever tiles use it)
 template <int TKW>
 __device__ __forceinline__ cand_t* tk_lists() {
@@ -534,21 +536,39 @@ __device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NP
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (n[0] <= 16 && n[1] <= 16 && n[2] <= 16 && n[3] <= 16) {
+          // every list fits one 16-key block: lanes 16 t .. 16 t + 15 rank token t's list together
+          const int tl = lane >> 4, il = lane & 15;
+          const int nt = tl == 0 ? n[0] : (tl == 1 ? n[1] : (tl == 2 ? n[2] : n[3]));
+          const cand_t* Lt = L + tl * TK_CAP;
+          const cand_t mine = Lt[il];
+          ulonglong2 kv[8];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const cand_t* Lt = L + t * TK_CAP;
-          const cand_t mine = Lt[lane < n[t] ? lane : 0];
+          for (int i = 0; i < 8; ++i) kv[i] = *reinterpret_cast<const ulonglong2*>(Lt + 2 * i);
           unsigned r = 0;
-          for (int j0 = 0; j0 < n[t]; j0 += 16) {  // blocks of 16 keys, all reads issued first
-            ulonglong2 kv[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) kv[i] = *reinterpret_cast<const ulonglong2*>(Lt + j0 + 2 * i);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) r += (kv[i].x > mine) + (kv[i].y > mine);
+          for (int i = 0; i < 8; ++i) r += (kv[i].x > mine) + (kv[i].y > mine);
+          if (store && il < nt && r < (unsigned)k) {
+            out[tl * k + (int)r] = cand_value(mine);
+            oslot[tl * k + (int)r] = (int)~(unsigned)mine;
           }
-          if (store && lane < n[t] && r < (unsigned)k) {
-            out[t * k + (int)r] = cand_value(mine);
-            oslot[t * k + (int)r] = (int)~(unsigned)mine;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const cand_t* Lt = L + t * TK_CAP;
+            const cand_t mine = Lt[lane < n[t] ? lane : 0];
+            unsigned r = 0;
+            for (int j0 = 0; j0 < n[t]; j0 += 16) {  // blocks of 16 keys, all reads issued first
+              ulonglong2 kv[8];
+#pragma unroll
+              for (int i = 0; i < 8; ++i) kv[i] = *reinterpret_cast<const ulonglong2*>(Lt + j0 + 2 * i);
+#pragma unroll
+              for (int i = 0; i < 8; ++i) r += (kv[i].x > mine) + (kv[i].y > mine);
+            }
+            if (store && lane < n[t] && r < (unsigned)k) {
+              out[t * k + (int)r] = cand_value(mine);
+              oslot[t * k + (int)r] = (int)~(unsigned)mine;
+            }
           }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the next tile's lists overwrite these
