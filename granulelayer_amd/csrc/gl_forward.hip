@@ -459,24 +459,21 @@ __device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NP
       for (int kk = 0; kk < RA; ++kk) xc[kk] = xn[kk];
     }
   }
-  unsigned o[4][4], sl[4][4];  // the sorted lists as value-order and ~slot words
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {  // sorting network for 4
-    cand_cmpex(c[t][0], c[t][1]);
-    cand_cmpex(c[t][2], c[t][3]);
-    cand_cmpex(c[t][0], c[t][2]);
-    cand_cmpex(c[t][1], c[t][3]);
-    cand_cmpex(c[t][1], c[t][2]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[t][i] = (unsigned)(c[t][i] >> 32), sl[t][i] = (unsigned)c[t][i];
-  }
   if constexpr (TKW > 0) {
     if (k <= 8) {
-      // the lane's best value order per token, reduce-scattered to quads as in wave_max4_u32: lane l
-      // ends with its quad's maximum for token wave_sum4_token(l)
+      // value-order words of the lane's (unsorted) candidates; the lane's best per token,
+      // reduce-scattered to quads as in wave_max4_u32: lane l ends with its quad's maximum for token
+      // wave_sum4_token(l)
+      unsigned hw[4][4], h[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hw[t][i] = (unsigned)(c[t][i] >> 32);
+        h[t] = umax(umax(hw[t][0], hw[t][1]), umax(hw[t][2], hw[t][3]));
+      }
       const bool odd = lane & 1, hi2 = lane & 2;
-      const unsigned b0 = umax(odd ? o[2][0] : o[0][0], dppu<0xB1>(odd ? o[0][0] : o[2][0]));
-      const unsigned b1 = umax(odd ? o[3][0] : o[1][0], dppu<0xB1>(odd ? o[1][0] : o[3][0]));
+      const unsigned b0 = umax(odd ? h[2] : h[0], dppu<0xB1>(odd ? h[0] : h[2]));
+      const unsigned b1 = umax(odd ? h[3] : h[1], dppu<0xB1>(odd ? h[1] : h[3]));
       unsigned q = umax(hi2 ? b1 : b0, dppu<0x4E>(hi2 ? b0 : b1));
       // bitonic sort (ascending) of each token's 16 quad maxima across the quads (element i = lane
       // bits 2-5; partner i ^ jj = lane ^ 4 jj): the 8th largest ends in quad 8.  Each exchange
@@ -510,8 +507,8 @@ __device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NP
         const unsigned bnd = (unsigned)__builtin_amdgcn_readlane((int)q, 32 + ((t == 1) ? 2 : (t == 2) ? 1 : t));
         n[t] = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {  // a lane's list is sorted: its survivors are a prefix
-          m[t][i] = __builtin_amdgcn_ballot_w64(o[t][i] >= bnd);
+        for (int i = 0; i < 4; ++i) {  // any of a lane's 4 candidates may reach the bound
+          m[t][i] = __builtin_amdgcn_ballot_w64(hw[t][i] >= bnd);
           n[t] += (int)__builtin_popcountll(m[t][i]);
         }
         over |= n[t] > 64;
@@ -523,7 +520,7 @@ __device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NP
           int base = t * TK_CAP;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            if (m[t][i] == 0) break;
+            if (m[t][i] == 0) continue;
             const unsigned pos = __builtin_amdgcn_mbcnt_hi((unsigned)(m[t][i] >> 32),
                                                            __builtin_amdgcn_mbcnt_lo((unsigned)m[t][i], 0u));
             if ((m[t][i] >> lane) & 1) L[base + (int)pos] = c[t][i];
@@ -577,6 +574,17 @@ __device__ __forceinline__ void fwd_tile_topk(SRC xsb, const unsigned (&addr)[NP
         return;
       }
     }
+  }
+  unsigned o[4][4], sl[4][4];  // the sorted lists as value-order and ~slot words
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {  // sorting network for 4
+    cand_cmpex(c[t][0], c[t][1]);
+    cand_cmpex(c[t][2], c[t][3]);
+    cand_cmpex(c[t][0], c[t][2]);
+    cand_cmpex(c[t][1], c[t][3]);
+    cand_cmpex(c[t][1], c[t][2]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[t][i] = (unsigned)(c[t][i] >> 32), sl[t][i] = (unsigned)c[t][i];
   }
   constexpr unsigned NONE_O = (unsigned)(CAND_NONE >> 32), NONE_S = (unsigned)CAND_NONE;
   const int tok = wave_sum4_token(lane);
