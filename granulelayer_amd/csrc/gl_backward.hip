@@ -1163,6 +1163,16 @@ struct BsK {
   int wbf;      // W and bias stored as bf16 (widened in the kernel)
 };
 
+// one step of a 4 x 4 transpose within a lane quad: lanes with b set give a, take the partner's c
+template <int CTRL>
+__device__ __forceinline__ void qswap(float4& a, float4& c, bool b) {
+  // component-wise selects (a select of the two references would put the array in memory)
+  const float s0 = b ? a.x : c.x, s1 = b ? a.y : c.y, s2 = b ? a.z : c.z, s3 = b ? a.w : c.w;
+  const float r0 = dpp<CTRL>(s0), r1 = dpp<CTRL>(s1), r2 = dpp<CTRL>(s2), r3 = dpp<CTRL>(s3);
+  a = make_float4(b ? r0 : a.x, b ? r1 : a.y, b ? r2 : a.z, b ? r3 : a.w);
+  c = make_float4(b ? c.x : r0, b ? c.y : r1, b ? c.z : r2, b ? c.w : r3);
+}
+
 // Neuron-stationary recompute pass of a smooth pool: per token tile z, dz = c1 f(z, c2, c3), db and dW
 // accumulated in registers over the chunk's tokens and added to the caller's buffers once; dz of
 // every valid neuron stored for the dX pass.  Token tiles stream through LDS as in bwd_w_kernel.
@@ -1276,13 +1286,54 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
       __syncthreads();
     }
    }
+    if constexpr (SB == 8) {
+      // 4 x 4 transposes within each lane quad of pieces 0-3 and 4-7 of the runs: lane 4g + i ends
+      // with piece 4h + i of neuron 4g + e's run in dzb[j][4h + e], so each store writes 64
+      // contiguous bytes per quad where the lanes' own runs wrote 16 bytes per lane (a row apart):
+      // C2 LogMeanExp recompute 36.2 -> 31.3 ms per 128-token chunk
+      const bool q1 = lane & 1, q2 = lane & 2;
+      const int qi = lane & 3;
 #pragma unroll
-    for (int j = 0; j < NPL; ++j)
-      if (active && slot[j] >= 0) {
-        float4* dst = reinterpret_cast<float4*>(p.dz + (nb + slot[j]) * (long long)p.cap + t0 * BT);
-#pragma unroll
-        for (int tt = 0; tt < SB; ++tt) dst[tt] = dzb[j][tt];
+      for (int j = 0; j < NPL; ++j) {
+        qswap<0xB1>(dzb[j][0], dzb[j][1], q1);
+        qswap<0xB1>(dzb[j][2], dzb[j][3], q1);
+        qswap<0x4E>(dzb[j][0], dzb[j][2], q2);
+        qswap<0x4E>(dzb[j][1], dzb[j][3], q2);
+        qswap<0xB1>(dzb[j][4], dzb[j][5], q1);
+        qswap<0xB1>(dzb[j][6], dzb[j][7], q1);
+        qswap<0x4E>(dzb[j][4], dzb[j][6], q2);
+        qswap<0x4E>(dzb[j][5], dzb[j][7], q2);
+        // the slots of the quad's 4 neurons (quad_perm broadcasts; -1: past the pool)
+        const int s0 = __builtin_amdgcn_update_dpp(0, slot[j], 0x00, 0xf, 0xf, false);
+        const int s1 = __builtin_amdgcn_update_dpp(0, slot[j], 0x55, 0xf, 0xf, false);
+        const int s2 = __builtin_amdgcn_update_dpp(0, slot[j], 0xAA, 0xf, 0xf, false);
+        const int s3 = __builtin_amdgcn_update_dpp(0, slot[j], 0xFF, 0xf, 0xf, false);
+        if (active && s0 >= 0) {
+          float4* dst = reinterpret_cast<float4*>(p.dz + (nb + s0) * (long long)p.cap + t0 * BT);
+          dst[qi] = dzb[j][0], dst[4 + qi] = dzb[j][4];
+        }
+        if (active && s1 >= 0) {
+          float4* dst = reinterpret_cast<float4*>(p.dz + (nb + s1) * (long long)p.cap + t0 * BT);
+          dst[qi] = dzb[j][1], dst[4 + qi] = dzb[j][5];
+        }
+        if (active && s2 >= 0) {
+          float4* dst = reinterpret_cast<float4*>(p.dz + (nb + s2) * (long long)p.cap + t0 * BT);
+          dst[qi] = dzb[j][2], dst[4 + qi] = dzb[j][6];
+        }
+        if (active && s3 >= 0) {
+          float4* dst = reinterpret_cast<float4*>(p.dz + (nb + s3) * (long long)p.cap + t0 * BT);
+          dst[qi] = dzb[j][3], dst[4 + qi] = dzb[j][7];
+        }
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NPL; ++j)
+        if (active && slot[j] >= 0) {
+          float4* dst = reinterpret_cast<float4*>(p.dz + (nb + slot[j]) * (long long)p.cap + t0 * BT);
+#pragma unroll
+          for (int tt = 0; tt < SB; ++tt) dst[tt] = dzb[j][tt];
+        }
+    }
   }
   if (!active) return;
 #pragma unroll
