@@ -662,6 +662,27 @@ def test_topk_ranked_tiles_equal_the_rounds(act):
     assert_close(s8["pre"].cpu().numpy(), want, rtol=1e-5, atol=1e-6, what="top-8 pre")
 
 
+def test_topk_tied_levels_rank_token_by_token():
+    """z on 8 levels (zero weights, each neuron's bias one of 8 values): ~32 of a chunk's 256
+    candidates share the top level, so a token's list holds 17-64 keys and the ranked tile ranks
+    token by token (not 4 tokens at once); the ties go to the smaller slots. The top-8 slots
+    equal the first 8 of the rounds' top-16 list, and pre matches the oracle."""
+    D, H, G, K, B = 256, 32768, 32, 8, 9
+    L, idx, w, b, x, _ = make_case(D, H, G, K, B)
+    w = torch.zeros_like(w)
+    gen = torch.Generator().manual_seed(7)
+    b = (torch.randint(0, 8, b.shape, generator=gen).float() * 0.125).contiguous()
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    s8 = _runtime_topk(L, idx, "identity", 8).forward(xd, wd, bd, track_ids=True)
+    s16 = _runtime_topk(L, idx, "identity", 16).forward(xd, wd, bd, track_ids=True)
+    assert torch.equal(s8["topk_slot"].cpu(), s16["topk_slot"].cpu()[..., :8])
+    fi, fw, fb = flat(L, idx, w, b)
+    counts = L.counts_tensor("cpu").numpy()
+    want, wslots, _ = O.forward_topk(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, 8, "identity")
+    assert_close(s8["pre"].cpu().numpy(), want, rtol=1e-6, atol=1e-7, what="top-8 pre")
+    assert (np.sort(s8["topk_slot"].cpu().numpy(), -1) == np.sort(wslots, -1)).all()
+
+
 def test_topk_all_tied_takes_the_smallest_slots():
     """Every z of a pool equal (zero weights, one bias value): all 256 candidates of a chunk reach
     the ranked tile's bound, more than its 64-entry lists hold, so the tile takes the rounds; the
