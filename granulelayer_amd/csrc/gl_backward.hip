@@ -1325,6 +1325,19 @@ __global__ void __launch_bounds__(WAVES * 64) bwd_smooth_kernel(BsK p) {
           dst[qi] = dzb[j][3], dst[4 + qi] = dzb[j][7];
         }
       }
+    } else if constexpr (SB == 2) {
+      // fan-in 16 (2-tile runs): a 2 x 2 transpose within each lane pair, so each store writes 32
+      // contiguous bytes per pair (C5-shape LogMeanExp recompute 66.1 -> 60.8 ms per 256-token chunk)
+      const bool q1 = lane & 1;
+      const int qi = lane & 1;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        qswap<0xB1>(dzb[j][0], dzb[j][1], q1);
+        const int s0 = __builtin_amdgcn_update_dpp(0, slot[j], 0xA0, 0xf, 0xf, false);  // quad_perm(0,0,2,2)
+        const int s1 = __builtin_amdgcn_update_dpp(0, slot[j], 0xF5, 0xf, 0xf, false);  // quad_perm(1,1,3,3)
+        if (active && s0 >= 0) reinterpret_cast<float4*>(p.dz + (nb + s0) * (long long)p.cap + t0 * BT)[qi] = dzb[j][0];
+        if (active && s1 >= 0) reinterpret_cast<float4*>(p.dz + (nb + s1) * (long long)p.cap + t0 * BT)[qi] = dzb[j][1];
+      }
     } else {
 #pragma unroll
       for (int j = 0; j < NPL; ++j)
