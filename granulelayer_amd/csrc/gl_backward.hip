@@ -1422,8 +1422,11 @@ __global__ void __launch_bounds__(64) dx_dense_kernel(DxK p, const float* __rest
       }
       __syncthreads();
       // DB edges at a time: their dz rows are loaded together (DB loads in flight per wave, where
-      // one dependent load per edge exposed each load's latency), then added in edge order
-      constexpr int DB = T == 4 ? 4 : 8;
+      // one dependent load per edge exposed each load's latency), then added in edge order.  With
+      // the unit-range passes most rows come from the caches, and fewer rows in flight (fewer
+      // VGPRs, more waves) pay: at 2 tokens per lane (C2, 128-token chunks) 3.63 / 3.37 / 3.24 /
+      // 3.40 ms per pass for DB = 8 / 4 / 3 / 2; at 4 tokens per lane (C5 shape) DB = 4 3.58 ms, 2 3.99
+      constexpr int DB = T == 4 ? 4 : (T == 2 ? 3 : 8);
       for (int i0 = 0; i0 < n; i0 += DB) {
         float v[DB][T], wv[DB];
         int f[DB];
