@@ -271,8 +271,9 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 4 : 1) bwd_w_kernel(BwK p)
   // XG (D > XTILE_SB): no LDS tile, the lanes gather from the token tiles in global memory.
   // TB: tokens per tile, 4 or 2 (two-token tiles in the two buffers of DBUF: D <= 2 XTILE_DB)
   static_assert(TB == BT || (TB == 2 && DBUF && !WS && !XG), "two-token tiles: double-buffered only");
-  // XB: 4-token tiles of raw bf16 (8-byte slots, bf16 X), double-buffered
-  static_assert(!XB || (TB == BT && (DBUF || SMALL) && !WS && !XG), "bf16 tiles: double- or small-buffered");
+  // XB: 4-token tiles of raw bf16 (8-byte slots, bf16 X), double- or small-buffered, or pool windows
+  // staged from them
+  static_assert(!XB || (TB == BT && (DBUF || SMALL || WS) && !XG), "bf16 tiles: double- or small-buffered, windows");
   // SMALL: one single-buffered 64-KiB tile per workgroup, two workgroups per CU (128 VGPRs at most)
   static_assert(!SMALL || (!DBUF && !WS && !XG && TB == BT), "small: one 4-token tile per workgroup");
   // FM: the mask bits come from the forward (p.fm): no z recompute, W and bias are not read
@@ -314,7 +315,7 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 4 : 1) bwd_w_kernel(BwK p)
         const int k = sched_k<K>(order, ks);
         int d = rec_index(p.idx, n, k, K, p.rs);
         d = (d < 0 || !valid) ? 0 : (d >= p.D ? p.D - 1 : d);  // host validates; clamp keeps LDS reads in bounds
-        addr[j][ks] = win_addr(d, pk, lo, p.ww);
+        addr[j][ks] = win_addr<SLOT>(d, pk, lo, p.ww);
         if constexpr (!FM) {
           const float wl = ld_param(p.W, p.wbf, n * K + k);
           w[j][ks] = valid ? wl : 0.f;
@@ -378,9 +379,10 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 4 : 1) bwd_w_kernel(BwK p)
   // window staging: WS_TILES tiles per stage and barrier; tile t at slot (t mod 2 WS_TILES) * nsl
   const WinLayout L{p.win, p.ww, p.npw, g_first, p.G};
   const int nsl = p.npw * p.ww;
-  const unsigned tstep = (unsigned)nsl * 16u;
+  const unsigned tstep = (unsigned)nsl * SLOT;
+  const int rslots = WS_TILES * nsl * (int)SLOT / 16;  // 16-byte slots per stage region
   if constexpr (WS) {
-    dma_window_stage(p.xt, xs, 0, p.n_tiles, p.D, L, WAVES);
+    dma_window_stage<SLOT>(p.xt, xs, 0, p.n_tiles, p.D, L, WAVES);
     stage_wait();
     __syncthreads();
   } else if constexpr (DBUF) {
@@ -410,13 +412,17 @@ __global__ void __launch_bounds__(WAVES * 64, SMALL ? 4 : 1) bwd_w_kernel(BwK p)
         const int r = (ts0 / WS_TILES) & 1;
         // region r ^ 1 was last read in the previous stage, which every wave finished before the barrier
         if (ts0 + WS_TILES < p.n_tiles)
-          dma_window_stage(p.xt, xs + (r ^ 1) * WS_TILES * nsl, ts0 + WS_TILES, p.n_tiles, p.D, L, WAVES);
+          dma_window_stage<SLOT>(p.xt, xs + (r ^ 1) * rslots, ts0 + WS_TILES, p.n_tiles, p.D, L, WAVES);
         const int tn = p.n_tiles - ts0 < WS_TILES ? p.n_tiles - ts0 : WS_TILES;
         for (int tt = 0; tt < tn; ++tt) {
           const int t = ts0 + tt;
           const float4 c1 = ld_uniform4(c1row, t * BT);
-          bwd_w_tile<K, NPL, ACT, RA, false, const char*, FM>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias,
-                                                             dw, dbv, mw, fbits(t));
+          if constexpr (XB)
+            bwd_w_tile_bf4<K, NPL, ACT, RA, false, FM>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias, dw, dbv,
+                                                       mw, fbits(t));
+          else
+            bwd_w_tile<K, NPL, ACT, RA, false, const char*, FM>(reinterpret_cast<const char*>(xs), t, c1, addr, w, bias,
+                                                               dw, dbv, mw, fbits(t));
           // next tile's slot; after the last tile of region 1 back to region 0 (uniform step, no branch)
           const unsigned step = (t & (2 * WS_TILES - 1)) == 2 * WS_TILES - 1 ? tstep - 2u * WS_TILES * tstep : tstep;
 #pragma unroll
@@ -1629,7 +1635,8 @@ void edge_layout(int D, int G, int S, int K, EdgeHeader* h, size_t* total) {
 
 template <int K, int NPL, int WAVES, int ACT, int RA>
 static int launch_bwd_w(const BwK& k, hipStream_t s) {
-  auto fn = k.win ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, true>
+  auto fn = k.win ? (k.xb ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, true, false, BT, true>
+                          : bwd_w_kernel<K, NPL, WAVES, ACT, RA, false, true>)
                   : k.xb ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true, false, false, BT, true>
                   : k.tb == 2 ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true, false, false, 2>
                   : (k.D <= XTILE_DB ? bwd_w_kernel<K, NPL, WAVES, ACT, RA, true>
@@ -1660,8 +1667,9 @@ static int launch_bwd_w_fm(const BwK& k, hipStream_t s) {
   }
   if (k.win) {
     constexpr int WW = BWD_FM_WIN_WAVES;
-    GL_LAUNCH(GL_KERNEL_BWD_W_WIN, (bwd_w_kernel<K, NPL, WW, A, BWD_FM_WIN_RA, false, true, false, BT, false, true>),
-              dim3((unsigned)ceil_div(k.n_chunks, WW)), dim3(WW * 64), 0, s, k);
+    auto fw = k.xb ? bwd_w_kernel<K, NPL, WW, A, BWD_FM_WIN_RA, false, true, false, BT, true, true>
+                   : bwd_w_kernel<K, NPL, WW, A, BWD_FM_WIN_RA, false, true, false, BT, false, true>;
+    GL_LAUNCH(GL_KERNEL_BWD_W_WIN, fw, dim3((unsigned)ceil_div(k.n_chunks, WW)), dim3(WW * 64), 0, s, k);
     GL_CHECK_LAUNCH();
     return 0;
   }
@@ -1848,11 +1856,17 @@ extern "C" int gl_bwd(const GlBwdArgs* a, void* stream) {
     // the staged windows cover the pools of one workgroup: size them for the dW launch that runs
     // (16 waves with the forward's ReLU bits, else bwd_waves)
     const int dw_waves = a->relu_mask && a->K == 8 ? BWD_FM_WIN_WAVES : q.waves;
-    const bool win = dense && window_staging(a->win, a->win_width, a->D, dw_waves, q.cpg, a->G, &ww, &npw);
+    // bf16 X staged in pool windows keeps its bf16 values (8-byte inputs, windows from an even input),
+    // as the forward's windows do: with the forward's ReLU bits (159 VGPRs) or identity neurons;
+    // the ReLU recompute at 12 waves would spill 60 bytes per lane, and keeps fp32 windows
+    const bool xbw = dense && a->x_dtype == GL_DTYPE_BF16 && a->D % 2 == 0 && a->D <= 2 * XTILE_DB &&
+                     (a->relu_mask || a->act == GL_ACT_IDENTITY);
+    const bool win = dense && window_staging(a->win, a->win_width, a->D, dw_waves, q.cpg, a->G, &ww, &npw, WS_SLOTS,
+                                             xbw ? 8 : 16);
     const bool wide = dense && !win && tiles_of_two(a->D);
     // bf16 X keeps its bf16 values, 4 tokens per 8-byte slot (C4 dW 114.3 -> 90.2 ms against
     // two-token fp32 tiles: half the gathers and tile overheads per token for one widening per value)
-    const bool xb = wide && a->x_dtype == GL_DTYPE_BF16;
+    const bool xb = (wide && a->x_dtype == GL_DTYPE_BF16) || (win && xbw);
     const int tb = wide && !xb ? 2 : BT;
     if (xb)
       GL_TRY(launch_tile_x_bf16x4(a->X, a->sxb, a->B, a->D, b0, n_tiles, xt, s));

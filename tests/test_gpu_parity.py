@@ -120,12 +120,14 @@ WIN_CASES = [(2048, 8192, 8, 8, 37, 256), (1536, 4800, 16, 8, 70, 120), (2048, 2
              (2048, 8192, 8, 8, 300, 256)]
 
 
+@pytest.mark.parametrize("act", ["relu", "identity"])
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("case", WIN_CASES, ids=lambda c: f"D{c[0]}H{c[1]}G{c[2]}K{c[3]}B{c[4]}w{c[5]}")
-def test_window_staging_matches_full_staging_and_oracle(case, x_dtype):
+def test_window_staging_matches_full_staging_and_oracle(case, x_dtype, act):
     """Pool-window staging (gl_window_build_host) runs the window kernels and gives bit-identical
     results to full-width staging, within the oracle's bar.  bf16 X stages 4 raw bf16 tokens per
-    8-byte input (windows from an even input) in the forward, fp32 X 16-byte inputs."""
+    8-byte input (windows from an even input) in the forward, and in the dW pass of identity neurons
+    (and of ReLU neurons with the forward's bits, test_gpu_relu_bits.py); fp32 X 16-byte inputs."""
     from granulelayer_amd import _native as N
 
     D, H, G, K, B, width = case
@@ -135,7 +137,7 @@ def test_window_staging_matches_full_staging_and_oracle(case, x_dtype):
     try:
         for ws in (True, False):
             be.window_staging = ws
-            rt = runtime(L, idx, "sum", "relu")
+            rt = runtime(L, idx, "sum", act)
             dw = torch.zeros(L.weight_shape, device=DEV)
             db = torch.zeros(L.bias_shape, device=DEV)
             with N.KernelTrace() as tr:
@@ -154,9 +156,9 @@ def test_window_staging_matches_full_staging_and_oracle(case, x_dtype):
     pre, dw, db, dx = (t.numpy() for t in outs[True])
     fi, fw, fb = flat(L, idx, w, b)
     counts = L.counts_tensor("cpu").numpy()
-    want, mag = O.forward(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, "relu", "sum", with_mag=True)
+    want, mag = O.forward(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, act, "sum", with_mag=True)
     assert_parity(pre, want, mag, what="pre")
-    wdW, wdb, wdX, bnd = O.backward(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, dy.numpy(), "relu", "sum",
+    wdW, wdb, wdX, bnd = O.backward(x.float().numpy(), fi, fw, fb, counts, L.slots_per_group, dy.numpy(), act, "sum",
                                     with_bounds=True)
     (mW, mb, mX), (uW, ub, uX) = bnd["mag"], bnd["unc"]
     assert_parity(dx, wdX, mX, uX, what="dX")
